@@ -1,0 +1,253 @@
+/*
+ * tx_plugin.h -- C ABI of libtxamd.so, the MI355X (gfx950) op library that
+ * replaces the data-parallel ops Triton lowers for the reference's plugin path.
+ *
+ * Two layers, both plain C (no HIP, torch or MLIR types cross this boundary):
+ *
+ *  1. The registration surface.  txGetPluginInfo() returns a table of ops in
+ *     the shape of the reference's PluginInfo (support/Export.h:15,
+ *     support/Export.cpp:58-97, extensions/utlx/uTLXPlugin.cpp:700-814):
+ *     {api_version, name, version, ops*, num_ops, target}.  Each entry is
+ *     {name, fn, signature}, keyed by the Triton op it implements.  The op
+ *     calling convention follows the reference's OpInfo callbacks
+ *     (uTLXPlugin.cpp:40-50, ops/NewOps.cpp:295-302): operands[0] is the
+ *     result slot, inputs start at operands[1], scalar options follow as
+ *     integer constants.  Unlike the reference, txReleasePluginInfo is
+ *     defined (it is only declared at support/Export.h:17).
+ *
+ *  2. Typed entry points, one per op, taking device pointers, sizes, strides
+ *     and a stream.  The table's fn pointers unpack operands and call these.
+ *
+ * Conventions (all entry points):
+ *  - The caller owns every device buffer; no entry point allocates device
+ *    memory.  The library owns its code-object handles, loaded once per
+ *    device on first use (or by txInit) and unloaded by txShutdown.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *    and is stream-ordered; entry points return after enqueueing.
+ *  - Errors are returned as tx_status (0 = success, as TP_SUCCESS in
+ *    support/Export.h:25-28); txGetLastError() gives the calling thread's
+ *    last message.  No exception or abort crosses the ABI.
+ *  - Entry points are reentrant; concurrent calls on different streams are
+ *    allowed.
+ */
+#ifndef TX_PLUGIN_H
+#define TX_PLUGIN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define TX_API __attribute__((visibility("default")))
+#else
+#define TX_API
+#endif
+
+#define TX_PLUGIN_API_VERSION 1u
+
+typedef void *tx_stream_t; /* hipStream_t */
+
+typedef enum tx_status {
+  TX_SUCCESS = 0,            /* TP_SUCCESS, support/Export.h:26 */
+  TX_GENERIC_FAILURE = 1,    /* TP_GENERIC_FAILURE, support/Export.h:27 */
+  TX_INVALID_ARGUMENT = 2,   /* null pointer, negative size, bad stride */
+  TX_UNSUPPORTED = 3,        /* valid request this library does not serve */
+  TX_NO_DEVICE = 4,          /* no HIP device, or not a gfx950 device */
+  TX_CODE_OBJECT_ERROR = 5,  /* a gfx950 code object failed to load */
+  TX_LAUNCH_ERROR = 6,       /* the HIP runtime rejected a launch */
+  TX_UNKNOWN_OP = 7          /* no op of that name in the table */
+} tx_status;
+
+/* Element types (the tt dtypes of the path: tl.float32, tl.float8e4nv,
+ * tl.float8e5, tl.bfloat16, tl.int32; utility.py:92-105 names the fp8 ones
+ * "e4m3" and "e5m2"). */
+typedef enum tx_dtype {
+  TX_F32 = 0,
+  TX_FP8E4M3FN = 1,
+  TX_FP8E5M2 = 2,
+  TX_BF16 = 3,
+  TX_I32 = 4,
+  TX_U32 = 5
+} tx_dtype;
+
+/* Rounding modes, numbered as the rounding operand of
+ * utlx_fp_to_fp_with_rbits (ops/NewOps.cpp:270-286): 0 rtne, 1 rtz, 2 rs. */
+typedef enum tx_rounding { TX_RTNE = 0, TX_RTZ = 1, TX_RS = 2 } tx_rounding;
+
+/* Read-modify-write kinds of tt.atomic_rmw (Triton's RMWOp). */
+typedef enum tx_rmw_op {
+  TX_RMW_ADD = 0,  /* integer add, wraps modulo 2^32 */
+  TX_RMW_FADD = 1, /* fp32 add */
+  TX_RMW_MAX = 2,  /* signed int32 max */
+  TX_RMW_MIN = 3,  /* signed int32 min */
+  TX_RMW_UMAX = 4, /* unsigned int32 max */
+  TX_RMW_UMIN = 5, /* unsigned int32 min */
+  TX_RMW_AND = 6,
+  TX_RMW_OR = 7,
+  TX_RMW_XOR = 8
+} tx_rmw_op;
+
+/* ----------------------------------------------------------------------- */
+/* Registration surface                                                     */
+/* ----------------------------------------------------------------------- */
+
+typedef enum tx_value_kind { TX_VALUE_PTR = 0, TX_VALUE_INT = 1 } tx_value_kind;
+
+/* One operand: a device pointer or an integer constant (the reference passes
+ * scalar options as arith.constant values, decoded by extractConstantInt,
+ * uTLXPlugin.cpp:40-50). */
+typedef struct tx_value {
+  int32_t kind; /* tx_value_kind */
+  int32_t reserved;
+  union {
+    void *ptr;
+    int64_t i;
+  } u;
+} tx_value;
+
+/* Op callback: the counterpart of plugin::OpInfo::add (support/Export.cpp:82-84). */
+typedef tx_status (*tx_op_fn)(tx_value *operands, size_t num_operands,
+                              tx_stream_t stream);
+
+typedef struct tx_op_info {
+  const char *name;      /* Triton op name, e.g. "tt.fp_to_fp" */
+  tx_op_fn fn;
+  const char *signature; /* operand list, human readable */
+} tx_op_info;
+
+/* Counterpart of plugin::PluginInfo (uTLXPlugin.cpp:801-812). */
+typedef struct tx_plugin_info {
+  uint32_t api_version; /* TX_PLUGIN_API_VERSION */
+  const char *name;     /* "txamd" */
+  const char *version;  /* library version string */
+  const tx_op_info *ops;
+  size_t num_ops;
+  const char *target;   /* "gfx950" */
+} tx_plugin_info;
+
+/* Replaces tritonGetPluginInfo (support/Export.h:15, uTLXPlugin.cpp:700).
+ * Each call returns a fresh table that stays valid until released. */
+TX_API const tx_plugin_info *txGetPluginInfo(void);
+
+/* Replaces tritonReleasePluginInfo (declared, never defined, at
+ * support/Export.h:17).  Frees a table from txGetPluginInfo; NULL is a no-op. */
+TX_API void txReleasePluginInfo(const tx_plugin_info *info);
+
+/* Look an op up by name in the registry (NULL if absent). */
+TX_API const tx_op_info *txFindOp(const char *name);
+
+/* Invoke a registered op by name (TX_UNKNOWN_OP if absent). */
+TX_API tx_status txInvokeOp(const char *name, tx_value *operands,
+                            size_t num_operands, tx_stream_t stream);
+
+/* Thread-local message for the calling thread's last failing call ("" if none). */
+TX_API const char *txGetLastError(void);
+
+/* Load the gfx950 code objects on the current device (optional: every entry
+ * point does this on first use).  TX_NO_DEVICE without a gfx950 device. */
+TX_API tx_status txInit(void);
+
+/* Unload code objects on every device this process initialised. */
+TX_API void txShutdown(void);
+
+/* Library version string. */
+TX_API const char *txVersion(void);
+
+/* ----------------------------------------------------------------------- */
+/* Typed entry points                                                       */
+/* ----------------------------------------------------------------------- */
+
+/*
+ * tt.fp_to_fp, elementwise over n contiguous elements.
+ * Replaces Triton's lowering of tt.fp_to_fp (emitted by semantic.cast,
+ * semantic.py:807-827; passed through at uTLXConversionPatterns.cpp:577;
+ * re-created with a rounding attribute by createFpToFpWithRbits,
+ * ops/NewOps.cpp:249-303).
+ *  - TX_F32 -> TX_FP8E4M3FN / TX_FP8E5M2 with rounding TX_RTNE or TX_RTZ.
+ *    saturate = 0: overflow and +-Inf become NaN (e4m3fn) or +-Inf (e5m2).
+ *    saturate = 1: the reference's clamp(x, -max, max)-then-convert idiom
+ *    (mxfp8_utils.py:17-21, 36-38): overflow and +-Inf become +-max, NaN
+ *    stays NaN.  NaN input gives 0x7F with the input's sign bit.
+ *  - TX_FP8E4M3FN / TX_FP8E5M2 -> TX_F32 (exact; NaN codes give 0x7FC00000
+ *    with the code's sign).
+ * TX_RS needs random bits: use tx_fp_to_fp_with_rbits.
+ */
+TX_API tx_status tx_fp_to_fp(const void *src, tx_dtype src_type, void *dst,
+                             tx_dtype dst_type, int64_t n,
+                             tx_rounding rounding, int saturate,
+                             tx_stream_t stream);
+
+/*
+ * tt.atomic_rmw in scatter form: for every i < n with mask[i] != 0 (mask may
+ * be NULL) and 0 <= idx[i] < nbins, atomically bins[idx[i]] = bins[idx[i]]
+ * (op) val[i].  Replaces Triton's per-lane lowering of tl.atomic_add and
+ * friends (tt.atomic_rmw, passed through at uTLXConversionPatterns.cpp:611;
+ * used at test_tlx.py:7627-7629 and 7687).  bins_type is TX_I32 or TX_U32 for
+ * the integer ops and TX_F32 for TX_RMW_FADD.  Updates are pre-aggregated
+ * (in registers, within a wavefront, and in an LDS table per workgroup)
+ * before they reach global memory, so fp32 sums are order-dependent within
+ * rounding.
+ * If old != NULL, every update instead returns the bin's value before it was
+ * applied (the tt.atomic_rmw result) in old[i] (0 for dropped updates), and
+ * no pre-aggregation is done.
+ */
+TX_API tx_status tx_atomic_rmw_scatter(void *bins, tx_dtype bins_type,
+                                       int64_t nbins, const int32_t *idx,
+                                       const void *val, const uint8_t *mask,
+                                       int64_t n, tx_rmw_op op, void *old,
+                                       tx_stream_t stream);
+
+/*
+ * tt.dot with bf16 operands, fp32 accumulation and bf16 output:
+ * C[m,n] = bf16_rne(sum_k A[m,k] * B[k,n]).
+ * Replaces Triton's MFMA lowering of tt.dot (TritonDotPattern,
+ * uTLXConversionPatterns.cpp:227-296; the kernel at
+ * test_amd_gemm_pipelined.py:184-300 and its host wrapper :303-331).
+ * A: row-major M x K, row stride lda (elements).
+ * B: column-major K x N, i.e. N rows of K elements, row stride ldb.
+ * C: row-major M x N, row stride ldc.
+ * Any M, N, K >= 0 (K = 0 gives zeros); strides >= the row length.
+ */
+TX_API tx_status tx_dot_bf16(const void *A, int64_t lda, const void *B,
+                             int64_t ldb, void *C, int64_t ldc, int64_t M,
+                             int64_t N, int64_t K, tx_stream_t stream);
+
+/*
+ * tt.dot on fp8 operands with a per-row / per-column scale epilogue:
+ * C[m,n] = bf16_rne(scale_a[m] * scale_b[n] * sum_k f32(A[m,k]) * f32(B[k,n])).
+ * No reference kernel exists; the closed form follows the scaled-dot check
+ * at test_tlx.py:2271-2292 with fp32 per-row/per-column scales in place of
+ * e8m0 block scales.  a_type/b_type are TX_FP8E4M3FN or TX_FP8E5M2.
+ * A: row-major M x K bytes (lda); B: column-major, N rows of K bytes (ldb);
+ * C: row-major bf16 (ldc).  scale_a has M floats, scale_b has N floats.
+ */
+TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
+                                   const float *scale_a, const void *B,
+                                   tx_dtype b_type, int64_t ldb,
+                                   const float *scale_b, void *C, int64_t ldc,
+                                   int64_t M, int64_t N, int64_t K,
+                                   tx_stream_t stream);
+
+/*
+ * fp8 weight-only dequant GEMV / skinny GEMM:
+ * y[m,n] = bf16_rne(sum_g scales[n,g] * sum_{k in group g} x[m,k] * f32(W[n,k])).
+ * No reference kernel exists (the nearest is the fp8 tt.dot of
+ * tx_dot_fp8_scaled).  x: bf16 row-major M x K (ldx); W: fp8 (w_type) row-major
+ * N x K bytes (ldw); scales: fp32 row-major N x ceil(K/group) (ld_scales);
+ * y: bf16 row-major M x N (ldy).  group is a multiple of 32; M <= 64.
+ */
+TX_API tx_status tx_gemv_fp8_dequant(const void *x, int64_t ldx, const void *W,
+                                     tx_dtype w_type, int64_t ldw,
+                                     const float *scales, int64_t ld_scales,
+                                     int64_t group, void *y, int64_t ldy,
+                                     int64_t M, int64_t N, int64_t K,
+                                     tx_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* TX_PLUGIN_H */

@@ -1,0 +1,212 @@
+"""ctypes wrapper around oracle/libtxoracle.so -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may
+import this module, and only as the checker (or, for the baseline, as the timed
+CPU port).  The product path never routes through it.
+
+Each wrapper mirrors one C function of ``tx_oracle.c``; the C file states which
+reference call site fixes each op's semantics.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libtxoracle.so")
+
+E4M3FN = 1
+E5M2 = 2
+MAX_FINITE = {E4M3FN: 448.0, E5M2: 57344.0}
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc + OpenMP)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"],
+                       check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        I = ctypes.c_int
+        L.txo_init.argtypes = []
+        L.txo_encode1.argtypes = [I, ctypes.c_float, I]
+        L.txo_encode1.restype = ctypes.c_uint8
+        L.txo_decode1.argtypes = [I, ctypes.c_uint8]
+        L.txo_decode1.restype = ctypes.c_float
+        L.txo_encode.argtypes = [P, P, I64, I, I, I]
+        L.txo_decode.argtypes = [P, P, I64, I, I]
+        L.txo_encode_rtz.argtypes = [P, P, I64, I, I, I]
+        L.txo_scatter_add_i32.argtypes = [P, I64, P, P, P, I64]
+        L.txo_scatter_add_f32_ref.argtypes = [P, P, I64, P, P, P, I64]
+        L.txo_scatter_add_f32_seq.argtypes = [P, I64, P, P, P, I64]
+        L.txo_scatter_add_i32_mt.argtypes = [P, I64, P, P, I64, I]
+        L.txo_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.txo_f32_to_bf16.restype = ctypes.c_uint16
+        L.txo_gemm_bf16_rows.argtypes = [P, I64, P, I64, I64, I64, I64, I64,
+                                         P, P, I]
+        L.txo_gemm_fp8_scaled_rows.argtypes = [P, I64, P, I64, P, P, I64, I64,
+                                               I, I, I64, I64, P, P, I]
+        L.txo_gemv_fp8_dequant.argtypes = [P, I64, P, I64, P, I64, I64, I64,
+                                           I64, I64, I, P, P, I]
+        L.txo_init()
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# --------------------------------------------------------------------- fp8
+def encode(x, fmt: int, sat: bool, nthreads: int = 0) -> np.ndarray:
+    """fp32 -> fp8 codes (uint8), RNE; sat selects the clamp-then-convert form."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().txo_encode(_p(x), _p(out), x.size, fmt, int(bool(sat)), nthreads)
+    return out
+
+
+def encode_rtz(x, fmt: int, sat: bool, nthreads: int = 0) -> np.ndarray:
+    """fp32 -> fp8 codes, round toward zero (finite values clamp to max)."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().txo_encode_rtz(_p(x), _p(out), x.size, fmt, int(bool(sat)), nthreads)
+    return out
+
+
+def decode(codes, fmt: int, nthreads: int = 0) -> np.ndarray:
+    """fp8 codes -> fp32 (exact; NaN -> 0x7FC00000 with the code's sign)."""
+    c = _c(codes, np.uint8)
+    out = np.empty(c.shape, np.float32)
+    lib().txo_decode(_p(c), _p(out), c.size, fmt, nthreads)
+    return out
+
+
+def encode1(x: float, fmt: int, sat: bool) -> int:
+    return int(lib().txo_encode1(fmt, ctypes.c_float(x), int(bool(sat))))
+
+
+def decode1(code: int, fmt: int) -> float:
+    return float(lib().txo_decode1(fmt, code))
+
+
+# ----------------------------------------------------------------- scatter
+def scatter_add_i32(bins, idx, val, mask=None) -> np.ndarray:
+    """bins (copied) += val at idx; int32 wraps modulo 2^32."""
+    b = np.array(bins, dtype=np.int32, copy=True)
+    idx = _c(idx, np.int32)
+    val = _c(val, np.int32)
+    m = None if mask is None else _c(mask, np.uint8)
+    lib().txo_scatter_add_i32(_p(b), b.size, _p(idx), _p(val), _p(m), idx.size)
+    return b
+
+
+def scatter_add_i32_mt(nbins, idx, val, nthreads: int = 0) -> np.ndarray:
+    b = np.zeros(nbins, np.int32)
+    idx = _c(idx, np.int32)
+    val = _c(val, np.int32)
+    lib().txo_scatter_add_i32_mt(_p(b), nbins, _p(idx), _p(val), idx.size,
+                                 nthreads)
+    return b
+
+
+def scatter_add_f32_ref(nbins, idx, val, mask=None):
+    """Return (fp64 per-bin sums, fp64 per-bin sums of |v|)."""
+    s = np.empty(nbins, np.float64)
+    a = np.empty(nbins, np.float64)
+    idx = _c(idx, np.int32)
+    val = _c(val, np.float32)
+    m = None if mask is None else _c(mask, np.uint8)
+    lib().txo_scatter_add_f32_ref(_p(s), _p(a), nbins, _p(idx), _p(val), _p(m),
+                                  idx.size)
+    return s, a
+
+
+def scatter_add_f32_seq(bins, idx, val, mask=None) -> np.ndarray:
+    b = np.array(bins, dtype=np.float32, copy=True)
+    idx = _c(idx, np.int32)
+    val = _c(val, np.float32)
+    m = None if mask is None else _c(mask, np.uint8)
+    lib().txo_scatter_add_f32_seq(_p(b), b.size, _p(idx), _p(val), _p(m),
+                                  idx.size)
+    return b
+
+
+# -------------------------------------------------------------------- bf16
+def f32_to_bf16(x) -> np.ndarray:
+    """Vectorised RNE fp32 -> bf16 bits (numpy restatement of the C helper)."""
+    u = _c(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (_c(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# -------------------------------------------------------------------- gemm
+def gemm_bf16_rows(A, B, r0: int, r1: int, nthreads: int = 0):
+    """Rows [r0, r1) of A @ B^T-stored-B (B given as N x K, K contiguous).
+
+    A: uint16 (bf16 bits) M x K, B: uint16 N x K.  Returns (fp32 of the fp64
+    accumulation, bf16 RNE bits)."""
+    A = _c(A, np.uint16)
+    B = _c(B, np.uint16)
+    K = A.shape[1]
+    N = B.shape[0]
+    o32 = np.empty((r1 - r0, N), np.float32)
+    o16 = np.empty((r1 - r0, N), np.uint16)
+    lib().txo_gemm_bf16_rows(_p(A), K, _p(B), K, N, K, r0, r1, _p(o32),
+                             _p(o16), nthreads)
+    return o32, o16
+
+
+def gemm_fp8_scaled_rows(A, B, sa, sb, r0: int, r1: int, fmt_a=E4M3FN,
+                         fmt_b=E4M3FN, nthreads: int = 0):
+    """Rows [r0, r1) of diag(sa) (Aq . Bq^T) diag(sb); Aq M x K, Bq N x K codes."""
+    A = _c(A, np.uint8)
+    B = _c(B, np.uint8)
+    sa = _c(sa, np.float32)
+    sb = _c(sb, np.float32)
+    K = A.shape[1]
+    N = B.shape[0]
+    o32 = np.empty((r1 - r0, N), np.float32)
+    o16 = np.empty((r1 - r0, N), np.uint16)
+    lib().txo_gemm_fp8_scaled_rows(_p(A), K, _p(B), K, _p(sa), _p(sb), N, K,
+                                   fmt_a, fmt_b, r0, r1, _p(o32), _p(o16),
+                                   nthreads)
+    return o32, o16
+
+
+def gemv_fp8_dequant(x, W, s, group: int = 128, fmt_w=E5M2, nthreads: int = 0):
+    """y = x (M x K bf16 bits) times dequant(W (N x K codes), s (N x K/group))^T."""
+    x = _c(x, np.uint16)
+    W = _c(W, np.uint8)
+    s = _c(s, np.float32)
+    M, K = x.shape
+    N = W.shape[0]
+    o32 = np.empty((M, N), np.float32)
+    o16 = np.empty((M, N), np.uint16)
+    lib().txo_gemv_fp8_dequant(_p(x), K, _p(W), K, _p(s), s.shape[1], M, N, K,
+                               group, fmt_w, _p(o32), _p(o16), nthreads)
+    return o32, o16

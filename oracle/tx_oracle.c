@@ -1,0 +1,439 @@
+/*
+ * tx_oracle.c -- CPU oracle for the tx op library.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product path (the HIP kernels,
+ * the C-ABI library, the Python host mirror) may call, link or load this
+ * file.  It is used by tests/ as the checker, by __graft_entry__.smoke() as
+ * the checker, and by bench.py's cpu_baseline leg as the timed CPU port.
+ *
+ * Every function restates, in plain C, the semantics of one op on the
+ * reference's hot path.  The reference itself never spells out the
+ * arithmetic (it is produced by upstream Triton's lowering of tt.* ops), so
+ * each function cites the reference call site that fixes the semantics and
+ * the public specification it follows.  The methods here are deliberately
+ * different from the GPU kernels' (value-space search instead of bit tricks,
+ * fp64 accumulation instead of MFMA fp32), so that the two implementations
+ * check each other rather than repeat each other.
+ *
+ * Pinning (what each function is checked against, in tests/):
+ *   fp8 decode   : all 256 codes of both formats vs. closed-form ldexp
+ *                  values and vs. PyTorch's CPU float8 dtypes.
+ *   fp8 encode   : PyTorch's RNE non-saturating conversion on random,
+ *                  special and strided-exhaustive fp32 bit patterns; the
+ *                  saturating mode vs. PyTorch applied after clamp(+-max)
+ *                  (the reference's idiom, mxfp8_utils.py:36-38); explicit
+ *                  tie/binade cases whose answer follows from the spec.
+ *   scatter      : brute-force loops on tiny inputs; int32 wrap mod 2^32;
+ *                  conservation of the total.
+ *   gemm / gemv  : brute force on tiny shapes vs. numpy float64; linearity.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define TXO_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------ */
+/* fp8 formats (OCP 8-bit floating point specification, v1.0)               */
+/*   E4M3FN: bias 7, 3 mantissa bits, no infinities, S.1111.111 is NaN,     */
+/*           max finite 448 (code 0x7E).                                    */
+/*   E5M2  : bias 15, 2 mantissa bits, IEEE-like: exp 31 mant 0 is Inf,     */
+/*           exp 31 mant != 0 is NaN, max finite 57344 (code 0x7B).         */
+/* Format ids match the library's tx_dtype values: 1 = e4m3fn, 2 = e5m2.     */
+/* ------------------------------------------------------------------------ */
+
+enum { TXO_E4M3FN = 1, TXO_E5M2 = 2 };
+
+typedef struct {
+  int mbits;
+  int bias;
+  int max_code;    /* largest finite positive code */
+  uint8_t nan_code;/* code produced for NaN input (sign OR-ed in) */
+  uint8_t ovf_code;/* code produced by non-saturating overflow */
+} fp8_fmt;
+
+static const fp8_fmt FMT_E4M3FN = {3, 7, 0x7E, 0x7F, 0x7F};
+static const fp8_fmt FMT_E5M2 = {2, 15, 0x7B, 0x7F, 0x7C};
+
+static const fp8_fmt *fmt_of(int f) {
+  return f == TXO_E5M2 ? &FMT_E5M2 : &FMT_E4M3FN;
+}
+
+/* Magnitude of a positive finite code, computed from the spec's definition
+ * (subnormal: mant * 2^(1-bias-m); normal: (1 + mant/2^m) * 2^(exp-bias)). */
+static double code_value(const fp8_fmt *F, int code) {
+  int e = code >> F->mbits;
+  int m = code & ((1 << F->mbits) - 1);
+  if (e == 0) return ldexp((double)m, 1 - F->bias - F->mbits);
+  return ldexp(1.0 + ldexp((double)m, -F->mbits), e - F->bias);
+}
+
+static double mag_table[3][128];
+static int tables_ready = 0;
+static void init_tables(void) {
+  if (tables_ready) return;
+  for (int f = 1; f <= 2; ++f)
+    for (int c = 0; c < 128; ++c) mag_table[f][c] = code_value(fmt_of(f), c);
+  tables_ready = 1;
+}
+
+/*
+ * fp32 -> fp8, round to nearest, ties to even (rtz == 0) or toward zero
+ * (rtz != 0, the "rtz" rounding of tt.fp_to_fp, ops/NewOps.cpp:270-286:
+ * the largest-magnitude code not above |x|, clamped to max), following
+ * tt.fp_to_fp with the
+ * default rounding of Triton's downcast (semantic.py:809, emitted at
+ * semantic.py:823-827, passed through by uTLXConversionPatterns.cpp:577).
+ *   sat == 0: overflow goes to NaN (e4m3fn) or Inf (e5m2); Inf likewise.
+ *   sat != 0: the reference's saturating idiom, clamp(x, -max, max) then
+ *             convert (mxfp8_utils.py:17-21, 36-38): |x| > max and +-Inf give
+ *             +-max; NaN stays NaN.
+ * Method: binary search of the 128 exact magnitudes, then a comparison of
+ * the two distances in double precision (exact for every fp32 input), with
+ * ties sent to the code whose lowest bit is 0.
+ */
+static uint8_t encode_one(const fp8_fmt *F, int fid, float x, int sat, int rtz) {
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  uint8_t sign = (uint8_t)((bits >> 24) & 0x80);
+  uint32_t abits = bits & 0x7FFFFFFFu;
+  if (abits > 0x7F800000u) return (uint8_t)(F->nan_code | sign);
+  if (abits == 0x7F800000u)
+    return (uint8_t)((sat ? F->max_code : F->ovf_code) | sign);
+  double a = fabs((double)x);
+  const double *T = mag_table[fid];
+  double maxv = T[F->max_code];
+  if (a >= maxv) {
+    /* round toward zero never leaves the finite range */
+    if (sat || rtz || a == maxv) return (uint8_t)(F->max_code | sign);
+    /* the value one step above max (2^emax * (2 - 2^-m) + ulp) is the
+     * overflow point; rounding decides between max and overflow */
+    double ulp = maxv - T[F->max_code - 1];
+    double up = maxv + ulp;
+    double dlo = a - maxv, dhi = up - a;
+    int take_up;
+    if (dlo < dhi) take_up = 0;
+    else if (dlo > dhi) take_up = 1;
+    else take_up = (F->max_code & 1); /* tie: go to the even neighbour */
+    return (uint8_t)((take_up ? F->ovf_code : F->max_code) | sign);
+  }
+  /* largest code with value <= a */
+  int lo = 0, hi = F->max_code; /* T[lo] <= a < T[hi] holds after the loop */
+  while (hi - lo > 1) {
+    int mid = (lo + hi) >> 1;
+    if (T[mid] <= a) lo = mid; else hi = mid;
+  }
+  if (T[hi] <= a) lo = hi;
+  if (T[lo] == a || rtz) return (uint8_t)(lo | sign);
+  int nxt = lo + 1;
+  double dlo = a - T[lo], dhi = T[nxt] - a;
+  int c;
+  if (dlo < dhi) c = lo;
+  else if (dlo > dhi) c = nxt;
+  else c = (lo & 1) ? nxt : lo;
+  return (uint8_t)(c | sign);
+}
+
+/* fp8 -> fp32, exact.  NaN codes decode to the canonical quiet NaN with the
+ * code's sign (0x7FC00000 | sign); Inf (e5m2 only) to +-Inf. */
+static float decode_one(const fp8_fmt *F, int fid, uint8_t code) {
+  int sign = code >> 7;
+  int mag = code & 0x7F;
+  uint32_t out;
+  if (fid == TXO_E4M3FN && mag == 0x7F) {
+    out = 0x7FC00000u | ((uint32_t)sign << 31);
+  } else if (fid == TXO_E5M2 && mag >= 0x7C) {
+    out = (mag == 0x7C ? 0x7F800000u : 0x7FC00000u) | ((uint32_t)sign << 31);
+  } else {
+    float v = (float)mag_table[fid][mag];
+    if (sign) v = -v;
+    memcpy(&out, &v, 4);
+  }
+  float r;
+  memcpy(&r, &out, 4);
+  (void)F;
+  return r;
+}
+
+TXO_API void txo_init(void) { init_tables(); }
+
+TXO_API uint8_t txo_encode1(int fmt, float x, int sat) {
+  init_tables();
+  return encode_one(fmt_of(fmt), fmt == TXO_E5M2 ? 2 : 1, x, sat, 0);
+}
+
+TXO_API float txo_decode1(int fmt, uint8_t c) {
+  init_tables();
+  return decode_one(fmt_of(fmt), fmt == TXO_E5M2 ? 2 : 1, c);
+}
+
+/* Elementwise encode over a buffer (the tt.fp_to_fp fp32 -> fp8 op). */
+TXO_API void txo_encode(const float *src, uint8_t *dst, int64_t n, int fmt,
+                        int sat, int nthreads) {
+  init_tables();
+  const fp8_fmt *F = fmt_of(fmt);
+  int fid = fmt == TXO_E5M2 ? 2 : 1;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t i = 0; i < n; ++i) dst[i] = encode_one(F, fid, src[i], sat, 0);
+  (void)nthreads;
+}
+
+/* Elementwise encode with round toward zero. */
+TXO_API void txo_encode_rtz(const float *src, uint8_t *dst, int64_t n, int fmt,
+                            int sat, int nthreads) {
+  init_tables();
+  const fp8_fmt *F = fmt_of(fmt);
+  int fid = fmt == TXO_E5M2 ? 2 : 1;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t i = 0; i < n; ++i) dst[i] = encode_one(F, fid, src[i], sat, 1);
+  (void)nthreads;
+}
+
+/* Elementwise decode over a buffer (the tt.fp_to_fp fp8 -> fp32 op). */
+TXO_API void txo_decode(const uint8_t *src, float *dst, int64_t n, int fmt,
+                        int nthreads) {
+  init_tables();
+  const fp8_fmt *F = fmt_of(fmt);
+  int fid = fmt == TXO_E5M2 ? 2 : 1;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t i = 0; i < n; ++i) dst[i] = decode_one(F, fid, src[i]);
+  (void)nthreads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* tt.atomic_rmw scatter form: bins[idx[i]] (op)= val[i]                     */
+/* Semantics: each update is an atomic read-modify-write on one element      */
+/* (tl.atomic_add -> tt.atomic_rmw add/fadd, passed through at               */
+/* uTLXConversionPatterns.cpp:611; used at test_tlx.py:7627-7629, 7687).     */
+/* Updates whose index is outside [0, nbins) or whose mask byte is 0 are     */
+/* dropped.                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* int32 add: two's complement, wraps modulo 2^32, order independent. */
+TXO_API void txo_scatter_add_i32(int32_t *bins, int64_t nbins,
+                                 const int32_t *idx, const int32_t *val,
+                                 const uint8_t *mask, int64_t n) {
+  uint32_t *ub = (uint32_t *)bins;
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t b = idx[i];
+    if (b < 0 || b >= nbins) continue;
+    if (mask && !mask[i]) continue;
+    ub[b] += (uint32_t)val[i];
+  }
+}
+
+/* fp32 add, reference sums: per-bin sum in fp64 and per-bin sum of |v| in
+ * fp64 (the denominator of the order tolerance).  sum/abssum are written,
+ * not accumulated. */
+TXO_API void txo_scatter_add_f32_ref(double *sum, double *abssum,
+                                     int64_t nbins, const int32_t *idx,
+                                     const float *val, const uint8_t *mask,
+                                     int64_t n) {
+  for (int64_t b = 0; b < nbins; ++b) sum[b] = abssum[b] = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t b = idx[i];
+    if (b < 0 || b >= nbins) continue;
+    if (mask && !mask[i]) continue;
+    sum[b] += (double)val[i];
+    abssum[b] += fabs((double)val[i]);
+  }
+}
+
+/* fp32 add in fp32, in index order (one legal atomic serialization). */
+TXO_API void txo_scatter_add_f32_seq(float *bins, int64_t nbins,
+                                     const int32_t *idx, const float *val,
+                                     const uint8_t *mask, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t b = idx[i];
+    if (b < 0 || b >= nbins) continue;
+    if (mask && !mask[i]) continue;
+    bins[b] += val[i];
+  }
+}
+
+/* Multithreaded int32 scatter for the CPU baseline timing: per-thread
+ * private histograms then a reduction (same result, any order). */
+TXO_API void txo_scatter_add_i32_mt(int32_t *bins, int64_t nbins,
+                                    const int32_t *idx, const int32_t *val,
+                                    int64_t n, int nthreads) {
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+  uint32_t *priv = (uint32_t *)calloc((size_t)nthreads * (size_t)nbins, 4);
+#pragma omp parallel num_threads(nthreads)
+  {
+    int t = omp_get_thread_num();
+    uint32_t *h = priv + (size_t)t * (size_t)nbins;
+#pragma omp for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+      int64_t b = idx[i];
+      if (b >= 0 && b < nbins) h[b] += (uint32_t)val[i];
+    }
+  }
+  uint32_t *ub = (uint32_t *)bins;
+  for (int t = 0; t < nthreads; ++t)
+    for (int64_t b = 0; b < nbins; ++b) ub[b] += priv[(size_t)t * nbins + b];
+  free(priv);
+#else
+  txo_scatter_add_i32(bins, nbins, idx, val, NULL, n);
+  (void)nthreads;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* bf16 helpers                                                              */
+/* ------------------------------------------------------------------------ */
+
+static float bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* fp32 -> bf16 round to nearest even (NaN -> quiet NaN, sign kept).
+ * Value-space definition: pick the nearer of the two bf16 neighbours,
+ * ties to the one with an even last mantissa bit. */
+static uint16_t f32_to_bf16_rne(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040);
+  uint32_t lo = u & 0xFFFF0000u;         /* truncation toward zero */
+  uint32_t rem = u & 0x0000FFFFu;
+  uint16_t h = (uint16_t)(lo >> 16);
+  if (rem > 0x8000u || (rem == 0x8000u && (h & 1))) h = (uint16_t)(h + 1);
+  return h;
+}
+
+TXO_API uint16_t txo_f32_to_bf16(float x) { return f32_to_bf16_rne(x); }
+
+/* ------------------------------------------------------------------------ */
+/* tt.dot, bf16 operands, fp32 accumulate, bf16 output.                      */
+/* C[m,n] = sum_k A[m,k] * B[k,n]; the reference kernel accumulates in fp32  */
+/* and casts to the output type at the end (test_amd_gemm_pipelined.py:269,  */
+/* 274 accumulate; :294 cast; :297-300 masked store).  A is row-major M x K  */
+/* (lda), B is column-major K x N, stored as N rows of K (ldb), C row-major  */
+/* M x N.  The oracle accumulates in fp64 and returns both the unrounded     */
+/* fp64 result (as float) and its bf16 RNE rounding, for rows [r0, r1).      */
+/* ------------------------------------------------------------------------ */
+TXO_API void txo_gemm_bf16_rows(const uint16_t *A, int64_t lda,
+                                const uint16_t *B, int64_t ldb, int64_t N,
+                                int64_t K, int64_t r0, int64_t r1,
+                                float *out_f32, uint16_t *out_bf16,
+                                int nthreads) {
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+  for (int64_t m = r0; m < r1; ++m) {
+    float *arow = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
+    for (int64_t k = 0; k < K; ++k) arow[k] = bf16_to_f32(A[m * lda + k]);
+    for (int64_t n = 0; n < N; ++n) {
+      const uint16_t *bcol = B + n * ldb;
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k)
+        acc += (double)arow[k] * (double)bf16_to_f32(bcol[k]);
+      int64_t o = (m - r0) * N + n;
+      if (out_f32) out_f32[o] = (float)acc;
+      if (out_bf16) out_bf16[o] = f32_to_bf16_rne((float)acc);
+    }
+    free(arow);
+  }
+  (void)nthreads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp8 e4m3fn scaled dot (tt.dot on fp8 operands with a row/column scale     */
+/* epilogue):  C[m,n] = bf16_RNE( s_a[m] * s_b[n] * sum_k f32(Aq[m,k]) *     */
+/* f32(Bq[k,n]) ).  The closed form follows the reference's scaled-dot test  */
+/* (test_tlx.py:2271-2292: decode the fp8 operands, apply the scales, fp32   */
+/* dot) with one fp32 scale per row of A and per column of B instead of e8m0 */
+/* block scales.  Aq row-major M x K (lda bytes), Bq column-major (N rows of */
+/* K bytes, ldb), fmt_a/fmt_b select e4m3fn (1) or e5m2 (2).                 */
+/* ------------------------------------------------------------------------ */
+TXO_API void txo_gemm_fp8_scaled_rows(const uint8_t *A, int64_t lda,
+                                      const uint8_t *B, int64_t ldb,
+                                      const float *sa, const float *sb,
+                                      int64_t N, int64_t K, int fmt_a,
+                                      int fmt_b, int64_t r0, int64_t r1,
+                                      float *out_f32, uint16_t *out_bf16,
+                                      int nthreads) {
+  init_tables();
+  float lut_a[256], lut_b[256];
+  for (int c = 0; c < 256; ++c) {
+    lut_a[c] = txo_decode1(fmt_a, (uint8_t)c);
+    lut_b[c] = txo_decode1(fmt_b, (uint8_t)c);
+  }
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+  for (int64_t m = r0; m < r1; ++m) {
+    const uint8_t *arow = A + m * lda;
+    for (int64_t n = 0; n < N; ++n) {
+      const uint8_t *bcol = B + n * ldb;
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k)
+        acc += (double)lut_a[arow[k]] * (double)lut_b[bcol[k]];
+      double v = acc * (double)sa[m] * (double)sb[n];
+      int64_t o = (m - r0) * N + n;
+      if (out_f32) out_f32[o] = (float)v;
+      if (out_bf16) out_bf16[o] = f32_to_bf16_rne((float)v);
+    }
+  }
+  (void)nthreads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp8 weight-only dequant GEMV / skinny GEMM:                               */
+/*   y[m,n] = bf16_RNE( sum_g s[n,g] * sum_{k in g} x[m,k] * f32(Wq[n,k]) )   */
+/* x bf16 M x K row-major (ldx), Wq N x K row-major fp8 (ldw bytes), s fp32  */
+/* N x (K/group) row-major (lds), y bf16 M x N (ldy).  No reference          */
+/* implementation exists; the closed form is the fp8 tt.dot decode of the    */
+/* interpreter (interpreter.py:633-637: upcast fp8, then fp32 dot) with a    */
+/* per-group scale on W.                                                     */
+/* ------------------------------------------------------------------------ */
+TXO_API void txo_gemv_fp8_dequant(const uint16_t *x, int64_t ldx,
+                                  const uint8_t *W, int64_t ldw,
+                                  const float *s, int64_t lds, int64_t M,
+                                  int64_t N, int64_t K, int64_t group,
+                                  int fmt_w, float *out_f32,
+                                  uint16_t *out_bf16, int nthreads) {
+  init_tables();
+  float lut[256];
+  for (int c = 0; c < 256; ++c) lut[c] = txo_decode1(fmt_w, (uint8_t)c);
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t n = 0; n < N; ++n) {
+    const uint8_t *wrow = W + n * ldw;
+    for (int64_t m = 0; m < M; ++m) {
+      const uint16_t *xrow = x + m * ldx;
+      double total = 0.0;
+      for (int64_t g0 = 0; g0 < K; g0 += group) {
+        int64_t g1 = g0 + group < K ? g0 + group : K;
+        double part = 0.0;
+        for (int64_t k = g0; k < g1; ++k)
+          part += (double)bf16_to_f32(xrow[k]) * (double)lut[wrow[k]];
+        total += part * (double)s[n * lds + g0 / group];
+      }
+      if (out_f32) out_f32[m * N + n] = (float)total;
+      if (out_bf16) out_bf16[m * N + n] = f32_to_bf16_rne((float)total);
+    }
+  }
+  (void)nthreads;
+  (void)ldx;
+}

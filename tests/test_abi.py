@@ -1,0 +1,112 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol
+include/tx_plugin.h declares, serves the plugin table, and turns bad calls
+into status codes (never an abort)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    with open(os.path.join(REPO, "include", "tx_plugin.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"TX_API\s+[\w\s\*]+?\b(tx\w+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol(tx):
+    names = declared_symbols()
+    assert len(names) >= 13
+    lib = ctypes.CDLL(tx._lib.LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(tx._lib.EXPORTED) == names
+
+
+def test_plugin_table(tx):
+    name, version, target, ops = tx.plugin_info()
+    assert name == "txamd" and target == "gfx950" and version == tx.version()
+    names = [o[0] for o in ops]
+    assert {"tt.fp_to_fp", "tt.atomic_rmw", "tt.dot", "tt.dot_scaled.rowcol",
+            "tx.gemv_fp8_dequant"} <= set(names)
+    assert len(names) == len(set(names))
+    # each call returns a fresh table that txReleasePluginInfo frees
+    for _ in range(100):
+        p = tx.lib.txGetPluginInfo()
+        assert p and p.contents.api_version == 1
+        tx.lib.txReleasePluginInfo(p)
+    tx.lib.txReleasePluginInfo(None)
+
+
+def test_find_and_invoke_unknown_op(tx):
+    assert not tx.lib.txFindOp(b"tt.nope")
+    assert tx.lib.txFindOp(b"tt.dot")
+    vals = (tx._lib.TxValue * 1)()
+    st = tx.lib.txInvokeOp(b"tt.nope", vals, 0, None)
+    assert st == tx._lib.UNKNOWN_OP and "tt.nope" in tx._lib.last_error()
+
+
+def test_table_operand_validation(tx):
+    vals = (tx._lib.TxValue * 3)()
+    st = tx.lib.txInvokeOp(b"tt.fp_to_fp", vals, 3, None)
+    assert st == tx._lib.INVALID_ARGUMENT and "expected 7 operands" in tx._lib.last_error()
+    ops = [tx._lib.TxValue.int(0)] + [tx._lib.TxValue.ptr(None)] * 6
+    arr = (tx._lib.TxValue * 7)(*ops)
+    st = tx.lib.txInvokeOp(b"tt.fp_to_fp", arr, 7, None)
+    assert st == tx._lib.INVALID_ARGUMENT and "must be a pointer" in tx._lib.last_error()
+
+
+@pytest.mark.parametrize("call", [
+    lambda L: L.tx_fp_to_fp(None, 0, None, 1, -1, 0, 0, None),
+    lambda L: L.tx_fp_to_fp(None, 0, None, 1, 10, 0, 0, None),
+    lambda L: L.tx_atomic_rmw_scatter(None, 4, 10, None, None, None, 5, 0, None, None),
+    lambda L: L.tx_atomic_rmw_scatter(None, 4, 10, None, None, None, 5, 42, None, None),
+    lambda L: L.tx_dot_bf16(None, 4, None, 4, None, 4, -1, 4, 4, None),
+    lambda L: L.tx_dot_bf16(None, 4, None, 4, None, 4, 4, 4, 4, None),
+    lambda L: L.tx_dot_bf16(ctypes.c_void_p(64), 2, ctypes.c_void_p(64), 4, ctypes.c_void_p(64),
+                            4, 4, 4, 4, None),
+    lambda L: L.tx_dot_fp8_scaled(None, 0, 4, None, None, 1, 4, None, None, 4, 4, 4, 4, None),
+    lambda L: L.tx_gemv_fp8_dequant(None, 128, None, 2, 128, None, 1, 0, None, 4, 1, 4, 128, None),
+])
+def test_bad_arguments_are_status_codes(tx, call):
+    st = call(tx.lib)
+    assert st == tx._lib.INVALID_ARGUMENT, (st, tx._lib.last_error())
+    assert tx._lib.last_error()
+
+
+def test_unsupported_requests(tx):
+    L = tx.lib
+    st = L.tx_gemv_fp8_dequant(None, 100, None, 2, 100, None, 1, 128, None, 4, 65, 4, 100, None)
+    assert st == tx._lib.UNSUPPORTED
+    st = L.tx_fp_to_fp(ctypes.c_void_p(64), 0, ctypes.c_void_p(64), 3, 10, 0, 0, None)
+    assert st in (tx._lib.UNSUPPORTED, tx._lib.NO_DEVICE)
+    st = L.tx_fp_to_fp(ctypes.c_void_p(64), 0, ctypes.c_void_p(64), 1, 10, 2, 0, None)
+    assert st == tx._lib.UNSUPPORTED and "random bits" in tx._lib.last_error()
+
+
+def test_no_device_is_reported(tx):
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(tx.TxError, match="NO_DEVICE"):
+        tx.init()
+    st = tx.lib.tx_fp_to_fp(ctypes.c_void_p(64), 0, ctypes.c_void_p(64), 1, 4096, 0, 0, None)
+    assert st == tx._lib.NO_DEVICE
+
+
+def test_zero_sized_calls_succeed_without_device(tx):
+    L = tx.lib
+    assert L.tx_fp_to_fp(None, 0, None, 1, 0, 0, 0, None) == 0
+    assert L.tx_dot_bf16(None, 0, None, 0, None, 0, 0, 5, 5, None) == 0
+    assert L.tx_atomic_rmw_scatter(None, 4, 0, None, None, None, 0, 0, None, None) == 0
+
+
+def test_python_mirror_rejects_cpu_tensors(tx):
+    with pytest.raises(ValueError, match="GPU tensors only"):
+        tx.fp_to_fp(torch.zeros(4), torch.float8_e4m3fn)
+    assert tx.get_fp8_format_name(torch.float8_e5m2) == "e5m2"
+    assert tx.get_fp8_format_name(torch.float8_e4m3fn) == "e4m3"
+    with pytest.raises(AssertionError):
+        tx.get_fp8_format_name(torch.float16)

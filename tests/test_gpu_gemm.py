@@ -1,0 +1,204 @@
+"""GPU parity: tt.dot bf16, fp8 scaled dot and the fp8 dequant GEMV vs the oracle.
+
+Tolerances (stated per op): bf16 GEMM rel err <= 1e-2, fp8 scaled GEMM and
+GEMV rel err <= 2e-2, each measured as max|gpu - ref| / max|ref| and as the
+Frobenius ratio ||gpu - ref|| / ||ref||, against the oracle's fp64
+accumulation.  On top of that, outputs must be within 1 bf16 ulp of the
+oracle's own bf16 rounding for all but a tiny fraction of elements, which a
+wrong index, dropped term or transposed operand would break at any size.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+FP8_TOL = 2e-2
+
+
+def bf16_f32(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _t_bf16(bits_np, dev):
+    return torch.from_numpy(bits_np.view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _np_bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def check_close(got_bits, ref32, ref_bits, tol):
+    got = bf16_f32(got_bits).astype(np.float64)
+    ref = ref32.astype(np.float64)
+    scale = np.abs(ref).max() if ref.size else 0.0
+    if scale == 0:
+        assert np.all(got == 0)
+        return
+    rel_max = np.abs(got - ref).max() / scale
+    rel_fro = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-300)
+    assert rel_max <= tol and rel_fro <= tol, (rel_max, rel_fro)
+    # ulp distance to the oracle's bf16 rounding (sign-magnitude -> ordinal)
+    def ordinal(b):
+        b = b.astype(np.int32)
+        return np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    # fp32 accumulation order only moves results across a bf16 rounding
+    # boundary rarely (and by more than 2 ulps only for near-cancelling sums)
+    d = np.abs(ordinal(got_bits) - ordinal(ref_bits))
+    assert np.mean(d > 0) <= 0.05 and np.mean(d > 2) <= 0.002, \
+        (np.mean(d > 0), np.mean(d > 2), d.max())
+
+
+def sample_rows(M, k=24, seed=0):
+    g = np.random.default_rng(seed)
+    rows = set([0, 1, M - 1, M - 2] + list(g.integers(0, M, size=k)))
+    return sorted(r for r in rows if 0 <= r < M)
+
+
+# --------------------------------------------------------------------- bf16
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (17, 19, 23), (64, 64, 64), (128, 128, 128),
+                                   (255, 257, 130), (300, 64, 1000), (513, 129, 72),
+                                   (1024, 1024, 256), (33, 4097, 520)])
+def test_bf16_small_shapes(tx, oracle, dev, M, N, K):
+    from tx import workloads
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=M * 7 + N)
+    C = tx.dot(_t_bf16(A, dev), _t_bf16(B, dev))
+    r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
+    check_close(_np_bits(C), r32, r16, BF16_TOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (4095, 4097, 4100)])
+def test_bf16_config_shapes(tx, oracle, dev, M, N, K):
+    from tx import workloads
+    A, B = workloads.bf16_gemm_input(M, N, K)
+    C = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
+    rows = sample_rows(M)
+    for r in rows:
+        r32, r16 = oracle.gemm_bf16_rows(A, B, r, r + 1)
+        check_close(C[r:r + 1], r32, r16, BF16_TOL)
+    # full-size property: scaling A by 2 (exact in bf16) doubles every output bit-exactly
+    A2 = _t_bf16(A, dev) * 2
+    C2 = _np_bits(tx.dot(A2, _t_bf16(B, dev)))
+    assert np.array_equal(bf16_f32(C2), 2 * bf16_f32(C))
+
+
+def test_bf16_strided_and_unaligned(tx, oracle, dev):
+    from tx import workloads
+    M, N, K = 200, 150, 333
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=99)
+    # odd row strides force the narrow-load kernel variants
+    Ap = np.zeros((M, K + 3), np.uint16); Ap[:, :K] = A
+    Bp = np.zeros((N, K + 5), np.uint16); Bp[:, :K] = B
+    At = _t_bf16(Ap, dev)[:, :K]
+    Bt = _t_bf16(Bp, dev)[:, :K]
+    out = torch.zeros((M, N + 7), dtype=torch.bfloat16, device=dev)[:, :N]
+    tx.dot(At, Bt, out=out)
+    r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
+    check_close(_np_bits(out), r32, r16, BF16_TOL)
+
+
+def test_bf16_degenerate(tx, dev):
+    a = torch.ones((5, 0), dtype=torch.bfloat16, device=dev)
+    b = torch.ones((3, 0), dtype=torch.bfloat16, device=dev)
+    c = tx.dot(a, b)
+    assert torch.all(c == 0)
+    e = tx.dot(torch.ones((0, 4), dtype=torch.bfloat16, device=dev),
+               torch.ones((3, 4), dtype=torch.bfloat16, device=dev))
+    assert e.shape == (0, 3)
+
+
+def test_bf16_matmul_wrapper_and_table(tx, oracle, dev):
+    from tx import workloads
+    M, N, K = 96, 80, 64
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=5)
+    b_kn = _t_bf16(B, dev).t()  # column-major K x N view
+    C1 = tx.matmul(_t_bf16(A, dev), b_kn)
+    C2 = torch.empty_like(C1)
+    tx.invoke("tt.dot", [C2, _t_bf16(A, dev), _t_bf16(B, dev), M, N, K, K, K, N])
+    r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
+    check_close(_np_bits(C1), r32, r16, BF16_TOL)
+    assert torch.equal(C1, C2)
+
+
+# ---------------------------------------------------------------------- fp8
+def _fp8_run(tx, dev, aq, sa, bq, sb, fa=torch.float8_e4m3fn, fb=torch.float8_e4m3fn):
+    A = torch.from_numpy(aq).to(dev).view(fa)
+    B = torch.from_numpy(bq).to(dev).view(fb)
+    return _np_bits(tx.dot_scaled_rowcol(A, torch.from_numpy(sa).to(dev), B,
+                                         torch.from_numpy(sb).to(dev)))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (16, 48, 128), (100, 200, 300), (256, 256, 512),
+                                   (16, 1000, 4096), (600, 300, 260)])
+def test_fp8_small_shapes(tx, oracle, dev, M, N, K):
+    from tx import workloads
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=M + 3 * N)
+    C = _fp8_run(tx, dev, aq, sa, bq, sb)
+    r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, M)
+    check_close(C, r32, r16, FP8_TOL)
+
+
+@pytest.mark.parametrize("fa,fb", [(2, 2), (1, 2), (2, 1)])
+def test_fp8_format_mixes(tx, oracle, dev, fa, fb):
+    g = np.random.default_rng(fa * 10 + fb)
+    M, N, K = 130, 190, 384
+    aq = g.integers(0, 256, size=(M, K), dtype=np.uint8)
+    bq = g.integers(0, 256, size=(N, K), dtype=np.uint8)
+    # keep codes finite: clear NaN / Inf encodings
+    for q, f in ((aq, fa), (bq, fb)):
+        mag = q & 0x7F
+        if f == 1:
+            q[mag == 0x7F] &= 0xFE
+        else:
+            q[mag >= 0x7C] = 0x3C
+    sa = g.uniform(0.5, 2, M).astype(np.float32) * 1e-3
+    sb = g.uniform(0.5, 2, N).astype(np.float32) * 1e-3
+    td = {1: torch.float8_e4m3fn, 2: torch.float8_e5m2}
+    C = _fp8_run(tx, dev, aq, sa, bq, sb, td[fa], td[fb])
+    r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, M, fa, fb)
+    check_close(C, r32, r16, FP8_TOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (512, 14336, 4096), (16, 4096, 14336),
+                                   (512, 4096, 14336), (8192, 8192, 8192)])
+def test_fp8_config_shapes(tx, oracle, dev, M, N, K):
+    from tx import workloads
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
+    C = _fp8_run(tx, dev, aq, sa, bq, sb)
+    for r in sample_rows(M, k=8 if M * N * K > 1e11 else 16):
+        r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r, r + 1)
+        check_close(C[r:r + 1], r32, r16, FP8_TOL)
+    # full-size property: scale linearity, C(2 * sa) == 2 * C bit-exactly
+    C2 = _fp8_run(tx, dev, aq, (2 * sa).astype(np.float32), bq, sb)
+    assert np.array_equal(bf16_f32(C2), 2 * bf16_f32(C))
+
+
+# --------------------------------------------------------------------- gemv
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_config_full(tx, oracle, dev, M):
+    from tx import workloads
+    x, wq, s = workloads.gemv_input(M)
+    y = tx.gemv_fp8_dequant(_t_bf16(x, dev), torch.from_numpy(wq).to(dev).view(torch.float8_e5m2),
+                            torch.from_numpy(s).to(dev))
+    r32, r16 = oracle.gemv_fp8_dequant(x, wq, s)
+    check_close(_np_bits(y), r32, r16, FP8_TOL)
+
+
+@pytest.mark.parametrize("M,N,K,group,fmt", [(3, 100, 256, 128, 2), (33, 77, 1024, 256, 2),
+                                             (64, 50, 384, 384, 1), (5, 1, 128, 128, 1)])
+def test_gemv_shapes(tx, oracle, dev, M, N, K, group, fmt):
+    g = np.random.default_rng(M * N)
+    x = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
+    wq = g.integers(0, 256, size=(N, K), dtype=np.uint8)
+    mag = wq & 0x7F
+    if fmt == 1:
+        wq[mag == 0x7F] = 0x38
+    else:
+        wq[mag >= 0x7C] = 0x3C
+    s = g.uniform(0.1, 1.0, size=(N, K // group)).astype(np.float32) * 1e-3
+    td = {1: torch.float8_e4m3fn, 2: torch.float8_e5m2}
+    y = tx.gemv_fp8_dequant(_t_bf16(x, dev), torch.from_numpy(wq).to(dev).view(td[fmt]),
+                            torch.from_numpy(s).to(dev), group=group)
+    r32, r16 = oracle.gemv_fp8_dequant(x, wq, s, group=group, fmt_w=fmt)
+    check_close(_np_bits(y), r32, r16, FP8_TOL)

@@ -1,0 +1,125 @@
+// tt.atomic_rmw scatter entry point and its table registration.
+//
+// Reference: tl.atomic_add / tl.atomic_max ... lower to tt.atomic_rmw, which
+// the plugin passes through unchanged (uTLXConversionPatterns.cpp:611); the
+// reference's only uses are counters that check the returned old values
+// (test_tlx.py:7627-7629, 7672-7723).  The scatter form bins[idx[i]] op= v[i]
+// is the data-parallel op this entry point serves.
+#include <algorithm>
+#include <climits>
+#include <cstdio>
+
+#include "tx_kernel_args.h"
+#include "tx_ops.h"
+
+namespace tx {
+namespace {
+
+constexpr int kAggBlock = 1024;     // threads of the aggregating kernels
+constexpr int64_t kAggStep = 4 * kAggBlock;
+constexpr int64_t kDirectSlots = 36864;
+
+const char *op_name(tx_rmw_op op) {
+  switch (op) {
+    case TX_RMW_ADD: return "add";
+    case TX_RMW_FADD: return "fadd";
+    case TX_RMW_MAX: return "max";
+    case TX_RMW_MIN: return "min";
+    case TX_RMW_UMAX: return "umax";
+    case TX_RMW_UMIN: return "umin";
+    case TX_RMW_AND: return "and";
+    case TX_RMW_OR: return "or";
+    case TX_RMW_XOR: return "xor";
+  }
+  return nullptr;
+}
+
+}  // namespace
+
+static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbins,
+                                    const int32_t *idx, const void *val,
+                                    const uint8_t *mask, int64_t n, tx_rmw_op op,
+                                    void *old, tx_stream_t stream) {
+  const char *name = op_name(op);
+  if (!name) return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: unknown op %d", int(op));
+  if (n < 0 || nbins < 0)
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: n = %lld, nbins = %lld",
+                (long long)n, (long long)nbins);
+  if (nbins > INT32_MAX)
+    return fail(TX_UNSUPPORTED, "tx_atomic_rmw_scatter: nbins %lld exceeds int32 indexing",
+                (long long)nbins);
+  if (op == TX_RMW_FADD) {
+    if (bins_type != TX_F32)
+      return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: fadd needs TX_F32 bins");
+  } else if (bins_type != TX_I32 && bins_type != TX_U32) {
+    return fail(TX_INVALID_ARGUMENT,
+                "tx_atomic_rmw_scatter: integer ops need TX_I32 or TX_U32 bins");
+  }
+  if (n == 0) return TX_SUCCESS;
+  if (!idx || !val || (!bins && nbins > 0))
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: NULL buffer");
+  if (!aligned(idx, 4) || !aligned(val, 4) || (bins && !aligned(bins, 4)) ||
+      (old && !aligned(old, 4)))
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: buffers must be 4-byte aligned");
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int cus = cu_count();
+  tx_scatter_args args{bins, idx, val, mask, old, n, int32_t(nbins), 0};
+  char kname[64];
+  if (old) {
+    std::snprintf(kname, sizeof kname, "tx_scatter_%s_old", name);
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+    const int64_t grid = std::min<int64_t>((n + 255) / 256, int64_t(cus) * 64);
+    return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, kname);
+  }
+  if (nbins == 0) return TX_SUCCESS;  // every update is out of range
+  const bool direct = nbins <= kDirectSlots;
+  std::snprintf(kname, sizeof kname, "tx_scatter_%s_%s", name, direct ? "direct" : "hashed");
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+  // One workgroup per CU (the LDS table fills most of a CU's LDS); each takes
+  // a contiguous range of updates, a multiple of 4 * blockDim.
+  int64_t per = (n + cus - 1) / cus;
+  per = (per + kAggStep - 1) / kAggStep * kAggStep;
+  if (per > INT32_MAX) per = INT32_MAX / kAggStep * kAggStep;
+  args.per_block = int32_t(per);
+  const int64_t grid = (n + per - 1) / per;
+  return launch(fn, unsigned(grid), 1, kAggBlock, s, &args, sizeof args, kname);
+}
+
+// Table form: operands = {bins (result slot), idx, val, mask, old, nbins, n,
+// bins_type, op}.  mask and old may be NULL pointers.
+static tx_status atomic_rmw_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.atomic_rmw"};
+  TX_TRY(o.need(9));
+  void *bins, *idx, *val, *mask, *old;
+  int64_t nbins, n, bt, op;
+  TX_TRY(o.ptr(0, &bins));
+  TX_TRY(o.ptr(1, &idx));
+  TX_TRY(o.ptr(2, &val));
+  TX_TRY(o.ptr(3, &mask));
+  TX_TRY(o.ptr(4, &old));
+  TX_TRY(o.integer(5, &nbins));
+  TX_TRY(o.integer(6, &n));
+  TX_TRY(o.integer(7, &bt));
+  TX_TRY(o.integer(8, &op));
+  return atomic_rmw_scatter(bins, tx_dtype(bt), nbins, static_cast<const int32_t *>(idx), val,
+                            static_cast<const uint8_t *>(mask), n, tx_rmw_op(op), old, stream);
+}
+
+static const bool registered = register_op(
+    "tt.atomic_rmw", atomic_rmw_op,
+    "bins(result), idx:i32*, val, mask:u8*|null, old|null, nbins:i64, n:i64, "
+    "bins_type:i32, op:i32");
+
+}  // namespace tx
+
+extern "C" TX_API tx_status tx_atomic_rmw_scatter(void *bins, tx_dtype bins_type,
+                                                  int64_t nbins, const int32_t *idx,
+                                                  const void *val, const uint8_t *mask,
+                                                  int64_t n, tx_rmw_op op, void *old,
+                                                  tx_stream_t stream) {
+  tx::clear_error();
+  return tx::atomic_rmw_scatter(bins, bins_type, nbins, idx, val, mask, n, op, old, stream);
+}

@@ -1,0 +1,255 @@
+// tt.dot entry points (bf16, and fp8 with row/column scales), the fp8
+// dequant GEMV, and their table registrations.
+//
+// Reference: tt.dot is converted by TritonDotPattern
+// (uTLXConversionPatterns.cpp:227-296) and lowered to MFMA by Triton's AMD
+// backend (accelerate_matmul, custom_stages.py:84-85); the only AMD kernel in
+// the tree is matmul_kernel_pipelined_mi300 with its host wrapper
+// (test_amd_gemm_pipelined.py:184-331): grouped tile rasterisation
+// (:204-212), fp32 accumulation (:259-292), cast and masked store (:294-300).
+#include <algorithm>
+#include <climits>
+#include <cstdio>
+
+#include "tx_kernel_args.h"
+#include "tx_ops.h"
+
+namespace tx {
+namespace {
+
+constexpr int kGroupM = 8;
+
+// Largest load width (bytes) that every operand row start and the row length
+// are aligned to, among `widths` (descending).
+int pick_vec(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t k_b,
+             const int *widths, int nw) {
+  for (int i = 0; i < nw; ++i) {
+    const int w = widths[i];
+    if (aligned(A, w) && aligned(B, w) && lda_b % w == 0 && ldb_b % w == 0 && k_b % w == 0)
+      return w;
+  }
+  return widths[nw - 1];
+}
+
+tx_status check_gemm(const char *what, const void *A, int64_t lda, const void *B, int64_t ldb,
+                     const void *C, int64_t ldc, int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(TX_INVALID_ARGUMENT, "%s: negative size (M=%lld N=%lld K=%lld)", what,
+                (long long)M, (long long)N, (long long)K);
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 4)
+    return fail(TX_UNSUPPORTED, "%s: size exceeds 32-bit tile indexing", what);
+  if (M == 0 || N == 0) return TX_SUCCESS;
+  if (!C || (K > 0 && (!A || !B))) return fail(TX_INVALID_ARGUMENT, "%s: NULL buffer", what);
+  if (lda < K || ldb < K || ldc < N)
+    return fail(TX_INVALID_ARGUMENT, "%s: stride smaller than row length (lda=%lld ldb=%lld ldc=%lld)",
+                what, (long long)lda, (long long)ldb, (long long)ldc);
+  if (!aligned(C, 2)) return fail(TX_INVALID_ARGUMENT, "%s: C must be 2-byte aligned", what);
+  return TX_SUCCESS;
+}
+
+// Pick the tile: 256x256 when it still yields at least one tile per CU,
+// otherwise 128x128.
+bool use_big_tile(int64_t M, int64_t N) {
+  const int64_t big = ((M + 255) / 256) * ((N + 255) / 256);
+  return big >= cu_count();
+}
+
+tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int tile,
+                      hipStream_t s) {
+  args.tiles_m = int32_t((args.M + tile - 1) / tile);
+  args.tiles_n = int32_t((args.N + tile - 1) / tile);
+  args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
+  hipFunction_t fn;
+  TX_TRY(get_kernel(co, kname, &fn));
+  const int64_t grid = int64_t(args.tiles_m) * args.tiles_n;
+  if (grid > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: too many tiles", kname);
+  return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, kname);
+}
+
+const char *fp8_name(tx_dtype t) {
+  return t == TX_FP8E4M3FN ? "e4m3fn" : (t == TX_FP8E5M2 ? "e5m2" : nullptr);
+}
+
+}  // namespace
+
+static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  TX_TRY(check_gemm("tx_dot_bf16", A, lda, B, ldb, C, ldc, M, N, K));
+  if (M == 0 || N == 0) return TX_SUCCESS;
+  static const int widths[] = {16, 8, 2};
+  const int vec = pick_vec(A, lda * 2, B, ldb * 2, K * 2, widths, 3);
+  const int tile = use_big_tile(M, N) ? 256 : 128;
+  char kname[64];
+  std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
+  tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
+                    int32_t(K), 0, 0, 0};
+  return launch_gemm(kname, CodeObject::GemmBf16, args, tile, static_cast<hipStream_t>(stream));
+}
+
+static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
+                                const void *B, tx_dtype b_type, int64_t ldb, const float *sb,
+                                void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                tx_stream_t stream) {
+  TX_TRY(check_gemm("tx_dot_fp8_scaled", A, lda, B, ldb, C, ldc, M, N, K));
+  const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
+  if (!fa || !fb)
+    return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: operand types must be fp8 (got %d, %d)",
+                int(a_type), int(b_type));
+  if (M == 0 || N == 0) return TX_SUCCESS;
+  if (!sa || !sb) return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: NULL scale vector");
+  if (!aligned(sa, 4) || !aligned(sb, 4))
+    return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: scales must be 4-byte aligned");
+  static const int widths[] = {16, 4, 1};
+  const int vec = pick_vec(A, lda, B, ldb, K, widths, 3);
+  const int tile = (vec != 1 && use_big_tile(M, N)) ? 256 : 128;
+  char kname[80];
+  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
+  tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+  return launch_gemm(kname, CodeObject::GemmFp8, args, tile, static_cast<hipStream_t>(stream));
+}
+
+static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,
+                                  int64_t ldw, const float *scales, int64_t ld_scales,
+                                  int64_t group, void *y, int64_t ldy, int64_t M, int64_t N,
+                                  int64_t K, tx_stream_t stream) {
+  const char *what = "tx_gemv_fp8_dequant";
+  const char *fw = fp8_name(w_type);
+  if (!fw) return fail(TX_INVALID_ARGUMENT, "%s: W must be fp8 (got %d)", what, int(w_type));
+  if (M < 0 || N < 0 || K < 0 || group <= 0)
+    return fail(TX_INVALID_ARGUMENT, "%s: bad size (M=%lld N=%lld K=%lld group=%lld)", what,
+                (long long)M, (long long)N, (long long)K, (long long)group);
+  if (M > 64) return fail(TX_UNSUPPORTED, "%s: M = %lld > 64 (use tx_dot_fp8_scaled)", what, (long long)M);
+  if (N > INT32_MAX / 2 || K > INT32_MAX / 2)
+    return fail(TX_UNSUPPORTED, "%s: size exceeds 32-bit indexing", what);
+  if (M == 0 || N == 0) return TX_SUCCESS;
+  if (K % 128 != 0 || group % 128 != 0)
+    return fail(TX_UNSUPPORTED, "%s: K (%lld) and group (%lld) must be multiples of 128", what,
+                (long long)K, (long long)group);
+  if (!y || (K > 0 && (!x || !W || !scales)))
+    return fail(TX_INVALID_ARGUMENT, "%s: NULL buffer", what);
+  const int64_t ngroups = (K + group - 1) / group;
+  if (ldx < K || ldw < K || ldy < N || ld_scales < ngroups)
+    return fail(TX_INVALID_ARGUMENT, "%s: stride smaller than row length", what);
+  if (!aligned(x, 16) || ldx % 8 != 0 || !aligned(W, 16) || ldw % 16 != 0 ||
+      !aligned(scales, 4) || !aligned(y, 2))
+    return fail(TX_UNSUPPORTED,
+                "%s: needs 16-byte aligned x and W rows (ldx %% 8 == 0, ldw %% 16 == 0)", what);
+  char kname[48];
+  std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s", fw);
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::Gemv, kname, &fn));
+  tx_gemv_args args{static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(W), scales,
+                    static_cast<uint16_t *>(y), ldx, ldw, ld_scales, ldy, int32_t(M), int32_t(N),
+                    int32_t(K), int32_t(group)};
+  const int64_t grid = (N + 15) / 16;
+  return launch(fn, unsigned(grid), 1, 256, static_cast<hipStream_t>(stream), &args, sizeof args,
+                kname);
+}
+
+// Table forms.
+// tt.dot: {C (result), A, B, M, N, K, lda, ldb, ldc}
+static tx_status dot_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.dot"};
+  TX_TRY(o.need(9));
+  void *C, *A, *B;
+  int64_t M, N, K, lda, ldb, ldc;
+  TX_TRY(o.ptr(0, &C));
+  TX_TRY(o.ptr(1, &A));
+  TX_TRY(o.ptr(2, &B));
+  TX_TRY(o.integer(3, &M));
+  TX_TRY(o.integer(4, &N));
+  TX_TRY(o.integer(5, &K));
+  TX_TRY(o.integer(6, &lda));
+  TX_TRY(o.integer(7, &ldb));
+  TX_TRY(o.integer(8, &ldc));
+  return dot_bf16(A, lda, B, ldb, C, ldc, M, N, K, stream);
+}
+
+// tt.dot_scaled.rowcol: {C (result), A, B, scale_a, scale_b, M, N, K, lda, ldb,
+// ldc, a_type, b_type}
+static tx_status dot_fp8_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.dot_scaled.rowcol"};
+  TX_TRY(o.need(13));
+  void *C, *A, *B, *sa, *sb;
+  int64_t M, N, K, lda, ldb, ldc, at, bt;
+  TX_TRY(o.ptr(0, &C));
+  TX_TRY(o.ptr(1, &A));
+  TX_TRY(o.ptr(2, &B));
+  TX_TRY(o.ptr(3, &sa));
+  TX_TRY(o.ptr(4, &sb));
+  TX_TRY(o.integer(5, &M));
+  TX_TRY(o.integer(6, &N));
+  TX_TRY(o.integer(7, &K));
+  TX_TRY(o.integer(8, &lda));
+  TX_TRY(o.integer(9, &ldb));
+  TX_TRY(o.integer(10, &ldc));
+  TX_TRY(o.integer(11, &at));
+  TX_TRY(o.integer(12, &bt));
+  return dot_fp8_scaled(A, tx_dtype(at), lda, static_cast<const float *>(sa), B, tx_dtype(bt), ldb,
+                        static_cast<const float *>(sb), C, ldc, M, N, K, stream);
+}
+
+// tx.gemv_fp8_dequant: {y (result), x, W, scales, M, N, K, group, ldx, ldw,
+// ld_scales, ldy, w_type}
+static tx_status gemv_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tx.gemv_fp8_dequant"};
+  TX_TRY(o.need(13));
+  void *y, *x, *W, *s;
+  int64_t M, N, K, group, ldx, ldw, lds, ldy, wt;
+  TX_TRY(o.ptr(0, &y));
+  TX_TRY(o.ptr(1, &x));
+  TX_TRY(o.ptr(2, &W));
+  TX_TRY(o.ptr(3, &s));
+  TX_TRY(o.integer(4, &M));
+  TX_TRY(o.integer(5, &N));
+  TX_TRY(o.integer(6, &K));
+  TX_TRY(o.integer(7, &group));
+  TX_TRY(o.integer(8, &ldx));
+  TX_TRY(o.integer(9, &ldw));
+  TX_TRY(o.integer(10, &lds));
+  TX_TRY(o.integer(11, &ldy));
+  TX_TRY(o.integer(12, &wt));
+  return gemv_fp8_dequant(x, ldx, W, tx_dtype(wt), ldw, static_cast<const float *>(s), lds, group,
+                          y, ldy, M, N, K, stream);
+}
+
+static const bool reg_dot = register_op(
+    "tt.dot", dot_op, "C:bf16*(result), A:bf16*, B:bf16* (N x K), M, N, K, lda, ldb, ldc");
+static const bool reg_dot_fp8 = register_op(
+    "tt.dot_scaled.rowcol", dot_fp8_op,
+    "C:bf16*(result), A:fp8*, B:fp8* (N x K), scale_a:f32*, scale_b:f32*, M, N, K, lda, ldb, "
+    "ldc, a_type:i32, b_type:i32");
+static const bool reg_gemv = register_op(
+    "tx.gemv_fp8_dequant", gemv_op,
+    "y:bf16*(result), x:bf16*, W:fp8* (N x K), scales:f32* (N x K/group), M, N, K, group, ldx, "
+    "ldw, ld_scales, ldy, w_type:i32");
+
+}  // namespace tx
+
+extern "C" {
+
+TX_API tx_status tx_dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot_bf16(A, lda, B, ldb, C, ldc, M, N, K, stream);
+}
+
+TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
+                                   const float *scale_a, const void *B, tx_dtype b_type,
+                                   int64_t ldb, const float *scale_b, void *C, int64_t ldc,
+                                   int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot_fp8_scaled(A, a_type, lda, scale_a, B, b_type, ldb, scale_b, C, ldc, M, N, K,
+                            stream);
+}
+
+TX_API tx_status tx_gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,
+                                     int64_t ldw, const float *scales, int64_t ld_scales,
+                                     int64_t group, void *y, int64_t ldy, int64_t M, int64_t N,
+                                     int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::gemv_fp8_dequant(x, ldx, W, w_type, ldw, scales, ld_scales, group, y, ldy, M, N, K,
+                              stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// tt.fp_to_fp entry point (fp32 <-> fp8) and its table registration.
+//
+// Reference: tt.fp_to_fp is emitted by semantic.cast (semantic.py:807-827,
+// default rounding RTNE at :809), passed through the plugin's conversion
+// (uTLXConversionPatterns.cpp:577) and re-created with a rounding operand by
+// createFpToFpWithRbits (ops/NewOps.cpp:249-303; rounding 0 rtne, 1 rtz,
+// 2 rs at :270-286).  The saturating variant is the reference's
+// clamp-then-convert idiom (mxfp8_utils.py:17-21, 36-38).
+#include <algorithm>
+#include <cstdio>
+
+#include "tx_kernel_args.h"
+#include "tx_ops.h"
+
+namespace tx {
+namespace {
+
+constexpr unsigned kBlock = 256;
+constexpr int64_t kChunk = 4096;  // elements per block step of the vector kernels
+
+const char *fmt_name(tx_dtype t) {
+  return t == TX_FP8E4M3FN ? "e4m3fn" : "e5m2";
+}
+
+tx_status run(const char *vec_name, const char *tail_name, const void *src,
+              void *dst, int64_t n, bool vec_ok, hipStream_t stream) {
+  tx_fp8_codec_args args{src, dst, 0, n};
+  int64_t n_vec = vec_ok ? (n / kChunk) * kChunk : 0;
+  const int cus = cu_count();
+  if (n_vec > 0) {
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::Fp8Codec, vec_name, &fn));
+    args.start = 0;
+    args.n = n_vec;
+    // One block step per chunk, capped at 32 resident blocks per CU; the
+    // kernels loop over the remaining chunks.
+    int64_t grid = std::min<int64_t>(n_vec / kChunk, int64_t(cus) * 32);
+    TX_TRY(launch(fn, unsigned(grid), 1, kBlock, stream, &args, sizeof args, vec_name));
+  }
+  if (n_vec < n) {
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::Fp8Codec, tail_name, &fn));
+    args.start = n_vec;
+    args.n = n;
+    int64_t grid = std::min<int64_t>((n - n_vec + kBlock - 1) / kBlock, int64_t(cus) * 32);
+    TX_TRY(launch(fn, unsigned(grid), 1, kBlock, stream, &args, sizeof args, tail_name));
+  }
+  return TX_SUCCESS;
+}
+
+}  // namespace
+
+static tx_status fp_to_fp(const void *src, tx_dtype src_type, void *dst,
+                          tx_dtype dst_type, int64_t n, tx_rounding rounding,
+                          int saturate, tx_stream_t stream) {
+  if (n < 0) return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: n = %lld < 0", (long long)n);
+  if (n == 0) return TX_SUCCESS;
+  if (!src || !dst) return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: NULL buffer");
+  const bool src_fp8 = src_type == TX_FP8E4M3FN || src_type == TX_FP8E5M2;
+  const bool dst_fp8 = dst_type == TX_FP8E4M3FN || dst_type == TX_FP8E5M2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char vec[64], tail[64];
+  if (src_type == TX_F32 && dst_fp8) {
+    if (rounding == TX_RS)
+      return fail(TX_UNSUPPORTED,
+                  "tx_fp_to_fp: stochastic rounding needs random bits "
+                  "(tx_fp_to_fp_with_rbits)");
+    if (rounding != TX_RTNE && rounding != TX_RTZ)
+      return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: rounding %d", int(rounding));
+    const char *r = rounding == TX_RTZ ? "rtz" : "rtne";
+    const char *sat = saturate ? "_sat" : "";
+    std::snprintf(vec, sizeof vec, "tx_fp8_encode_%s_%s%s_vec", fmt_name(dst_type), r, sat);
+    std::snprintf(tail, sizeof tail, "tx_fp8_encode_%s_%s%s_tail", fmt_name(dst_type), r, sat);
+    const bool vec_ok = aligned(src, 16) && aligned(dst, 4);
+    return run(vec, tail, src, dst, n, vec_ok, s);
+  }
+  if (src_fp8 && dst_type == TX_F32) {
+    std::snprintf(vec, sizeof vec, "tx_fp8_decode_%s_vec", fmt_name(src_type));
+    std::snprintf(tail, sizeof tail, "tx_fp8_decode_%s_tail", fmt_name(src_type));
+    const bool vec_ok = aligned(src, 4) && aligned(dst, 16);
+    return run(vec, tail, src, dst, n, vec_ok, s);
+  }
+  return fail(TX_UNSUPPORTED, "tx_fp_to_fp: conversion %d -> %d is not served",
+              int(src_type), int(dst_type));
+}
+
+// Table form: operands = {dst (result slot), src, n, src_type, dst_type,
+// rounding, saturate}.
+static tx_status fp_to_fp_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.fp_to_fp"};
+  TX_TRY(o.need(7));
+  void *dst, *src;
+  int64_t n, st, dt, rnd, sat;
+  TX_TRY(o.ptr(0, &dst));
+  TX_TRY(o.ptr(1, &src));
+  TX_TRY(o.integer(2, &n));
+  TX_TRY(o.integer(3, &st));
+  TX_TRY(o.integer(4, &dt));
+  TX_TRY(o.integer(5, &rnd));
+  TX_TRY(o.integer(6, &sat));
+  return fp_to_fp(src, tx_dtype(st), dst, tx_dtype(dt), n, tx_rounding(rnd),
+                  int(sat), stream);
+}
+
+static const bool registered = register_op(
+    "tt.fp_to_fp", fp_to_fp_op,
+    "dst(result), src, n:i64, src_type:i32, dst_type:i32, rounding:i32, saturate:i32");
+
+}  // namespace tx
+
+extern "C" TX_API tx_status tx_fp_to_fp(const void *src, tx_dtype src_type,
+                                        void *dst, tx_dtype dst_type, int64_t n,
+                                        tx_rounding rounding, int saturate,
+                                        tx_stream_t stream) {
+  tx::clear_error();
+  return tx::fp_to_fp(src, src_type, dst, dst_type, n, rounding, saturate, stream);
+}

@@ -1,0 +1,210 @@
+// tt.fp_to_fp for fp32 <-> fp8 (OCP E4M3FN and E5M2) on gfx950.
+//
+// Streaming kernels: every load is a 128-bit, wave-contiguous global load and
+// every store is wave-contiguous, so each wave instruction moves whole cache
+// lines.  The conversion itself is integer bit manipulation on the fp32
+// encoding (no hardware fp8 convert instruction is used), so the rounding,
+// saturation and NaN rules are exactly the ones written here:
+//
+//  encode (fp32 -> fp8), round to nearest even:
+//   * normal range (|x| >= 2^(1-bias)): re-bias the fp32 exponent field to
+//     the fp8 bias, add half an fp8 ulp minus one plus the lowest kept bit
+//     (ties-to-even), and keep the top bits.  A carry out of the mantissa
+//     moves into the exponent field by itself.
+//   * subnormal range: add the power of two 2^k whose fp32 ulp equals the fp8
+//     subnormal quantum 2^(1-bias-m) (k = 24 - bias - m); the fp32 adder
+//     rounds to nearest even at exactly that position, and the low bits of
+//     the sum are the fp8 code (the 'magic number' method of rounding by
+//     addition).  fp32 denormal inputs round to zero with either denormal
+//     mode.
+//   * overflow: codes above the largest finite code are clamped to max
+//     (saturating, and round-toward-zero) or to the overflow code (NaN 0x7F
+//     for e4m3fn, Inf 0x7C for e5m2); NaN input gives 0x7F; the sign bit is
+//     OR-ed in last.
+//  decode (fp8 -> fp32), exact: normal codes are re-biased by a shift and an
+//  add; subnormal codes are mant * 2^(1-bias-m), computed as an exact
+//  int->float conversion times a power of two; NaN codes give 0x7FC00000
+//  and e5m2 Inf codes give Inf, each with the code's sign.
+//
+// Semantics follow tt.fp_to_fp (semantic.py:807-827, default RTNE at :809)
+// and the reference's saturating idiom clamp-then-convert
+// (mxfp8_utils.py:17-21, 36-38).
+#include "tx_device.h"
+
+namespace {
+
+enum { E4M3FN = 1, E5M2 = 2 };
+
+template <int FMT>
+struct Fp8Format {
+  static constexpr int M = (FMT == E4M3FN) ? 3 : 2;           // mantissa bits
+  static constexpr int BIAS = (FMT == E4M3FN) ? 7 : 15;
+  static constexpr uint32_t MAXC = (FMT == E4M3FN) ? 0x7Eu : 0x7Bu;
+  static constexpr uint32_t OVF = (FMT == E4M3FN) ? 0x7Fu : 0x7Cu;
+  static constexpr int SH = 23 - M;                           // dropped bits
+  static constexpr uint32_t MIN_NORM_BITS = uint32_t(128 - BIAS) << 23;
+  static constexpr uint32_t REBIAS = uint32_t(127 - BIAS) << 23;
+  static constexpr uint32_t MAGIC_BITS = uint32_t(127 + 24 - BIAS - M) << 23;
+};
+
+// fp32 bits -> fp8 code, round to nearest even.
+template <int FMT, bool SAT>
+__device__ __forceinline__ uint32_t encode_rtne(uint32_t u) {
+  using F = Fp8Format<FMT>;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  const uint32_t lsb = (a >> F::SH) & 1u;
+  const uint32_t nrm = (a - F::REBIAS + ((1u << (F::SH - 1)) - 1u) + lsb) >> F::SH;
+  const float f = __uint_as_float(a) + __uint_as_float(F::MAGIC_BITS);
+  const uint32_t sub = __float_as_uint(f) - F::MAGIC_BITS;
+  uint32_t code = (a < F::MIN_NORM_BITS) ? sub : nrm;
+  code = min(code, SAT ? F::MAXC : F::OVF);
+  if (SAT || FMT == E5M2) code = (a > 0x7F800000u) ? 0x7Fu : code;
+  return code | ((u >> 24) & 0x80u);
+}
+
+// fp32 bits -> fp8 code, round toward zero.
+template <int FMT, bool SAT>
+__device__ __forceinline__ uint32_t encode_rtz(uint32_t u) {
+  using F = Fp8Format<FMT>;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  const uint32_t nrm = (a - F::REBIAS) >> F::SH;
+  const uint32_t e = a >> 23;
+  const uint32_t sig = (a & 0x7FFFFFu) | (e ? 0x800000u : 0u);
+  const uint32_t s = uint32_t(151 - F::BIAS - F::M) - (e ? e : 1u);
+  const uint32_t sub = (s > 31u) ? 0u : (sig >> s);
+  uint32_t code = (a < F::MIN_NORM_BITS) ? sub : nrm;
+  code = min(code, F::MAXC);  // finite values never round away from zero
+  if (a == 0x7F800000u) code = SAT ? F::MAXC : F::OVF;
+  if (a > 0x7F800000u) code = 0x7Fu;
+  return code | ((u >> 24) & 0x80u);
+}
+
+template <int FMT, bool SAT, bool RTZ>
+__device__ __forceinline__ uint32_t encode(uint32_t u) {
+  if constexpr (RTZ) return encode_rtz<FMT, SAT>(u);
+  else return encode_rtne<FMT, SAT>(u);
+}
+
+// fp8 code (0..255) -> fp32 bits, exact.
+template <int FMT>
+__device__ __forceinline__ uint32_t decode(uint32_t c) {
+  using F = Fp8Format<FMT>;
+  const uint32_t mag = c & 0x7Fu;
+  const uint32_t nrm = (mag << F::SH) + F::REBIAS;
+  // subnormal quantum 2^(1-bias-m) as fp32 bits
+  constexpr uint32_t QBITS = uint32_t(127 + 1 - F::BIAS - F::M) << 23;
+  const uint32_t sub = __float_as_uint(float(mag) * __uint_as_float(QBITS));
+  uint32_t r = (mag < (1u << F::M)) ? sub : nrm;
+  if constexpr (FMT == E4M3FN) {
+    r = (mag == 0x7Fu) ? 0x7FC00000u : r;
+  } else {
+    r = (mag >= 0x7Cu) ? ((mag == 0x7Cu) ? 0x7F800000u : 0x7FC00000u) : r;
+  }
+  return r | ((c & 0x80u) << 24);
+}
+
+constexpr int kBlock = 256;
+constexpr int kVecPerThread = 4;                         // float4 loads per thread
+constexpr int kChunk = kBlock * kVecPerThread * 4;       // elements per block step
+
+// Vector encode: [start, n) with (n - start) a multiple of kChunk, src 16-byte
+// aligned, dst 4-byte aligned, start a multiple of 4.
+template <int FMT, bool SAT, bool RTZ>
+__device__ __forceinline__ void encode_vec(const tx_fp8_codec_args &a) {
+  const txd::u32x4 *src = reinterpret_cast<const txd::u32x4 *>(a.src) + a.start / 4;
+  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst) + a.start / 4;
+  const int64_t nchunks = (a.n - a.start) / kChunk;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t w0 = c * (kChunk / 4) + threadIdx.x;
+    txd::u32x4 v[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j)
+      v[j] = __builtin_nontemporal_load(src + w0 + j * kBlock);
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      const uint32_t b0 = encode<FMT, SAT, RTZ>(v[j].x);
+      const uint32_t b1 = encode<FMT, SAT, RTZ>(v[j].y);
+      const uint32_t b2 = encode<FMT, SAT, RTZ>(v[j].z);
+      const uint32_t b3 = encode<FMT, SAT, RTZ>(v[j].w);
+      __builtin_nontemporal_store(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24),
+                                  dst + w0 + j * kBlock);
+    }
+  }
+}
+
+template <int FMT, bool SAT, bool RTZ>
+__device__ __forceinline__ void encode_tail(const tx_fp8_codec_args &a) {
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(a.src);
+  uint8_t *dst = reinterpret_cast<uint8_t *>(a.dst);
+  for (int64_t i = a.start + int64_t(blockIdx.x) * kBlock + threadIdx.x; i < a.n;
+       i += int64_t(gridDim.x) * kBlock)
+    dst[i] = uint8_t(encode<FMT, SAT, RTZ>(src[i]));
+}
+
+// Vector decode: [start, n) with (n - start) a multiple of kChunk, src 4-byte
+// aligned, dst 16-byte aligned, start a multiple of 4.
+template <int FMT>
+__device__ __forceinline__ void decode_vec(const tx_fp8_codec_args &a) {
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(a.src) + a.start / 4;
+  txd::u32x4 *dst = reinterpret_cast<txd::u32x4 *>(a.dst) + a.start / 4;
+  const int64_t nchunks = (a.n - a.start) / kChunk;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t w0 = c * (kChunk / 4) + threadIdx.x;
+    uint32_t v[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j)
+      v[j] = __builtin_nontemporal_load(src + w0 + j * kBlock);
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      txd::u32x4 o;
+      o.x = decode<FMT>(v[j] & 0xFFu);
+      o.y = decode<FMT>((v[j] >> 8) & 0xFFu);
+      o.z = decode<FMT>((v[j] >> 16) & 0xFFu);
+      o.w = decode<FMT>(v[j] >> 24);
+      __builtin_nontemporal_store(o, dst + w0 + j * kBlock);
+    }
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ void decode_tail(const tx_fp8_codec_args &a) {
+  const uint8_t *src = reinterpret_cast<const uint8_t *>(a.src);
+  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst);
+  for (int64_t i = a.start + int64_t(blockIdx.x) * kBlock + threadIdx.x; i < a.n;
+       i += int64_t(gridDim.x) * kBlock)
+    dst[i] = decode<FMT>(src[i]);
+}
+
+}  // namespace
+
+#define TX_ENCODE_KERNELS(NAME, FMT, SAT, RTZ)                                      \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_encode_##NAME##_vec(              \
+      const tx_fp8_codec_args a) {                                                  \
+    encode_vec<FMT, SAT, RTZ>(a);                                                   \
+  }                                                                                 \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_encode_##NAME##_tail(             \
+      const tx_fp8_codec_args a) {                                                  \
+    encode_tail<FMT, SAT, RTZ>(a);                                                  \
+  }
+
+TX_ENCODE_KERNELS(e4m3fn_rtne, E4M3FN, false, false)
+TX_ENCODE_KERNELS(e4m3fn_rtne_sat, E4M3FN, true, false)
+TX_ENCODE_KERNELS(e4m3fn_rtz, E4M3FN, false, true)
+TX_ENCODE_KERNELS(e4m3fn_rtz_sat, E4M3FN, true, true)
+TX_ENCODE_KERNELS(e5m2_rtne, E5M2, false, false)
+TX_ENCODE_KERNELS(e5m2_rtne_sat, E5M2, true, false)
+TX_ENCODE_KERNELS(e5m2_rtz, E5M2, false, true)
+TX_ENCODE_KERNELS(e5m2_rtz_sat, E5M2, true, true)
+
+TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e4m3fn_vec(const tx_fp8_codec_args a) {
+  decode_vec<E4M3FN>(a);
+}
+TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e4m3fn_tail(const tx_fp8_codec_args a) {
+  decode_tail<E4M3FN>(a);
+}
+TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e5m2_vec(const tx_fp8_codec_args a) {
+  decode_vec<E5M2>(a);
+}
+TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e5m2_tail(const tx_fp8_codec_args a) {
+  decode_tail<E5M2>(a);
+}

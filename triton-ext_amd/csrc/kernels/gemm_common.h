@@ -1,0 +1,110 @@
+// Shared GEMM machinery for the bf16 and fp8 tt.dot kernels on gfx950.
+//
+// Layout contract (both operands K-contiguous, as tt.dot's A row-major /
+// B column-major case at test_amd_gemm_pipelined.py:303-331 with B stored as
+// N rows of K):
+//   A: M rows of K elements (row stride lda), B: N rows of K (row stride ldb),
+//   C: row-major M x N bf16 (row stride ldc).
+//
+// Tiling: a workgroup owns a BM x BN tile of C and walks K in steps of one
+// 128-byte row slice (64 bf16 or 128 fp8 elements).  Each step stages the
+// BM x 128 B slice of A and the BN x 128 B slice of B in LDS; every 128-byte
+// LDS row holds 8 chunks of 16 bytes stored at chunk ^ (row & 7), so that 8
+// lanes reading the same logical chunk of 8 consecutive rows (one
+// ds_read_b128 phase) touch 8 different bank groups.  Two LDS stages are
+// used: global loads for step k+1 are in flight (in registers) while step k
+// is multiplied, then written to the other stage, with one barrier per step.
+//
+// MFMA roles: the B tile feeds the MFMA "A" operand and the A tile the MFMA
+// "B" operand, so an MFMA result block is C^T: lane l, register j holds
+// C[m0 + (l % 16)][n0 + 4 * (l / 16) + j].  Each lane therefore owns 4
+// consecutive columns of one row, which the epilogue writes as one 8-byte
+// store.  Within one MFMA the K order of the operand lanes is a free choice
+// as long as both operands use the same one: lane group g = l / 16 holds the
+// two 16-byte chunks 2g and 2g+1 of the 128-byte slice.
+#pragma once
+
+#include "tx_device.h"
+
+namespace txg {
+
+using txd::f32x4;
+using txd::i32x8;
+using txd::u32x4;
+
+constexpr int kRowBytes = 128;  // one K step of one row, in bytes
+constexpr int kChunks = 8;      // 16-byte chunks per row
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+
+// Byte offset of (row, chunk) inside one LDS operand stage.
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * kRowBytes + swz(row, chunk) * 16;
+}
+
+// Load one 16-byte chunk of a K-contiguous row with pieces of VEC bytes,
+// zero-filling pieces past the end of the row (kb_end bytes) or invalid rows.
+template <int VEC>
+__device__ __forceinline__ u32x4 load_chunk(const uint8_t *row_ptr, int kb, int kb_end, bool row_ok) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if constexpr (VEC == 16) {
+    if (row_ok && kb < kb_end) v = *reinterpret_cast<const u32x4 *>(row_ptr + kb);
+  } else if constexpr (VEC == 8) {
+    txd::u32x2 lo = {0u, 0u}, hi = {0u, 0u};
+    if (row_ok && kb < kb_end) lo = *reinterpret_cast<const txd::u32x2 *>(row_ptr + kb);
+    if (row_ok && kb + 8 < kb_end) hi = *reinterpret_cast<const txd::u32x2 *>(row_ptr + kb + 8);
+    v.x = lo.x; v.y = lo.y; v.z = hi.x; v.w = hi.y;
+  } else if constexpr (VEC == 4) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (row_ok && kb + 4 * i < kb_end) ? *reinterpret_cast<const uint32_t *>(row_ptr + kb + 4 * i) : 0u;
+    v.x = w[0]; v.y = w[1]; v.z = w[2]; v.w = w[3];
+  } else if constexpr (VEC == 2) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t lo = (row_ok && kb + 4 * i < kb_end) ? *reinterpret_cast<const uint16_t *>(row_ptr + kb + 4 * i) : 0u;
+      uint32_t hi = (row_ok && kb + 4 * i + 2 < kb_end) ? *reinterpret_cast<const uint16_t *>(row_ptr + kb + 4 * i + 2) : 0u;
+      w[i] = lo | (hi << 16);
+    }
+    v.x = w[0]; v.y = w[1]; v.z = w[2]; v.w = w[3];
+  } else {  // VEC == 1
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int o = kb + 4 * i + b;
+        const uint32_t byte = (row_ok && o < kb_end) ? row_ptr[o] : 0u;
+        acc |= byte << (8 * b);
+      }
+      w[i] = acc;
+    }
+    v.x = w[0]; v.y = w[1]; v.z = w[2]; v.w = w[3];
+  }
+  return v;
+}
+
+// Map a linear workgroup id to a (tile_m, tile_n) pair: first regroup the ids
+// so that each of the 8 XCDs (workgroups are dispatched round-robin over
+// XCDs) gets a contiguous range of tile ids, then rasterise tile ids in
+// groups of group_m tile rows so neighbouring tiles share A and B panels in
+// the XCD's L2.
+__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int group_m,
+                                            int *tm, int *tn) {
+  const int total = tiles_m * tiles_n;
+  const int per = total / 8, rem = total % 8;
+  const int x = wg % 8, i = wg / 8;
+  const int pid = x * per + (x < rem ? x : rem) + i;
+  const int in_group = group_m * tiles_n;
+  const int gid = pid / in_group;
+  const int first_m = gid * group_m;
+  const int gsz = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+  const int r = pid % in_group;
+  *tm = first_m + r % gsz;
+  *tn = r / gsz;
+}
+
+}  // namespace txg

@@ -1,0 +1,26 @@
+// tt.dot on fp8 operands with the per-row / per-column fp32 scale epilogue,
+// bf16 output, on gfx950 (v_mfma_f32_16x16x128_f8f6f4).  Variants: tile
+// 256x256 and 128x128, operand formats e4m3fn/e5m2 for A and B, global load
+// width 16, 4 or 1 bytes (1-byte loads only with the 128x128 tile, where
+// their extra registers fit; see gemm_common.h for the layout contract).
+#include "gemm_tile.h"
+
+using namespace txg;
+
+#define TX_GEMM_FP8(FA, FB, ELA, ELB, NAME, BM, BN, WM, WN, VEC)                         \
+  TX_KERNEL void __launch_bounds__(64 * WM * WN) tx_gemm_fp8_##FA##_##FB##_##NAME##_v##VEC( \
+      const tx_gemm_args a) {                                                           \
+    gemm_tile<GemmCfg<ELA, ELB, BM, BN, WM, WN, VEC>>(a);                               \
+  }
+
+#define TX_GEMM_FP8_FORMATS(NAME, BM, BN, WM, WN, VEC)                             \
+  TX_GEMM_FP8(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3, NAME, BM, BN, WM, WN, VEC)         \
+  TX_GEMM_FP8(e5m2, e5m2, EL_E5M2, EL_E5M2, NAME, BM, BN, WM, WN, VEC)             \
+  TX_GEMM_FP8(e4m3fn, e5m2, EL_E4M3, EL_E5M2, NAME, BM, BN, WM, WN, VEC)           \
+  TX_GEMM_FP8(e5m2, e4m3fn, EL_E5M2, EL_E4M3, NAME, BM, BN, WM, WN, VEC)
+
+TX_GEMM_FP8_FORMATS(256x256, 256, 256, 2, 2, 16)
+TX_GEMM_FP8_FORMATS(256x256, 256, 256, 2, 2, 4)
+TX_GEMM_FP8_FORMATS(128x128, 128, 128, 2, 2, 16)
+TX_GEMM_FP8_FORMATS(128x128, 128, 128, 2, 2, 4)
+TX_GEMM_FP8_FORMATS(128x128, 128, 128, 2, 2, 1)

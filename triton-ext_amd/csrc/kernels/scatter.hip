@@ -1,0 +1,260 @@
+// tt.atomic_rmw in scatter form, bins[idx[i]] (op)= val[i], on gfx950.
+//
+// Triton lowers tl.atomic_add(bins + idx, v) to one global atomic per lane
+// (tt.atomic_rmw, passed through at uTLXConversionPatterns.cpp:611), which
+// serialises in L2 on hot bins.  These kernels reduce in three levels before
+// global memory is touched:
+//   1. registers: each lane loads 4 updates with one 128-bit load of indices
+//      and one of values;
+//   2. wavefront: runs of equal keys inside a wavefront are combined with a
+//      ballot/read-lane loop before they reach a shared atomic (spill path);
+//   3. workgroup: an LDS table owned by the workgroup.  When all bins fit in
+//      LDS the table is direct-mapped (slot = bin); otherwise it is an open
+//      addressing hash table (Fibonacci hash, bounded linear probing) keyed
+//      by bin, and updates whose probe sequence is full spill to global
+//      atomics.  At the end the table is flushed with one global atomic per
+//      occupied slot.
+// Every combine is an associative, commutative op, so integer results are
+// exact and order independent; fp32 sums differ from a sequential sum only
+// by rounding order.
+#include "tx_device.h"
+
+namespace {
+
+enum Op { ADD = 0, FADD = 1, MAX = 2, MIN = 3, UMAX = 4, UMIN = 5, AND = 6, OR = 7, XOR = 8 };
+
+constexpr int kBlock = 1024;
+constexpr int kDirectSlots = 36864;          // 144 KiB of 4-byte counters
+constexpr int kHashLog2 = 14;                // 16384 slots, 128 KiB keys + values
+constexpr int kHashSlots = 1 << kHashLog2;
+constexpr int kProbes = 4;
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+
+template <int OP> struct OpTraits;
+template <> struct OpTraits<ADD> { using T = uint32_t; static __device__ T id() { return 0u; } };
+template <> struct OpTraits<FADD> { using T = float; static __device__ T id() { return 0.0f; } };
+template <> struct OpTraits<MAX> { using T = int32_t; static __device__ T id() { return INT32_MIN; } };
+template <> struct OpTraits<MIN> { using T = int32_t; static __device__ T id() { return INT32_MAX; } };
+template <> struct OpTraits<UMAX> { using T = uint32_t; static __device__ T id() { return 0u; } };
+template <> struct OpTraits<UMIN> { using T = uint32_t; static __device__ T id() { return 0xFFFFFFFFu; } };
+template <> struct OpTraits<AND> { using T = uint32_t; static __device__ T id() { return 0xFFFFFFFFu; } };
+template <> struct OpTraits<OR> { using T = uint32_t; static __device__ T id() { return 0u; } };
+template <> struct OpTraits<XOR> { using T = uint32_t; static __device__ T id() { return 0u; } };
+
+template <int OP, typename T>
+__device__ __forceinline__ T combine(T a, T b) {
+  if constexpr (OP == ADD || OP == FADD) return a + b;
+  else if constexpr (OP == MAX || OP == UMAX) return a > b ? a : b;
+  else if constexpr (OP == MIN || OP == UMIN) return a < b ? a : b;
+  else if constexpr (OP == AND) return a & b;
+  else if constexpr (OP == OR) return a | b;
+  else return a ^ b;
+}
+
+// Atomic combine into LDS or global memory (the address space follows p).
+template <int OP, typename T>
+__device__ __forceinline__ void atomic_combine(T *p, T v) {
+  if constexpr (OP == ADD || OP == FADD) atomicAdd(p, v);
+  else if constexpr (OP == MAX || OP == UMAX) atomicMax(p, v);
+  else if constexpr (OP == MIN || OP == UMIN) atomicMin(p, v);
+  else if constexpr (OP == AND) atomicAnd(p, v);
+  else if constexpr (OP == OR) atomicOr(p, v);
+  else atomicXor(p, v);
+}
+
+template <int OP, typename T>
+__device__ __forceinline__ bool is_identity(T v) {
+  // Integer identities can be skipped when flushing; an fp32 +0 cannot
+  // (adding +0 turns a -0 bin into +0), so fp32 slots always flush.
+  if constexpr (OP == FADD) return false;
+  else return v == OpTraits<OP>::id();
+}
+
+// Wavefront-level combine for the lanes in `pending` (a subset of active
+// lanes): repeatedly take the lowest pending lane's key, gather every pending
+// lane holding the same key, reduce their values across the wavefront, and
+// let the leader issue one global atomic.
+template <int OP, typename T>
+__device__ __forceinline__ void wave_combine_global(T *bins, bool pending, uint32_t key, T v) {
+  uint64_t todo = __ballot(pending);
+  while (todo) {
+    const int leader = __ffsll((unsigned long long)todo) - 1;
+    const uint32_t lkey = __shfl(key, leader);
+    const bool match = pending && key == lkey;
+    const uint64_t mm = __ballot(match);
+    T mine = match ? v : OpTraits<OP>::id();
+    // butterfly reduction over the wavefront (identity for non-matching lanes)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mine = combine<OP, T>(mine, __shfl_xor(mine, off));
+    if (threadIdx.x % 64 == unsigned(leader)) atomic_combine<OP, T>(bins + lkey, mine);
+    if (match) pending = false;
+    todo &= ~mm;
+  }
+}
+
+template <int OP>
+struct Scatter {
+  using T = typename OpTraits<OP>::T;
+
+  // Load up to 4 updates for this lane starting at element e (e % 4 == 0).
+  // `full` means all 4 are in range and the buffers are 16-byte aligned.
+  static __device__ __forceinline__ void load4(const tx_scatter_args &a, int64_t e, int64_t end,
+                                               bool vec, uint32_t key[4], T val[4],
+                                               bool ok[4]) {
+    const int32_t *idx = a.idx;
+    const T *vals = reinterpret_cast<const T *>(a.val);
+    if (vec && e + 4 <= end) {
+      const txd::i32x4 k4 = __builtin_nontemporal_load(reinterpret_cast<const txd::i32x4 *>(idx + e));
+      const txd::u32x4 v4 = __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(vals + e));
+      uint32_t mbits = 0xFFFFFFFFu;
+      if (a.mask) mbits = *reinterpret_cast<const uint32_t *>(a.mask + e);
+      const int32_t kk[4] = {k4.x, k4.y, k4.z, k4.w};
+      const uint32_t vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        key[j] = uint32_t(kk[j]);
+        val[j] = __builtin_bit_cast(T, vv[j]);
+        ok[j] = kk[j] >= 0 && kk[j] < a.nbins && ((mbits >> (8 * j)) & 0xFFu) != 0;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t i = e + j;
+        ok[j] = i < end;
+        key[j] = 0;
+        val[j] = OpTraits<OP>::id();
+        if (ok[j]) {
+          const int32_t k = idx[i];
+          key[j] = uint32_t(k);
+          val[j] = vals[i];
+          ok[j] = k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0);
+        }
+      }
+    }
+  }
+
+  // Direct-mapped LDS privatisation: all bins fit in LDS.
+  static __device__ void direct(const tx_scatter_args &a) {
+    __shared__ T table[kDirectSlots];
+    const int nb = a.nbins;
+    for (int s = threadIdx.x; s < nb; s += kBlock) table[s] = OpTraits<OP>::id();
+    __syncthreads();
+    const int64_t begin = int64_t(blockIdx.x) * a.per_block;
+    const int64_t end = begin + a.per_block < a.n ? begin + a.per_block : a.n;
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
+                     (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
+    for (int64_t e = begin + 4 * int64_t(threadIdx.x); e < end; e += 4 * kBlock) {
+      uint32_t key[4];
+      T val[4];
+      bool ok[4];
+      load4(a, e, end, vec, key, val, ok);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (ok[j]) atomic_combine<OP, T>(&table[key[j]], val[j]);
+    }
+    __syncthreads();
+    T *bins = reinterpret_cast<T *>(a.bins);
+    for (int s = threadIdx.x; s < nb; s += kBlock) {
+      const T v = table[s];
+      if (!is_identity<OP, T>(v)) atomic_combine<OP, T>(bins + s, v);
+    }
+  }
+
+  // Hash-table LDS cache with global spill.
+  static __device__ void hashed(const tx_scatter_args &a) {
+    __shared__ uint32_t keys[kHashSlots];
+    __shared__ T vals[kHashSlots];
+    for (int s = threadIdx.x; s < kHashSlots; s += kBlock) {
+      keys[s] = kEmpty;
+      vals[s] = OpTraits<OP>::id();
+    }
+    __syncthreads();
+    T *bins = reinterpret_cast<T *>(a.bins);
+    const int64_t begin = int64_t(blockIdx.x) * a.per_block;
+    const int64_t end = begin + a.per_block < a.n ? begin + a.per_block : a.n;
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
+                     (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
+    // Loop bound is uniform across the workgroup so that every lane takes part
+    // in the wavefront-level combine of the spill path.
+    const int64_t span = end > begin ? end - begin : 0;
+    const int64_t iters = (span + 4 * kBlock - 1) / (4 * kBlock);
+    for (int64_t it = 0; it < iters; ++it) {
+      const int64_t e = begin + it * 4 * kBlock + 4 * int64_t(threadIdx.x);
+      uint32_t key[4];
+      T val[4];
+      bool ok[4];
+      load4(a, e, end, vec, key, val, ok);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bool spill = false;
+        if (ok[j]) {
+          spill = true;
+          const uint32_t h = (key[j] * 2654435769u) >> (32 - kHashLog2);
+#pragma unroll
+          for (int p = 0; p < kProbes; ++p) {
+            const uint32_t slot = (h + p) & (kHashSlots - 1);
+            uint32_t k = __atomic_load_n(&keys[slot], __ATOMIC_RELAXED);
+            if (k == kEmpty) k = atomicCAS(&keys[slot], kEmpty, key[j]);
+            if (k == kEmpty || k == key[j]) {
+              atomic_combine<OP, T>(&vals[slot], val[j]);
+              spill = false;
+              break;
+            }
+          }
+        }
+        wave_combine_global<OP, T>(bins, spill, key[j], val[j]);
+      }
+    }
+    __syncthreads();
+    for (int s = threadIdx.x; s < kHashSlots; s += kBlock) {
+      const uint32_t k = keys[s];
+      const T v = vals[s];
+      if (k != kEmpty && !is_identity<OP, T>(v)) atomic_combine<OP, T>(bins + k, v);
+    }
+  }
+
+  // One returning atomic per update: old[i] is the bin's prior value.
+  static __device__ void with_old(const tx_scatter_args &a) {
+    T *bins = reinterpret_cast<T *>(a.bins);
+    const T *vals = reinterpret_cast<const T *>(a.val);
+    T *old = reinterpret_cast<T *>(a.old);
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) {
+      const int32_t k = a.idx[i];
+      T r = T(0);
+      if (k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0)) {
+        T *p = bins + k;
+        const T v = vals[i];
+        if constexpr (OP == ADD || OP == FADD) r = atomicAdd(p, v);
+        else if constexpr (OP == MAX || OP == UMAX) r = atomicMax(p, v);
+        else if constexpr (OP == MIN || OP == UMIN) r = atomicMin(p, v);
+        else if constexpr (OP == AND) r = atomicAnd(p, v);
+        else if constexpr (OP == OR) r = atomicOr(p, v);
+        else r = atomicXor(p, v);
+      }
+      old[i] = r;
+    }
+  }
+};
+
+}  // namespace
+
+#define TX_SCATTER_KERNELS(NAME, OP)                                                   \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_scatter_##NAME##_direct(const tx_scatter_args a) { \
+    Scatter<OP>::direct(a);                                                            \
+  }                                                                                    \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_scatter_##NAME##_hashed(const tx_scatter_args a) { \
+    Scatter<OP>::hashed(a);                                                            \
+  }                                                                                    \
+  TX_KERNEL void __launch_bounds__(256) tx_scatter_##NAME##_old(const tx_scatter_args a) { \
+    Scatter<OP>::with_old(a);                                                          \
+  }
+
+TX_SCATTER_KERNELS(add, ADD)
+TX_SCATTER_KERNELS(fadd, FADD)
+TX_SCATTER_KERNELS(max, MAX)
+TX_SCATTER_KERNELS(min, MIN)
+TX_SCATTER_KERNELS(umax, UMAX)
+TX_SCATTER_KERNELS(umin, UMIN)
+TX_SCATTER_KERNELS(and, AND)
+TX_SCATTER_KERNELS(or, OR)
+TX_SCATTER_KERNELS(xor, XOR)

@@ -1,0 +1,68 @@
+/*
+ * Kernel argument blocks, shared by the host launchers (csrc/host) and the
+ * gfx950 kernels (csrc/kernels).  Each kernel takes exactly one of these
+ * structs by value, so the kernarg segment is the struct itself.
+ * Plain C layout only: fixed-width integers and raw pointers.
+ */
+#ifndef TX_KERNEL_ARGS_H
+#define TX_KERNEL_ARGS_H
+
+#include <stdint.h>
+
+/* fp8 codec: n elements; vector kernels process n_vec = a multiple of their
+ * block chunk, the tail kernel processes [start, n). */
+typedef struct tx_fp8_codec_args {
+  const void *src;
+  void *dst;
+  int64_t start; /* first element this launch handles */
+  int64_t n;     /* one past the last element this launch handles */
+} tx_fp8_codec_args;
+
+/* scatter-reduce */
+typedef struct tx_scatter_args {
+  void *bins;
+  const int32_t *idx;
+  const void *val;
+  const uint8_t *mask; /* may be NULL */
+  void *old;           /* may be NULL (aggregating kernels ignore it) */
+  int64_t n;
+  int32_t nbins;
+  int32_t per_block;   /* updates per workgroup (multiple of 4 * blockDim) */
+} tx_scatter_args;
+
+/* GEMM, both operands K-contiguous ("A row-major, B column-major").
+ * Element strides for bf16; byte strides for fp8. */
+typedef struct tx_gemm_args {
+  const void *A;
+  const void *B;
+  void *C;
+  const float *scale_a; /* fp8 only */
+  const float *scale_b; /* fp8 only */
+  int64_t lda;
+  int64_t ldb;
+  int64_t ldc;
+  int32_t M;
+  int32_t N;
+  int32_t K;
+  int32_t tiles_m;   /* ceil(M / tile) */
+  int32_t tiles_n;   /* ceil(N / tile) */
+  int32_t group_m;   /* rasterisation group height in tiles */
+} tx_gemm_args;
+
+/* fp8 dequant GEMV */
+typedef struct tx_gemv_args {
+  const uint16_t *x; /* bf16 bits */
+  const uint8_t *W;
+  const float *scales;
+  uint16_t *y;       /* bf16 bits */
+  int64_t ldx;
+  int64_t ldw;
+  int64_t ld_scales;
+  int64_t ldy;
+  int32_t M;
+  int32_t N;
+  int32_t K;
+  int32_t group;
+} tx_gemv_args;
+
+#endif /* TX_KERNEL_ARGS_H */

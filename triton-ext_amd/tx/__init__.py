@@ -1,0 +1,251 @@
+"""tx: MI355X (gfx950) kernels for the data-parallel ops of the reference's
+Triton-extension path, behind the C ABI of libtxamd.so.
+
+Python host mirror of that path.  Each function takes torch tensors that
+already live on the GPU (torch provides device memory and the current stream
+only) and calls one C entry point; nothing here computes on the CPU and there
+is no fallback: a missing library raises at import, a failing call raises
+``TxError``.
+
+Op names follow the Triton ops they replace:
+  fp_to_fp          tt.fp_to_fp        (semantic.py:807-827; NewOps.cpp:249-303)
+  atomic_rmw        tt.atomic_rmw      (uTLXConversionPatterns.cpp:611)
+  dot / matmul      tt.dot, bf16       (test_amd_gemm_pipelined.py:184-331)
+  dot_scaled_rowcol tt.dot, fp8 + row/column scale epilogue
+  gemv_fp8_dequant  fp8 weight-only dequant GEMV
+plus the registration surface (plugin_info, invoke) mirroring
+tritonGetPluginInfo (support/Export.cpp:58-97).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import TxError, check, lib
+
+__all__ = [
+    "TxError", "fp_to_fp", "atomic_rmw", "dot", "matmul", "dot_scaled_rowcol",
+    "gemv_fp8_dequant", "plugin_info", "invoke", "get_fp8_format_name",
+    "version", "init", "RTNE", "RTZ", "RS",
+]
+
+RTNE, RTZ, RS = _lib.RTNE, _lib.RTZ, _lib.RS
+_ROUNDING = {"rtne": RTNE, "rtz": RTZ, "rs": RS, RTNE: RTNE, RTZ: RTZ, RS: RS}
+
+_TX_DTYPE = {
+    torch.float32: _lib.F32,
+    torch.float8_e4m3fn: _lib.FP8E4M3FN,
+    torch.float8_e5m2: _lib.FP8E5M2,
+    torch.bfloat16: _lib.BF16,
+    torch.int32: _lib.I32,
+    torch.uint32: _lib.U32,
+}
+_FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
+
+
+def version() -> str:
+    return lib.txVersion().decode()
+
+
+def init() -> None:
+    """Load the gfx950 code objects on the current device (else lazily)."""
+    check(lib.txInit())
+
+
+def get_fp8_format_name(dtype) -> str:
+    """Name of an fp8 dtype, as utility.py:92-105 names tl.float8e5/float8e4nv."""
+    if dtype == torch.float8_e5m2:
+        return "e5m2"
+    if dtype == torch.float8_e4m3fn:
+        return "e4m3"
+    raise AssertionError(
+        f"get_fp8_format_name only supports float8_e5m2 (e5m2) and float8_e4m3fn (e4m3), got {dtype}")
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _on_gpu(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("tx ops take GPU tensors only (no CPU path)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+# --------------------------------------------------------------------------
+def fp_to_fp(x: torch.Tensor, dtype, rounding="rtne", saturate: bool = False,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """tt.fp_to_fp: fp32 -> fp8 (e4m3fn / e5m2) or fp8 -> fp32, elementwise.
+
+    rounding: "rtne" (Triton's default downcast, semantic.py:809) or "rtz".
+    saturate: the reference's clamp(x, -max, max)-then-convert idiom
+    (mxfp8_utils.py:36-38); without it overflow gives NaN (e4m3fn) / Inf (e5m2).
+    """
+    _on_gpu(x, out)
+    if not x.is_contiguous():
+        raise ValueError("fp_to_fp needs a contiguous input")
+    if x.dtype not in _TX_DTYPE or dtype not in _TX_DTYPE:
+        raise ValueError(f"unsupported conversion {x.dtype} -> {dtype}")
+    if out is None:
+        out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    elif out.dtype != dtype or out.numel() != x.numel() or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the target dtype and size")
+    check(lib.tx_fp_to_fp(_ptr(x), _TX_DTYPE[x.dtype], _ptr(out), _TX_DTYPE[dtype],
+                          x.numel(), _ROUNDING[rounding], int(bool(saturate)), _stream(x)))
+    return out
+
+
+def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor,
+               mask: torch.Tensor | None = None, return_old: bool = False):
+    """tt.atomic_rmw, scatter form: bins[idx[i]] (op)= val[i] for all i, in place.
+
+    op: add | fadd | max | min | umax | umin | and | or | xor (as tl.atomic_*).
+    Updates with idx outside [0, len(bins)) or mask[i] == 0 are dropped.
+    return_old=True returns, per update, the bin's value before it (the
+    tt.atomic_rmw result); that form does no pre-aggregation.
+    """
+    _on_gpu(bins, idx, val, mask)
+    if op not in _lib.RMW:
+        raise ValueError(f"unknown rmw op {op!r}")
+    if idx.dtype != torch.int32:
+        raise ValueError("idx must be int32")
+    for t in (bins, idx, val) + ((mask,) if mask is not None else ()):
+        if not t.is_contiguous():
+            raise ValueError("atomic_rmw needs contiguous tensors")
+    if val.numel() != idx.numel() or (mask is not None and mask.numel() != idx.numel()):
+        raise ValueError("idx, val (and mask) must have the same number of elements")
+    if mask is not None and mask.dtype not in (torch.uint8, torch.bool):
+        raise ValueError("mask must be uint8 or bool")
+    if val.dtype != bins.dtype:
+        raise ValueError("val and bins must have the same dtype")
+    old = torch.empty_like(val) if return_old else None
+    check(lib.tx_atomic_rmw_scatter(_ptr(bins), _TX_DTYPE[bins.dtype], bins.numel(), _ptr(idx),
+                                    _ptr(val), _ptr(mask), idx.numel(), _lib.RMW[op], _ptr(old),
+                                    _stream(bins)))
+    return old if return_old else bins
+
+
+def dot(a: torch.Tensor, b_nk: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """tt.dot on bf16: out[M,N] = a[M,K] @ b where b is column-major K x N,
+    passed as its N x K (K-contiguous) storage ``b_nk``.  fp32 accumulate,
+    bf16 output."""
+    _on_gpu(a, b_nk, out)
+    if a.dtype != torch.bfloat16 or b_nk.dtype != torch.bfloat16:
+        raise ValueError("dot takes bf16 operands")
+    if a.dim() != 2 or b_nk.dim() != 2 or a.shape[1] != b_nk.shape[1]:
+        raise ValueError(f"incompatible shapes {tuple(a.shape)} and {tuple(b_nk.shape)} (N x K)")
+    if a.stride(1) != 1 or b_nk.stride(1) != 1:
+        raise ValueError("operands must be K-contiguous")
+    M, K = a.shape
+    N = b_nk.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major bf16 M x N tensor")
+    check(lib.tx_dot_bf16(_ptr(a), a.stride(0), _ptr(b_nk), b_nk.stride(0), _ptr(out),
+                          out.stride(0), M, N, K, _stream(a)))
+    return out
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Host wrapper in the shape of the reference's matmul(a, b)
+    (test_amd_gemm_pipelined.py:303-331): a is M x K, b is K x N; allocates
+    the output.  b must be column-major (b.stride(0) == 1), i.e. a transposed
+    view of an N x K tensor."""
+    assert a.shape[1] == b.shape[0], "Incompatible dimensions"
+    if b.stride(0) != 1:
+        raise ValueError("b must be column-major (K-contiguous); pass w.t() of an N x K tensor")
+    return dot(a, b.t())
+
+
+def dot_scaled_rowcol(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
+                      scale_b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp8 tt.dot with fp32 per-row (scale_a[M]) and per-column (scale_b[N])
+    scales: out = bf16(scale_a[:,None] * scale_b[None,:] * (a_q @ b_q))."""
+    _on_gpu(a_q, scale_a, b_q_nk, scale_b, out)
+    if a_q.dtype not in _FP8 or b_q_nk.dtype not in _FP8:
+        raise ValueError("dot_scaled_rowcol takes fp8 operands")
+    if a_q.dim() != 2 or b_q_nk.dim() != 2 or a_q.shape[1] != b_q_nk.shape[1]:
+        raise ValueError("incompatible shapes")
+    if a_q.stride(1) != 1 or b_q_nk.stride(1) != 1:
+        raise ValueError("operands must be K-contiguous")
+    M, K = a_q.shape
+    N = b_q_nk.shape[0]
+    if scale_a.dtype != torch.float32 or scale_b.dtype != torch.float32 or \
+            scale_a.numel() != M or scale_b.numel() != N or \
+            not scale_a.is_contiguous() or not scale_b.is_contiguous():
+        raise ValueError("scales must be contiguous fp32 vectors of length M and N")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a_q.device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major bf16 M x N tensor")
+    check(lib.tx_dot_fp8_scaled(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
+                                _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0),
+                                _ptr(scale_b), _ptr(out), out.stride(0), M, N, K, _stream(a_q)))
+    return out
+
+
+def gemv_fp8_dequant(x: torch.Tensor, w_q: torch.Tensor, scales: torch.Tensor, group: int = 128,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Weight-only fp8 GEMV: out[M,N] = bf16(x[M,K] @ (w_q[N,K] * scales[N, k//group]).T)."""
+    _on_gpu(x, w_q, scales, out)
+    if x.dtype != torch.bfloat16 or w_q.dtype not in _FP8 or scales.dtype != torch.float32:
+        raise ValueError("x bf16, w_q fp8, scales fp32")
+    M, K = x.shape
+    N = w_q.shape[0]
+    if w_q.shape[1] != K or scales.shape[0] != N:
+        raise ValueError("incompatible shapes")
+    if x.stride(1) != 1 or w_q.stride(1) != 1 or scales.stride(1) != 1:
+        raise ValueError("rows must be contiguous")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    check(lib.tx_gemv_fp8_dequant(_ptr(x), x.stride(0), _ptr(w_q), _TX_DTYPE[w_q.dtype],
+                                  w_q.stride(0), _ptr(scales), scales.stride(0), group,
+                                  _ptr(out), out.stride(0), M, N, K, _stream(x)))
+    return out
+
+
+# --------------------------------------------------------------------------
+def plugin_info():
+    """The op table, as tritonGetPluginInfo exposes the reference's ops:
+    returns (name, version, target, [(op name, signature), ...])."""
+    info = lib.txGetPluginInfo()
+    if not info:
+        raise TxError(_lib.GENERIC_FAILURE, _lib.last_error())
+    try:
+        p = info.contents
+        ops = [(p.ops[i].name.decode(), p.ops[i].signature.decode()) for i in range(p.num_ops)]
+        return p.name.decode(), p.version.decode(), p.target.decode(), ops
+    finally:
+        lib.txReleasePluginInfo(info)
+
+
+def invoke(name: str, operands, stream=None) -> None:
+    """Call a registered op through the table.  operands: tensors (passed as
+    device pointers), None (NULL pointer) or ints (integer constants);
+    operands[0] is the result slot."""
+    vals = (_lib.TxValue * max(1, len(operands)))()
+    for i, o in enumerate(operands):
+        if o is None:
+            vals[i] = _lib.TxValue.ptr(None)
+        elif isinstance(o, torch.Tensor):
+            vals[i] = _lib.TxValue.ptr(o.data_ptr())
+        else:
+            vals[i] = _lib.TxValue.int(o)
+    if stream is None and torch.cuda.is_available():
+        stream = torch.cuda.current_stream().cuda_stream
+    check(lib.txInvokeOp(name.encode(), vals, len(operands), ctypes.c_void_p(stream)))

@@ -1,0 +1,139 @@
+"""Seeded synthetic inputs for the five measured configurations.
+
+Host-side numpy generators (identical bytes on any host for a given seed), used
+by bench.py and the tests.  Each returns numpy arrays; callers copy them to
+the GPU.  Base seed 20261201; config c uses seed ``BASE ^ (c << 32)``.
+
+  c=1 fp8 round trip: 16,777,216 fp32 values z * 2^u (z ~ N(0,1), u ~ U[-10, 9])
+      with 1 % of positions replaced by special values.
+  c=2 scatter-reduce: 67,108,864 updates into 65,536 bins, bin = Zipf(1.1) rank - 1;
+      int32 values U[0, 1000) or fp32 values N(0, 1).
+  c=3 bf16 GEMM: A M x K and B N x K (B column-major K x N), U(-1, 1) -> bf16 RNE.
+  c=4 fp8 scaled GEMM: A, B ~ N(0, 1); per-row / per-column absmax scales,
+      e4m3fn RNE with saturation of x * (448 / absmax).
+  c=5 dequant GEMV: x bf16 N(0, 1) M x K; W ~ N(0, 0.02) N x K quantised to
+      e5m2 with one fp32 scale per 128 consecutive k (absmax / 57344).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+BASE_SEED = 20261201
+
+
+def rng(config: int, stream: int = 0) -> np.random.Generator:
+    return np.random.default_rng([BASE_SEED ^ (config << 32), stream])
+
+
+# ----------------------------------------------------------------- fp8 (c=1)
+def fp8_specials() -> np.ndarray:
+    """The special fp32 values mixed into the fp8 conversion input."""
+    def f(bits):
+        return np.array(bits, dtype=np.uint32).view(np.float32)
+
+    def around(v):
+        b = np.array([v], dtype=np.float32).view(np.uint32)[0]
+        return [b - 1, b, b + 1]
+
+    bits = [0x00000000, 0x80000000, 0x7F800000, 0xFF800000,       # +-0, +-Inf
+            0x7FC00000, 0xFFC00000, 0x7F800001, 0xFF800001,       # NaNs
+            0x00000001, 0x007FFFFF, 0x80000001, 0x807FFFFF]       # fp32 denormals
+    edges = [448.0, 464.0, 480.0, 57344.0, 61440.0, 65536.0,
+             2.0 ** -6, 2.0 ** -9, 2.0 ** -10, 1.5 * 2.0 ** -9,  # e4m3fn min normal / subnormal
+             2.0 ** -14, 2.0 ** -16, 2.0 ** -17, 1.5 * 2.0 ** -16]  # e5m2
+    for e in edges:
+        for s in (1.0, -1.0):
+            bits += around(np.float32(s * e))
+    return f(bits)
+
+
+def fp8_input(n: int = 16_777_216, seed_stream: int = 0) -> np.ndarray:
+    g = rng(1, seed_stream)
+    z = g.standard_normal(n, dtype=np.float32)
+    u = g.uniform(-10.0, 9.0, n).astype(np.float32)
+    x = (z * np.exp2(u)).astype(np.float32)
+    sp = fp8_specials()
+    nspec = max(1, n // 100) if n >= 100 else 0
+    if nspec:
+        pos = g.choice(n, size=nspec, replace=False)
+        rand_den = g.integers(1, 1 << 23, size=nspec, dtype=np.uint32).view(np.float32)
+        vals = np.resize(sp, nspec).copy()
+        # every fourth special is a random fp32 denormal
+        vals[3::4] = rand_den[3::4]
+        x[pos] = vals
+    return x
+
+
+# ------------------------------------------------------------- scatter (c=2)
+def zipf_cdf(nbins: int = 65536, s: float = 1.1) -> np.ndarray:
+    w = np.arange(1, nbins + 1, dtype=np.float64) ** (-s)
+    c = np.cumsum(w)
+    return c / c[-1]
+
+
+def scatter_input(n: int = 67_108_864, nbins: int = 65536, kind: str = "i32",
+                  s: float = 1.1, seed_stream: int = 0):
+    """Returns (idx int32[n], val int32|float32[n])."""
+    g = rng(2, seed_stream)
+    cdf = zipf_cdf(nbins, s)
+    idx = np.searchsorted(cdf, g.random(n), side="right").astype(np.int32)
+    np.minimum(idx, nbins - 1, out=idx)
+    if kind == "i32":
+        val = g.integers(0, 1000, size=n, dtype=np.int32)
+    elif kind == "f32":
+        val = g.standard_normal(n, dtype=np.float32)
+    else:
+        raise ValueError(kind)
+    return idx, val
+
+
+# ------------------------------------------------------------- bf16 (c=3)
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 RNE bits via torch's CPU conversion."""
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16) \
+        .view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_gemm_input(M: int, N: int, K: int, seed_stream: int = 0):
+    """Returns (A bits uint16[M,K], B bits uint16[N,K])."""
+    g = rng(3, seed_stream)
+    a = g.uniform(-1.0, 1.0, size=(M, K)).astype(np.float32)
+    b = g.uniform(-1.0, 1.0, size=(N, K)).astype(np.float32)
+    return to_bf16_bits(a), to_bf16_bits(b)
+
+
+# -------------------------------------------------------------- fp8 (c=4)
+def _quant_rows(x: np.ndarray, fmax: float, dtype):
+    absmax = np.abs(x).max(axis=1).astype(np.float32)
+    absmax = np.where(absmax > 0, absmax, np.float32(1.0))
+    q = (x * (np.float32(fmax) / absmax)[:, None]).astype(np.float32)
+    q = np.clip(q, -fmax, fmax)
+    codes = torch.from_numpy(q).to(dtype).view(torch.uint8).numpy()
+    return codes, (absmax / np.float32(fmax)).astype(np.float32)
+
+
+def fp8_gemm_input(M: int, N: int, K: int, seed_stream: int = 0):
+    """Returns (Aq uint8[M,K], sa f32[M], Bq uint8[N,K], sb f32[N]), e4m3fn codes."""
+    g = rng(4, seed_stream)
+    a = g.standard_normal((M, K), dtype=np.float32)
+    aq, sa = _quant_rows(a, 448.0, torch.float8_e4m3fn)
+    del a
+    b = g.standard_normal((N, K), dtype=np.float32)
+    bq, sb = _quant_rows(b, 448.0, torch.float8_e4m3fn)
+    return aq, sa, bq, sb
+
+
+# -------------------------------------------------------------- gemv (c=5)
+def gemv_input(M: int, N: int = 14336, K: int = 4096, group: int = 128, seed_stream: int = 0):
+    """Returns (x bf16 bits uint16[M,K], Wq e5m2 uint8[N,K], s f32[N, K/group])."""
+    g = rng(5, seed_stream)
+    x = to_bf16_bits(g.standard_normal((M, K), dtype=np.float32))
+    w = (g.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    wg = w.reshape(N, K // group, group)
+    absmax = np.abs(wg).max(axis=2).astype(np.float32)
+    absmax = np.where(absmax > 0, absmax, np.float32(1.0))
+    s = (absmax / np.float32(57344.0)).astype(np.float32)
+    q = np.clip(wg / s[:, :, None], -57344.0, 57344.0).astype(np.float32).reshape(N, K)
+    wq = torch.from_numpy(q).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    return x, wq, s
