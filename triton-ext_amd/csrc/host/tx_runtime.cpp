@@ -45,8 +45,10 @@ const CodeObjectImage kImages[static_cast<int>(CodeObject::Count)] = {
 constexpr int kMaxDevices = 64;
 constexpr int kMaxKernels = 96;
 
+constexpr size_t kMaxKernelName = 96;
+
 struct KernelSlot {
-  const char *name;  // points at a string literal of the caller
+  char name[kMaxKernelName];  // a copy: callers pass transient buffers
   int co;
   hipFunction_t fn;
 };
@@ -152,8 +154,12 @@ tx_status get_kernel(CodeObject co, const char *name, hipFunction_t *out) {
   if (e != hipSuccess)
     return fail(TX_CODE_OBJECT_ERROR, "kernel '%s' not found in code object '%s': %s",
                 name, kImages[ci].name, hipGetErrorString(e));
-  if (st->num_kernels < kMaxKernels)
-    st->kernels[st->num_kernels++] = KernelSlot{name, ci, fn};
+  if (st->num_kernels < kMaxKernels && std::strlen(name) < kMaxKernelName) {
+    KernelSlot &slot = st->kernels[st->num_kernels++];
+    std::memcpy(slot.name, name, std::strlen(name) + 1);
+    slot.co = ci;
+    slot.fn = fn;
+  }
   *out = fn;
   return TX_SUCCESS;
 }
