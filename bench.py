@@ -1,0 +1,272 @@
+"""Benchmark of the tx op library on one MI355X.
+
+Prints ONE JSON line.  The headline metric pairs two numbers:
+  * value: fp8 e4m3fn scaled GEMM at M = N = K = 8192 (per-row / per-column
+    fp32 scales, bf16 output), TFLOP/s, with its MFMA roofline fraction;
+  * fp8_convert: tt.fp_to_fp fp32 -> e4m3fn (RNE, non-saturating) over
+    16,777,216 values, GB/s of algorithmic traffic (5 B per value), with its
+    HBM roofline fraction.
+The other configurations are reported under "secondary".
+
+A step is one launch of the op over one batch of synthetic input already
+resident in HBM.  Each measurement runs W untimed launches, then exactly K
+launches between two HIP events on the stream the op is launched on (torch's
+current stream, which tx passes to the library), with torch.cuda.synchronize()
+before and after.  Inputs rotate over enough buffer sets that the working set
+exceeds twice the 256 MB Infinity Cache for the memory-bound ops.
+
+cpu_baseline: the CPU oracle (oracle/, a C port of the path's semantics,
+OpenMP over all host cores) timed on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "triton-ext_amd"))
+
+METRIC = "fp8 GEMM TFLOP/s + % MFMA peak @8192^3; fp8 convert GB/s + % HBM peak"
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA
+BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--quick", action="store_true", help="headline ops only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return p.parse_args()
+
+
+def timed(fn, steps, warmup):
+    """Average ms per launch of fn(i) over exactly `steps` launches."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(warmup + i)
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def ring_count(set_bytes):
+    return max(1, -(-2 * MALL_BYTES // set_bytes))
+
+
+# ------------------------------------------------------------------ ops
+def bench_fp8_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
+    from tx import workloads
+    dev = torch.device("cuda:0")
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
+    bufs = []
+    for s in range(sets):
+        A = torch.from_numpy(aq).to(dev).view(torch.float8_e4m3fn)
+        B = torch.from_numpy(bq).to(dev).view(torch.float8_e4m3fn)
+        bufs.append((A, torch.from_numpy(sa).to(dev), B, torch.from_numpy(sb).to(dev),
+                     torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
+    del aq, bq
+
+    def step(i):
+        A, a_s, B, b_s, C = bufs[i % sets]
+        tx.dot_scaled_rowcol(A, a_s, B, b_s, out=C)
+
+    ms = timed(step, steps, warmup)
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tflops, "flops": flops,
+            "bytes": M * K + N * K + 4 * (M + N) + 2 * M * N}
+
+
+def bench_bf16_gemm(tx, torch, M, N, K, steps, warmup):
+    from tx import workloads
+    import numpy as np
+    dev = torch.device("cuda:0")
+    A, B = workloads.bf16_gemm_input(M, N, K)
+    At = torch.from_numpy(A.view(np.int16)).to(dev).view(torch.bfloat16)
+    Bt = torch.from_numpy(B.view(np.int16)).to(dev).view(torch.bfloat16)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms = timed(lambda i: tx.dot(At, Bt, out=C), steps, warmup)
+    flops = 2.0 * M * N * K
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+
+
+def bench_fp8_convert(tx, torch, steps, warmup, n=16_777_216):
+    from tx import workloads
+    dev = torch.device("cuda:0")
+    x_np = workloads.fp8_input(n)
+    sets = ring_count(5 * n)
+    xs = [torch.from_numpy(x_np).to(dev) for _ in range(sets)]
+    qs = [torch.empty(n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(sets)]
+    ms = timed(lambda i: tx.fp_to_fp(xs[i % sets], torch.float8_e4m3fn, out=qs[i % sets]),
+               steps, warmup)
+    enc_gbs = 5.0 * n / (ms * 1e-3) / 1e9
+    fs = [torch.empty(n, dtype=torch.float32, device=dev) for _ in range(sets)]
+    ms_dec = timed(lambda i: tx.fp_to_fp(qs[i % sets], torch.float32, out=fs[i % sets]),
+                   steps, warmup)
+    dec_gbs = 5.0 * n / (ms_dec * 1e-3) / 1e9
+    return {"ms": ms, "gbs": enc_gbs, "bytes": 5.0 * n, "sets": sets,
+            "decode_ms": ms_dec, "decode_gbs": dec_gbs}
+
+
+def bench_scatter(tx, torch, kind, steps, warmup, n=67_108_864, nbins=65536):
+    from tx import workloads
+    dev = torch.device("cuda:0")
+    idx_np, val_np = workloads.scatter_input(n=n, nbins=nbins, kind=kind)
+    sets = 2  # 2 x 512 MB of updates > 2 x MALL
+    idx = [torch.from_numpy(idx_np).to(dev) for _ in range(sets)]
+    val = [torch.from_numpy(val_np).to(dev) for _ in range(sets)]
+    bins = torch.zeros(nbins, dtype=torch.int32 if kind == "i32" else torch.float32, device=dev)
+    op = "add" if kind == "i32" else "fadd"
+    ms = timed(lambda i: tx.atomic_rmw(op, bins, idx[i % sets], val[i % sets]), steps, warmup)
+    algo = 8.0 * n + 8.0 * nbins
+    return {"ms": ms, "gbs": algo / (ms * 1e-3) / 1e9, "bytes": algo,
+            "updates_per_s": n / (ms * 1e-3)}
+
+
+def bench_gemv(tx, torch, M, steps, warmup, N=14336, K=4096, group=128):
+    from tx import workloads
+    import numpy as np
+    dev = torch.device("cuda:0")
+    x, wq, s = workloads.gemv_input(M, N, K, group)
+    xt = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
+    wbytes = N * K + 4 * s.size
+    sets = ring_count(wbytes)
+    ws = [torch.from_numpy(wq).to(dev).view(torch.float8_e5m2) for _ in range(sets)]
+    ss = [torch.from_numpy(s).to(dev) for _ in range(sets)]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms = timed(lambda i: tx.gemv_fp8_dequant(xt, ws[i % sets], ss[i % sets], group, out=y),
+               steps, warmup)
+    algo = N * K + 4.0 * N * (K // group) + 2.0 * M * K + 2.0 * M * N
+    return {"ms": ms, "gbs": algo / (ms * 1e-3) / 1e9, "bytes": algo, "sets": sets}
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline():
+    """Time the oracle (C, OpenMP) on bounded samples of the two headline workloads."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    from tx import workloads
+    oracle.build()
+    cores = os.cpu_count() or 1
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    # fp8 GEMM: R rows of C for the 8192^3 problem (2 * R * N * K flops)
+    M = N = K = 8192
+    R = 64
+    g = np.random.default_rng(1)
+    aq = g.integers(0, 0x7F, size=(R, K), dtype=np.uint8)
+    bq = np.ascontiguousarray(workloads.fp8_gemm_input(16, N, K)[2])
+    sa = np.ones(R, np.float32)
+    sb = np.ones(N, np.float32)
+    t0 = time.perf_counter()
+    oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, R, nthreads=cores)
+    dt = time.perf_counter() - t0
+    gemm_tflops = 2.0 * R * N * K / dt / 1e12
+    # fp8 convert: the full 16 Mi-value encode, repeated for a few seconds
+    x = workloads.fp8_input()
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 3.0:
+        oracle.encode(x, 1, False, nthreads=cores)
+        reps += 1
+    dt_conv = (time.perf_counter() - t0) / reps
+    return {
+        "value": gemm_tflops, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+        "sample": f"oracle fp8 scaled GEMM, {R} of 8192 rows of M=N=K=8192 "
+                  f"({2.0 * R * N * K / 1e9:.1f} GFLOP in {dt:.2f} s, fp64 accumulate)",
+        "fp8_convert": {"value": 5.0 * x.size / dt_conv / 1e9, "unit": "GB/s",
+                        "sample": f"oracle encode e4m3fn RNE of 16,777,216 values x {reps}"},
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: every op runs on one "
+                                   "MI355X; multi-GPU sharding is described, not run"}))
+        sys.exit(2)
+    import torch
+    import tx
+    tx.init()
+    K, W = args.steps, args.warmup
+
+    gemm = bench_fp8_gemm(tx, torch, 8192, 8192, 8192, K, W)
+    conv = bench_fp8_convert(tx, torch, max(K, 50), W)
+    secondary = []
+    if not args.quick:
+        for (m, n, k) in [(16, 14336, 4096), (512, 14336, 4096), (8192, 14336, 4096),
+                          (16, 4096, 14336), (512, 4096, 14336), (8192, 4096, 14336)]:
+            r = bench_fp8_gemm(tx, torch, m, n, k, K, W, sets=1)
+            secondary.append({"op": "fp8 scaled GEMM", "shape": [m, n, k], "ms": r["ms"],
+                              "tflops": r["tflops"],
+                              "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
+                              "gbs": r["bytes"] / (r["ms"] * 1e-3) / 1e9})
+        for (m, n, k) in [(4096, 4096, 4096), (4095, 4097, 4100)]:
+            r = bench_bf16_gemm(tx, torch, m, n, k, K, W)
+            secondary.append({"op": "bf16 GEMM", "shape": [m, n, k], "ms": r["ms"],
+                              "tflops": r["tflops"], "frac_mfma": r["tflops"] / BF16_PEAK_TFLOPS})
+        for kind in ("i32", "f32"):
+            r = bench_scatter(tx, torch, kind, K, W)
+            secondary.append({"op": f"scatter-reduce {kind} 64Mi->65536 Zipf(1.1)", "ms": r["ms"],
+                              "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS,
+                              "gupdates_per_s": r["updates_per_s"] / 1e9})
+        for m in (1, 4, 16):
+            r = bench_gemv(tx, torch, m, max(K, 50), W)
+            secondary.append({"op": "fp8 e5m2 dequant GEMV", "shape": [m, 14336, 4096],
+                              "ms": r["ms"], "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS})
+        secondary.append({"op": "fp8 decode e4m3fn->fp32 16Mi", "ms": conv["decode_ms"],
+                          "gbs": conv["decode_gbs"], "frac_hbm": conv["decode_gbs"] / HBM_PEAK_GBS})
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(gemm["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(gemm["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3fn",
+        "data": "synthetic (seeded N(0,1), absmax-quantised; see tx/workloads.py)",
+        "config": {"workload": "fp8 e4m3fn scaled GEMM M=N=K=8192, per-row/per-column fp32 "
+                               "scales, bf16 output; plus fp32->e4m3fn RNE convert of 16Mi values",
+                   "M": 8192, "N": 8192, "K": 8192},
+        "roofline": {"bound": "mfma", "achieved": round(gemm["tflops"], 2),
+                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm["tflops"] / FP8_PEAK_TFLOPS, 4), "traffic": None},
+        "fp8_convert": {"value": round(conv["gbs"], 1), "unit": "GB/s", "ms": round(conv["ms"], 5),
+                        "roofline": {"bound": "hbm", "achieved": round(conv["gbs"], 1),
+                                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(conv["gbs"] / HBM_PEAK_GBS, 4),
+                                     "traffic": None},
+                        "buffer_sets": conv["sets"]},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
