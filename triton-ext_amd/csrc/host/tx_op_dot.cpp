@@ -55,7 +55,7 @@ bool use_big_tile(int64_t M, int64_t N) {
 }
 
 tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int tile,
-                      hipStream_t s) {
+                      hipStream_t s, unsigned threads = 256) {
   args.tiles_m = int32_t((args.M + tile - 1) / tile);
   args.tiles_n = int32_t((args.N + tile - 1) / tile);
   args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
@@ -63,7 +63,21 @@ tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int 
   TX_TRY(get_kernel(co, kname, &fn));
   const int64_t grid = int64_t(args.tiles_m) * args.tiles_n;
   if (grid > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: too many tiles", kname);
-  return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, kname);
+  return launch(fn, unsigned(grid), 1, threads, s, &args, sizeof args, kname);
+}
+
+// Wavefronts per workgroup of the fast path: 8 (two per SIMD) measured faster
+// than 4 on MI355X for every config shape.
+constexpr int kFastWaves = 8;
+
+// The LDS-DMA fast path needs 16-byte aligned rows and a row length that is a
+// multiple of 16 bytes, and operands small enough that a 32-bit buffer offset
+// with the top bit clear addresses them (out-of-range lanes use 0x80000000).
+bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t k_b, int64_t M,
+             int64_t N) {
+  if (!aligned(A, 16) || !aligned(B, 16) || lda_b % 16 || ldb_b % 16 || k_b % 16) return false;
+  const int64_t lim = int64_t(1) << 31;
+  return (M - 1) * lda_b + k_b < lim && (N - 1) * ldb_b + k_b < lim;
 }
 
 const char *fp8_name(tx_dtype t) {
@@ -80,10 +94,17 @@ static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb
   const int vec = pick_vec(A, lda * 2, B, ldb * 2, K * 2, widths, 3);
   const int tile = use_big_tile(M, N) ? 256 : 128;
   char kname[64];
-  std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
+  unsigned threads = 256;
+  if (tile == 256 && fast_ok(A, lda * 2, B, ldb * 2, K * 2, M, N)) {
+    threads = 64 * kFastWaves;
+    std::snprintf(kname, sizeof kname, "tx_gemm_bf16_fast%s", threads == 512 ? "8" : "");
+  } else {
+    std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
+  }
   tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
                     int32_t(K), 0, 0, 0};
-  return launch_gemm(kname, CodeObject::GemmBf16, args, tile, static_cast<hipStream_t>(stream));
+  return launch_gemm(kname, CodeObject::GemmBf16, args, tile, static_cast<hipStream_t>(stream),
+                     threads);
 }
 
 static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
@@ -103,9 +124,17 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   const int vec = pick_vec(A, lda, B, ldb, K, widths, 3);
   const int tile = (vec != 1 && use_big_tile(M, N)) ? 256 : 128;
   char kname[80];
-  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
+  unsigned threads = 256;
+  if (tile == 256 && fast_ok(A, lda, B, ldb, K, M, N)) {
+    threads = 64 * kFastWaves;
+    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast%s", fa, fb,
+                  threads == 512 ? "8" : "");
+  } else {
+    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
+  }
   tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
-  return launch_gemm(kname, CodeObject::GemmFp8, args, tile, static_cast<hipStream_t>(stream));
+  return launch_gemm(kname, CodeObject::GemmFp8, args, tile, static_cast<hipStream_t>(stream),
+                     threads);
 }
 
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,

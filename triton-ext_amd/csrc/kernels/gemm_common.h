@@ -9,9 +9,12 @@
 // Tiling: a workgroup owns a BM x BN tile of C and walks K in steps of one
 // 128-byte row slice (64 bf16 or 128 fp8 elements).  Each step stages the
 // BM x 128 B slice of A and the BN x 128 B slice of B in LDS; every 128-byte
-// LDS row holds 8 chunks of 16 bytes stored at chunk ^ (row & 7), so that 8
-// lanes reading the same logical chunk of 8 consecutive rows (one
-// ds_read_b128 phase) touch 8 different bank groups.  Two LDS stages are
+// LDS row holds 8 chunks of 16 bytes stored at chunk ^ ((row >> 1) & 7).
+// gfx950's LDS serves a ds_read_b128 16 lanes at a time over 64 banks
+// (256 bytes); the fragment reads have 16 lanes read the same logical chunk
+// of 16 consecutive rows, and with this swizzle those 16 chunks fall in 16
+// different 16-byte bank groups (row parity picks the half of the 256-byte
+// bank window, (row >> 1) & 7 the chunk within it).  Two LDS stages are
 // used: global loads for step k+1 are in flight (in registers) while step k
 // is multiplied, then written to the other stage, with one barrier per step.
 //
@@ -35,7 +38,7 @@ using txd::u32x4;
 constexpr int kRowBytes = 128;  // one K step of one row, in bytes
 constexpr int kChunks = 8;      // 16-byte chunks per row
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // Byte offset of (row, chunk) inside one LDS operand stage.
 __device__ __forceinline__ int lds_off(int row, int chunk) {
