@@ -17,7 +17,8 @@ namespace {
 
 constexpr int kAggBlock = 1024;     // threads of the aggregating kernels
 constexpr int64_t kAggStep = 4 * kAggBlock;
-constexpr int64_t kDirectSlots = 36864;
+constexpr int64_t kDirectSlots = 36864;  // bins per LDS window
+constexpr int64_t kMaxWindows = 4;       // beyond this the hash-table kernel is used
 
 const char *op_name(tx_rmw_op op) {
   switch (op) {
@@ -64,7 +65,7 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int cus = cu_count();
-  tx_scatter_args args{bins, idx, val, mask, old, n, int32_t(nbins), 0};
+  tx_scatter_args args{bins, idx, val, mask, old, n, int32_t(nbins), 0, 0, 0};
   char kname[64];
   if (old) {
     std::snprintf(kname, sizeof kname, "tx_scatter_%s_old", name);
@@ -74,12 +75,28 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
     return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, kname);
   }
   if (nbins == 0) return TX_SUCCESS;  // every update is out of range
-  const bool direct = nbins <= kDirectSlots;
-  std::snprintf(kname, sizeof kname, "tx_scatter_%s_%s", name, direct ? "direct" : "hashed");
+  const int64_t windows = (nbins + kDirectSlots - 1) / kDirectSlots;
   hipFunction_t fn;
+  if (windows <= kMaxWindows) {
+    std::snprintf(kname, sizeof kname, "tx_scatter_%s_windowed", name);
+    TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+    // One workgroup per CU at a time (the table fills most of a CU's LDS);
+    // about one round of workgroups in total, `windows` of them per chunk.
+    const int64_t wgs = std::max<int64_t>(cus, 8 * windows);
+    int64_t chunks = std::max<int64_t>(1, wgs / windows);
+    int64_t per = (n + chunks - 1) / chunks;
+    per = (per + kAggStep - 1) / kAggStep * kAggStep;
+    if (per > INT32_MAX) per = INT32_MAX / kAggStep * kAggStep;
+    chunks = (n + per - 1) / per;
+    args.per_block = int32_t(per);
+    args.splits = int32_t(windows);
+    args.window = int32_t(kDirectSlots);
+    // workgroups come in groups of 8 chunks x `windows` windows
+    const int64_t grid = (chunks + 7) / 8 * 8 * windows;
+    return launch(fn, unsigned(grid), 1, kAggBlock, s, &args, sizeof args, kname);
+  }
+  std::snprintf(kname, sizeof kname, "tx_scatter_%s_hashed", name);
   TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
-  // One workgroup per CU (the LDS table fills most of a CU's LDS); each takes
-  // a contiguous range of updates, a multiple of 4 * blockDim.
   int64_t per = (n + cus - 1) / cus;
   per = (per + kAggStep - 1) / kAggStep * kAggStep;
   if (per > INT32_MAX) per = INT32_MAX / kAggStep * kAggStep;

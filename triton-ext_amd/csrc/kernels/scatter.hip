@@ -8,12 +8,14 @@
 //      and one of values;
 //   2. wavefront: runs of equal keys inside a wavefront are combined with a
 //      ballot/read-lane loop before they reach a shared atomic (spill path);
-//   3. workgroup: an LDS table owned by the workgroup.  When all bins fit in
-//      LDS the table is direct-mapped (slot = bin); otherwise it is an open
-//      addressing hash table (Fibonacci hash, bounded linear probing) keyed
-//      by bin, and updates whose probe sequence is full spill to global
-//      atomics.  At the end the table is flushed with one global atomic per
-//      occupied slot.
+//   3. workgroup: an LDS table owned by the workgroup.  Up to 4 x 36,864
+//      bins the table is direct-mapped (slot = bin - window start), with the
+//      bin range cut into windows that each fit in LDS and one workgroup per
+//      (chunk of updates, window); beyond that it is an open addressing hash
+//      table (Fibonacci hash, bounded linear probing) keyed by bin, and
+//      updates whose probe sequence is full spill to global atomics after a
+//      wavefront-level combine.  At the end the table is flushed with one
+//      global atomic per occupied slot.
 // Every combine is an associative, commutative op, so integer results are
 // exact and order independent; fp32 sums differ from a sequential sum only
 // by rounding order.
@@ -133,14 +135,27 @@ struct Scatter {
     }
   }
 
-  // Direct-mapped LDS privatisation: all bins fit in LDS.
-  static __device__ void direct(const tx_scatter_args &a) {
+  // Windowed LDS privatisation.  The bin range is cut into `splits` windows
+  // of `window` bins (each fits in LDS); `splits` workgroups read the same
+  // chunk of updates and each privatises one window, so every update lands
+  // in exactly one LDS histogram.  Workgroup b takes window (b / 8) % splits
+  // and chunk (b / (8 splits)) * 8 + b % 8: the workgroups sharing a chunk
+  // sit on the same XCD (workgroups are dispatched round-robin over 8 XCDs),
+  // so the repeated reads of a chunk are served by that XCD's L2 or the
+  // Infinity Cache rather than HBM.  With one window this is plain LDS
+  // privatisation of all bins.
+  static __device__ void windowed(const tx_scatter_args &a) {
     __shared__ T table[kDirectSlots];
-    const int nb = a.nbins;
-    for (int s = threadIdx.x; s < nb; s += kBlock) table[s] = OpTraits<OP>::id();
-    __syncthreads();
-    const int64_t begin = int64_t(blockIdx.x) * a.per_block;
+    const int b = blockIdx.x;
+    const int w = (b / 8) % a.splits;
+    const int64_t chunk = int64_t(b / (8 * a.splits)) * 8 + b % 8;
+    const int64_t begin = chunk * a.per_block;
+    if (begin >= a.n) return;  // uniform: the whole workgroup leaves
     const int64_t end = begin + a.per_block < a.n ? begin + a.per_block : a.n;
+    const uint32_t lo = uint32_t(w) * uint32_t(a.window);
+    const uint32_t nb = min(uint32_t(a.window), uint32_t(a.nbins) - lo);  // bins in this window
+    for (uint32_t s = threadIdx.x; s < nb; s += kBlock) table[s] = OpTraits<OP>::id();
+    __syncthreads();
     const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
                      (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
     for (int64_t e = begin + 4 * int64_t(threadIdx.x); e < end; e += 4 * kBlock) {
@@ -149,12 +164,14 @@ struct Scatter {
       bool ok[4];
       load4(a, e, end, vec, key, val, ok);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (ok[j]) atomic_combine<OP, T>(&table[key[j]], val[j]);
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t r = key[j] - lo;  // wraps for keys below the window
+        if (ok[j] && r < nb) atomic_combine<OP, T>(&table[r], val[j]);
+      }
     }
     __syncthreads();
-    T *bins = reinterpret_cast<T *>(a.bins);
-    for (int s = threadIdx.x; s < nb; s += kBlock) {
+    T *bins = reinterpret_cast<T *>(a.bins) + lo;
+    for (uint32_t s = threadIdx.x; s < nb; s += kBlock) {
       const T v = table[s];
       if (!is_identity<OP, T>(v)) atomic_combine<OP, T>(bins + s, v);
     }
@@ -239,8 +256,8 @@ struct Scatter {
 }  // namespace
 
 #define TX_SCATTER_KERNELS(NAME, OP)                                                   \
-  TX_KERNEL void __launch_bounds__(kBlock) tx_scatter_##NAME##_direct(const tx_scatter_args a) { \
-    Scatter<OP>::direct(a);                                                            \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_scatter_##NAME##_windowed(const tx_scatter_args a) { \
+    Scatter<OP>::windowed(a);                                                          \
   }                                                                                    \
   TX_KERNEL void __launch_bounds__(kBlock) tx_scatter_##NAME##_hashed(const tx_scatter_args a) { \
     Scatter<OP>::hashed(a);                                                            \

@@ -27,7 +27,9 @@ typedef struct tx_scatter_args {
   void *old;           /* may be NULL (aggregating kernels ignore it) */
   int64_t n;
   int32_t nbins;
-  int32_t per_block;   /* updates per workgroup (multiple of 4 * blockDim) */
+  int32_t per_block;   /* updates per chunk (multiple of 4 * blockDim) */
+  int32_t splits;      /* windowed kernels: bin windows (workgroups per chunk) */
+  int32_t window;      /* windowed kernels: bins per window */
 } tx_scatter_args;
 
 /* GEMM, both operands K-contiguous ("A row-major, B column-major").
