@@ -70,6 +70,22 @@ def test_fp32_add_random(tx, oracle, dev, nbins):
     _check_f32(got, init, nbins, idx, val, oracle)
 
 
+@pytest.mark.parametrize("nbins", [1000, 1 << 20])
+def test_fp32_signed_zeros(tx, dev, nbins):
+    """Zero signs follow sequential IEEE addition: -0 updates leave a bin as
+    it was, a +0 update turns -0 into +0, untouched bins keep their bits."""
+    init = np.where(np.arange(nbins) % 2 == 0, -0.0, 0.0).astype(np.float32)
+    idx = np.concatenate([np.repeat(np.arange(0, 100), 3), np.repeat(np.arange(100, 200), 3)])
+    val = np.concatenate([np.full(300, -0.0), np.full(300, 0.0)]).astype(np.float32)
+    perm = np.random.default_rng(3).permutation(idx.size)
+    idx, val = idx[perm].astype(np.int32), val[perm]
+    got = _run(tx, dev, "fadd", init, idx, val)
+    ref = init.copy()
+    np.add.at(ref, idx, val)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.signbit(got[0]) and not np.signbit(got[100]) and not np.signbit(got[1])
+
+
 @pytest.mark.parametrize("op,ufunc,dtype", [
     ("max", np.maximum, np.int32), ("min", np.minimum, np.int32),
     ("umax", np.maximum, np.uint32), ("umin", np.minimum, np.uint32),

@@ -17,6 +17,7 @@ namespace {
 
 constexpr int kAggBlock = 1024;     // threads of the aggregating kernels
 constexpr int64_t kAggStep = 4 * kAggBlock;
+constexpr int64_t kWinStep = 3 * kAggStep;  // windowed kernel: its pipelined loop takes 3 steps at a time
 constexpr int64_t kDirectSlots = 36864;  // bins per LDS window
 constexpr int64_t kMaxWindows = 4;       // beyond this the hash-table kernel is used
 
@@ -85,8 +86,8 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
     const int64_t wgs = std::max<int64_t>(cus, 8 * windows);
     int64_t chunks = std::max<int64_t>(1, wgs / windows);
     int64_t per = (n + chunks - 1) / chunks;
-    per = (per + kAggStep - 1) / kAggStep * kAggStep;
-    if (per > INT32_MAX) per = INT32_MAX / kAggStep * kAggStep;
+    per = (per + kWinStep - 1) / kWinStep * kWinStep;
+    if (per > INT32_MAX) per = INT32_MAX / kWinStep * kWinStep;
     chunks = (n + per - 1) / per;
     args.per_block = int32_t(per);
     args.splits = int32_t(windows);

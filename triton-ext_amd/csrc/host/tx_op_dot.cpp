@@ -66,8 +66,7 @@ tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int 
   return launch(fn, unsigned(grid), 1, threads, s, &args, sizeof args, kname);
 }
 
-// Wavefronts per workgroup of the fast path: 8 (two per SIMD) measured faster
-// than 4 on MI355X for every config shape.
+// Wavefronts per workgroup of the fast path (two per SIMD).
 constexpr int kFastWaves = 8;
 
 // The LDS-DMA fast path needs 16-byte aligned rows and a row length that is a
@@ -97,7 +96,7 @@ static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb
   unsigned threads = 256;
   if (tile == 256 && fast_ok(A, lda * 2, B, ldb * 2, K * 2, M, N)) {
     threads = 64 * kFastWaves;
-    std::snprintf(kname, sizeof kname, "tx_gemm_bf16_fast%s", threads == 512 ? "8" : "");
+    std::snprintf(kname, sizeof kname, "tx_gemm_bf16_fast");
   } else {
     std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
   }
@@ -127,8 +126,7 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   unsigned threads = 256;
   if (tile == 256 && fast_ok(A, lda, B, ldb, K, M, N)) {
     threads = 64 * kFastWaves;
-    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast%s", fa, fb,
-                  threads == 512 ? "8" : "");
+    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast", fa, fb);
   } else {
     std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
   }

@@ -22,9 +22,6 @@ TX_GEMM_BF16(128x128, 128, 128, 2, 2, 2)
 
 #include "gemm_fast.h"
 
-TX_KERNEL void __launch_bounds__(256) tx_gemm_bf16_fast(const tx_gemm_args a) {
-  gemm_fast_tile<GemmCfg<EL_BF16, EL_BF16, 256, 256, 2, 2, 16>, 4>(a);
-}
-TX_KERNEL void __launch_bounds__(512) tx_gemm_bf16_fast8(const tx_gemm_args a) {
-  gemm_fast_tile<GemmCfg<EL_BF16, EL_BF16, 256, 256, 2, 2, 16>, 8>(a);
+TX_KERNEL void __launch_bounds__(512) tx_gemm_bf16_fast(const tx_gemm_args a) {
+  gemm_fast_tile<GemmCfg<EL_BF16, EL_BF16, 256, 256, 2, 2, 16>>(a);
 }

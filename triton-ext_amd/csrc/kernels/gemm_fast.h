@@ -1,31 +1,39 @@
 // Fast-path GEMM body for aligned operands (both K-contiguous, 16-byte
-// aligned rows, K * element size a multiple of 16 bytes), 256 x 256 tile,
-// 8 wavefronts of 128 x 64 (two per SIMD) or 4 of 128 x 128.
+// aligned rows, K * element size a multiple of 16 bytes): 256 x 256 tile,
+// 8 wavefronts (two per SIMD), each owning a 128 x 64 block of C.
 //
-// Pipeline (per 64-byte K step, i.e. 32 bf16 or 64 fp8 of K):
-//  * LDS holds 4 stages of (256 A rows + 256 B rows) x 64 bytes = 4 x 32 KiB.
-//    Rows are 4 chunks of 16 bytes stored at chunk ^ ((row >> 2) & 3): a
+// Pipeline (per 128-byte K step, i.e. 64 bf16 or 128 fp8 of K):
+//  * LDS holds 2 stages of (256 A rows + 256 B rows) x 128 bytes = 2 x 64 KiB.
+//    Rows are 8 chunks of 16 bytes stored at chunk ^ ((row >> 1) & 7): a
 //    ds_read_b128 is served 16 lanes at a time over 256 bytes of banks, the
 //    fragment reads have 16 lanes read one logical chunk of 16 consecutive
-//    rows, and this swizzle spreads those over the 16 bank groups.
+//    rows, and this swizzle puts those 16 reads in 16 different 16-byte bank
+//    groups (row parity picks the half of the bank window, (row >> 1) & 7 the
+//    chunk within it).
 //  * global -> LDS bypasses registers: gfx950's `buffer_load_dwordx4 ... lds`
 //    writes each lane's 16 bytes at M0 + 16 * lane, so one instruction fills a
-//    1 KiB block = 16 rows; lane i lands in row i / 4, physical chunk i % 4 and
-//    therefore fetches logical chunk (i % 4) ^ (i / 16).  Out-of-range rows and
-//    the K tail use an offset past the buffer's range, which reads as zero.
-//  * loads run 4 steps ahead: at the top of step k every wave waits until its
-//    loads of step k+1 landed (vmcnt), one barrier publishes them, and the
-//    wave issues step k+4 into the stage that held step k (already copied to
-//    registers).  A load therefore has three steps of MFMA time to arrive.
-//  * LDS -> registers runs one step ahead: the MFMAs of step k consume
-//    fragments read during step k-1, while the fragments of step k+1 are read
-//    between them.
-//  * MFMA: v_mfma_f32_32x32x64_f8f6f4 (fp8) or 2 x v_mfma_f32_32x32x16_bf16.
-//    The B tile feeds the MFMA A operand, so lane l, accumulator register j
-//    holds C[m0 + l % 32][n0 + 8 * (j / 4) + 4 * (l / 32) + j % 4].
+//    1 KiB block = 8 rows of 128 bytes; lane i lands in row i / 8, physical
+//    chunk i % 8, and therefore fetches logical chunk (i % 8) ^ ((row >> 1) & 7).
+//    The 8 lanes of a row fetch one whole 128-byte line.  Out-of-range rows
+//    and the K tail use an offset past the buffer's range, which reads as zero.
+//  * A step is consumed in two K halves of 64 bytes (one 32x32x64 fp8 MFMA,
+//    or two 32x32x16 bf16 MFMAs, per 32 x 32 block).  Fragments run one half
+//    ahead in registers: while the MFMAs of half 0 run, half 1 is read; then
+//    every wave waits for its loads of step k+1, one barrier publishes them
+//    to the workgroup and frees the stage of step k (both halves are in
+//    registers), and while the MFMAs of half 1 run, the wave issues the loads
+//    of step k+2 into that stage and reads half 0 of step k+1.  A load has
+//    one full step of MFMA time to arrive.
+//  * The instruction order inside each half is fixed in the source and
+//    pinned with scheduling barriers: after each MFMA, a share of the LDS
+//    reads (all of them within the first half of the MFMAs, in the order the
+//    next half consumes them) and, in the second half, one of the loads.
+//  * MFMA roles: the B tile feeds the MFMA A operand, so lane l, accumulator
+//    register j holds C[m0 + l % 32][n0 + 8 * (j / 4) + 4 * (l / 32) + j % 4].
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "gemm_tile.h"
 
@@ -40,20 +48,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// Compile-time loop: f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 namespace fast {
-constexpr int kStep = 64;                  // K bytes per step
-constexpr int kStages = 4;
-constexpr int kRows = 512;                 // 256 A rows + 256 B rows
-constexpr int kStageBytes = kRows * kStep;  // 32 KiB
-constexpr int kAhead = kStages;            // steps in flight
+constexpr int kStep = 128;                   // K bytes per step
+constexpr int kRows = 512;                   // 256 A rows + 256 B rows
+constexpr int kStageBytes = kRows * kStep;   // 64 KiB
+constexpr int kWaves = 8;
 
 __device__ __forceinline__ int off(int row, int chunk) {
-  return row * kStep + ((chunk ^ ((row >> 2) & 3)) << 4);
+  return row * kStep + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+// n items spread evenly over the first `over` MFMAs of a half: items
+// [spread_lo, spread_hi) follow MFMA i.
+__host__ __device__ constexpr int spread_lo(int i, int n, int over) {
+  return i >= over ? n : (i * n) / over;
+}
+__host__ __device__ constexpr int spread_hi(int i, int n, int over) {
+  return i >= over ? n : ((i + 1) * n) / over;
 }
 }  // namespace fast
 
-// One 32x32 block product over a 64-byte K step.  Operands are i32x8 tuples
-// (32 bytes per lane: chunks 2g and 2g+1 of the lane's row).
+// One 32x32 block product over a 64-byte K half.  Operands are i32x8 tuples
+// (32 bytes per lane: chunks 2g and 2g+1 of the half, g = lane / 32).
 template <class C>
 __device__ __forceinline__ void mfma32(txd::f32x16 &acc, const i32x8 &mb, const i32x8 &ma) {
   if constexpr (!C::FP8) {
@@ -69,13 +95,6 @@ __device__ __forceinline__ void mfma32(txd::f32x16 &acc, const i32x8 &mb, const 
   }
 }
 
-// Two 16-byte LDS reads forming one operand tuple.
-__device__ __forceinline__ i32x8 lds_pair(const uint8_t *p0, const uint8_t *p1) {
-  const txd::i32x4 lo = *reinterpret_cast<const txd::i32x4 *>(p0);
-  const txd::i32x4 hi = *reinterpret_cast<const txd::i32x4 *>(p1);
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
 // Wait until at most N vector-memory loads of this wave are outstanding and
 // all its LDS operations are done, then meet the workgroup at a barrier.
 // (A plain __syncthreads() would also wait for every outstanding load, which
@@ -89,70 +108,79 @@ __device__ __forceinline__ void wait_and_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <class C, int WAVES>
+template <class C>
 __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
-  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 wavefronts");
   using namespace fast;
-  constexpr int WN = WAVES / 2;          // waves along N (2 along M)
-  constexpr int TN = 256 / WN;           // wave tile: 128 x TN
-  constexpr int FN = TN / 32;            // 32-column blocks per wave
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+  constexpr int WN = kWaves / 2;     // waves along N (2 along M)
+  constexpr int TN = 256 / WN;       // wave tile: 128 x TN
+  constexpr int FN = TN / 32;        // 32-column blocks per wave
+  constexpr int NM = 4 * FN;         // mfma32 calls per K half
+  constexpr int NF = 4 + FN;         // fragments per K half: A 0..3, B 4..
+  constexpr int NR = 2 * NF;         // ds_read_b128 per K half
+  constexpr int BLK = 32 / kWaves;   // 1 KiB blocks per operand per wave per step
+  constexpr int ND = 2 * BLK;        // loads per wave per step
+  static_assert(BLK % 2 == 0, "a wave's first block must have an even index");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
 
   int tm, tn;
   tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
   const int m0 = tm * 256, n0 = tn * 256;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS addresses scalar
   const int wm = wave & 1, wn = wave >> 1;
-  constexpr int BLK = 16 / WAVES;  // A (and B) 1 KiB blocks per wave per step
-  static_assert(BLK * WAVES == 16, "16 blocks per operand per stage");
   constexpr int ES = C::FP8 ? 1 : 2;
   const uint32_t kb_end = uint32_t(a.K) * ES;
   const int ksteps = int((kb_end + kStep - 1) / kStep);
   const uint32_t lda_b = uint32_t(a.lda) * ES, ldb_b = uint32_t(a.ldb) * ES;
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, uint32_t(a.M - 1) * lda_b + kb_end);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.B, uint32_t(a.N - 1) * ldb_b + kb_end);
+  const __amdgpu_buffer_rsrc_t rsrc[2] = {make_rsrc(a.A, uint32_t(a.M - 1) * lda_b + kb_end),
+                                          make_rsrc(a.B, uint32_t(a.N - 1) * ldb_b + kb_end)};
 
-  // DMA assignment: wave w fills A blocks BLK*w .. BLK*w+BLK-1 and the same B
-  // blocks (16 rows each); this lane's row in block j is 16 (BLK w + j) + lane / 4.
-  const uint32_t kch = 16u * uint32_t((lane & 3) ^ (lane >> 4));
-  uint32_t voa[BLK], vob[BLK];
+  // DMA assignment: wave w fills blocks BLK*w .. BLK*w+BLK-1 of A and of B.
+  // Lane i of block q covers row 8q + i/8 and logical chunk
+  // (i % 8) ^ ((row >> 1) & 7) = (i % 8) ^ ((4q + i/16) & 7), which depends on
+  // the parity of q only (BLK*w is even, so it is the parity of j).
+  const uint32_t kch[2] = {16u * uint32_t((lane & 7) ^ ((lane >> 4) & 7)),
+                           16u * uint32_t((lane & 7) ^ ((4 + (lane >> 4)) & 7))};
+  uint32_t vo[2][BLK];
 #pragma unroll
   for (int j = 0; j < BLK; ++j) {
-    const int row = 16 * (BLK * wave + j) + (lane >> 2);
+    const int row = 8 * (BLK * wave + j) + (lane >> 3);
     const int gm = m0 + row, gn = n0 + row;
-    voa[j] = gm < a.M ? uint32_t(gm) * lda_b + kch : kOob;
-    vob[j] = gn < a.N ? uint32_t(gn) * ldb_b + kch : kOob;
+    vo[0][j] = gm < a.M ? uint32_t(gm) * lda_b + kch[j & 1] : kOob;
+    vo[1][j] = gn < a.N ? uint32_t(gn) * ldb_b + kch[j & 1] : kOob;
   }
-  auto issue = [&](int ks) {
+  // Load d of step ks: operand d / BLK, block d % BLK.
+  auto load = [&](int ks, auto d_tag) {
+    constexpr int d = decltype(d_tag)::value, op = d / BLK, j = d % BLK;
     const uint32_t so = uint32_t(ks) * kStep;
-    const bool past = so + kch >= kb_end;  // K tail: this lane's chunk is past the row end
-    uint8_t *As = lds + (ks % kStages) * kStageBytes;
-    uint8_t *Bs = As + 256 * kStep;
-#pragma unroll
-    for (int j = 0; j < BLK; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(As + (BLK * wave + j) * 1024), 16,
-                                               past ? kOob : voa[j], so, 0, 0);
-#pragma unroll
-    for (int j = 0; j < BLK; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(Bs + (BLK * wave + j) * 1024), 16,
-                                               past ? kOob : vob[j], so, 0, 0);
+    const bool past = so + kch[j & 1] >= kb_end;  // K tail: this lane's chunk is past the row end
+    uint8_t *dst = lds + (ks & 1) * kStageBytes + op * (256 * kStep) + (BLK * wave + j) * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[op], (lds_void *)dst, 16, past ? kOob : vo[op][j],
+                                             so, 0, 0);
   };
 
-  // Fragment reads: lane l holds row l % 32 of a 32-row block, chunks 2g, 2g+1
-  // (g = l / 32).  Blocks 32 rows apart share the swizzle ((row >> 2) & 3 does
-  // not change by 32 rows), so they are one base plus 2 KiB steps.
+  // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
+  // h, chunks 4h + 2g and 4h + 2g + 1 (g = l / 32).  Blocks 32 rows apart
+  // share the swizzle ((row >> 1) & 7 does not change by 32 rows), so they
+  // are one base plus 4 KiB steps.
   const int frow = lane & 31, fg = lane >> 5;
-  const int a0 = off(wm * 128 + frow, 2 * fg), a1 = off(wm * 128 + frow, 2 * fg + 1);
-  const int b0 = 256 * kStep + off(wn * TN + frow, 2 * fg);
-  const int b1 = 256 * kStep + off(wn * TN + frow, 2 * fg + 1);
-  i32x8 fa[2][4], fb[2][FN];  // [register buffer][32-row block]
-  auto read = [&](int ks, auto buf_tag) {
-    constexpr int buf = decltype(buf_tag)::value;
-    const uint8_t *S = lds + (ks % kStages) * kStageBytes;
+  int ro[2][2][2];  // [operand][K half][piece]
 #pragma unroll
-    for (int f = 0; f < 4; ++f) fa[buf][f] = lds_pair(S + a0 + 2048 * f, S + a1 + 2048 * f);
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int f = 0; f < FN; ++f) fb[buf][f] = lds_pair(S + b0 + 2048 * f, S + b1 + 2048 * f);
+    for (int e = 0; e < 2; ++e) {
+      ro[0][h][e] = off(wm * 128 + frow, 4 * h + 2 * fg + e);
+      ro[1][h][e] = 256 * kStep + off(wn * TN + frow, 4 * h + 2 * fg + e);
+    }
+  txd::i32x4 fr[2][NF][2];  // [K half][fragment][16-byte piece]
+  // Read r of a K half: fragments in the order the MFMAs consume them
+  // (A0, B0, A1, A2, A3, B1, ...), two 16-byte pieces each.
+  auto read = [&](int ks, auto h_tag, auto r_tag) {
+    constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
+    constexpr int f = o == 0 ? 0 : o == 1 ? 4 : o <= 4 ? o - 1 : o;
+    const uint8_t *S = lds + (ks & 1) * kStageBytes;
+    const int byte = f < 4 ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - 4);
+    fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(S + byte);
   };
 
   txd::f32x16 acc[FN][4];
@@ -162,41 +190,58 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  // Prologue: steps 0..3 in flight (steps past the end read as zeros), step 0
-  // landed and in registers.
-#pragma unroll
-  for (int s = 0; s < kAhead; ++s) issue(s);
-  wait_and_barrier<(kAhead - 1) * 2 * BLK>();
-  read(0, std::integral_constant<int, 0>{});
-
-  // One K step; CUR is the register buffer holding step ks (compile-time, so
-  // the fragment arrays stay in registers).  Every step has the same shape:
-  // loads past the last step are still issued and fill a free stage with
-  // zeros, so the wait count is always "two steps may stay in flight".
-  auto step = [&](int ks, auto cur_tag) {
-    constexpr int CUR = decltype(cur_tag)::value;
-    // this wave's step ks+1 landed, then everyone's did, and stage ks % 4 is
-    // free (its contents are in registers)
-    wait_and_barrier<(kAhead - 2) * 2 * BLK>();
-    issue(ks + kAhead);
-    read(ks + 1, std::integral_constant<int, CUR ^ 1>{});
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-      for (int fm = 0; fm < 4; ++fm) mfma32<C>(acc[fn][fm], fb[CUR][fn], fa[CUR][fm]);
+  // MFMA i of a K half: B block i / 4 against A block i % 4.
+  auto mma = [&](auto h_tag, auto i_tag) {
+    constexpr int h = decltype(h_tag)::value, i = decltype(i_tag)::value, fn = i / 4, fm = i % 4;
+    const i32x8 va = __builtin_shufflevector(fr[h][fm][0], fr[h][fm][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const i32x8 vb = __builtin_shufflevector(fr[h][4 + fn][0], fr[h][4 + fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    mfma32<C>(acc[fn][fm], vb, va);
   };
-  int ks = 0;
-  for (; ks + 1 < ksteps; ks += 2) {
-    step(ks, std::integral_constant<int, 0>{});
-    step(ks + 1, std::integral_constant<int, 1>{});
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
+  constexpr int RW = NM / 2;  // reads follow the first RW MFMAs of a half
+
+  // Prologue: steps 0 and 1 in flight (steps past the end read as zeros),
+  // step 0 landed, half 0 of step 0 in registers.
+  static_for<ND>([&](auto d) { load(0, d); });
+  static_for<ND>([&](auto d) { load(1, d); });
+  wait_and_barrier<ND>();
+  static_for<NR>([&](auto r) { read(0, H0{}, r); });
+
+  for (int ks = 0; ks < ksteps; ++ks) {
+    static_for<NM>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      mma(H0{}, I);
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+      static_for<r1 - r0>([&](auto R) {
+        read(ks, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    // Step ks+1 landed for every wave; the stage of step ks is free.
+    wait_and_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<NM>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      mma(H1{}, I);
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
+      static_for<d1 - d0>([&](auto D) {
+        load(ks + 2, std::integral_constant<int, d0 + decltype(D)::value>{});
+      });
+      constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+      static_for<r1 - r0>([&](auto R) {
+        read(ks + 1, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
-  if (ks < ksteps) step(ks, std::integral_constant<int, 0>{});
   // Drain the trailing (zero-fill) loads before the workgroup's LDS is released.
   wait_and_barrier<0>();
 
   // Epilogue: lane owns, per (fm, fn, jj), C[m][n .. n+3] with
-  // m = m0 + wm*128 + fm*32 + l%32, n = n0 + wn*128 + fn*32 + 8*jj + 4*(l/32).
+  // m = m0 + wm*128 + fm*32 + l%32, n = n0 + wn*TN + fn*32 + 8*jj + 4*(l/32).
   uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
   const bool cvec = ((reinterpret_cast<uintptr_t>(a.C) & 7) == 0) && ((a.ldc & 3) == 0);
 #pragma unroll

@@ -27,12 +27,9 @@ TX_GEMM_FP8_FORMATS(128x128, 128, 128, 2, 2, 1)
 
 #include "gemm_fast.h"
 
-#define TX_GEMM_FP8_FAST(FA, FB, ELA, ELB)                                                  \
-  TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_##FA##_##FB##_fast(const tx_gemm_args a) {  \
-    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 4>(a);                             \
-  }                                                                                          \
-  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast8(const tx_gemm_args a) { \
-    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 8>(a);                             \
+#define TX_GEMM_FP8_FAST(FA, FB, ELA, ELB)                                                 \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast(const tx_gemm_args a) { \
+    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>>(a);                                  \
   }
 
 TX_GEMM_FP8_FAST(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)

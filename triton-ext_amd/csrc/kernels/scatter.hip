@@ -26,6 +26,8 @@ namespace {
 enum Op { ADD = 0, FADD = 1, MAX = 2, MIN = 3, UMAX = 4, UMIN = 5, AND = 6, OR = 7, XOR = 8 };
 
 constexpr int kBlock = 1024;
+constexpr int64_t kIter = 4 * kBlock;       // updates per workgroup iteration
+constexpr int kDepth = 3;                   // iterations of loads in flight (pipelined loop)
 constexpr int kDirectSlots = 36864;          // 144 KiB of 4-byte counters
 constexpr int kHashLog2 = 14;                // 16384 slots, 128 KiB keys + values
 constexpr int kHashSlots = 1 << kHashLog2;
@@ -34,7 +36,9 @@ constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 
 template <int OP> struct OpTraits;
 template <> struct OpTraits<ADD> { using T = uint32_t; static __device__ T id() { return 0u; } };
-template <> struct OpTraits<FADD> { using T = float; static __device__ T id() { return 0.0f; } };
+// -0.0 is the exact identity of IEEE addition (x + -0 == x for every x,
+// +0 included), so fp32 tables start at -0 and untouched slots can be skipped.
+template <> struct OpTraits<FADD> { using T = float; static __device__ T id() { return -0.0f; } };
 template <> struct OpTraits<MAX> { using T = int32_t; static __device__ T id() { return INT32_MIN; } };
 template <> struct OpTraits<MIN> { using T = int32_t; static __device__ T id() { return INT32_MAX; } };
 template <> struct OpTraits<UMAX> { using T = uint32_t; static __device__ T id() { return 0u; } };
@@ -64,11 +68,12 @@ __device__ __forceinline__ void atomic_combine(T *p, T v) {
   else atomicXor(p, v);
 }
 
+// Slots still holding the identity are skipped when flushing.  For fp32 the
+// test is on the bits: only -0 is an identity, +0 is not (it turns a -0 bin
+// into +0).
 template <int OP, typename T>
 __device__ __forceinline__ bool is_identity(T v) {
-  // Integer identities can be skipped when flushing; an fp32 +0 cannot
-  // (adding +0 turns a -0 bin into +0), so fp32 slots always flush.
-  if constexpr (OP == FADD) return false;
+  if constexpr (OP == FADD) return __builtin_bit_cast(uint32_t, v) == 0x80000000u;
   else return v == OpTraits<OP>::id();
 }
 
@@ -135,6 +140,57 @@ struct Scatter {
     }
   }
 
+  // One full iteration's worth of this lane's updates: 4 indices, 4 values
+  // and (MASK) 4 mask bytes, each fetched with one load.
+  template <bool MASK>
+  static __device__ __forceinline__ void fetch(const tx_scatter_args &a, int64_t e, txd::i32x4 &k,
+                                               txd::u32x4 &v, uint32_t &m) {
+    k = __builtin_nontemporal_load(reinterpret_cast<const txd::i32x4 *>(a.idx + e));
+    v = __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(a.val) + e / 4);
+    if constexpr (MASK) m = *reinterpret_cast<const uint32_t *>(a.mask + e);
+    else m = 0xFFFFFFFFu;
+  }
+
+  // Combine 4 updates into the LDS window [lo, lo + nb).  A key outside the
+  // window (negative keys included: they wrap to large unsigned values) or
+  // with a zero mask byte is dropped; lo + nb <= nbins <= INT32_MAX.
+  static __device__ __forceinline__ void apply(T *table, uint32_t lo, uint32_t nb,
+                                               const txd::i32x4 &k, const txd::u32x4 &v, uint32_t m) {
+    const int32_t kk[4] = {k.x, k.y, k.z, k.w};
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t r = uint32_t(kk[j]) - lo;
+      if (r < nb && ((m >> (8 * j)) & 0xFFu) != 0) atomic_combine<OP, T>(&table[r], __builtin_bit_cast(T, vv[j]));
+    }
+  }
+
+  // Pipelined pass over `groups` x kDepth full iterations starting at this
+  // lane's element e0 (16-byte aligned index and value buffers): the loads of
+  // the next kDepth iterations are in flight while an iteration's LDS atomics
+  // run.  Slot d always holds an iteration congruent to d mod kDepth, so the
+  // slots are compile-time registers; refills past the last iteration re-read
+  // the last one (in range, never applied).
+  template <bool MASK>
+  static __device__ void stream(const tx_scatter_args &a, T *table, uint32_t lo, uint32_t nb,
+                                int64_t e0, int64_t groups) {
+    txd::i32x4 k[kDepth];
+    txd::u32x4 v[kDepth];
+    uint32_t m[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) fetch<MASK>(a, e0 + d * kIter, k[d], v[d], m[d]);
+    const int64_t last = e0 + (groups * kDepth - 1) * kIter;
+    for (int64_t g = 0; g < groups; ++g) {
+      const int64_t eg = e0 + g * kDepth * kIter;
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        apply(table, lo, nb, k[d], v[d], m[d]);
+        const int64_t en = eg + (d + kDepth) * kIter;
+        fetch<MASK>(a, en < last ? en : last, k[d], v[d], m[d]);
+      }
+    }
+  }
+
   // Windowed LDS privatisation.  The bin range is cut into `splits` windows
   // of `window` bins (each fits in LDS); `splits` workgroups read the same
   // chunk of updates and each privatises one window, so every update lands
@@ -158,7 +214,17 @@ struct Scatter {
     __syncthreads();
     const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
                      (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
-    for (int64_t e = begin + 4 * int64_t(threadIdx.x); e < end; e += 4 * kBlock) {
+    int64_t e = begin + 4 * int64_t(threadIdx.x);
+    if (vec) {
+      // Whole groups of kDepth full iterations go through the pipelined loop.
+      const int64_t groups = (end - begin) / (kDepth * kIter);
+      if (groups > 0) {
+        if (a.mask) stream<true>(a, table, lo, nb, e, groups);
+        else stream<false>(a, table, lo, nb, e, groups);
+        e += groups * kDepth * kIter;
+      }
+    }
+    for (; e < end; e += kIter) {
       uint32_t key[4];
       T val[4];
       bool ok[4];
