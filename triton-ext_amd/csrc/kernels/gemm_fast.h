@@ -3,7 +3,9 @@
 // 8 wavefronts (two per SIMD), each owning a 128 x 64 block of C.
 //
 // Pipeline (per 128-byte K step, i.e. 64 bf16 or 128 fp8 of K):
-//  * LDS holds 2 stages of (256 A rows + 256 B rows) x 128 bytes = 2 x 64 KiB.
+//  * LDS is a ring of 5 slots of 32 KiB (all of gfx950's 160 KiB); a slot
+//    holds one operand of one step, 256 rows x 128 bytes.  Operand-step u
+//    (A of step k is u = 2k, B is u = 2k + 1) lives in slot u % 5.
 //    Rows are 8 chunks of 16 bytes stored at chunk ^ ((row >> 1) & 7): a
 //    ds_read_b128 is served 16 lanes at a time over 256 bytes of banks, the
 //    fragment reads have 16 lanes read one logical chunk of 16 consecutive
@@ -18,12 +20,13 @@
 //    and the K tail use an offset past the buffer's range, which reads as zero.
 //  * A step is consumed in two K halves of 64 bytes (one 32x32x64 fp8 MFMA,
 //    or two 32x32x16 bf16 MFMAs, per 32 x 32 block).  Fragments run one half
-//    ahead in registers: while the MFMAs of half 0 run, half 1 is read; then
-//    every wave waits for its loads of step k+1, one barrier publishes them
-//    to the workgroup and frees the stage of step k (both halves are in
-//    registers), and while the MFMAs of half 1 run, the wave issues the loads
-//    of step k+2 into that stage and reads half 0 of step k+1.  A load has
-//    one full step of MFMA time to arrive.
+//    ahead in registers: while the MFMAs of half 0 of step k run, half 1 is
+//    read.  Then every wave waits for its loads of step k+1, and one barrier
+//    publishes them to the workgroup and frees the two slots of step k (both
+//    halves are in registers).  While the MFMAs of half 1 run, the wave reads
+//    half 0 of step k+1 and loads B of step k+2 and A of step k+3 into the
+//    freed slots ((2k + 5) % 5 and (2k + 6) % 5 are the slots of A and B of
+//    step k).  B loads have one step of MFMA time to arrive, A loads two.
 //  * The instruction order inside each half is fixed in the source and
 //    pinned with scheduling barriers: after each MFMA, a share of the LDS
 //    reads (all of them within the first half of the MFMAs, in the order the
@@ -60,8 +63,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 
 namespace fast {
 constexpr int kStep = 128;                   // K bytes per step
-constexpr int kRows = 512;                   // 256 A rows + 256 B rows
-constexpr int kStageBytes = kRows * kStep;   // 64 KiB
+constexpr int kSlotBytes = 256 * kStep;      // one operand of one step: 32 KiB
+constexpr int kSlots = 5;
 constexpr int kWaves = 8;
 
 __device__ __forceinline__ int off(int row, int chunk) {
@@ -120,7 +123,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   constexpr int BLK = 32 / kWaves;   // 1 KiB blocks per operand per wave per step
   constexpr int ND = 2 * BLK;        // loads per wave per step
   static_assert(BLK % 2 == 0, "a wave's first block must have an even index");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
   int tm, tn;
   tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
@@ -149,14 +152,23 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     vo[0][j] = gm < a.M ? uint32_t(gm) * lda_b + kch[j & 1] : kOob;
     vo[1][j] = gn < a.N ? uint32_t(gn) * ldb_b + kch[j & 1] : kOob;
   }
-  // Load d of step ks: operand d / BLK, block d % BLK.
-  auto load = [&](int ks, auto d_tag) {
-    constexpr int d = decltype(d_tag)::value, op = d / BLK, j = d % BLK;
+  // Load block j of operand op of step ks into slot `slot`.
+  auto load_op = [&](int ks, int slot, auto op_tag, auto j_tag) {
+    constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     const uint32_t so = uint32_t(ks) * kStep;
     const bool past = so + kch[j & 1] >= kb_end;  // K tail: this lane's chunk is past the row end
-    uint8_t *dst = lds + (ks & 1) * kStageBytes + op * (256 * kStep) + (BLK * wave + j) * 1024;
+    uint8_t *dst = lds + slot * kSlotBytes + (BLK * wave + j) * 1024;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[op], (lds_void *)dst, 16, past ? kOob : vo[op][j],
                                              so, 0, 0);
+  };
+  using OpA = std::integral_constant<int, 0>;
+  using OpB = std::integral_constant<int, 1>;
+  // Load d of the second half of step ks: B of step ks+2 into the slot of A
+  // of step ks (d < BLK), then A of step ks+3 into the slot of B of step ks.
+  auto load = [&](int ks, int slot_a, int slot_b, auto d_tag) {
+    constexpr int d = decltype(d_tag)::value;
+    if constexpr (d < BLK) load_op(ks + 2, slot_a, OpB{}, std::integral_constant<int, d>{});
+    else load_op(ks + 3, slot_b, OpA{}, std::integral_constant<int, d - BLK>{});
   };
 
   // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
@@ -170,15 +182,15 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       ro[0][h][e] = off(wm * 128 + frow, 4 * h + 2 * fg + e);
-      ro[1][h][e] = 256 * kStep + off(wn * TN + frow, 4 * h + 2 * fg + e);
+      ro[1][h][e] = off(wn * TN + frow, 4 * h + 2 * fg + e);
     }
   txd::i32x4 fr[2][NF][2];  // [K half][fragment][16-byte piece]
   // Read r of a K half: fragments in the order the MFMAs consume them
   // (A0, B0, A1, A2, A3, B1, ...), two 16-byte pieces each.
-  auto read = [&](int ks, auto h_tag, auto r_tag) {
+  auto read = [&](int slot_a, int slot_b, auto h_tag, auto r_tag) {
     constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
     constexpr int f = o == 0 ? 0 : o == 1 ? 4 : o <= 4 ? o - 1 : o;
-    const uint8_t *S = lds + (ks & 1) * kStageBytes;
+    const uint8_t *S = lds + (f < 4 ? slot_a : slot_b) * kSlotBytes;
     const int byte = f < 4 ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - 4);
     fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(S + byte);
   };
@@ -201,26 +213,32 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using H1 = std::integral_constant<int, 1>;
   constexpr int RW = NM / 2;  // reads follow the first RW MFMAs of a half
 
-  // Prologue: steps 0 and 1 in flight (steps past the end read as zeros),
+  // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
   // step 0 landed, half 0 of step 0 in registers.
-  static_for<ND>([&](auto d) { load(0, d); });
-  static_for<ND>([&](auto d) { load(1, d); });
-  wait_and_barrier<ND>();
-  static_for<NR>([&](auto r) { read(0, H0{}, r); });
+  static_for<BLK>([&](auto j) { load_op(0, 0, OpA{}, j); });
+  static_for<BLK>([&](auto j) { load_op(0, 1, OpB{}, j); });
+  static_for<BLK>([&](auto j) { load_op(1, 2, OpA{}, j); });
+  static_for<BLK>([&](auto j) { load_op(1, 3, OpB{}, j); });
+  static_for<BLK>([&](auto j) { load_op(2, 4, OpA{}, j); });
+  wait_and_barrier<3 * BLK>();
+  static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
 
+  int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
   for (int ks = 0; ks < ksteps; ++ks) {
+    const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;  // step ks+1
     static_for<NM>([&](auto I) {
       constexpr int i = decltype(I)::value;
       mma(H0{}, I);
       __builtin_amdgcn_sched_barrier(0);
       constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
       static_for<r1 - r0>([&](auto R) {
-        read(ks, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+        read(sa, sb, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    // Step ks+1 landed for every wave; the stage of step ks is free.
-    wait_and_barrier<0>();
+    // A and B of step ks+1 landed for every wave (the BLK loads of A of step
+    // ks+2, issued last, may still be in flight); the slots of step ks are free.
+    wait_and_barrier<BLK>();
     __builtin_amdgcn_sched_barrier(0);
     static_for<NM>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -228,14 +246,16 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       __builtin_amdgcn_sched_barrier(0);
       constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
       static_for<d1 - d0>([&](auto D) {
-        load(ks + 2, std::integral_constant<int, d0 + decltype(D)::value>{});
+        load(ks, sa, sb, std::integral_constant<int, d0 + decltype(D)::value>{});
       });
       constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
       static_for<r1 - r0>([&](auto R) {
-        read(ks + 1, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+        read(na, nb, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
       });
       __builtin_amdgcn_sched_barrier(0);
     });
+    sa = na;
+    sb = nb;
   }
   // Drain the trailing (zero-fill) loads before the workgroup's LDS is released.
   wait_and_barrier<0>();
@@ -248,8 +268,8 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   for (int fm = 0; fm < 4; ++fm) {
     const int m = m0 + wm * 128 + fm * 32 + frow;
     if (m >= a.M) continue;
-    float sa = 1.0f;
-    if constexpr (C::FP8) sa = a.scale_a[m];
+    float scl_a = 1.0f;
+    if constexpr (C::FP8) scl_a = a.scale_a[m];
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
@@ -260,7 +280,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
         for (int t = 0; t < 4; ++t) v[t] = acc[fn][fm][4 * jj + t];
         if constexpr (C::FP8) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) v[t] = v[t] * sa * (n + t < a.N ? a.scale_b[n + t] : 0.0f);
+          for (int t = 0; t < 4; ++t) v[t] = v[t] * scl_a * (n + t < a.N ? a.scale_b[n + t] : 0.0f);
         }
         uint16_t *dst = Cb + int64_t(m) * a.ldc + n;
         if (cvec && n + 3 < a.N) {
