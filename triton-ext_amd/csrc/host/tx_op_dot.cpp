@@ -68,6 +68,8 @@ tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int 
 
 // Wavefronts per workgroup of the fast path (two per SIMD).
 constexpr int kFastWaves = 8;
+// Largest M served by the skinny fp8 kernel (4 blocks of 16 rows).
+constexpr int64_t kSkinnyMaxM = 64;
 
 // The LDS-DMA fast path needs 16-byte aligned rows and a row length that is a
 // multiple of 16 bytes, and operands small enough that a 32-bit buffer offset
@@ -119,10 +121,29 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   if (!sa || !sb) return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: NULL scale vector");
   if (!aligned(sa, 4) || !aligned(sb, 4))
     return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: scales must be 4-byte aligned");
+  char kname[80];
+  // Decode-sized M: stream B once with the skinny kernel (16 columns per
+  // workgroup, K split over its wavefronts).
+  if (M <= kSkinnyMaxM && K % 128 == 0 && aligned(A, 16) && aligned(B, 16) && lda % 16 == 0 &&
+      ldb % 16 == 0 && (N - 1) * ldb + K < (int64_t(1) << 31)) {
+    const int mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    const int64_t grid = (N + 15) / 16;
+    const int waves = grid >= 2 * int64_t(cu_count()) ? 8 : 16;
+    // A wave's K range in 128-byte slices; one LDS stage when it fits one
+    // chunk (4 slices at 8 wavefronts, 2 at 16).
+    const int64_t per_wave = (K / 128 + waves - 1) / waves;
+    const int stages = per_wave <= (waves == 8 ? 4 : 2) ? 1 : 2;
+    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_skinny_w%d_s%d_m%d", fa, fb, waves,
+                  stages, mb);
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
+    tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+    return launch(fn, unsigned(grid), 1, unsigned(64 * waves), static_cast<hipStream_t>(stream),
+                  &args, sizeof args, kname);
+  }
   static const int widths[] = {16, 4, 1};
   const int vec = pick_vec(A, lda, B, ldb, K, widths, 3);
   const int tile = (vec != 1 && use_big_tile(M, N)) ? 256 : 128;
-  char kname[80];
   unsigned threads = 256;
   if (tile == 256 && fast_ok(A, lda, B, ldb, K, M, N)) {
     threads = 64 * kFastWaves;
