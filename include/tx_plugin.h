@@ -237,7 +237,9 @@ TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
  * No reference kernel exists (the nearest is the fp8 tt.dot of
  * tx_dot_fp8_scaled).  x: bf16 row-major M x K (ldx); W: fp8 (w_type) row-major
  * N x K bytes (ldw); scales: fp32 row-major N x ceil(K/group) (ld_scales);
- * y: bf16 row-major M x N (ldy).  group is a multiple of 32; M <= 64.
+ * y: bf16 row-major M x N (ldy).  K and group are multiples of 128 (the last
+ * group may be partial), M <= 64, x and W rows 16-byte aligned, scales 4-byte
+ * aligned (TX_UNSUPPORTED otherwise).
  */
 TX_API tx_status tx_gemv_fp8_dequant(const void *x, int64_t ldx, const void *W,
                                      tx_dtype w_type, int64_t ldw,
