@@ -81,10 +81,12 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
   if (windows <= kMaxWindows) {
     std::snprintf(kname, sizeof kname, "tx_scatter_%s_windowed", name);
     TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
-    // One workgroup per CU at a time (the table fills most of a CU's LDS);
-    // about one round of workgroups in total, `windows` of them per chunk.
-    const int64_t wgs = std::max<int64_t>(cus, 8 * windows);
-    int64_t chunks = std::max<int64_t>(1, wgs / windows);
+    // One workgroup per CU at a time (the table fills most of a CU's LDS).
+    // One chunk of updates per CU and `windows` workgroups per chunk: when
+    // the key distribution loads one window more than the others (skewed
+    // keys), the CUs that finish the light windows take over the remaining
+    // workgroups of the heavy one.
+    int64_t chunks = std::max<int64_t>(8, cus);
     int64_t per = (n + chunks - 1) / chunks;
     per = (per + kWinStep - 1) / kWinStep * kWinStep;
     if (per > INT32_MAX) per = INT32_MAX / kWinStep * kWinStep;
