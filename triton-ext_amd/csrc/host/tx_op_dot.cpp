@@ -125,16 +125,13 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   // Decode-sized M: stream B once with the skinny kernel (16 columns per
   // workgroup, K split over its wavefronts).
   if (M <= kSkinnyMaxM && K % 128 == 0 && aligned(A, 16) && aligned(B, 16) && lda % 16 == 0 &&
-      ldb % 16 == 0 && (N - 1) * ldb + K < (int64_t(1) << 31)) {
+      ldb % 16 == 0) {
     const int mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     const int64_t grid = (N + 15) / 16;
-    const int waves = grid >= 2 * int64_t(cu_count()) ? 8 : 16;
-    // A wave's K range in 128-byte slices; one LDS stage when it fits one
-    // chunk (4 slices at 8 wavefronts, 2 at 16).
-    const int64_t per_wave = (K / 128 + waves - 1) / waves;
-    const int stages = per_wave <= (waves == 8 ? 4 : 2) ? 1 : 2;
-    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_skinny_w%d_s%d_m%d", fa, fb, waves,
-                  stages, mb);
+    // Many column blocks: 4 wavefronts each, with long K ranges per wave;
+    // few: 16 (8 with 4 blocks of M) to keep enough loads in flight.
+    const int waves = grid >= 2 * int64_t(cu_count()) ? 4 : (mb == 4 ? 8 : 16);
+    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_skinny_w%d_m%d", fa, fb, waves, mb);
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
     tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};

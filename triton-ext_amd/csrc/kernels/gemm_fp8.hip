@@ -39,23 +39,18 @@ TX_GEMM_FP8_FAST(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 
 #include "gemm_skinny.h"
 
-// Kernel names: tx_gemm_fp8_<a>_<b>_skinny_w<waves>_s<stages>_m<16-row blocks
-// of M>.  KC (K bytes per LDS stage): 512 at 8 wavefronts, 256 at 16, so a
-// workgroup's stages take 64 KiB (one stage) or 128 KiB (two).
-#define TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, S, MB, KC)                                        \
-  TX_KERNEL void __launch_bounds__(64 * W) tx_gemm_fp8_##FA##_##FB##_skinny_w##W##_s##S##_m##MB( \
-      const tx_gemm_args a) {                                                                    \
-    skinny_fp8_tile<ELA, ELB, W, MB, KC, S>(a);                                                  \
+// Kernel names: tx_gemm_fp8_<a>_<b>_skinny_w<waves>_m<16-row blocks of M>
+// (the small-grid variant with 4 blocks of M has 8 wavefronts: 16 would not
+// fit its registers in 128 VGPRs).
+#define TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, MB)                                       \
+  TX_KERNEL void __launch_bounds__(64 * W) tx_gemm_fp8_##FA##_##FB##_skinny_w##W##_m##MB( \
+      const tx_gemm_args a) {                                                            \
+    skinny_fp8_tile<ELA, ELB, W, MB>(a);                                                 \
   }
-#define TX_GEMM_FP8_SKINNY_WS(FA, FB, ELA, ELB, W, S, KC)                             \
-  TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, S, 1, KC)                                   \
-  TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, S, 2, KC)                                   \
-  TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, S, 4, KC)
-#define TX_GEMM_FP8_SKINNY_ALL(FA, FB, ELA, ELB)                                        \
-  TX_GEMM_FP8_SKINNY_WS(FA, FB, ELA, ELB, 8, 1, 512)                                    \
-  TX_GEMM_FP8_SKINNY_WS(FA, FB, ELA, ELB, 8, 2, 512)                                    \
-  TX_GEMM_FP8_SKINNY_WS(FA, FB, ELA, ELB, 16, 1, 256)                                   \
-  TX_GEMM_FP8_SKINNY_WS(FA, FB, ELA, ELB, 16, 2, 256)
+#define TX_GEMM_FP8_SKINNY_ALL(FA, FB, ELA, ELB)                                               \
+  TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, 4, 1) TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, 4, 2)       \
+  TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, 4, 4) TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, 16, 1)      \
+  TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, 16, 2) TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, 8, 4)
 
 TX_GEMM_FP8_SKINNY_ALL(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
 TX_GEMM_FP8_SKINNY_ALL(e5m2, e5m2, EL_E5M2, EL_E5M2)

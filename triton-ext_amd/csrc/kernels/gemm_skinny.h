@@ -4,37 +4,33 @@
 // row/column-scaled case with a decode-sized M.
 //
 // HBM-bound on B, which is read once.  A workgroup owns 16 rows of B (16
-// output columns) and splits K over its wavefronts.  Each wave streams its
-// 16 rows through a private LDS stage (double-buffered when its K range spans
-// several chunks; a single stage keeps two workgroups per CU) with gfx950's
-// `buffer_load_dwordx4 ... lds` (one instruction fills 1 KiB = 1024 / KC rows
-// of a KC-byte chunk, so the 64 lanes read whole contiguous lines of B), and
-// reads the MFMA fragments back from LDS.  The stage stores 16-byte chunk c of
-// row r at chunk c ^ (r & 15): the 16 lanes of a ds_read_b128 phase read one
-// logical chunk of 16 consecutive rows, which this places in 16 different
-// 16-byte bank groups.  Per 128-byte K slice a lane (row r = lane % 16,
-// group g = lane / 16) takes bytes [32g, 32g + 32) of the slice for both B and
-// A (A is a few KiB per slice for the whole grid, read from cache), and one
-// v_mfma_f32_16x16x128_f8f6f4 per 16-row block of A.  The per-wave partial
-// sums are reduced across the workgroup in LDS and the scales applied once,
-// in fp32, before the bf16 rounding.
+// output columns) and splits K over its wavefronts.  A wave streams its 16
+// rows in rounds of 256 bytes per row (two 128-byte K slices): each of the 4
+// loads of a round reads 4 whole 256-byte row segments (16 lanes x 16 bytes
+// per row), and two rounds are in flight in registers.  The MFMA wants lane
+// (r = lane % 16, g = lane / 16) to hold 32 bytes of row r, so each round is
+// transposed through a private 4 KiB LDS tile: 16-byte chunk c of row r is
+// stored at chunk c ^ (r & 15), which keeps both the writes (16 lanes of one
+// row) and the fragment reads (16 rows, one logical chunk) in 16 different
+// 16-byte bank groups.  Per slice a lane takes bytes [32g, 32g + 32) of the
+// slice for both B and A (A is a few KiB per slice for the whole grid, read
+// from cache), and one v_mfma_f32_16x16x128_f8f6f4 runs per 16-row block of
+// A.  The per-wave partial sums are reduced across the workgroup in LDS and
+// the scales applied once, in fp32, before the bf16 rounding.
 #pragma once
 
 #include "gemm_fast.h"
 
 namespace txg {
 
-template <int ELA, int ELB, int kWaves, int MB, int KC, int kStages>
+template <int ELA, int ELB, int kWaves, int MB>
 __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
-  static_assert(kStages == 1 || kStages == 2, "one or two stages per wave");
-  constexpr int kSlice = 128;             // K bytes per MFMA
-  constexpr int kSpc = KC / kSlice;       // slices per chunk
-  constexpr int kStage = 16 * KC;         // one wave's stage: 16 rows x KC bytes
-  constexpr int kRpi = 1024 / KC;         // rows per load instruction
-  constexpr int kCpr = KC / 16;           // 16-byte chunks per row
-  constexpr int kLoads = 16 / kRpi;       // load instructions per stage
-  static_assert(kCpr >= 16 && kLoads >= 1, "chunk of 256 bytes or more");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kWaves * kStages * kStage];
+  constexpr int kSlice = 128;        // K bytes per MFMA
+  constexpr int kRound = 2;          // slices per round: 256 bytes per row
+  constexpr int kDepth = 2;          // rounds in flight
+  constexpr int kTile = 16 * 256;    // one wave's transpose tile
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kWaves * kTile];
+  static_assert(kWaves * MB * 1024 <= kWaves * kTile, "reduction fits in the tiles");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -44,32 +40,29 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
   const int per_wave = (nslices + kWaves - 1) / kWaves;
   const int s_begin = min(nslices, wave * per_wave);
   const int s_end = min(nslices, s_begin + per_wave);
-  const int nchunks = (s_end - s_begin + kSpc - 1) / kSpc;
+  const int nrounds = (s_end - s_begin + kRound - 1) / kRound;
 
-  // Loads: instruction j covers rows kRpi*j .. kRpi*j + kRpi - 1; lane i lands
-  // in row kRpi*j + i / kCpr, physical chunk i % kCpr, and fetches logical
-  // chunk (i % kCpr) ^ (row & 15).  Rows past N read as zero (never stored).
-  const uint32_t kb_end = uint32_t(a.K);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.B, uint32_t(a.N - 1) * uint32_t(a.ldb) + kb_end);
-  uint32_t vo[kLoads], lc[kLoads];
+  // Load j (0..3) of a round: row 4j + lane / 16 of the block, bytes
+  // 16 (lane % 16) of that row's 256-byte segment.  Rows past N read the
+  // last row (valid memory) and are never stored.
+  const uint8_t *B = reinterpret_cast<const uint8_t *>(a.B);
+  const uint8_t *bp[4];
+  int wpos[4];
+  uint8_t *tile = lds + wave * kTile;
 #pragma unroll
-  for (int j = 0; j < kLoads; ++j) {
-    const int row = kRpi * j + lane / kCpr;
-    lc[j] = uint32_t((lane % kCpr) ^ (row & 15));
-    vo[j] = n0 + row < a.N ? uint32_t(n0 + row) * uint32_t(a.ldb) + 16u * lc[j] : kOob;
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    const int n = n0 + row;
+    bp[j] = B + int64_t(n < a.N ? n : a.N - 1) * a.ldb + 16 * (lane & 15);
+    wpos[j] = row * 256 + (((lane & 15) ^ (row & 15)) << 4);
   }
-  uint8_t *my = lds + wave * kStages * kStage;
-  auto issue = [&](int c) {
-    const int s = s_begin + c * kSpc;
-    const uint32_t kb = uint32_t(s) * kSlice;
-    const uint32_t valid = uint32_t(min(kSpc, s_end - s)) * kSlice;  // bytes of this chunk in range
-    uint8_t *st = my + (kStages == 2 ? (c & 1) * kStage : 0);
+  // Fragment read offsets: slice u of a round, pieces e = 0, 1 (logical
+  // chunks 8u + 2g + e of row r).
+  int rpos[kRound][2];
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(st + 1024 * j), 16,
-                                               16u * lc[j] < valid ? vo[j] : kOob, kb, 0, 0);
-  };
-
+  for (int u = 0; u < kRound; ++u)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) rpos[u][e] = r * 256 + (((8 * u + 2 * g + e) ^ r) << 4);
   // A rows past M read the last valid row and are never stored.
   const uint8_t *arow[MB];
 #pragma unroll
@@ -77,47 +70,46 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
     const int m = mb * 16 + r;
     arow[mb] = reinterpret_cast<const uint8_t *>(a.A) + int64_t(m < a.M ? m : a.M - 1) * a.lda + 32 * g;
   }
-  // Read offsets of this lane's two 16-byte pieces of slice u (logical chunks
-  // 8u + 2g and 8u + 2g + 1 of row r).
-  int ro[kSpc][2];
-#pragma unroll
-  for (int u = 0; u < kSpc; ++u)
-#pragma unroll
-    for (int e = 0; e < 2; ++e) ro[u][e] = r * KC + (((8 * u + 2 * g + e) ^ r) << 4);
 
+  struct Round {
+    txd::u32x4 w[4];
+  };
+  // Round q's loads; in a round with one slice left the upper half reads zeros.
+  auto fetch = [&](int q, Round &f) {
+    const int s = s_begin + q * kRound;
+    const int valid = min(kRound, s_end - s) * kSlice;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.w[j] = 16 * (lane & 15) < valid
+                   ? __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(bp[j] + int64_t(s) * kSlice))
+                   : txd::u32x4{0u, 0u, 0u, 0u};
+  };
   txd::f32x4 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = txd::f32x4{0.f, 0.f, 0.f, 0.f};
-
-  if (nchunks > 0) issue(0);
-  for (int c = 0; c < nchunks; ++c) {
-    const int s = s_begin + c * kSpc;
-    const int ns = min(kSpc, s_end - s);
-    // A pieces of this chunk (cache-resident); issued before the next chunk's
-    // loads so that loads completing in order lets the wait below leave only
-    // those in flight.
-    txd::u32x4 xa[kSpc][MB][2];
+  auto compute = [&](int q, const Round &f) {
+    const int s = s_begin + q * kRound;
+    const int ns = min(kRound, s_end - s);
+    txd::u32x4 xa[kRound][MB][2];
 #pragma unroll
-    for (int u = 0; u < kSpc; ++u)
+    for (int u = 0; u < kRound; ++u)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const txd::u32x4 *xp = reinterpret_cast<const txd::u32x4 *>(arow[mb] + (s + (u < ns ? u : 0)) * kSlice);
         xa[u][mb][0] = xp[0];
         xa[u][mb][1] = xp[1];
       }
-    if (kStages == 2 && c + 1 < nchunks) {
-      issue(c + 1);
-      __builtin_amdgcn_s_waitcnt((kLoads & 15) | (7 << 4) | (0xF << 8) | ((kLoads >> 4) << 14));
-    } else {
-      __builtin_amdgcn_s_waitcnt((7 << 4) | (0xF << 8));  // vmcnt(0)
-    }
-    asm volatile("" ::: "memory");
-    const uint8_t *st = my + (kStages == 2 ? (c & 1) * kStage : 0);
+    // Transpose through the wave's tile (LDS operations of one wave complete
+    // in order, so the reads see the writes and the next round's writes
+    // follow these reads).
 #pragma unroll
-    for (int u = 0; u < kSpc; ++u) {
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<txd::u32x4 *>(tile + wpos[j]) = f.w[j];
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < kRound; ++u) {
       if (u < ns) {
-        const txd::i32x4 w0 = *reinterpret_cast<const txd::i32x4 *>(st + ro[u][0]);
-        const txd::i32x4 w1 = *reinterpret_cast<const txd::i32x4 *>(st + ro[u][1]);
+        const txd::i32x4 w0 = *reinterpret_cast<const txd::i32x4 *>(tile + rpos[u][0]);
+        const txd::i32x4 w1 = *reinterpret_cast<const txd::i32x4 *>(tile + rpos[u][1]);
         const i32x8 wv = __builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
@@ -128,15 +120,28 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
         }
       }
     }
-    // The stage just read is refilled by the next load: its reads must be
-    // complete first.
-    __builtin_amdgcn_s_waitcnt((0xF) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
     asm volatile("" ::: "memory");
-    if (kStages == 1 && c + 1 < nchunks) issue(c + 1);
+  };
+
+  // Round slots are compile-time registers: slot d holds rounds congruent to
+  // d mod kDepth, refilled right after its round is consumed.
+  Round buf[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d)
+    if (d < nrounds) fetch(d, buf[d]);
+  for (int q0 = 0; q0 < nrounds; q0 += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      const int q = q0 + d;
+      if (q < nrounds) {
+        compute(q, buf[d]);
+        if (q + kDepth < nrounds) fetch(q + kDepth, buf[d]);
+      }
+    }
   }
 
-  // Cross-wave reduction in LDS (reusing the stage memory); MFMA result
-  // layout: lane holds D[m = 4 * (lane / 16) + i][n = lane % 16].
+  // Cross-wave reduction in LDS (reusing the tiles); MFMA result layout:
+  // lane holds D[m = 4 * (lane / 16) + i][n = lane % 16].
   __syncthreads();
   txd::f32x4 *red = reinterpret_cast<txd::f32x4 *>(lds);  // [kWaves][MB][64]
 #pragma unroll
