@@ -211,9 +211,13 @@ def test_gemv_config_full(tx, oracle, dev, M):
     check_close(_np_bits(y), r32, r16, FP8_TOL)
 
 
-@pytest.mark.parametrize("M,N,K,group,fmt", [(3, 100, 256, 128, 2), (33, 77, 1024, 256, 2),
+@pytest.mark.parametrize("M,N,K,group,fmt", [(8, 8200, 384, 128, 2), (20, 8200, 512, 128, 2),
+                                             (40, 8208, 256, 256, 1),
+                                             (3, 100, 256, 128, 2), (33, 77, 1024, 256, 2),
                                              (64, 50, 384, 384, 1), (5, 1, 128, 128, 1)])
 def test_gemv_shapes(tx, oracle, dev, M, N, K, group, fmt):
+    """Small and ragged shapes; N >= 8192 takes the wide variants (two W
+    blocks per wave when M > 4, with an odd number of 16-row blocks)."""
     g = np.random.default_rng(M * N)
     x = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
     wq = g.integers(0, 256, size=(N, K), dtype=np.uint8)

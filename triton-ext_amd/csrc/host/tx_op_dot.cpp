@@ -179,17 +179,22 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
       !aligned(scales, 4) || !aligned(y, 2))
     return fail(TX_UNSUPPORTED,
                 "%s: needs 16-byte aligned x and W rows (ldx %% 8 == 0, ldw %% 16 == 0)", what);
-  // K split over the workgroup's 4 wavefronts (measured faster than 2 or 8).
-  const int waves = 4;
+  // 16 or 32 W rows per workgroup, K split over its wavefronts.  Many column
+  // blocks: 4 wavefronts, each with two 16-row W blocks sharing its x reads
+  // once x has more than a few rows.  Few: one W block per workgroup and 16
+  // wavefronts (8 with 2 or 4 blocks of M) to keep enough loads in flight.
   const int mblocks = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const bool wide = (N + 15) / 16 >= 2 * int64_t(cu_count());
+  const int waves = wide ? 4 : (mblocks == 1 ? 16 : 8);
+  const int nb = (wide && M > 4) ? 2 : 1;
+  const int64_t grid = (N + 16 * nb - 1) / (16 * nb);
   char kname[48];
-  std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s_w%d_m%d", fw, waves, mblocks);
+  std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s_w%d_m%d_b%d", fw, waves, mblocks, nb);
   hipFunction_t fn;
   TX_TRY(get_kernel(CodeObject::Gemv, kname, &fn));
   tx_gemv_args args{static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(W), scales,
                     static_cast<uint16_t *>(y), ldx, ldw, ld_scales, ldy, int32_t(M), int32_t(N),
                     int32_t(K), int32_t(group)};
-  const int64_t grid = (N + 31) / 32;  // 32 W rows per workgroup
   return launch(fn, unsigned(grid), 1, unsigned(64 * waves), static_cast<hipStream_t>(stream), &args,
                 sizeof args, kname);
 }

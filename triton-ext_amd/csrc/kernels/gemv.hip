@@ -2,10 +2,14 @@
 //   y[m,n] = bf16_rne( sum_g s[n,g] * sum_{k in g} x[m,k] * W[n,k] )
 // x bf16 (M <= 64 rows), W fp8 N x K row-major, s fp32 N x (K/group).
 //
-// HBM-bound on W.  A workgroup owns 32 columns (rows of W) as two 16-row
-// blocks and splits K over its 4 wavefronts; each lane streams two 16-byte
-// pieces of each of its two W rows per 128-element slice (128-bit loads,
-// several slices in flight), and each x fragment feeds both blocks' MFMAs.
+// HBM-bound on W, which is read once.  A workgroup owns 16 rows of W (16
+// output columns) and splits K over its wavefronts.  A wave streams its rows
+// in rounds of 256 bytes per row: each of the 4 loads of a round reads 4
+// whole 256-byte row segments, two rounds are in flight in registers, and a
+// round is transposed through a private 4 KiB LDS tile (chunk c of row r at
+// chunk c ^ (r & 15): conflict-free for both the row writes and the fragment
+// reads) so that lane (r, g) holds 32 codes of row r per 128-element slice.
+// The per-wave partial sums are reduced across the workgroup in LDS.
 //
 // Dequantisation is bit placement, not arithmetic: an fp8 code's magnitude
 // bits shifted so its mantissa lands at the top of the bf16 mantissa, with
@@ -24,9 +28,7 @@
 
 namespace {
 
-constexpr int kNB = 2;                 // 16-row W blocks per wavefront
-constexpr int kCols = 16 * kNB;        // W rows (output columns) per workgroup
-constexpr int kSlice = 128;     // K elements per lane-group load step (2 x 16 B per lane)
+constexpr int kSlice = 128;     // K elements per slice (one group-scale unit)
 
 // Four fp8 codes (one 32-bit word) -> four bf16 (two words) holding
 // W * 2^-(127 - bias), by bit placement only:
@@ -52,39 +54,64 @@ __device__ __forceinline__ void fp8x4_to_bf16x4_scaled(uint32_t w, uint32_t &lo,
   hi = __builtin_bit_cast(uint32_t, q1) & KEEP;
 }
 
-template <int FMT, int kWaves, int kUnroll, int MB>
+template <int FMT, int kWaves, int MB, int NB>
 __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
   // The bit-placed weights are W * 2^-(127 - bias); the factor is split in
   // two halves: one folded into every group scale (safe for any scale below
   // 2^64), the other applied once to the final sum.
   constexpr float kHalf = (FMT == 2) ? 7.205759403792794e+16f   /* 2^56 */
                                      : 1.152921504606847e+18f;  /* 2^60 */
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * kCols;
-  const int col = lane & 15, g = lane >> 4;
+  constexpr int kRound = 2;          // slices per round: 256 bytes per W row
+  constexpr int kDepth = 2;          // rounds in flight
+  constexpr int kTile = 16 * 256;    // one wave's transpose tile
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kWaves * NB * kTile];
+  static_assert(MB * NB * 1024 <= NB * kTile, "reduction fits in the tiles");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 16 * NB;
+  const int r = lane & 15, g = lane >> 4;
   const int nslices = a.K / kSlice;  // host guarantees K % 128 == 0
   const int per_wave = (nslices + kWaves - 1) / kWaves;
   const int s_begin = min(nslices, wave * per_wave);
   const int s_end = min(nslices, s_begin + per_wave);
+  const int nrounds = (s_end - s_begin + kRound - 1) / kRound;
   const int slices_per_group = a.group / kSlice;  // host: group % 128 == 0
 
-  // The wave's NB blocks of 16 W rows (output columns).  Rows past N read
-  // row N-1 (always valid) and are never stored: no branch.
-  const uint8_t *wrow[kNB];
-  const float *srow[kNB];
+  // Load j (0..3) of a round of block b: W row 16b + 4j + lane / 16, bytes
+  // 16 (lane % 16) of that row's 256-byte segment.  Rows past N read the last
+  // row (valid memory) and are never stored.
+  const uint8_t *wp[NB][4];
+  int wpos[4];
+  uint8_t *tile = lds + wave * NB * kTile;
 #pragma unroll
-  for (int b = 0; b < kNB; ++b) {
-    const int n = n0 + 16 * b + col;
-    const int nn = n < a.N ? n : a.N - 1;
-    wrow[b] = a.W + int64_t(nn) * a.ldw + 16 * g;
-    srow[b] = a.scales + int64_t(nn) * a.ld_scales;
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * j + (lane >> 4);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int n = n0 + 16 * b + row;
+      wp[b][j] = a.W + int64_t(n < a.N ? n : a.N - 1) * a.ldw + 16 * (lane & 15);
+    }
+    wpos[j] = row * 256 + (((lane & 15) ^ (row & 15)) << 4);
   }
-  // Group scales of this wave's slices, loaded once (up to 8 groups; longer
-  // ranges fall back to a load per group).
-  const int g_first = s_begin / slices_per_group;
-  float scl[kNB][8];
+  int rpos[kRound][2];
 #pragma unroll
-  for (int b = 0; b < kNB; ++b)
+  for (int u = 0; u < kRound; ++u)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) rpos[u][e] = r * 256 + (((8 * u + 2 * g + e) ^ r) << 4);
+
+  // This lane's output columns (W rows 16b + r) and their group scales,
+  // loaded once (up to 8 groups; longer ranges fall back to a load per group).
+  const float *srow[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int nc = n0 + 16 * b + r;
+    srow[b] = a.scales + int64_t(nc < a.N ? nc : a.N - 1) * a.ld_scales;
+  }
+  const int g_first = s_begin / slices_per_group;
+  float scl[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int gi = g_first + j;
@@ -97,134 +124,160 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
     for (int t = 1; t < 8; ++t) v = (j == t) ? scl[b][t] : v;
     return v;
   };
-
   // x rows past M read row M-1: MFMA output rows are independent and rows
   // past M are never stored, so no masking is needed.
   const uint16_t *xrow[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    const int m = mb * 16 + col;
-    xrow[mb] = a.x + int64_t(m < a.M ? m : a.M - 1) * a.ldx + 16 * g;
+    const int m = mb * 16 + r;
+    xrow[mb] = a.x + int64_t(m < a.M ? m : a.M - 1) * a.ldx + 32 * g;
   }
 
-  txd::f32x4 acc[kNB][MB], part[kNB][MB];
+  struct Round {
+    txd::u32x4 w[NB][4];
+  };
+  auto fetch = [&](int q, Round &f) {
+    const int s = s_begin + q * kRound;
+    const int valid = min(kRound, s_end - s) * kSlice;
 #pragma unroll
-  for (int b = 0; b < kNB; ++b)
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        f.w[b][j] = 16 * (lane & 15) < valid
+                        ? __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(wp[b][j] + int64_t(s) * kSlice))
+                        : txd::u32x4{0u, 0u, 0u, 0u};
+  };
+
+  txd::f32x4 acc[NB][MB], part[NB][MB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[b][i] = part[b][i] = txd::f32x4{0.f, 0.f, 0.f, 0.f};
   bool fresh = true;  // the next MFMA chain starts from zero
 
-  // Lane group g holds bytes [16g, 16g+16) and [64+16g, 64+16g+16) of each
-  // 128-byte slice, so a load instruction covers contiguous 64-byte halves of
-  // the 16 rows' lines; MFMA i of a slice takes k = 64 (i/2) + 16g + 8 (i%2) + 0..7
-  // for both x and W.  Each x fragment feeds the MFMAs of all kNB W blocks.
-  auto slice = [&](int s, const txd::u32x4 (&w)[kNB][2]) {
-    uint32_t wb[kNB][16];
+  // Slice s: lane (r, g) holds 32 codes of W row r at k = 32g .. 32g + 31 of
+  // the slice; MFMA i takes k = 32g + 8i .. +7 of both W and x.
+  auto compute = [&](int q, const Round &f) {
+    const int s = s_begin + q * kRound;
+    const int ns = min(kRound, s_end - s);
 #pragma unroll
-    for (int b = 0; b < kNB; ++b) {
-      const uint32_t words[8] = {w[b][0].x, w[b][0].y, w[b][0].z, w[b][0].w,
-                                 w[b][1].x, w[b][1].y, w[b][1].z, w[b][1].w};
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) fp8x4_to_bf16x4_scaled<FMT>(words[q], wb[b][2 * q], wb[b][2 * q + 1]);
-    }
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<txd::u32x4 *>(tile + b * kTile + wpos[j]) = f.w[b][j];
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const uint16_t *xp = xrow[mb] + s * kSlice;
+    for (int u = 0; u < kRound; ++u) {
+      if (u < ns) {
+        const int su = s + u;
+        txd::u32x4 xv[MB][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const txd::u32x4 xv = *reinterpret_cast<const txd::u32x4 *>(xp + (i >> 1) * 64 + (i & 1) * 8);
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int b = 0; b < kNB; ++b) {
-          const txd::u32x4 wq = {wb[b][4 * i], wb[b][4 * i + 1], wb[b][4 * i + 2], wb[b][4 * i + 3]};
-          const txd::f32x4 c = (i == 0 && fresh) ? txd::f32x4{0.f, 0.f, 0.f, 0.f} : part[b][mb];
-          part[b][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(txd::bf16x8, xv), __builtin_bit_cast(txd::bf16x8, wq), c, 0, 0, 0);
+          for (int i = 0; i < 4; ++i)
+            xv[mb][i] = *reinterpret_cast<const txd::u32x4 *>(xrow[mb] + su * kSlice + 8 * i);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const txd::u32x4 c0 = *reinterpret_cast<const txd::u32x4 *>(tile + b * kTile + rpos[u][0]);
+          const txd::u32x4 c1 = *reinterpret_cast<const txd::u32x4 *>(tile + b * kTile + rpos[u][1]);
+          const uint32_t words[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+          uint32_t wb[16];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) fp8x4_to_bf16x4_scaled<FMT>(words[t], wb[2 * t], wb[2 * t + 1]);
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const txd::u32x4 wq = {wb[4 * i], wb[4 * i + 1], wb[4 * i + 2], wb[4 * i + 3]};
+              const txd::f32x4 c = (i == 0 && fresh) ? txd::f32x4{0.f, 0.f, 0.f, 0.f} : part[b][mb];
+              part[b][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(txd::bf16x8, xv[mb][i]), __builtin_bit_cast(txd::bf16x8, wq), c, 0, 0, 0);
+            }
+        }
+        fresh = false;
+        // close the group when its last slice is done (uniform)
+        if ((su + 1) % slices_per_group == 0 || su + 1 == nslices) {
+          const int grp = su / slices_per_group;
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const float sc = scale_of(b, grp) * kHalf;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
+          }
+          fresh = true;
         }
       }
     }
-    fresh = false;
-    // close the group when its last slice is done (uniform)
-    if ((s + 1) % slices_per_group == 0 || s + 1 == nslices) {
-      const int grp = s / slices_per_group;
-#pragma unroll
-      for (int b = 0; b < kNB; ++b) {
-        const float sc = scale_of(b, grp) * kHalf;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
-      }
-      fresh = true;
-    }
+    asm volatile("" ::: "memory");
   };
 
-  int s0 = s_begin;
-  for (; s0 + kUnroll <= s_end; s0 += kUnroll) {
-    txd::u32x4 wv[kUnroll][kNB][2];
+  Round buf[kDepth];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
+  for (int d = 0; d < kDepth; ++d)
+    if (d < nrounds) fetch(d, buf[d]);
+  for (int q0 = 0; q0 < nrounds; q0 += kDepth) {
 #pragma unroll
-      for (int b = 0; b < kNB; ++b) {
-        const txd::u32x4 *p = reinterpret_cast<const txd::u32x4 *>(wrow[b] + (s0 + u) * kSlice);
-        wv[u][b][0] = __builtin_nontemporal_load(p);
-        wv[u][b][1] = __builtin_nontemporal_load(p + 4);
+    for (int d = 0; d < kDepth; ++d) {
+      const int q = q0 + d;
+      if (q < nrounds) {
+        compute(q, buf[d]);
+        if (q + kDepth < nrounds) fetch(q + kDepth, buf[d]);
       }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) slice(s0 + u, wv[u]);
-  }
-  for (; s0 < s_end; ++s0) {
-    txd::u32x4 wv[kNB][2];
-#pragma unroll
-    for (int b = 0; b < kNB; ++b) {
-      const txd::u32x4 *p = reinterpret_cast<const txd::u32x4 *>(wrow[b] + s0 * kSlice);
-      wv[b][0] = __builtin_nontemporal_load(p);
-      wv[b][1] = __builtin_nontemporal_load(p + 4);
     }
-    slice(s0, wv);
   }
   // A group split across two waves leaves a partial in both; scale it here.
   if (!fresh) {
     const int grp = (s_end - 1) / slices_per_group;
 #pragma unroll
-    for (int b = 0; b < kNB; ++b) {
+    for (int b = 0; b < NB; ++b) {
       const float sc = scale_of(b, grp) * kHalf;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
     }
   }
 
-  // Cross-wave reduction in LDS, one (W block, 16-row block of M) at a time.
-  __shared__ txd::f32x4 red[kWaves][64];
+  // Cross-wave reduction in LDS (reusing the tiles), one W block at a time;
+  // MFMA result layout: lane holds D[m = 4 * (lane / 16) + i][n = lane % 16].
+  txd::f32x4 *red = reinterpret_cast<txd::f32x4 *>(lds);  // [kWaves][MB][64]
 #pragma unroll
-  for (int b = 0; b < kNB; ++b)
+  for (int b = 0; b < NB; ++b) {
+    __syncthreads();
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      red[wave][lane] = acc[b][mb];
-      __syncthreads();
-      if (wave == 0) {
-        txd::f32x4 t = red[0][lane];
+    for (int mb = 0; mb < MB; ++mb) red[(wave * MB + mb) * 64 + lane] = acc[b][mb];
+    __syncthreads();
+    if (wave < MB) {
+      const int mb = wave;
+      txd::f32x4 t = red[mb * 64 + lane];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) t += red[w][lane];
-        t *= kHalf;
-        // MFMA result layout: lane holds D[m = 4*(lane/16) + r][n = lane % 16]
-        const int n = n0 + 16 * b + col;
+      for (int w = 1; w < kWaves; ++w) t += red[(w * MB + mb) * 64 + lane];
+      t *= kHalf;
+      const int ncol = n0 + 16 * b + r;
+      if (ncol < a.N) {
         const float v[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = mb * 16 + 4 * g + r;
-          if (m < a.M && n < a.N) a.y[int64_t(m) * a.ldy + n] = uint16_t(txd::f32_to_bf16_bits(v[r]));
+        for (int i = 0; i < 4; ++i) {
+          const int m = mb * 16 + 4 * g + i;
+          if (m < a.M) a.y[int64_t(m) * a.ldy + ncol] = uint16_t(txd::f32_to_bf16_bits(v[i]));
         }
       }
-      __syncthreads();
     }
+  }
 }
 
 }  // namespace
 
-// Kernel names: tx_gemv_fp8_<w format>_w<waves>_m<16-row blocks of M>.
-#define TX_GEMV(NAME, FMT, W, U, MB)                                                      \
-  TX_KERNEL void __launch_bounds__(64 * W) tx_gemv_fp8_##NAME##_w##W##_m##MB(const tx_gemv_args a) { \
-    gemv_body<FMT, W, U, MB>(a);                                                          \
+// Kernel names: tx_gemv_fp8_<w format>_w<waves>_m<16-row blocks of M>_b<W
+// blocks per wave>.  Two W blocks per wave share each x fragment (for M above
+// a few rows the x reads from cache would otherwise outweigh the W stream);
+// the small-grid variants with 2 or 4 blocks of M have 8 wavefronts (16 would
+// not fit their registers in 128 VGPRs).
+#define TX_GEMV(NAME, FMT, W, MB, NB)                                                         \
+  TX_KERNEL void __launch_bounds__(64 * W) tx_gemv_fp8_##NAME##_w##W##_m##MB##_b##NB(         \
+      const tx_gemv_args a) {                                                                 \
+    gemv_body<FMT, W, MB, NB>(a);                                                             \
   }
-#define TX_GEMV_MB(NAME, FMT, W, U) \
-  TX_GEMV(NAME, FMT, W, U, 1) TX_GEMV(NAME, FMT, W, U, 2) TX_GEMV(NAME, FMT, W, U, 4)
-TX_GEMV_MB(e5m2, 2, 4, 4)
-TX_GEMV_MB(e4m3fn, 1, 4, 4)
+#define TX_GEMV_ALL(NAME, FMT)                                                                   \
+  TX_GEMV(NAME, FMT, 4, 1, 1) TX_GEMV(NAME, FMT, 4, 1, 2) TX_GEMV(NAME, FMT, 4, 2, 2)           \
+  TX_GEMV(NAME, FMT, 4, 4, 2) TX_GEMV(NAME, FMT, 16, 1, 1) TX_GEMV(NAME, FMT, 8, 2, 1)          \
+  TX_GEMV(NAME, FMT, 8, 4, 1)
+TX_GEMV_ALL(e5m2, 2)
+TX_GEMV_ALL(e4m3fn, 1)
