@@ -45,6 +45,13 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="headline ops only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="run only a 256 MiB device copy (known-size kernel for scaling the "
+                        "FETCH_SIZE / WRITE_SIZE counters)")
+    p.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV",
+                                                     "CAL_WRITE_CSV"),
+                   help="print the HBM traffic table from rocprofv3 counter_collection.csv files "
+                        "of a --quick run and of a --calibrate-copy run")
     return p.parse_args()
 
 
@@ -197,8 +204,83 @@ def cpu_baseline():
     }
 
 
+COPY_BYTES = 256 << 20
+TRAFFIC_TABLE = os.path.join(REPO, "profiles", "hbm_traffic_fp8_gemm_8192_fp8_convert_16Mi.md")
+
+
+def calibrate_copy():
+    """A device-to-device copy of COPY_BYTES, 5 launches (the known-size kernel)."""
+    import torch
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0").uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes": COPY_BYTES, "launches": 5}))
+
+
+def _pmc_per_kernel(path, counter):
+    """Average per-dispatch value of `counter` for each kernel in a rocprofv3
+    counter_collection.csv (values of one dispatch are summed first)."""
+    import csv
+    per_dispatch = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            key = (row["Dispatch_Id"], row["Kernel_Name"])
+            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
+    out = {}
+    for (_, name), v in per_dispatch.items():
+        out.setdefault(name, []).append(v)
+    return out
+
+
+def pmc_summary(fetch_csv, write_csv, cal_fetch_csv, cal_write_csv):
+    fetch = _pmc_per_kernel(fetch_csv, "FETCH_SIZE")
+    write = _pmc_per_kernel(write_csv, "WRITE_SIZE")
+    # the copy's dispatches are the ones that move the most data
+    cal_f = sorted(v for vs in _pmc_per_kernel(cal_fetch_csv, "FETCH_SIZE").values() for v in vs)[-5:]
+    cal_w = sorted(v for vs in _pmc_per_kernel(cal_write_csv, "WRITE_SIZE").values() for v in vs)[-5:]
+    kib = COPY_BYTES / 1024
+    f_scale = kib / (sum(cal_f) / len(cal_f))
+    w_scale = kib / (sum(cal_w) / len(cal_w))
+    print(f"copy calibration: {COPY_BYTES} B copied; FETCH_SIZE reads "
+          f"{sum(cal_f) / len(cal_f):.0f} KiB, WRITE_SIZE {sum(cal_w) / len(cal_w):.0f} KiB per "
+          f"launch; scale factors fetch {f_scale:.4f}, write {w_scale:.4f}")
+    print()
+    print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes per launch |")
+    print("|---|---|---|---|---|")
+    for name in sorted(set(fetch) | set(write)):
+        fv, wv = fetch.get(name, [0.0]), write.get(name, [0.0])
+        fk, wk = sum(fv) / len(fv), sum(wv) / len(wv)
+        traffic = (fk * f_scale + wk * w_scale) * 1024
+        print(f"| {name[:90]} | {len(fv)} | {fk:.0f} | {wk:.0f} | {traffic:.0f} |")
+
+
+def traffic_from_table(kernel_prefix):
+    """HBM bytes per launch of a kernel from the committed counter summary, or None."""
+    if not os.path.exists(TRAFFIC_TABLE):
+        return None
+    with open(TRAFFIC_TABLE) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) == 5 and cells[0].startswith(kernel_prefix):
+                try:
+                    return int(float(cells[4]))
+                except ValueError:
+                    return None
+    return None
+
+
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only: every op runs on one "
@@ -215,7 +297,9 @@ def main():
     if not args.quick:
         for (m, n, k) in [(16, 14336, 4096), (512, 14336, 4096), (8192, 14336, 4096),
                           (16, 4096, 14336), (512, 4096, 14336), (8192, 4096, 14336)]:
-            r = bench_fp8_gemm(tx, torch, m, n, k, K, W, sets=1)
+            # small M streams B from HBM: rotate buffer sets past the Infinity Cache
+            r = bench_fp8_gemm(tx, torch, m, n, k, K, W,
+                               sets=ring_count(m * k + n * k) if m <= 512 else 1)
             secondary.append({"op": "fp8 scaled GEMM", "shape": [m, n, k], "ms": r["ms"],
                               "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
@@ -255,12 +339,13 @@ def main():
                    "M": 8192, "N": 8192, "K": 8192},
         "roofline": {"bound": "mfma", "achieved": round(gemm["tflops"], 2),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm["tflops"] / FP8_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(gemm["tflops"] / FP8_PEAK_TFLOPS, 4),
+                     "traffic": traffic_from_table("tx_gemm_fp8_e4m3fn_e4m3fn_fast")},
         "fp8_convert": {"value": round(conv["gbs"], 1), "unit": "GB/s", "ms": round(conv["ms"], 5),
                         "roofline": {"bound": "hbm", "achieved": round(conv["gbs"], 1),
                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                      "frac": round(conv["gbs"] / HBM_PEAK_GBS, 4),
-                                     "traffic": None},
+                                     "traffic": traffic_from_table("tx_fp8_encode_e4m3fn_rtne_vec")},
                         "buffer_sets": conv["sets"]},
         "cpu_baseline": cpu,
         "secondary": secondary,
