@@ -70,6 +70,29 @@ def test_bf16_small_shapes(tx, oracle, dev, M, N, K):
     check_close(_np_bits(C), r32, r16, BF16_TOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(600, 1000, 256), (300, 500, 4096), (257, 501, 2048)])
+def test_bf16_narrow_tile_and_split_k(tx, oracle, dev, M, N, K):
+    """Fewer 256x256 tiles than CUs: 256x128 tiles, and K split into fp32
+    partial planes (8 and 4 splits here, N not a multiple of 4 in the last)."""
+    from tx import workloads
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=M + N)
+    C = tx.dot(_t_bf16(A, dev), _t_bf16(B, dev))
+    r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
+    check_close(_np_bits(C), r32, r16, BF16_TOL)
+
+
+def test_bf16_padded_fast_path(tx, oracle, dev):
+    """Rows not 16-byte aligned in a product of >= 2^30 multiply-adds: the
+    operands are copied into zero-padded rows and take the fast path."""
+    from tx import workloads
+    M, N, K = 1100, 1040, 1003
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=77)
+    C = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
+    for r in sample_rows(M, k=40):
+        r32, r16 = oracle.gemm_bf16_rows(A, B, r, r + 1)
+        check_close(C[r:r + 1], r32, r16, BF16_TOL)
+
+
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (4095, 4097, 4100)])
 def test_bf16_config_shapes(tx, oracle, dev, M, N, K):
     from tx import workloads
@@ -160,6 +183,50 @@ def test_fp8_format_mixes(tx, oracle, dev, fa, fb):
     C = _fp8_run(tx, dev, aq, sa, bq, sb, td[fa], td[fb])
     r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, M, fa, fb)
     check_close(C, r32, r16, FP8_TOL)
+
+
+@pytest.mark.parametrize("M,N,K,fa,fb", [(300, 500, 8192, 1, 1), (130, 777, 2048, 2, 1)])
+def test_fp8_narrow_tile_and_split_k(tx, oracle, dev, M, N, K, fa, fb):
+    """256x128 tiles with K split into fp32 partial planes; the scales are
+    applied by the reduction."""
+    from tx import workloads
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=M * 3 + N)
+    td = {1: torch.float8_e4m3fn, 2: torch.float8_e5m2}
+    if fa == 2:  # reinterpret the e4m3 codes as e5m2: finite, wider range
+        aq = np.where((aq & 0x7F) >= 0x7C, aq & 0x80, aq).astype(np.uint8)
+    C = _fp8_run(tx, dev, aq, sa, bq, sb, td[fa], td[fb])
+    r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, M, fa, fb)
+    check_close(C, r32, r16, FP8_TOL)
+
+
+def test_column_tail_strip(tx, oracle, dev):
+    """N just past a multiple of 256 where the last tile column would cost a
+    whole round: the full columns take the fast kernel, the tail the generic one."""
+    from tx import workloads
+    M, N, K = 4096, 4112, 1024
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=21)
+    C = _fp8_run(tx, dev, aq, sa, bq, sb)
+    for r in sample_rows(M, k=12):
+        r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r, r + 1)
+        check_close(C[r:r + 1], r32, r16, FP8_TOL)
+    M, N, K = 4096, 4100, 512
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=22)
+    Cb = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
+    for r in sample_rows(M, k=12):
+        r32, r16 = oracle.gemm_bf16_rows(A, B, r, r + 1)
+        check_close(Cb[r:r + 1], r32, r16, BF16_TOL)
+
+
+def test_fp8_padded_fast_path(tx, oracle, dev):
+    """Odd K (rows not 16-byte aligned) in a product of >= 2^30 multiply-adds:
+    zero-padded copies of the operands take the fast path."""
+    from tx import workloads
+    M, N, K = 1000, 1100, 1001
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=13)
+    C = _fp8_run(tx, dev, aq, sa, bq, sb)
+    for r in sample_rows(M, k=40):
+        r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r, r + 1)
+        check_close(C[r:r + 1], r32, r16, FP8_TOL)
 
 
 @pytest.mark.parametrize("M,N,K,fa,fb", [(1, 17, 128, 1, 1), (5, 33, 256, 2, 2), (16, 16, 1024, 1, 2),

@@ -54,14 +54,14 @@ bool use_big_tile(int64_t M, int64_t N) {
   return big >= cu_count();
 }
 
-tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int tile,
-                      hipStream_t s, unsigned threads = 256) {
-  args.tiles_m = int32_t((args.M + tile - 1) / tile);
-  args.tiles_n = int32_t((args.N + tile - 1) / tile);
+tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int tile_m, int tile_n,
+                      hipStream_t s, unsigned threads = 256, int splits = 1) {
+  args.tiles_m = int32_t((args.M + tile_m - 1) / tile_m);
+  args.tiles_n = int32_t((args.N + tile_n - 1) / tile_n);
   args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
   hipFunction_t fn;
   TX_TRY(get_kernel(co, kname, &fn));
-  const int64_t grid = int64_t(args.tiles_m) * args.tiles_n;
+  const int64_t grid = int64_t(args.tiles_m) * args.tiles_n * splits;
   if (grid > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: too many tiles", kname);
   return launch(fn, unsigned(grid), 1, threads, s, &args, sizeof args, kname);
 }
@@ -70,6 +70,9 @@ tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int 
 constexpr int kFastWaves = 8;
 // Largest M served by the skinny fp8 kernel (4 blocks of 16 rows).
 constexpr int64_t kSkinnyMaxM = 64;
+// Split K only while every split keeps at least this many 128-byte K steps.
+constexpr int64_t kMinStepsPerSplit = 8;
+constexpr int64_t kMaxSplits = 8;
 
 // The LDS-DMA fast path needs 16-byte aligned rows and a row length that is a
 // multiple of 16 bytes, and operands small enough that a 32-bit buffer offset
@@ -79,6 +82,123 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
   if (!aligned(A, 16) || !aligned(B, 16) || lda_b % 16 || ldb_b % 16 || k_b % 16) return false;
   const int64_t lim = int64_t(1) << 31;
   return (M - 1) * lda_b + k_b < lim && (N - 1) * ldb_b + k_b < lim;
+}
+
+// Launch the fast path (kernel `base`, or `base`_n128): 256x256 tiles while
+// they give at least one tile per CU (see kStripMaxN for a narrow column
+// tail); otherwise 256x128 tiles, and when those
+// still leave CUs idle, K is split (at most 8 ways, at least 8 K steps per
+// split) into fp32 partial planes in a stream-ordered workspace that the
+// `reduce` kernel sums, scales and rounds into C.
+// A narrow tail of columns past the last full 256-column block (at most
+// kStripMaxN) that would cost a whole extra round of 256x256 tiles is left
+// to the generic kernel `strip` (128x128 tiles) instead.
+constexpr int64_t kStripMaxN = 64;
+
+tx_status launch_fast(const char *base, const char *reduce, const char *strip, CodeObject co,
+                      tx_gemm_args &args, int64_t k_bytes, int es, hipStream_t s) {
+  const int64_t cus = cu_count();
+  const int64_t tiles_m = (args.M + 255) / 256;
+  char kname[96];
+  if (tiles_m * ((args.N + 255) / 256) >= cus) {
+    std::snprintf(kname, sizeof kname, "%s", base);
+    const int64_t full = args.N / 256, tail = args.N % 256;
+    const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
+    const int64_t rounds_main = (tiles_m * full + cus - 1) / cus;
+    if (tail > 0 && tail <= kStripMaxN && rounds_main < rounds_all) {
+      tx_gemm_args strip_args = args;
+      const int64_t n0 = full * 256;
+      strip_args.B = static_cast<const uint8_t *>(args.B) + n0 * args.ldb * es;
+      strip_args.C = static_cast<uint16_t *>(args.C) + n0;
+      if (args.scale_b) strip_args.scale_b = args.scale_b + n0;
+      strip_args.N = int32_t(tail);
+      args.N = int32_t(n0);
+      TX_TRY(launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves));
+      return launch_gemm(strip, co, strip_args, 128, 128, s);
+    }
+    return launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves);
+  }
+  std::snprintf(kname, sizeof kname, "%s_n128", base);
+  const int64_t tiles = tiles_m * ((args.N + 127) / 128);
+  const int64_t ksteps = (k_bytes + 127) / 128;
+  int64_t splits = std::min({kMaxSplits, cus / tiles, ksteps / kMinStepsPerSplit});
+  void *part = nullptr;
+  if (splits >= 2) {
+    const int64_t per = (ksteps + splits - 1) / splits;
+    splits = (ksteps + per - 1) / per;  // no empty split
+    const size_t bytes = size_t(splits) * size_t(args.M) * size_t(args.N) * sizeof(float);
+    if (hipMallocAsync(&part, bytes, s) != hipSuccess) {
+      (void)hipGetLastError();  // no workspace: run unsplit
+      part = nullptr;
+    } else {
+      args.splits = int32_t(splits);
+      args.ksteps_split = int32_t(per);
+      args.part = static_cast<float *>(part);
+    }
+  }
+  if (!part) return launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves);
+  tx_status st = launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves, int(args.splits));
+  if (st == TX_SUCCESS) {
+    hipFunction_t fn;
+    st = get_kernel(co, reduce, &fn);
+    if (st == TX_SUCCESS) {
+      const int64_t quads = args.M * ((args.N + 3) / 4);
+      const int64_t grid = std::min<int64_t>((quads + 255) / 256, cus * 16);
+      st = launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, reduce);
+    }
+  }
+  if (hipFreeAsync(part, s) != hipSuccess && st == TX_SUCCESS)
+    st = fail(TX_LAUNCH_ERROR, "%s: releasing the split-K workspace failed", base);
+  return st;
+}
+
+// Operands the fast path cannot take (rows not 16-byte aligned or K * size
+// not a multiple of 16 bytes) in a product of at least kPadMinWork
+// multiply-adds are first copied into zero-padded rows of a stream-ordered
+// workspace (K rounded up to 16 bytes; the zeros add nothing to the sums).
+// Returns TX_UNSUPPORTED without launching anything when that is not
+// possible, and the caller takes the generic kernel.
+constexpr int64_t kPadMinWork = int64_t(1) << 30;
+
+tx_status launch_padded(const char *base, const char *reduce, const char *pad, const char *strip,
+                        CodeObject co, tx_gemm_args &args, int es, hipStream_t s) {
+  const int64_t per = 16 / es;
+  const int64_t kp = (int64_t(args.K) + per - 1) / per * per;
+  if (int64_t(args.M) * args.N * args.K < kPadMinWork ||
+      (int64_t(std::max(args.M, args.N)) * kp) * es >= (int64_t(1) << 31))
+    return TX_UNSUPPORTED;
+  const size_t a_bytes = size_t(args.M) * size_t(kp) * es;
+  const size_t b_bytes = size_t(args.N) * size_t(kp) * es;
+  void *ws = nullptr;
+  if (hipMallocAsync(&ws, a_bytes + b_bytes, s) != hipSuccess) {
+    (void)hipGetLastError();
+    return TX_UNSUPPORTED;
+  }
+  hipFunction_t fn;
+  tx_status st = get_kernel(co, pad, &fn);
+  const int64_t cus = cu_count();
+  uint8_t *wa = static_cast<uint8_t *>(ws), *wb = wa + a_bytes;
+  if (st == TX_SUCCESS) {
+    tx_pad_args pa{args.A, wa, args.lda, kp, args.M, args.K, int32_t(kp), 0};
+    const int64_t ga = std::min<int64_t>((int64_t(args.M) * kp / per + 255) / 256, cus * 16);
+    st = launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, pad);
+  }
+  if (st == TX_SUCCESS) {
+    tx_pad_args pb{args.B, wb, args.ldb, kp, args.N, args.K, int32_t(kp), 0};
+    const int64_t gb = std::min<int64_t>((int64_t(args.N) * kp / per + 255) / 256, cus * 16);
+    st = launch(fn, unsigned(gb), 1, 256, s, &pb, sizeof pb, pad);
+  }
+  if (st == TX_SUCCESS) {
+    args.A = wa;
+    args.lda = kp;
+    args.B = wb;
+    args.ldb = kp;
+    args.K = int32_t(kp);
+    st = launch_fast(base, reduce, strip, co, args, kp * es, es, s);
+  }
+  if (hipFreeAsync(ws, s) != hipSuccess && st == TX_SUCCESS)
+    st = fail(TX_LAUNCH_ERROR, "%s: releasing the padded operands failed", base);
+  return st;
 }
 
 const char *fp8_name(tx_dtype t) {
@@ -91,21 +211,26 @@ static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb
                           int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
   TX_TRY(check_gemm("tx_dot_bf16", A, lda, B, ldb, C, ldc, M, N, K));
   if (M == 0 || N == 0) return TX_SUCCESS;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
+                    int32_t(K), 0, 0, 0};
+  if (fast_ok(A, lda * 2, B, ldb * 2, K * 2, M, N))
+    return launch_fast("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce",
+                       "tx_gemm_bf16_128x128_v16", CodeObject::GemmBf16, args, K * 2, 2, s);
+  {
+    tx_gemm_args padded = args;
+    const tx_status st = launch_padded("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce",
+                                       "tx_gemm_bf16_pad_rows", "tx_gemm_bf16_128x128_v16",
+                                       CodeObject::GemmBf16, padded, 2, s);
+    if (st != TX_UNSUPPORTED) return st;
+    clear_error();
+  }
   static const int widths[] = {16, 8, 2};
   const int vec = pick_vec(A, lda * 2, B, ldb * 2, K * 2, widths, 3);
   const int tile = use_big_tile(M, N) ? 256 : 128;
   char kname[64];
-  unsigned threads = 256;
-  if (tile == 256 && fast_ok(A, lda * 2, B, ldb * 2, K * 2, M, N)) {
-    threads = 64 * kFastWaves;
-    std::snprintf(kname, sizeof kname, "tx_gemm_bf16_fast");
-  } else {
-    std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
-  }
-  tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
-                    int32_t(K), 0, 0, 0};
-  return launch_gemm(kname, CodeObject::GemmBf16, args, tile, static_cast<hipStream_t>(stream),
-                     threads);
+  std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
+  return launch_gemm(kname, CodeObject::GemmBf16, args, tile, tile, s);
 }
 
 static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
@@ -138,19 +263,26 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
     return launch(fn, unsigned(grid), 1, unsigned(64 * waves), static_cast<hipStream_t>(stream),
                   &args, sizeof args, kname);
   }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast", fa, fb);
+  char strip[80];
+  std::snprintf(strip, sizeof strip, "tx_gemm_fp8_%s_%s_128x128_v16", fa, fb);
+  if (fast_ok(A, lda, B, ldb, K, M, N))
+    return launch_fast(kname, "tx_gemm_fp8_splitk_reduce", strip, CodeObject::GemmFp8, args, K, 1,
+                       s);
+  {
+    tx_gemm_args padded = args;
+    const tx_status st = launch_padded(kname, "tx_gemm_fp8_splitk_reduce", "tx_gemm_fp8_pad_rows",
+                                       strip, CodeObject::GemmFp8, padded, 1, s);
+    if (st != TX_UNSUPPORTED) return st;
+    clear_error();
+  }
   static const int widths[] = {16, 4, 1};
   const int vec = pick_vec(A, lda, B, ldb, K, widths, 3);
   const int tile = (vec != 1 && use_big_tile(M, N)) ? 256 : 128;
-  unsigned threads = 256;
-  if (tile == 256 && fast_ok(A, lda, B, ldb, K, M, N)) {
-    threads = 64 * kFastWaves;
-    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast", fa, fb);
-  } else {
-    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
-  }
-  tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
-  return launch_gemm(kname, CodeObject::GemmFp8, args, tile, static_cast<hipStream_t>(stream),
-                     threads);
+  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
+  return launch_gemm(kname, CodeObject::GemmFp8, args, tile, tile, s);
 }
 
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,

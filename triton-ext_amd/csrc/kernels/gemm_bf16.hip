@@ -23,5 +23,13 @@ TX_GEMM_BF16(128x128, 128, 128, 2, 2, 2)
 #include "gemm_fast.h"
 
 TX_KERNEL void __launch_bounds__(512) tx_gemm_bf16_fast(const tx_gemm_args a) {
-  gemm_fast_tile<GemmCfg<EL_BF16, EL_BF16, 256, 256, 2, 2, 16>>(a);
+  gemm_fast_tile<GemmCfg<EL_BF16, EL_BF16, 256, 256, 2, 2, 16>, 256>(a);
 }
+TX_KERNEL void __launch_bounds__(512) tx_gemm_bf16_fast_n128(const tx_gemm_args a) {
+  gemm_fast_tile<GemmCfg<EL_BF16, EL_BF16, 256, 128, 2, 2, 16>, 128>(a);
+}
+TX_KERNEL void __launch_bounds__(256) tx_gemm_bf16_splitk_reduce(const tx_gemm_args a) {
+  splitk_reduce<false>(a);
+}
+
+TX_KERNEL void __launch_bounds__(256) tx_gemm_bf16_pad_rows(const tx_pad_args a) { pad_rows<2>(a); }

@@ -27,6 +27,8 @@
 // two 16-byte chunks 2g and 2g+1 of the 128-byte slice.
 #pragma once
 
+#include <type_traits>
+
 #include "tx_device.h"
 
 namespace txg {
@@ -108,6 +110,32 @@ __device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, in
   const int r = pid % in_group;
   *tm = first_m + r % gsz;
   *tn = r / gsz;
+}
+
+// Copy rows into a zero-padded buffer (see tx_pad_args): one 16-byte chunk of
+// a destination row per thread, source read element by element (the source
+// rows are what the fast path could not take: not 16-byte aligned).
+template <int ES>
+__device__ __forceinline__ void pad_rows(const tx_pad_args &a) {
+  constexpr int PER = 16 / ES;  // elements per 16-byte chunk
+  const int64_t chunks_per_row = a.dst_cols / PER;
+  const int64_t total = int64_t(a.rows) * chunks_per_row;
+  using E = typename std::conditional<ES == 2, uint16_t, uint8_t>::type;
+  const E *src = reinterpret_cast<const E *>(a.src);
+  for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = t / chunks_per_row;
+    const int c0 = int(t % chunks_per_row) * PER;
+    const E *s = src + r * a.src_ld;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint32_t v = (c0 + i < a.cols) ? uint32_t(s[c0 + i]) : 0u;
+      w[(i * ES) / 4] |= v << (8 * ((i * ES) % 4));
+    }
+    *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(a.dst) + (r * a.dst_ld + c0) * ES) =
+        u32x4{w[0], w[1], w[2], w[3]};
+  }
 }
 
 }  // namespace txg

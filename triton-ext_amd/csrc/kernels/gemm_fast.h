@@ -111,64 +111,80 @@ __device__ __forceinline__ void wait_and_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <class C>
+template <class C, int BN>
 __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using namespace fast;
+  static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   constexpr int WN = kWaves / 2;     // waves along N (2 along M)
-  constexpr int TN = 256 / WN;       // wave tile: 128 x TN
+  constexpr int TN = BN / WN;        // wave tile: 128 x TN
   constexpr int FN = TN / 32;        // 32-column blocks per wave
   constexpr int NM = 4 * FN;         // mfma32 calls per K half
   constexpr int NF = 4 + FN;         // fragments per K half: A 0..3, B 4..
   constexpr int NR = 2 * NF;         // ds_read_b128 per K half
-  constexpr int BLK = 32 / kWaves;   // 1 KiB blocks per operand per wave per step
-  constexpr int ND = 2 * BLK;        // loads per wave per step
-  static_assert(BLK % 2 == 0, "a wave's first block must have an even index");
+  constexpr int BLKA = 32 / kWaves;  // 1 KiB blocks of A per wave per step
+  constexpr int BLKB = BN / 8 / kWaves;  // ... of B
+  constexpr int ND = BLKA + BLKB;    // loads per wave per step
+  static_assert(BLKA % 2 == 0 && BLKB % 2 == 0, "a wave's first block must have an even index");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
+  // Split K: workgroup b computes split b % splits of tile b / splits.
+  const int splits = a.splits > 1 ? a.splits : 1;
+  const int split = int(blockIdx.x) % splits;
   int tm, tn;
-  tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
-  const int m0 = tm * 256, n0 = tn * 256;
+  tile_coords(int(blockIdx.x) / splits, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
+  const int m0 = tm * 256, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS addresses scalar
   const int wm = wave & 1, wn = wave >> 1;
   constexpr int ES = C::FP8 ? 1 : 2;
   const uint32_t kb_end = uint32_t(a.K) * ES;
-  const int ksteps = int((kb_end + kStep - 1) / kStep);
+  const int ksteps_all = int((kb_end + kStep - 1) / kStep);
+  const int kfirst = splits > 1 ? split * a.ksteps_split : 0;  // first K step of this split
+  const int ksteps = splits > 1 ? min(a.ksteps_split, ksteps_all - kfirst) : ksteps_all;
+  const uint32_t kbase = uint32_t(kfirst) * kStep;
   const uint32_t lda_b = uint32_t(a.lda) * ES, ldb_b = uint32_t(a.ldb) * ES;
   const __amdgpu_buffer_rsrc_t rsrc[2] = {make_rsrc(a.A, uint32_t(a.M - 1) * lda_b + kb_end),
                                           make_rsrc(a.B, uint32_t(a.N - 1) * ldb_b + kb_end)};
 
-  // DMA assignment: wave w fills blocks BLK*w .. BLK*w+BLK-1 of A and of B.
+  // DMA assignment: wave w fills blocks BLKA*w .. of A and BLKB*w .. of B.
   // Lane i of block q covers row 8q + i/8 and logical chunk
   // (i % 8) ^ ((row >> 1) & 7) = (i % 8) ^ ((4q + i/16) & 7), which depends on
-  // the parity of q only (BLK*w is even, so it is the parity of j).
+  // the parity of q only (a wave's first block index is even, so it is the
+  // parity of j).
   const uint32_t kch[2] = {16u * uint32_t((lane & 7) ^ ((lane >> 4) & 7)),
                            16u * uint32_t((lane & 7) ^ ((4 + (lane >> 4)) & 7))};
-  uint32_t vo[2][BLK];
+  uint32_t vo[2][BLKA];
 #pragma unroll
-  for (int j = 0; j < BLK; ++j) {
-    const int row = 8 * (BLK * wave + j) + (lane >> 3);
-    const int gm = m0 + row, gn = n0 + row;
+  for (int j = 0; j < BLKA; ++j) {
+    const int row = 8 * (BLKA * wave + j) + (lane >> 3);
+    const int gm = m0 + row;
     vo[0][j] = gm < a.M ? uint32_t(gm) * lda_b + kch[j & 1] : kOob;
+  }
+#pragma unroll
+  for (int j = 0; j < BLKB; ++j) {
+    const int row = 8 * (BLKB * wave + j) + (lane >> 3);
+    const int gn = n0 + row;
     vo[1][j] = gn < a.N ? uint32_t(gn) * ldb_b + kch[j & 1] : kOob;
   }
-  // Load block j of operand op of step ks into slot `slot`.
+  // Load block j of operand op of (split-local) step ks into slot `slot`.
+  // Steps past the split's end are loaded but never multiplied.
   auto load_op = [&](int ks, int slot, auto op_tag, auto j_tag) {
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
-    const uint32_t so = uint32_t(ks) * kStep;
+    constexpr int blk = op == 0 ? BLKA : BLKB;
+    const uint32_t so = kbase + uint32_t(ks) * kStep;
     const bool past = so + kch[j & 1] >= kb_end;  // K tail: this lane's chunk is past the row end
-    uint8_t *dst = lds + slot * kSlotBytes + (BLK * wave + j) * 1024;
+    uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[op], (lds_void *)dst, 16, past ? kOob : vo[op][j],
                                              so, 0, 0);
   };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
   // Load d of the second half of step ks: B of step ks+2 into the slot of A
-  // of step ks (d < BLK), then A of step ks+3 into the slot of B of step ks.
+  // of step ks (d < BLKB), then A of step ks+3 into the slot of B of step ks.
   auto load = [&](int ks, int slot_a, int slot_b, auto d_tag) {
     constexpr int d = decltype(d_tag)::value;
-    if constexpr (d < BLK) load_op(ks + 2, slot_a, OpB{}, std::integral_constant<int, d>{});
-    else load_op(ks + 3, slot_b, OpA{}, std::integral_constant<int, d - BLK>{});
+    if constexpr (d < BLKB) load_op(ks + 2, slot_a, OpB{}, std::integral_constant<int, d>{});
+    else load_op(ks + 3, slot_b, OpA{}, std::integral_constant<int, d - BLKB>{});
   };
 
   // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
@@ -215,12 +231,12 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 
   // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
   // step 0 landed, half 0 of step 0 in registers.
-  static_for<BLK>([&](auto j) { load_op(0, 0, OpA{}, j); });
-  static_for<BLK>([&](auto j) { load_op(0, 1, OpB{}, j); });
-  static_for<BLK>([&](auto j) { load_op(1, 2, OpA{}, j); });
-  static_for<BLK>([&](auto j) { load_op(1, 3, OpB{}, j); });
-  static_for<BLK>([&](auto j) { load_op(2, 4, OpA{}, j); });
-  wait_and_barrier<3 * BLK>();
+  static_for<BLKA>([&](auto j) { load_op(0, 0, OpA{}, j); });
+  static_for<BLKB>([&](auto j) { load_op(0, 1, OpB{}, j); });
+  static_for<BLKA>([&](auto j) { load_op(1, 2, OpA{}, j); });
+  static_for<BLKB>([&](auto j) { load_op(1, 3, OpB{}, j); });
+  static_for<BLKA>([&](auto j) { load_op(2, 4, OpA{}, j); });
+  wait_and_barrier<2 * BLKA + BLKB>();
   static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
 
   int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
@@ -236,9 +252,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    // A and B of step ks+1 landed for every wave (the BLK loads of A of step
+    // A and B of step ks+1 landed for every wave (the BLKA loads of A of step
     // ks+2, issued last, may still be in flight); the slots of step ks are free.
-    wait_and_barrier<BLK>();
+    wait_and_barrier<BLKA>();
     __builtin_amdgcn_sched_barrier(0);
     static_for<NM>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -262,6 +278,33 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 
   // Epilogue: lane owns, per (fm, fn, jj), C[m][n .. n+3] with
   // m = m0 + wm*128 + fm*32 + l%32, n = n0 + wn*TN + fn*32 + 8*jj + 4*(l/32).
+  // With K split, the unscaled fp32 sums go to the split's partial plane
+  // (row-major M x N); a reduction kernel combines the planes.
+  if (splits > 1) {
+    float *P = a.part + int64_t(split) * a.M * a.N;
+    const bool pvec = (a.N & 3) == 0;
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm) {
+      const int m = m0 + wm * 128 + fm * 32 + frow;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int n = n0 + wn * TN + fn * 32 + 8 * jj + 4 * fg;
+          float *dst = P + int64_t(m) * a.N + n;
+          if (pvec && n + 3 < a.N) {
+            *reinterpret_cast<txd::f32x4 *>(dst) =
+                txd::f32x4{acc[fn][fm][4 * jj], acc[fn][fm][4 * jj + 1], acc[fn][fm][4 * jj + 2], acc[fn][fm][4 * jj + 3]};
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (n + t < a.N) dst[t] = acc[fn][fm][4 * jj + t];
+          }
+        }
+    }
+    return;
+  }
   uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
   const bool cvec = ((reinterpret_cast<uintptr_t>(a.C) & 7) == 0) && ((a.ldc & 3) == 0);
 #pragma unroll
@@ -292,6 +335,43 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
             if (n + t < a.N) dst[t] = uint16_t(txd::f32_to_bf16_bits(v[t]));
         }
       }
+  }
+}
+
+// Split-K reduction: C[m, n] = bf16_rne(scale_a[m] * scale_b[n] * sum_s P[s][m][n])
+// (scales for fp8 only), four consecutive n per thread.
+template <bool FP8>
+__device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
+  const int64_t quads_per_row = (a.N + 3) / 4;
+  const int64_t total = int64_t(a.M) * quads_per_row;
+  const int64_t plane = int64_t(a.M) * a.N;
+  uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
+  for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int m = int(t / quads_per_row);
+    const int n = int(t % quads_per_row) * 4;
+    const float *p = a.part + int64_t(m) * a.N + n;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if ((a.N & 3) == 0) {
+      for (int s = 0; s < a.splits; ++s) {
+        const txd::f32x4 x = *reinterpret_cast<const txd::f32x4 *>(p + s * plane);
+        v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
+      }
+    } else {
+      for (int s = 0; s < a.splits; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n + i < a.N) v[i] += p[s * plane + i];
+    }
+    float sa = 1.0f;
+    if constexpr (FP8) sa = a.scale_a[m];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (n + i >= a.N) break;
+      float r = v[i];
+      if constexpr (FP8) r = r * sa * a.scale_b[n + i];
+      Cb[int64_t(m) * a.ldc + n + i] = uint16_t(txd::f32_to_bf16_bits(r));
+    }
   }
 }
 

@@ -27,10 +27,17 @@ TX_GEMM_FP8_FORMATS(128x128, 128, 128, 2, 2, 1)
 
 #include "gemm_fast.h"
 
-#define TX_GEMM_FP8_FAST(FA, FB, ELA, ELB)                                                 \
-  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast(const tx_gemm_args a) { \
-    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>>(a);                                  \
+#define TX_GEMM_FP8_FAST(FA, FB, ELA, ELB)                                                      \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast(const tx_gemm_args a) {      \
+    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256>(a);                                  \
+  }                                                                                                 \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast_n128(const tx_gemm_args a) { \
+    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128>(a);                                  \
   }
+
+TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_splitk_reduce(const tx_gemm_args a) {
+  splitk_reduce<true>(a);
+}
 
 TX_GEMM_FP8_FAST(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
 TX_GEMM_FP8_FAST(e5m2, e5m2, EL_E5M2, EL_E5M2)
@@ -56,3 +63,5 @@ TX_GEMM_FP8_SKINNY_ALL(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
 TX_GEMM_FP8_SKINNY_ALL(e5m2, e5m2, EL_E5M2, EL_E5M2)
 TX_GEMM_FP8_SKINNY_ALL(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
 TX_GEMM_FP8_SKINNY_ALL(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
+
+TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_pad_rows(const tx_pad_args a) { pad_rows<1>(a); }

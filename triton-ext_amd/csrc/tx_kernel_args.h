@@ -49,7 +49,24 @@ typedef struct tx_gemm_args {
   int32_t tiles_m;   /* ceil(M / tile) */
   int32_t tiles_n;   /* ceil(N / tile) */
   int32_t group_m;   /* rasterisation group height in tiles */
+  int32_t splits;    /* fast path: K splits (<= 1: none) */
+  int32_t ksteps_split; /* fast path: 128-byte K steps per split */
+  float *part;       /* fast path with splits > 1: splits x M x N fp32 partial sums */
 } tx_gemm_args;
+
+/* Row copy into a zero-padded buffer: dst[r][c] = c < cols ? src[r][c] : 0
+ * for c < dst_cols (elements of elem_bytes bytes; dst rows 16-byte aligned,
+ * dst_cols a multiple of 16 / elem_bytes). */
+typedef struct tx_pad_args {
+  const void *src;
+  void *dst;
+  int64_t src_ld;    /* elements */
+  int64_t dst_ld;    /* elements */
+  int32_t rows;
+  int32_t cols;
+  int32_t dst_cols;
+  int32_t reserved;
+} tx_pad_args;
 
 /* fp8 dequant GEMV */
 typedef struct tx_gemv_args {
