@@ -81,11 +81,13 @@ def test_bf16_narrow_tile_and_split_k(tx, oracle, dev, M, N, K):
     check_close(_np_bits(C), r32, r16, BF16_TOL)
 
 
-def test_bf16_padded_fast_path(tx, oracle, dev):
+@pytest.mark.parametrize("K", [1003, 1002, 1004])
+def test_bf16_padded_fast_path(tx, oracle, dev, K):
     """Rows not 16-byte aligned in a product of >= 2^30 multiply-adds: the
-    operands are copied into zero-padded rows and take the fast path."""
+    operands are copied into zero-padded rows and take the fast path (row
+    lengths of 2006, 2004 and 2008 bytes: source loads of 2, 4 and 8 bytes)."""
     from tx import workloads
-    M, N, K = 1100, 1040, 1003
+    M, N = 1100, 1040
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=77)
     C = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
     for r in sample_rows(M, k=40):
@@ -201,7 +203,8 @@ def test_fp8_narrow_tile_and_split_k(tx, oracle, dev, M, N, K, fa, fb):
 
 def test_column_tail_strip(tx, oracle, dev):
     """N just past a multiple of 256 where the last tile column would cost a
-    whole round: the full columns take the fast kernel, the tail the generic one."""
+    whole round: the full columns take 256x256 tiles, the tail a second,
+    split-K product."""
     from tx import workloads
     M, N, K = 4096, 4112, 1024
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=21)
@@ -215,6 +218,27 @@ def test_column_tail_strip(tx, oracle, dev):
     for r in sample_rows(M, k=12):
         r32, r16 = oracle.gemm_bf16_rows(A, B, r, r + 1)
         check_close(Cb[r:r + 1], r32, r16, BF16_TOL)
+
+
+def test_tall_narrow_fast_path(tx, oracle, dev):
+    """N below one 256-column block with enough row tiles to fill every CU:
+    no column strip is split off (it would leave nothing for the main tiles)."""
+    from tx import workloads
+    # rows are few columns wide: check the sampled rows as one set
+    M, N, K = 65536 + 40, 40, 256
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=23)
+    Cb = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
+    rows = sample_rows(M, k=32)
+    refs = [oracle.gemm_bf16_rows(A, B, r, r + 1) for r in rows]
+    check_close(Cb[rows], np.concatenate([x[0] for x in refs]), np.concatenate([x[1] for x in refs]),
+                BF16_TOL)
+    M, N, K = 65536 + 8, 16, 128
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=24)
+    C = _fp8_run(tx, dev, aq, sa, bq, sb)
+    rows = sample_rows(M, k=32)
+    refs = [oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r, r + 1) for r in rows]
+    check_close(C[rows], np.concatenate([x[0] for x in refs]), np.concatenate([x[1] for x in refs]),
+                FP8_TOL)
 
 
 def test_fp8_padded_fast_path(tx, oracle, dev):

@@ -91,12 +91,12 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 // split) into fp32 partial planes in a stream-ordered workspace that the
 // `reduce` kernel sums, scales and rounds into C.
 // A narrow tail of columns past the last full 256-column block (at most
-// kStripMaxN) that would cost a whole extra round of 256x256 tiles is left
-// to the generic kernel `strip` (128x128 tiles) instead.
+// kStripMaxN) that would cost a whole extra round of 256x256 tiles is a
+// separate, second fast-path product (few tiles, so 256x128 with K split).
 constexpr int64_t kStripMaxN = 64;
 
-tx_status launch_fast(const char *base, const char *reduce, const char *strip, CodeObject co,
-                      tx_gemm_args &args, int64_t k_bytes, int es, hipStream_t s) {
+tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_gemm_args &args,
+                      int64_t k_bytes, int es, hipStream_t s) {
   const int64_t cus = cu_count();
   const int64_t tiles_m = (args.M + 255) / 256;
   char kname[96];
@@ -105,7 +105,7 @@ tx_status launch_fast(const char *base, const char *reduce, const char *strip, C
     const int64_t full = args.N / 256, tail = args.N % 256;
     const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
     const int64_t rounds_main = (tiles_m * full + cus - 1) / cus;
-    if (tail > 0 && tail <= kStripMaxN && rounds_main < rounds_all) {
+    if (full > 0 && tail > 0 && tail <= kStripMaxN && rounds_main < rounds_all) {
       tx_gemm_args strip_args = args;
       const int64_t n0 = full * 256;
       strip_args.B = static_cast<const uint8_t *>(args.B) + n0 * args.ldb * es;
@@ -114,7 +114,7 @@ tx_status launch_fast(const char *base, const char *reduce, const char *strip, C
       strip_args.N = int32_t(tail);
       args.N = int32_t(n0);
       TX_TRY(launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves));
-      return launch_gemm(strip, co, strip_args, 128, 128, s);
+      return launch_fast(base, reduce, co, strip_args, k_bytes, es, s);
     }
     return launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves);
   }
@@ -160,8 +160,16 @@ tx_status launch_fast(const char *base, const char *reduce, const char *strip, C
 // possible, and the caller takes the generic kernel.
 constexpr int64_t kPadMinWork = int64_t(1) << 30;
 
-tx_status launch_padded(const char *base, const char *reduce, const char *pad, const char *strip,
-                        CodeObject co, tx_gemm_args &args, int es, hipStream_t s) {
+// Widest source load (8, 4, 2 or 1 bytes) that divides the base address,
+// the row pitch and the row length of a padded copy's source.
+int pad_load_bytes(const void *src, int64_t ld_bytes, int64_t row_bytes) {
+  for (int w = 8; w > 1; w /= 2)
+    if (aligned(src, w) && ld_bytes % w == 0 && row_bytes % w == 0) return w;
+  return 1;
+}
+
+tx_status launch_padded(const char *base, const char *reduce, const char *pad, CodeObject co,
+                        tx_gemm_args &args, int es, hipStream_t s) {
   const int64_t per = 16 / es;
   const int64_t kp = (int64_t(args.K) + per - 1) / per * per;
   if (int64_t(args.M) * args.N * args.K < kPadMinWork ||
@@ -179,12 +187,14 @@ tx_status launch_padded(const char *base, const char *reduce, const char *pad, c
   const int64_t cus = cu_count();
   uint8_t *wa = static_cast<uint8_t *>(ws), *wb = wa + a_bytes;
   if (st == TX_SUCCESS) {
-    tx_pad_args pa{args.A, wa, args.lda, kp, args.M, args.K, int32_t(kp), 0};
+    tx_pad_args pa{args.A, wa, args.lda, kp, args.M, args.K, int32_t(kp),
+                   pad_load_bytes(args.A, args.lda * es, int64_t(args.K) * es)};
     const int64_t ga = std::min<int64_t>((int64_t(args.M) * kp / per + 255) / 256, cus * 16);
     st = launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, pad);
   }
   if (st == TX_SUCCESS) {
-    tx_pad_args pb{args.B, wb, args.ldb, kp, args.N, args.K, int32_t(kp), 0};
+    tx_pad_args pb{args.B, wb, args.ldb, kp, args.N, args.K, int32_t(kp),
+                   pad_load_bytes(args.B, args.ldb * es, int64_t(args.K) * es)};
     const int64_t gb = std::min<int64_t>((int64_t(args.N) * kp / per + 255) / 256, cus * 16);
     st = launch(fn, unsigned(gb), 1, 256, s, &pb, sizeof pb, pad);
   }
@@ -194,7 +204,7 @@ tx_status launch_padded(const char *base, const char *reduce, const char *pad, c
     args.B = wb;
     args.ldb = kp;
     args.K = int32_t(kp);
-    st = launch_fast(base, reduce, strip, co, args, kp * es, es, s);
+    st = launch_fast(base, reduce, co, args, kp * es, es, s);
   }
   if (hipFreeAsync(ws, s) != hipSuccess && st == TX_SUCCESS)
     st = fail(TX_LAUNCH_ERROR, "%s: releasing the padded operands failed", base);
@@ -215,13 +225,12 @@ static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb
   tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
                     int32_t(K), 0, 0, 0};
   if (fast_ok(A, lda * 2, B, ldb * 2, K * 2, M, N))
-    return launch_fast("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce",
-                       "tx_gemm_bf16_128x128_v16", CodeObject::GemmBf16, args, K * 2, 2, s);
+    return launch_fast("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce", CodeObject::GemmBf16,
+                       args, K * 2, 2, s);
   {
     tx_gemm_args padded = args;
     const tx_status st = launch_padded("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce",
-                                       "tx_gemm_bf16_pad_rows", "tx_gemm_bf16_128x128_v16",
-                                       CodeObject::GemmBf16, padded, 2, s);
+                                       "tx_gemm_bf16_pad_rows", CodeObject::GemmBf16, padded, 2, s);
     if (st != TX_UNSUPPORTED) return st;
     clear_error();
   }
@@ -266,15 +275,12 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
   std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast", fa, fb);
-  char strip[80];
-  std::snprintf(strip, sizeof strip, "tx_gemm_fp8_%s_%s_128x128_v16", fa, fb);
   if (fast_ok(A, lda, B, ldb, K, M, N))
-    return launch_fast(kname, "tx_gemm_fp8_splitk_reduce", strip, CodeObject::GemmFp8, args, K, 1,
-                       s);
+    return launch_fast(kname, "tx_gemm_fp8_splitk_reduce", CodeObject::GemmFp8, args, K, 1, s);
   {
     tx_gemm_args padded = args;
     const tx_status st = launch_padded(kname, "tx_gemm_fp8_splitk_reduce", "tx_gemm_fp8_pad_rows",
-                                       strip, CodeObject::GemmFp8, padded, 1, s);
+                                       CodeObject::GemmFp8, padded, 1, s);
     if (st != TX_UNSUPPORTED) return st;
     clear_error();
   }

@@ -113,28 +113,44 @@ __device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, in
 }
 
 // Copy rows into a zero-padded buffer (see tx_pad_args): one 16-byte chunk of
-// a destination row per thread, source read element by element (the source
-// rows are what the fast path could not take: not 16-byte aligned).
-template <int ES>
-__device__ __forceinline__ void pad_rows(const tx_pad_args &a) {
+// a destination row per thread.  The source is read LW bytes at a time, LW
+// (a.load_bytes: 8, 4, 2 or 1) dividing the source base address, its row
+// pitch and its row length in bytes, so every load lies wholly inside or
+// wholly past the row (the source rows are what the fast path could not
+// take: not 16-byte aligned).
+template <int ES, int LW>
+__device__ __forceinline__ void pad_rows_w(const tx_pad_args &a) {
   constexpr int PER = 16 / ES;  // elements per 16-byte chunk
+  using L = typename std::conditional<
+      LW == 8, uint64_t,
+      typename std::conditional<LW == 4, uint32_t,
+                                typename std::conditional<LW == 2, uint16_t, uint8_t>::type>::type>::type;
   const int64_t chunks_per_row = a.dst_cols / PER;
   const int64_t total = int64_t(a.rows) * chunks_per_row;
-  using E = typename std::conditional<ES == 2, uint16_t, uint8_t>::type;
-  const E *src = reinterpret_cast<const E *>(a.src);
+  const int64_t row_bytes = int64_t(a.cols) * ES;
   for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
        t += int64_t(gridDim.x) * blockDim.x) {
     const int64_t r = t / chunks_per_row;
-    const int c0 = int(t % chunks_per_row) * PER;
-    const E *s = src + r * a.src_ld;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    const int64_t b0 = (t % chunks_per_row) * 16;
+    const uint8_t *s = reinterpret_cast<const uint8_t *>(a.src) + r * a.src_ld * ES;
+    uint8_t chunk[16] __attribute__((aligned(16)));
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint32_t v = (c0 + i < a.cols) ? uint32_t(s[c0 + i]) : 0u;
-      w[(i * ES) / 4] |= v << (8 * ((i * ES) % 4));
+    for (int i = 0; i < 16 / LW; ++i) {
+      const int64_t off = b0 + i * LW;
+      *reinterpret_cast<L *>(chunk + i * LW) = off < row_bytes ? *reinterpret_cast<const L *>(s + off) : L(0);
     }
-    *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(a.dst) + (r * a.dst_ld + c0) * ES) =
-        u32x4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(a.dst) + r * a.dst_ld * ES + b0) =
+        *reinterpret_cast<const u32x4 *>(chunk);
+  }
+}
+
+template <int ES>
+__device__ __forceinline__ void pad_rows(const tx_pad_args &a) {
+  switch (a.load_bytes) {
+    case 8: pad_rows_w<ES, 8>(a); break;
+    case 4: pad_rows_w<ES, 4>(a); break;
+    case 2: pad_rows_w<ES, 2>(a); break;
+    default: pad_rows_w<ES, 1>(a); break;
   }
 }
 

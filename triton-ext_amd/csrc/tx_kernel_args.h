@@ -65,7 +65,7 @@ typedef struct tx_pad_args {
   int32_t rows;
   int32_t cols;
   int32_t dst_cols;
-  int32_t reserved;
+  int32_t load_bytes; /* source load width: 8, 4, 2 or 1 (see pad_rows) */
 } tx_pad_args;
 
 /* fp8 dequant GEMV */
