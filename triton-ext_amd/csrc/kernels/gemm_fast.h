@@ -305,36 +305,73 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     }
     return;
   }
-  uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
-  const bool cvec = ((reinterpret_cast<uintptr_t>(a.C) & 7) == 0) && ((a.ldc & 3) == 0);
+  // Epilogue: scale (fp8), round to bf16 and stage the whole tile in LDS (the
+  // ring is free after the drain above), then write whole row segments of C
+  // with 16-byte stores.  Staged 16-byte chunk c of tile row r sits at chunk
+  // c ^ (r % CH): the 32 rows of a fragment column write 32 (BN 256) or 16
+  // twice-used (BN 128) different chunks, the minimum two passes for 512
+  // bytes, and the CH lanes reading one row cover every chunk once.
+  constexpr int CH = BN / 8;        // 16-byte chunks per staged row
+  constexpr int ROWB = BN * 2;      // staged row bytes
+  constexpr int RPI = 64 / CH;      // rows per store instruction
+  static_assert(256 * ROWB <= kSlots * kSlotBytes, "staged tile fits in LDS");
+  float sav[4], sbv[FN][4][4];
+  if constexpr (C::FP8) {
+    // all scale loads in one batch ahead of their use
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm) {
+      const int m = m0 + wm * 128 + fm * 32 + frow;
+      sav[fm] = m < a.M ? a.scale_a[m] : 0.0f;
+    }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int n = n0 + wn * TN + fn * 32 + 8 * jj + 4 * fg + t;
+          sbv[fn][jj][t] = n < a.N ? a.scale_b[n] : 0.0f;
+        }
+  }
 #pragma unroll
   for (int fm = 0; fm < 4; ++fm) {
-    const int m = m0 + wm * 128 + fm * 32 + frow;
-    if (m >= a.M) continue;
-    float scl_a = 1.0f;
-    if constexpr (C::FP8) scl_a = a.scale_a[m];
+    const int row = wm * 128 + fm * 32 + frow;
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int n = n0 + wn * TN + fn * 32 + 8 * jj + 4 * fg;
         float v[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = acc[fn][fm][4 * jj + t];
-        if constexpr (C::FP8) {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) v[t] = v[t] * scl_a * (n + t < a.N ? a.scale_b[n + t] : 0.0f);
+        for (int t = 0; t < 4; ++t) {
+          v[t] = acc[fn][fm][4 * jj + t];
+          if constexpr (C::FP8) v[t] = v[t] * sav[fm] * sbv[fn][jj][t];
         }
-        uint16_t *dst = Cb + int64_t(m) * a.ldc + n;
-        if (cvec && n + 3 < a.N) {
-          txd::u32x2 p = {txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
-          *reinterpret_cast<txd::u32x2 *>(dst) = p;
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            if (n + t < a.N) dst[t] = uint16_t(txd::f32_to_bf16_bits(v[t]));
-        }
+        const int c = (wn * TN + fn * 32 + 8 * jj) / 8;
+        *reinterpret_cast<txd::u32x2 *>(lds + row * ROWB + ((c ^ (row & (CH - 1))) << 4) + 8 * fg) =
+            txd::u32x2{txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
       }
+  }
+  __syncthreads();
+  uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
+  const bool cvec = ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0) && ((a.ldc & 7) == 0);
+  const int sc = lane % CH;
+  const int n = n0 + 8 * sc;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int row = wave * 32 + i * RPI + lane / CH;
+    const int m = m0 + row;
+    const txd::u32x4 w = *reinterpret_cast<const txd::u32x4 *>(lds + row * ROWB + ((sc ^ (row & (CH - 1))) << 4));
+    if (m < a.M && n < a.N) {
+      uint16_t *dst = Cb + int64_t(m) * a.ldc + n;
+      if (cvec && n + 7 < a.N) {
+        *reinterpret_cast<txd::u32x4 *>(dst) = w;
+      } else {
+        const uint32_t h[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          if (n + t < a.N) dst[t] = uint16_t(h[t / 2] >> (16 * (t % 2)));
+      }
+    }
   }
 }
 
