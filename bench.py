@@ -9,10 +9,13 @@ Prints ONE JSON line.  The headline metric pairs two numbers:
 The other configurations are reported under "secondary".
 
 A step is one launch of the op over one batch of synthetic input already
-resident in HBM.  Each measurement runs W untimed launches, then exactly K
-launches between two HIP events on the stream the op is launched on (torch's
-current stream, which tx passes to the library), with torch.cuda.synchronize()
-before and after.  Inputs rotate over enough buffer sets that the working set
+resident in HBM.  Each measurement first runs the same step, untimed, for
+PREROLL_S seconds: the GPU's power manager raises the clocks only after some
+milliseconds of sustained load, and an op timed straight after the idle host
+work that builds its inputs would be timed on the clock ramp.  Then come W
+untimed launches, then exactly K launches between two HIP events on the
+stream the op is launched on (torch's current stream, which tx passes to the
+library), with torch.cuda.synchronize() before and after.  Inputs rotate over enough buffer sets that the working set
 exceeds twice the 256 MB Infinity Cache for the memory-bound ops.
 
 cpu_baseline: the CPU oracle (oracle/, a C port of the path's semantics,
@@ -55,9 +58,20 @@ def parse():
     return p.parse_args()
 
 
+PREROLL_S = 0.25
+
+
 def timed(fn, steps, warmup):
-    """Average ms per launch of fn(i) over exactly `steps` launches."""
+    """Average ms per launch of fn(i) over exactly `steps` launches, after the
+    clock pre-roll and `warmup` untimed launches."""
     import torch
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < PREROLL_S:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -336,7 +350,7 @@ def main():
         "data": "synthetic (seeded N(0,1), absmax-quantised; see tx/workloads.py)",
         "config": {"workload": "fp8 e4m3fn scaled GEMM M=N=K=8192, per-row/per-column fp32 "
                                "scales, bf16 output; plus fp32->e4m3fn RNE convert of 16Mi values",
-                   "M": 8192, "N": 8192, "K": 8192},
+                   "M": 8192, "N": 8192, "K": 8192, "preroll_s": PREROLL_S},
         "roofline": {"bound": "mfma", "achieved": round(gemm["tflops"], 2),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm["tflops"] / FP8_PEAK_TFLOPS, 4),

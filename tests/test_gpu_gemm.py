@@ -110,6 +110,39 @@ def test_bf16_config_shapes(tx, oracle, dev, M, N, K):
     assert np.array_equal(bf16_f32(C2), 2 * bf16_f32(C))
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 64), (512, 384, 64), (600, 1000, 8), (300, 500, 4096),
+                                   (100, 200, 7)])
+def test_bf16_output_rounding_exact(tx, oracle, dev, M, N, K):
+    """One nonzero per row of A, so every output is a single bf16 x bf16
+    product, exact in fp32: the kernel's rounding to bf16 must equal the
+    oracle's round-to-nearest-even bit for bit (about one product in 256 is a
+    tie).  Row 0 of A holds +Inf, row 1 a NaN: Inf * b keeps b's sign, Inf * 0
+    and NaN * b are NaN.  Shapes cover the 256x256 and 256x128 tiles, split K
+    and the generic kernel."""
+    from tx import workloads
+    g = np.random.default_rng(M + K)
+    a = np.zeros((M, K), np.float32)
+    a[np.arange(M), np.arange(M) % K] = g.uniform(0.5, 2.0, M) * g.choice([-1.0, 1.0], M)
+    b = (g.uniform(0.5, 2.0, (N, K)) * g.choice([-1.0, 1.0], (N, K))).astype(np.float32)
+    b[5, :] = 0.0
+    A, B = workloads.to_bf16_bits(a), workloads.to_bf16_bits(b)
+    A[0, 0] = 0x7F80
+    A[1, 1] = 0x7FC0
+    C = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
+    Cf = bf16_f32(C)
+    bsign = np.signbit(bf16_f32(B[:, 0]))
+    inf_cols = np.arange(N) != 5
+    assert np.all(np.isinf(Cf[0, inf_cols])) and np.array_equal(np.signbit(Cf[0, inf_cols]), bsign[inf_cols])
+    assert np.isnan(Cf[0, 5]) and np.all(np.isnan(Cf[1]))
+    rows = [r for r in sample_rows(M, k=40) if r >= 2]
+    for r in rows:
+        _, r16 = oracle.gemm_bf16_rows(A, B, r, r + 1)
+        got, want = C[r], r16[0]
+        nz = bf16_f32(want) != 0
+        assert np.array_equal(got[nz], want[nz]), (r, np.flatnonzero(got[nz] != want[nz])[:5])
+        assert np.all(bf16_f32(got[~nz]) == 0)
+
+
 def test_bf16_strided_and_unaligned(tx, oracle, dev):
     from tx import workloads
     M, N, K = 200, 150, 333

@@ -111,18 +111,19 @@ __device__ __forceinline__ void wait_and_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <class C, int BN>
+template <class C, int BN, int NW = fast::kWaves>
 __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
-  constexpr int WN = kWaves / 2;     // waves along N (2 along M)
+  static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
+  constexpr int WN = NW / 2;         // waves along N (2 along M)
   constexpr int TN = BN / WN;        // wave tile: 128 x TN
   constexpr int FN = TN / 32;        // 32-column blocks per wave
   constexpr int NM = 4 * FN;         // mfma32 calls per K half
   constexpr int NF = 4 + FN;         // fragments per K half: A 0..3, B 4..
   constexpr int NR = 2 * NF;         // ds_read_b128 per K half
-  constexpr int BLKA = 32 / kWaves;  // 1 KiB blocks of A per wave per step
-  constexpr int BLKB = BN / 8 / kWaves;  // ... of B
+  constexpr int BLKA = 32 / NW;      // 1 KiB blocks of A per wave per step
+  constexpr int BLKB = BN / 8 / NW;  // ... of B
   constexpr int ND = BLKA + BLKB;    // loads per wave per step
   static_assert(BLKA % 2 == 0 && BLKB % 2 == 0, "a wave's first block must have an even index");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
@@ -153,7 +154,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   // parity of j).
   const uint32_t kch[2] = {16u * uint32_t((lane & 7) ^ ((lane >> 4) & 7)),
                            16u * uint32_t((lane & 7) ^ ((4 + (lane >> 4)) & 7))};
-  uint32_t vo[2][BLKA];
+  uint32_t vo[2][BLKA > BLKB ? BLKA : BLKB];
 #pragma unroll
   for (int j = 0; j < BLKA; ++j) {
     const int row = 8 * (BLKA * wave + j) + (lane >> 3);
@@ -167,24 +168,29 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     vo[1][j] = gn < a.N ? uint32_t(gn) * ldb_b + kch[j & 1] : kOob;
   }
   // Load block j of operand op of (split-local) step ks into slot `slot`.
-  // Steps past the split's end are loaded but never multiplied.
-  auto load_op = [&](int ks, int slot, auto op_tag, auto j_tag) {
+  // Steps past the split's end are loaded but never multiplied.  With TAIL
+  // (K * element size not a multiple of the step), a lane whose chunk lies
+  // past the row end reads zeros; otherwise no chunk ever does, and the load
+  // takes its per-lane offset as it is (no vector instructions per load).
+  auto load_op = [&](int ks, int slot, auto op_tag, auto j_tag, auto tail_tag) {
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     constexpr int blk = op == 0 ? BLKA : BLKB;
     const uint32_t so = kbase + uint32_t(ks) * kStep;
-    const bool past = so + kch[j & 1] >= kb_end;  // K tail: this lane's chunk is past the row end
+    uint32_t voff = vo[op][j];
+    if constexpr (decltype(tail_tag)::value) {
+      if (so + kch[j & 1] >= kb_end) voff = kOob;
+    }
     uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[op], (lds_void *)dst, 16, past ? kOob : vo[op][j],
-                                             so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[op], (lds_void *)dst, 16, voff, so, 0, 0);
   };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
   // Load d of the second half of step ks: B of step ks+2 into the slot of A
   // of step ks (d < BLKB), then A of step ks+3 into the slot of B of step ks.
-  auto load = [&](int ks, int slot_a, int slot_b, auto d_tag) {
+  auto load = [&](int ks, int slot_a, int slot_b, auto d_tag, auto tail_tag) {
     constexpr int d = decltype(d_tag)::value;
-    if constexpr (d < BLKB) load_op(ks + 2, slot_a, OpB{}, std::integral_constant<int, d>{});
-    else load_op(ks + 3, slot_b, OpA{}, std::integral_constant<int, d - BLKB>{});
+    if constexpr (d < BLKB) load_op(ks + 2, slot_a, OpB{}, std::integral_constant<int, d>{}, tail_tag);
+    else load_op(ks + 3, slot_b, OpA{}, std::integral_constant<int, d - BLKB>{}, tail_tag);
   };
 
   // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
@@ -229,50 +235,55 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using H1 = std::integral_constant<int, 1>;
   constexpr int RW = NM / 2;  // reads follow the first RW MFMAs of a half
 
-  // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
-  // step 0 landed, half 0 of step 0 in registers.
-  static_for<BLKA>([&](auto j) { load_op(0, 0, OpA{}, j); });
-  static_for<BLKB>([&](auto j) { load_op(0, 1, OpB{}, j); });
-  static_for<BLKA>([&](auto j) { load_op(1, 2, OpA{}, j); });
-  static_for<BLKB>([&](auto j) { load_op(1, 3, OpB{}, j); });
-  static_for<BLKA>([&](auto j) { load_op(2, 4, OpA{}, j); });
-  wait_and_barrier<2 * BLKA + BLKB>();
-  static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
+  // The prologue and the K loop, with or without the K-tail zero fill.
+  auto pipeline = [&](auto tail) {
+    // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
+    // step 0 landed, half 0 of step 0 in registers.
+    static_for<BLKA>([&](auto j) { load_op(0, 0, OpA{}, j, tail); });
+    static_for<BLKB>([&](auto j) { load_op(0, 1, OpB{}, j, tail); });
+    static_for<BLKA>([&](auto j) { load_op(1, 2, OpA{}, j, tail); });
+    static_for<BLKB>([&](auto j) { load_op(1, 3, OpB{}, j, tail); });
+    static_for<BLKA>([&](auto j) { load_op(2, 4, OpA{}, j, tail); });
+    wait_and_barrier<2 * BLKA + BLKB>();
+    static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
 
-  int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;  // step ks+1
-    static_for<NM>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      mma(H0{}, I);
-      __builtin_amdgcn_sched_barrier(0);
-      constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
-      static_for<r1 - r0>([&](auto R) {
-        read(sa, sb, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+    int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
+    for (int ks = 0; ks < ksteps; ++ks) {
+      const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;  // step ks+1
+      static_for<NM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        mma(H0{}, I);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+        static_for<r1 - r0>([&](auto R) {
+          read(sa, sb, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+        });
+        __builtin_amdgcn_sched_barrier(0);
       });
+      // A and B of step ks+1 landed for every wave (the BLKA loads of A of step
+      // ks+2, issued last, may still be in flight); the slots of step ks are free.
+      wait_and_barrier<BLKA>();
       __builtin_amdgcn_sched_barrier(0);
-    });
-    // A and B of step ks+1 landed for every wave (the BLKA loads of A of step
-    // ks+2, issued last, may still be in flight); the slots of step ks are free.
-    wait_and_barrier<BLKA>();
-    __builtin_amdgcn_sched_barrier(0);
-    static_for<NM>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      mma(H1{}, I);
-      __builtin_amdgcn_sched_barrier(0);
-      constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
-      static_for<d1 - d0>([&](auto D) {
-        load(ks, sa, sb, std::integral_constant<int, d0 + decltype(D)::value>{});
+      static_for<NM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        mma(H1{}, I);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
+        static_for<d1 - d0>([&](auto D) {
+          load(ks, sa, sb, std::integral_constant<int, d0 + decltype(D)::value>{}, tail);
+        });
+        constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+        static_for<r1 - r0>([&](auto R) {
+          read(na, nb, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+        });
+        __builtin_amdgcn_sched_barrier(0);
       });
-      constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
-      static_for<r1 - r0>([&](auto R) {
-        read(na, nb, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
-      });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    sa = na;
-    sb = nb;
-  }
+      sa = na;
+      sb = nb;
+    }
+  };
+  if (kb_end % kStep == 0) pipeline(std::false_type{});
+  else pipeline(std::true_type{});
   // Drain the trailing (zero-fill) loads before the workgroup's LDS is released.
   wait_and_barrier<0>();
 
@@ -357,8 +368,8 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   const int sc = lane % CH;
   const int n = n0 + 8 * sc;
 #pragma unroll
-  for (int i = 0; i < 32 / RPI; ++i) {
-    const int row = wave * 32 + i * RPI + lane / CH;
+  for (int i = 0; i < 256 / NW / RPI; ++i) {
+    const int row = wave * (256 / NW) + i * RPI + lane / CH;
     const int m = m0 + row;
     const txd::u32x4 w = *reinterpret_cast<const txd::u32x4 *>(lds + row * ROWB + ((sc ^ (row & (CH - 1))) << 4));
     if (m < a.M && n < a.N) {
