@@ -155,7 +155,9 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
 // Operands the fast path cannot take (rows not 16-byte aligned or K * size
 // not a multiple of 16 bytes) in a product of at least kPadMinWork
 // multiply-adds are first copied into zero-padded rows of a stream-ordered
-// workspace (K rounded up to 16 bytes; the zeros add nothing to the sums).
+// workspace.  K is rounded up to a whole 128-byte step: the zeros add nothing
+// to the sums, every row starts on a 128-byte line (a row segment of a step
+// is then one cache line, not two), and no step needs the K-tail fill.
 // Returns TX_UNSUPPORTED without launching anything when that is not
 // possible, and the caller takes the generic kernel.
 constexpr int64_t kPadMinWork = int64_t(1) << 30;
@@ -170,8 +172,8 @@ int pad_load_bytes(const void *src, int64_t ld_bytes, int64_t row_bytes) {
 
 tx_status launch_padded(const char *base, const char *reduce, const char *pad, CodeObject co,
                         tx_gemm_args &args, int es, hipStream_t s) {
-  const int64_t per = 16 / es;
-  const int64_t kp = (int64_t(args.K) + per - 1) / per * per;
+  const int64_t per = 16 / es, step = 128 / es;
+  const int64_t kp = (int64_t(args.K) + step - 1) / step * step;
   if (int64_t(args.M) * args.N * args.K < kPadMinWork ||
       (int64_t(std::max(args.M, args.N)) * kp) * es >= (int64_t(1) << 31))
     return TX_UNSUPPORTED;

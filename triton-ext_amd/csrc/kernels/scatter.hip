@@ -33,6 +33,11 @@ constexpr int kHashLog2 = 14;                // 16384 slots, 128 KiB keys + valu
 constexpr int kHashSlots = 1 << kHashLog2;
 constexpr int kProbes = 4;
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+// fp32 hot keys (see HotKeys): up to kHot keys, sampled in a 2048-slot table.
+constexpr int kHot = 8;  // HotKeys::take names each of the kHot sums
+constexpr int kSampleLog2 = 11;
+constexpr int kSampleSlots = 1 << kSampleLog2;
+constexpr uint32_t kHotMinCount = 16;        // of at most 4 x kBlock samples
 
 template <int OP> struct OpTraits;
 template <> struct OpTraits<ADD> { using T = uint32_t; static __device__ T id() { return 0u; } };
@@ -120,6 +125,45 @@ __device__ __forceinline__ void wave_combine_global(T *bins, bool pending, uint3
   }
 }
 
+// Hot keys of one workgroup's fp32 window.  ds_add_f32 retires about 0.3
+// lanes per clock per CU however its addresses fall, so the compare-and-swap
+// in wave_lds_combine carries fp32 adds; it loses whenever several lanes of
+// an instruction, or several wavefronts at once, hit one bin, and skewed keys
+// (Zipf: the top 8 of 65,536 bins draw a third of the updates) make that
+// common.  Each workgroup therefore samples the first 4 x kBlock updates of
+// its chunk, counts the in-window keys in a small LDS hash table, and takes
+// up to kHot keys seen at least kHotMinCount times.  Their updates never touch
+// LDS: every lane sums them in registers (one accumulator per hot key), and
+// the sums are reduced over the wavefront and added to the table once, at the
+// end of the chunk.  Which keys are chosen only moves work between the two
+// paths; the sums are the same either way (up to fp32 rounding order).
+struct HotKeys {
+  int n = 0;            // number of hot keys (workgroup-uniform)
+  uint32_t r[kHot];     // their window-relative slots (same in every lane); unused: kEmpty
+  float acc[kHot];      // this lane's partial sums
+
+  // Route one update: a pending update on a hot slot is added to that slot's
+  // sum and stops pending.  Lanes that are not pending add -0, which changes
+  // no sum; no pending slot equals kEmpty (pending slots are below the window
+  // size).
+  __device__ __forceinline__ void take(bool &pend, uint32_t slot, float v) {
+    const float x = pend ? v : -0.0f;
+    bool hit = false;
+#pragma unroll
+    for (int t = 0; t < kHot; ++t) {
+      const bool m = slot == r[t];
+      acc[t] += m ? x : -0.0f;
+      hit = hit || m;
+    }
+    // The sums are complete here, before any LDS atomic of this update: left
+    // to itself the compiler sinks the adds past the atomics and keeps all
+    // kHot compare masks alive in scalar registers across them.
+    asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]),
+                 "+v"(acc[5]), "+v"(acc[6]), "+v"(acc[7])::"memory");
+    pend = pend && !hit;
+  }
+};
+
 template <int OP>
 struct Scatter {
   using T = typename OpTraits<OP>::T;
@@ -175,14 +219,18 @@ struct Scatter {
   // Combine 4 updates into the LDS window [lo, lo + nb).  A key outside the
   // window (negative keys included: they wrap to large unsigned values) or
   // with a zero mask byte is dropped; lo + nb <= nbins <= INT32_MAX.
-  static __device__ __forceinline__ void apply(T *table, uint32_t lo, uint32_t nb,
+  template <bool HOT>
+  static __device__ __forceinline__ void apply(T *table, uint32_t lo, uint32_t nb, HotKeys &hot,
                                                const txd::i32x4 &k, const txd::u32x4 &v, uint32_t m) {
     const int32_t kk[4] = {k.x, k.y, k.z, k.w};
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t r = uint32_t(kk[j]) - lo;
-      wave_lds_combine<OP, T>(table, r < nb && ((m >> (8 * j)) & 0xFFu) != 0, r, __builtin_bit_cast(T, vv[j]));
+      bool pend = r < nb && ((m >> (8 * j)) & 0xFFu) != 0;
+      const T x = __builtin_bit_cast(T, vv[j]);
+      if constexpr (OP == FADD && HOT) hot.take(pend, r, x);
+      wave_lds_combine<OP, T>(table, pend, r, x);
     }
   }
 
@@ -192,9 +240,9 @@ struct Scatter {
   // run.  Slot d always holds an iteration congruent to d mod kDepth, so the
   // slots are compile-time registers; refills past the last iteration re-read
   // the last one (in range, never applied).
-  template <bool MASK>
-  static __device__ void stream(const tx_scatter_args &a, T *table, uint32_t lo, uint32_t nb,
-                                int64_t e0, int64_t groups) {
+  template <bool MASK, bool HOT>
+  static __device__ __forceinline__ void stream(const tx_scatter_args &a, T *table, uint32_t lo,
+                                                uint32_t nb, HotKeys &hot, int64_t e0, int64_t groups) {
     txd::i32x4 k[kDepth];
     txd::u32x4 v[kDepth];
     uint32_t m[kDepth];
@@ -205,10 +253,96 @@ struct Scatter {
       const int64_t eg = e0 + g * kDepth * kIter;
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        apply(table, lo, nb, k[d], v[d], m[d]);
+        apply<HOT>(table, lo, nb, hot, k[d], v[d], m[d]);
         const int64_t en = eg + (d + kDepth) * kIter;
         fetch<MASK>(a, en < last ? en : last, k[d], v[d], m[d]);
       }
+    }
+  }
+
+  // Picks the workgroup's hot keys (HotKeys) from the first 4 x kBlock
+  // updates of its chunk; on return every lane holds the same set, with
+  // zeroed sums.  Needs the whole workgroup; ends with a barrier.
+  static __device__ void sample_hot(const tx_scatter_args &a, uint32_t lo, uint32_t nb, int64_t begin,
+                                    int64_t end, bool vec, HotKeys &hot) {
+    __shared__ uint32_t skey[kSampleSlots];
+    __shared__ uint32_t scnt[kSampleSlots];
+    for (int s = threadIdx.x; s < kSampleSlots; s += kBlock) {
+      skey[s] = kEmpty;
+      scnt[s] = 0u;
+    }
+    __syncthreads();
+    {
+      uint32_t key[4];
+      T val[4];
+      bool ok[4];
+      load4(a, begin + 4 * int64_t(threadIdx.x), end, vec, key, val, ok);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t r = key[j] - lo;
+        if (!(ok[j] && r < nb)) continue;
+        const uint32_t h = (r * 2654435769u) >> (32 - kSampleLog2);
+#pragma unroll
+        for (int p = 0; p < kProbes; ++p) {
+          const uint32_t slot = (h + p) & (kSampleSlots - 1);
+          uint32_t k = __atomic_load_n(&skey[slot], __ATOMIC_RELAXED);
+          if (k == kEmpty) k = atomicCAS(&skey[slot], kEmpty, r);
+          if (k == kEmpty || k == r) {
+            atomicAdd(&scnt[slot], 1u);
+            break;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // Wavefront 0 takes the kHot largest counts (ties: lower slot first) and
+    // then publishes them in the table's first slots: skey[0 .. kHot) holds
+    // the keys, scnt[0] their number.
+    if (threadIdx.x < 64) {
+      uint32_t res[kHot];
+      const int lane = threadIdx.x;
+      auto best_of_lane = [&]() {
+        uint64_t b = 0;
+        for (int s = lane; s < kSampleSlots; s += 64) {
+          const uint64_t c = (uint64_t(scnt[s]) << 32) | uint32_t(kSampleSlots - 1 - s);
+          b = c > b ? c : b;
+        }
+        return b;
+      };
+      uint64_t mine = best_of_lane();
+      int n = 0;
+      for (int t = 0; t < kHot; ++t) {
+        uint64_t b = mine;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          const uint32_t lo32 = __shfl_xor(uint32_t(b), off), hi32 = __shfl_xor(uint32_t(b >> 32), off);
+          const uint64_t o = (uint64_t(hi32) << 32) | lo32;
+          b = o > b ? o : b;
+        }
+        if (uint32_t(b >> 32) < kHotMinCount) break;
+        const int slot = kSampleSlots - 1 - int(uint32_t(b));
+        res[t] = __builtin_amdgcn_readfirstlane(skey[slot]);
+        if (slot % 64 == lane) {
+          scnt[slot] = 0u;
+          mine = best_of_lane();
+        }
+        n = t + 1;
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < kHot; ++t)
+          if (t < n) skey[t] = res[t];
+        scnt[0] = uint32_t(n);
+      }
+    }
+    __syncthreads();
+    hot.n = int(__builtin_amdgcn_readfirstlane(scnt[0]));
+#pragma unroll
+    for (int t = 0; t < kHot; ++t) {
+      // kept in vector registers: scalar registers are the scarcer resource
+      // in the unrolled update loop
+      hot.r[t] = t < hot.n ? skey[t] : kEmpty;
+      hot.acc[t] = -0.0f;
     }
   }
 
@@ -232,16 +366,23 @@ struct Scatter {
     const uint32_t lo = uint32_t(w) * uint32_t(a.window);
     const uint32_t nb = min(uint32_t(a.window), uint32_t(a.nbins) - lo);  // bins in this window
     for (uint32_t s = threadIdx.x; s < nb; s += kBlock) table[s] = OpTraits<OP>::id();
-    __syncthreads();
     const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
                      (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
+    HotKeys hot;
+    if constexpr (OP == FADD) sample_hot(a, lo, nb, begin, end, vec, hot);
+    __syncthreads();
     int64_t e = begin + 4 * int64_t(threadIdx.x);
     if (vec) {
       // Whole groups of kDepth full iterations go through the pipelined loop.
       const int64_t groups = (end - begin) / (kDepth * kIter);
       if (groups > 0) {
-        if (a.mask) stream<true>(a, table, lo, nb, e, groups);
-        else stream<false>(a, table, lo, nb, e, groups);
+        if (OP == FADD && hot.n > 0) {
+          if (a.mask) stream<true, true>(a, table, lo, nb, hot, e, groups);
+          else stream<false, true>(a, table, lo, nb, hot, e, groups);
+        } else {
+          if (a.mask) stream<true, false>(a, table, lo, nb, hot, e, groups);
+          else stream<false, false>(a, table, lo, nb, hot, e, groups);
+        }
         e += groups * kDepth * kIter;
       }
     }
@@ -256,7 +397,23 @@ struct Scatter {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t r = key[j] - lo;  // wraps for keys below the window
-        wave_lds_combine<OP, T>(table, ok[j] && r < nb, r, val[j]);
+        bool pend = ok[j] && r < nb;
+        if constexpr (OP == FADD) {
+          if (hot.n > 0) hot.take(pend, r, val[j]);
+        }
+        wave_lds_combine<OP, T>(table, pend, r, val[j]);
+      }
+    }
+    if constexpr (OP == FADD) {
+      // the hot keys' sums: one LDS add per wavefront and key
+#pragma unroll
+      for (int t = 0; t < kHot; ++t) {
+        if (t < hot.n) {
+          float x = hot.acc[t];
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+          if ((threadIdx.x & 63) == 0) atomicAdd(&table[hot.r[t]], x);
+        }
       }
     }
     __syncthreads();
