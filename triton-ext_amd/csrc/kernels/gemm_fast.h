@@ -1,6 +1,7 @@
 // Fast-path GEMM body for aligned operands (both K-contiguous, 16-byte
 // aligned rows, K * element size a multiple of 16 bytes): 256 x 256 tile,
-// 8 wavefronts (two per SIMD), each owning a 128 x 64 block of C.
+// 8 wavefronts (two per SIMD), each owning a 128 x 64 block of C (64 x 64 in
+// the 256 x 128 variant).
 //
 // Pipeline (per 128-byte K step, i.e. 64 bf16 or 128 fp8 of K):
 //  * LDS is a ring of 5 slots of 32 KiB (all of gfx950's 160 KiB); a slot
@@ -116,11 +117,17 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
-  constexpr int WN = NW / 2;         // waves along N (2 along M)
-  constexpr int TN = BN / WN;        // wave tile: 128 x TN
+  // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per
+  // wave): LDS reads per step are then (64 + 64) x 8 rows instead of
+  // (128 + 32) x 8, which matters because narrow tiles are LDS-bound.
+  constexpr int WM = (BN == 128 && NW == 8) ? 4 : 2;
+  constexpr int WN = NW / WM;
+  constexpr int TM = 256 / WM;       // wave tile: TM x TN
+  constexpr int TN = BN / WN;
+  constexpr int FM = TM / 32;        // 32-row blocks per wave
   constexpr int FN = TN / 32;        // 32-column blocks per wave
-  constexpr int NM = 4 * FN;         // mfma32 calls per K half
-  constexpr int NF = 4 + FN;         // fragments per K half: A 0..3, B 4..
+  constexpr int NM = FM * FN;        // mfma32 calls per K half
+  constexpr int NF = FM + FN;        // fragments per K half: A 0..FM-1, B FM..
   constexpr int NR = 2 * NF;         // ds_read_b128 per K half
   constexpr int BLKA = 32 / NW;      // 1 KiB blocks of A per wave per step
   constexpr int BLKB = BN / 8 / NW;  // ... of B
@@ -136,7 +143,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   const int m0 = tm * 256, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS addresses scalar
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WM, wn = wave / WM;
   constexpr int ES = C::FP8 ? 1 : 2;
   const uint32_t kb_end = uint32_t(a.K) * ES;
   const int ksteps_all = int((kb_end + kStep - 1) / kStep);
@@ -203,32 +210,32 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      ro[0][h][e] = off(wm * 128 + frow, 4 * h + 2 * fg + e);
+      ro[0][h][e] = off(wm * TM + frow, 4 * h + 2 * fg + e);
       ro[1][h][e] = off(wn * TN + frow, 4 * h + 2 * fg + e);
     }
   txd::i32x4 fr[2][NF][2];  // [K half][fragment][16-byte piece]
   // Read r of a K half: fragments in the order the MFMAs consume them
-  // (A0, B0, A1, A2, A3, B1, ...), two 16-byte pieces each.
+  // (A0, B0, A1 .. A(FM-1), B1 .., two 16-byte pieces each.
   auto read = [&](int slot_a, int slot_b, auto h_tag, auto r_tag) {
     constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
-    constexpr int f = o == 0 ? 0 : o == 1 ? 4 : o <= 4 ? o - 1 : o;
-    const uint8_t *S = lds + (f < 4 ? slot_a : slot_b) * kSlotBytes;
-    const int byte = f < 4 ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - 4);
+    constexpr int f = o == 0 ? 0 : o == 1 ? FM : o <= FM ? o - 1 : o;
+    const uint8_t *S = lds + (f < FM ? slot_a : slot_b) * kSlotBytes;
+    const int byte = f < FM ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - FM);
     fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(S + byte);
   };
 
-  txd::f32x16 acc[FN][4];
+  txd::f32x16 acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < FM; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  // MFMA i of a K half: B block i / 4 against A block i % 4.
+  // MFMA i of a K half: B block i / FM against A block i % FM.
   auto mma = [&](auto h_tag, auto i_tag) {
-    constexpr int h = decltype(h_tag)::value, i = decltype(i_tag)::value, fn = i / 4, fm = i % 4;
+    constexpr int h = decltype(h_tag)::value, i = decltype(i_tag)::value, fn = i / FM, fm = i % FM;
     const i32x8 va = __builtin_shufflevector(fr[h][fm][0], fr[h][fm][1], 0, 1, 2, 3, 4, 5, 6, 7);
-    const i32x8 vb = __builtin_shufflevector(fr[h][4 + fn][0], fr[h][4 + fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const i32x8 vb = __builtin_shufflevector(fr[h][FM + fn][0], fr[h][FM + fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
     mfma32<C>(acc[fn][fm], vb, va);
   };
   using H0 = std::integral_constant<int, 0>;
@@ -288,15 +295,15 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   wait_and_barrier<0>();
 
   // Epilogue: lane owns, per (fm, fn, jj), C[m][n .. n+3] with
-  // m = m0 + wm*128 + fm*32 + l%32, n = n0 + wn*TN + fn*32 + 8*jj + 4*(l/32).
+  // m = m0 + wm*TM + fm*32 + l%32, n = n0 + wn*TN + fn*32 + 8*jj + 4*(l/32).
   // With K split, the unscaled fp32 sums go to the split's partial plane
   // (row-major M x N); a reduction kernel combines the planes.
   if (splits > 1) {
     float *P = a.part + int64_t(split) * a.M * a.N;
     const bool pvec = (a.N & 3) == 0;
 #pragma unroll
-    for (int fm = 0; fm < 4; ++fm) {
-      const int m = m0 + wm * 128 + fm * 32 + frow;
+    for (int fm = 0; fm < FM; ++fm) {
+      const int m = m0 + wm * TM + fm * 32 + frow;
       if (m >= a.M) continue;
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
@@ -326,12 +333,12 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   constexpr int ROWB = BN * 2;      // staged row bytes
   constexpr int RPI = 64 / CH;      // rows per store instruction
   static_assert(256 * ROWB <= kSlots * kSlotBytes, "staged tile fits in LDS");
-  float sav[4], sbv[FN][4][4];
+  float sav[FM], sbv[FN][4][4];
   if constexpr (C::FP8) {
     // all scale loads in one batch ahead of their use
 #pragma unroll
-    for (int fm = 0; fm < 4; ++fm) {
-      const int m = m0 + wm * 128 + fm * 32 + frow;
+    for (int fm = 0; fm < FM; ++fm) {
+      const int m = m0 + wm * TM + fm * 32 + frow;
       sav[fm] = m < a.M ? a.scale_a[m] : 0.0f;
     }
 #pragma unroll
@@ -345,8 +352,8 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
         }
   }
 #pragma unroll
-  for (int fm = 0; fm < 4; ++fm) {
-    const int row = wm * 128 + fm * 32 + frow;
+  for (int fm = 0; fm < FM; ++fm) {
+    const int row = wm * TM + fm * 32 + frow;
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
