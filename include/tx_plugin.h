@@ -20,15 +20,18 @@
  *
  * Conventions (all entry points):
  *  - The caller owns every input and output buffer.  tx_dot_bf16 and
- *    tx_dot_fp8_scaled may take a stream-ordered workspace on `stream`
- *    (hipMallocAsync before their launches, hipFreeAsync after): fp32
- *    split-K partial planes (at most 8 x M x N x 4 bytes) when the output
- *    tiles leave CUs idle, and zero-padded copies of A and B when rows are
- *    not 16-byte aligned in a product of at least 2^30 multiply-adds; if
- *    that allocation fails they run without it.  No other entry point
- *    allocates device memory.  The library owns its code-object handles,
- *    loaded once per device on first use (or by txInit) and unloaded by
- *    txShutdown.
+ *    tx_dot_fp8_scaled may use device scratch that the library keeps per
+ *    (device, stream): fp32 split-K partial planes (at most 8 x M x N x 4
+ *    bytes) when the output tiles leave CUs idle, and zero-padded copies of
+ *    A and B when rows are not 16-byte aligned in a product of at least
+ *    2^30 multiply-adds.  The scratch is allocated stream-ordered
+ *    (hipMallocAsync on `stream`) the first time a stream needs it, grown
+ *    the same way, and reused by later calls, so steady-state calls
+ *    allocate nothing; requests above 512 MiB get a buffer per call.  If
+ *    the allocation fails they run without it.  No other entry point
+ *    allocates device memory.  txShutdown frees the kept scratch.  The
+ *    library owns its code-object handles, loaded once per device on first
+ *    use (or by txInit) and unloaded by txShutdown.
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
  *    and is stream-ordered; entry points return after enqueueing.
  *  - Errors are returned as tx_status (0 = success, as TP_SUCCESS in

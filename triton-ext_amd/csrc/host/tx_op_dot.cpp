@@ -88,8 +88,9 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 // they give at least one tile per CU (see kStripMaxN for a narrow column
 // tail); otherwise 256x128 tiles, and when those
 // still leave CUs idle, K is split (at most 8 ways, at least 8 K steps per
-// split) into fp32 partial planes in a stream-ordered workspace that the
-// `reduce` kernel sums, scales and rounds into C.
+// split) into fp32 partial planes in the library's stream scratch
+// (ScratchLease, slot 1) that the `reduce` kernel sums, scales and rounds
+// into C.
 // A narrow tail of columns past the last full 256-column block (at most
 // kStripMaxN) that would cost a whole extra round of 256x256 tiles is a
 // separate, second fast-path product (few tiles, so 256x128 with K split).
@@ -122,42 +123,35 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
   const int64_t tiles = tiles_m * ((args.N + 127) / 128);
   const int64_t ksteps = (k_bytes + 127) / 128;
   int64_t splits = std::min({kMaxSplits, cus / tiles, ksteps / kMinStepsPerSplit});
-  void *part = nullptr;
+  ScratchLease part;  // held until every launch using it is enqueued
   if (splits >= 2) {
     const int64_t per = (ksteps + splits - 1) / splits;
     splits = (ksteps + per - 1) / per;  // no empty split
     const size_t bytes = size_t(splits) * size_t(args.M) * size_t(args.N) * sizeof(float);
-    if (hipMallocAsync(&part, bytes, s) != hipSuccess) {
-      (void)hipGetLastError();  // no workspace: run unsplit
-      part = nullptr;
+    if (part.acquire(s, 1, bytes) != TX_SUCCESS) {
+      clear_error();  // no workspace: run unsplit
     } else {
       args.splits = int32_t(splits);
       args.ksteps_split = int32_t(per);
-      args.part = static_cast<float *>(part);
+      args.part = static_cast<float *>(part.ptr());
     }
   }
-  if (!part) return launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves);
-  tx_status st = launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves, int(args.splits));
-  if (st == TX_SUCCESS) {
-    hipFunction_t fn;
-    st = get_kernel(co, reduce, &fn);
-    if (st == TX_SUCCESS) {
-      const int64_t quads = args.M * ((args.N + 3) / 4);
-      const int64_t grid = std::min<int64_t>((quads + 255) / 256, cus * 16);
-      st = launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, reduce);
-    }
-  }
-  if (hipFreeAsync(part, s) != hipSuccess && st == TX_SUCCESS)
-    st = fail(TX_LAUNCH_ERROR, "%s: releasing the split-K workspace failed", base);
-  return st;
+  if (!part.ptr()) return launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves);
+  TX_TRY(launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves, int(args.splits)));
+  hipFunction_t fn;
+  TX_TRY(get_kernel(co, reduce, &fn));
+  const int64_t quads = args.M * ((args.N + 3) / 4);
+  const int64_t grid = std::min<int64_t>((quads + 255) / 256, cus * 16);
+  return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, reduce);
 }
 
 // Operands the fast path cannot take (rows not 16-byte aligned or K * size
 // not a multiple of 16 bytes) in a product of at least kPadMinWork
-// multiply-adds are first copied into zero-padded rows of a stream-ordered
-// workspace.  K is rounded up to a whole 128-byte step: the zeros add nothing
-// to the sums, every row starts on a 128-byte line (a row segment of a step
-// is then one cache line, not two), and no step needs the K-tail fill.
+// multiply-adds are first copied into zero-padded rows in the library's
+// stream scratch (ScratchLease, slot 0).  K is rounded up to a whole
+// 128-byte step: the zeros add nothing to the sums, every row starts on a
+// 128-byte line (a row segment of a step is then one cache line, not two),
+// and no step needs the K-tail fill.
 // Returns TX_UNSUPPORTED without launching anything when that is not
 // possible, and the caller takes the generic kernel.
 constexpr int64_t kPadMinWork = int64_t(1) << 30;
@@ -179,15 +173,15 @@ tx_status launch_padded(const char *base, const char *reduce, const char *pad, C
     return TX_UNSUPPORTED;
   const size_t a_bytes = size_t(args.M) * size_t(kp) * es;
   const size_t b_bytes = size_t(args.N) * size_t(kp) * es;
-  void *ws = nullptr;
-  if (hipMallocAsync(&ws, a_bytes + b_bytes, s) != hipSuccess) {
-    (void)hipGetLastError();
+  ScratchLease ws;  // held until every launch using it is enqueued
+  if (ws.acquire(s, 0, a_bytes + b_bytes) != TX_SUCCESS) {
+    clear_error();
     return TX_UNSUPPORTED;
   }
   hipFunction_t fn;
   tx_status st = get_kernel(co, pad, &fn);
   const int64_t cus = cu_count();
-  uint8_t *wa = static_cast<uint8_t *>(ws), *wb = wa + a_bytes;
+  uint8_t *wa = static_cast<uint8_t *>(ws.ptr()), *wb = wa + a_bytes;
   if (st == TX_SUCCESS) {
     tx_pad_args pa{args.A, wa, args.lda, kp, args.M, args.K, int32_t(kp),
                    pad_load_bytes(args.A, args.lda * es, int64_t(args.K) * es)};
@@ -208,8 +202,6 @@ tx_status launch_padded(const char *base, const char *reduce, const char *pad, C
     args.K = int32_t(kp);
     st = launch_fast(base, reduce, co, args, kp * es, es, s);
   }
-  if (hipFreeAsync(ws, s) != hipSuccess && st == TX_SUCCESS)
-    st = fail(TX_LAUNCH_ERROR, "%s: releasing the padded operands failed", base);
   return st;
 }
 

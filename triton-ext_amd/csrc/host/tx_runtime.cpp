@@ -8,11 +8,14 @@
 // device with hipModuleLoadData the first time an op runs there.
 #include "tx_runtime.h"
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
 
 // Embedded code objects (see the generated tx_embedded.S).
 extern "C" {
@@ -53,6 +56,11 @@ struct KernelSlot {
   hipFunction_t fn;
 };
 
+struct KeptScratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+
 struct DeviceState {
   std::once_flag once;
   tx_status status = TX_GENERIC_FAILURE;
@@ -62,6 +70,10 @@ struct DeviceState {
   std::mutex mu;
   KernelSlot kernels[kMaxKernels] = {};
   int num_kernels = 0;
+  // kept scratch buffers, keyed by (stream, slot); recursive so that one
+  // call can hold a lease on each slot
+  std::recursive_mutex scratch_mu;
+  std::map<std::pair<hipStream_t, int>, KeptScratch> scratch;
 };
 
 DeviceState g_devices[kMaxDevices];
@@ -164,6 +176,62 @@ tx_status get_kernel(CodeObject co, const char *name, hipFunction_t *out) {
   return TX_SUCCESS;
 }
 
+tx_status ScratchLease::acquire(hipStream_t stream, int slot, size_t bytes) {
+  DeviceState *st = nullptr;
+  tx_status s = device_state(&st);
+  if (s != TX_SUCCESS) return s;
+  if (lock_) return fail(TX_GENERIC_FAILURE, "scratch lease acquired twice");
+  st->scratch_mu.lock();
+  lock_ = &st->scratch_mu;
+  stream_ = stream;
+  if (bytes > kKeptScratch) {
+    hipError_t e = hipMallocAsync(&ptr_, bytes, stream);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      ptr_ = nullptr;
+      return fail(TX_GENERIC_FAILURE, "scratch of %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    own_ = true;
+    return TX_SUCCESS;
+  }
+  KeptScratch &k = st->scratch[{stream, slot}];
+  if (k.bytes < bytes) {
+    if (k.ptr && hipFreeAsync(k.ptr, stream) != hipSuccess) (void)hipGetLastError();
+    k.ptr = nullptr;
+    k.bytes = 0;
+    // round up so that slowly growing requests do not reallocate every call
+    const size_t want = std::min(kKeptScratch, (bytes + (size_t(4) << 20) - 1) / (size_t(4) << 20) * (size_t(4) << 20));
+    hipError_t e = hipMallocAsync(&k.ptr, want, stream);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      k.ptr = nullptr;
+      return fail(TX_GENERIC_FAILURE, "scratch of %zu bytes: %s", want, hipGetErrorString(e));
+    }
+    k.bytes = want;
+  }
+  ptr_ = k.ptr;
+  return TX_SUCCESS;
+}
+
+ScratchLease::~ScratchLease() {
+  if (own_ && ptr_ && hipFreeAsync(ptr_, stream_) != hipSuccess) (void)hipGetLastError();
+  if (lock_) static_cast<std::recursive_mutex *>(lock_)->unlock();
+}
+
+void release_all_scratch() {
+  for (int d = 0; d < kMaxDevices; ++d) {
+    DeviceState &st = g_devices[d];
+    std::lock_guard<std::recursive_mutex> lock(st.scratch_mu);
+    if (st.scratch.empty()) continue;
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(d) != hipSuccess) continue;
+    for (auto &kv : st.scratch)
+      if (kv.second.ptr && hipFree(kv.second.ptr) != hipSuccess) (void)hipGetLastError();
+    st.scratch.clear();
+    hipSetDevice(cur);
+  }
+}
+
 int cu_count() {
   DeviceState *st = nullptr;
   if (device_state(&st) != TX_SUCCESS) return 0;
@@ -201,6 +269,7 @@ TX_API tx_status txInit(void) {
 }
 
 TX_API void txShutdown(void) {
+  tx::release_all_scratch();
   for (int d = 0; d < tx::kMaxDevices; ++d) {
     tx::DeviceState &st = tx::g_devices[d];
     if (st.status != TX_SUCCESS) continue;

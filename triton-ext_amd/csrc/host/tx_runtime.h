@@ -41,6 +41,41 @@ tx_status launch(hipFunction_t fn, unsigned grid_x, unsigned grid_y,
 // Number of compute units of the current device (cached per device).
 int cu_count();
 
+// Stream-ordered device scratch for the ops that need a workspace.  The
+// library keeps one buffer per (device, stream, slot), up to kKeptScratch
+// bytes, and later calls on that stream reuse it, so steady-state calls
+// allocate nothing.  Growing a kept buffer frees the old one and allocates
+// the new one in stream order (hipFreeAsync / hipMallocAsync on the stream):
+// work already enqueued keeps its memory.  Larger requests get a buffer of
+// their own, freed in stream order when the lease ends.  A lease holds the
+// device's scratch lock from acquire() until it is destroyed, so the caller
+// enqueues every launch that uses the buffer while holding it; two calls on
+// one stream from different threads therefore never see one buffer change
+// under them.  (A stream handle that is destroyed and handed out again keeps
+// its predecessor's buffer; its work must have finished, as for any reuse of
+// memory.)  txShutdown frees the kept buffers.
+constexpr size_t kKeptScratch = size_t(512) << 20;
+
+class ScratchLease {
+ public:
+  ScratchLease() = default;
+  ScratchLease(const ScratchLease &) = delete;
+  ScratchLease &operator=(const ScratchLease &) = delete;
+  ~ScratchLease();
+  // `slot` (0 or 1) separates the buffers one call needs at the same time.
+  tx_status acquire(hipStream_t stream, int slot, size_t bytes);
+  void *ptr() const { return ptr_; }
+
+ private:
+  void *ptr_ = nullptr;
+  hipStream_t stream_ = nullptr;
+  bool own_ = false;    // a per-call buffer, freed by the destructor
+  void *lock_ = nullptr;  // the device's scratch mutex while held
+};
+
+// Free every kept scratch buffer of every device (txShutdown).
+void release_all_scratch();
+
 // True if p is aligned to `bytes`.
 inline bool aligned(const void *p, size_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
