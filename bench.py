@@ -15,11 +15,14 @@ milliseconds of sustained load, and an op timed straight after the idle host
 work that builds its inputs would be timed on the clock ramp.  Then come W
 untimed launches, then exactly K launches between two HIP events on the
 stream the op is launched on (torch's current stream, which tx passes to the
-library), with torch.cuda.synchronize() before and after.  Inputs rotate over enough buffer sets that the working set
-exceeds twice the 256 MB Infinity Cache for the memory-bound ops.
+library), with torch.cuda.synchronize() before and after.  Inputs rotate
+over enough buffer sets that the working set exceeds twice the 256 MB
+Infinity Cache for the memory-bound ops.
 
 cpu_baseline: the CPU oracle (oracle/, a C port of the path's semantics,
-OpenMP over all host cores) timed on a bounded sample of the same workload.
+OpenMP over all host cores) timed on bounded samples of the same workloads:
+rows of the 8192^3 GEMM for CPU_GEMM_S seconds and whole 16 Mi-value
+encodes for CPU_CONVERT_S seconds.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -178,6 +181,10 @@ def bench_gemv(tx, torch, M, steps, warmup, N=14336, K=4096, group=128):
 
 
 # ------------------------------------------------------------ CPU baseline
+CPU_GEMM_S = 8.0
+CPU_CONVERT_S = 5.0
+
+
 def cpu_baseline():
     """Time the oracle (C, OpenMP) on bounded samples of the two headline workloads."""
     import numpy as np
@@ -190,7 +197,8 @@ def cpu_baseline():
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         pass
-    # fp8 GEMM: R rows of C for the 8192^3 problem (2 * R * N * K flops)
+    # fp8 GEMM: batches of R rows of C for the 8192^3 problem (2 * R * N * K
+    # flops each), repeated until CPU_GEMM_S seconds have passed
     M = N = K = 8192
     R = 64
     g = np.random.default_rng(1)
@@ -198,21 +206,23 @@ def cpu_baseline():
     bq = np.ascontiguousarray(workloads.fp8_gemm_input(16, N, K)[2])
     sa = np.ones(R, np.float32)
     sb = np.ones(N, np.float32)
-    t0 = time.perf_counter()
-    oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, R, nthreads=cores)
+    rows, t0 = 0, time.perf_counter()
+    while rows == 0 or (time.perf_counter() - t0 < CPU_GEMM_S and rows < M):
+        oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, R, nthreads=cores)
+        rows += R
     dt = time.perf_counter() - t0
-    gemm_tflops = 2.0 * R * N * K / dt / 1e12
-    # fp8 convert: the full 16 Mi-value encode, repeated for a few seconds
+    gemm_tflops = 2.0 * rows * N * K / dt / 1e12
+    # fp8 convert: the full 16 Mi-value encode, repeated for CPU_CONVERT_S seconds
     x = workloads.fp8_input()
     reps, t0 = 0, time.perf_counter()
-    while reps < 3 or time.perf_counter() - t0 < 3.0:
+    while reps < 3 or time.perf_counter() - t0 < CPU_CONVERT_S:
         oracle.encode(x, 1, False, nthreads=cores)
         reps += 1
     dt_conv = (time.perf_counter() - t0) / reps
     return {
         "value": gemm_tflops, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-        "sample": f"oracle fp8 scaled GEMM, {R} of 8192 rows of M=N=K=8192 "
-                  f"({2.0 * R * N * K / 1e9:.1f} GFLOP in {dt:.2f} s, fp64 accumulate)",
+        "sample": f"oracle fp8 scaled GEMM, {rows} of 8192 rows of M=N=K=8192 "
+                  f"({2.0 * rows * N * K / 1e9:.0f} GFLOP in {dt:.1f} s, fp64 accumulate)",
         "fp8_convert": {"value": 5.0 * x.size / dt_conv / 1e9, "unit": "GB/s",
                         "sample": f"oracle encode e4m3fn RNE of 16,777,216 values x {reps}"},
     }
