@@ -72,7 +72,7 @@ typedef enum tx_status {
 } tx_status;
 
 /* Element types (the tt dtypes of the path: tl.float32, tl.float8e4nv,
- * tl.float8e5, tl.bfloat16, tl.int32; utility.py:92-105 names the fp8 ones
+ * tl.float8e5, tl.bfloat16, tl.float16, tl.int32; utility.py:92-105 names the fp8 ones
  * "e4m3" and "e5m2"). */
 typedef enum tx_dtype {
   TX_F32 = 0,
@@ -80,7 +80,8 @@ typedef enum tx_dtype {
   TX_FP8E5M2 = 2,
   TX_BF16 = 3,
   TX_I32 = 4,
-  TX_U32 = 5
+  TX_U32 = 5,
+  TX_F16 = 6
 } tx_dtype;
 
 /* Rounding modes, numbered as the rounding operand of
@@ -176,19 +177,43 @@ TX_API const char *txVersion(void);
  * semantic.py:807-827; passed through at uTLXConversionPatterns.cpp:577;
  * re-created with a rounding attribute by createFpToFpWithRbits,
  * ops/NewOps.cpp:249-303).
- *  - TX_F32 -> TX_FP8E4M3FN / TX_FP8E5M2 with rounding TX_RTNE or TX_RTZ.
- *    saturate = 0: overflow and +-Inf become NaN (e4m3fn) or +-Inf (e5m2).
+ *  - TX_F32 -> TX_FP8E4M3FN / TX_FP8E5M2 / TX_F16 / TX_BF16 with rounding
+ *    TX_RTNE or TX_RTZ.
+ *    saturate = 0: overflow and +-Inf become NaN (e4m3fn) or +-Inf (e5m2,
+ *    fp16, bf16); round toward zero keeps finite values finite.
  *    saturate = 1: the reference's clamp(x, -max, max)-then-convert idiom
  *    (mxfp8_utils.py:17-21, 36-38): overflow and +-Inf become +-max, NaN
- *    stays NaN.  NaN input gives 0x7F with the input's sign bit.
+ *    stays NaN.  NaN input gives 0x7F (fp8), 0x7E00 (fp16) or 0x7FC0
+ *    (bf16) with the input's sign bit.
  *  - TX_FP8E4M3FN / TX_FP8E5M2 -> TX_F32 (exact; NaN codes give 0x7FC00000
  *    with the code's sign).
- * TX_RS needs random bits: use tx_fp_to_fp_with_rbits.
+ * TX_RS needs random bits: use tx_fp_to_fp_with_rbits (TX_UNSUPPORTED here).
  */
 TX_API tx_status tx_fp_to_fp(const void *src, tx_dtype src_type, void *dst,
                              tx_dtype dst_type, int64_t n,
                              tx_rounding rounding, int saturate,
                              tx_stream_t stream);
+
+/*
+ * tt.fp_to_fp with a random-bits operand, as built by
+ * utlx_fp_to_fp_with_rbits (createFpToFpWithRbits, ops/NewOps.cpp:249-303;
+ * used by tlx.stoch_round, test_tlx.py:5138-5153).  With TX_RTNE / TX_RTZ it
+ * is tx_fp_to_fp (rbits unused, may be NULL).  With TX_RS (stochastic
+ * rounding): src_type must be TX_F32 and dst_type one of TX_F16, TX_BF16,
+ * TX_FP8E5M2, TX_FP8E4M3FN (others: TX_INVALID_ARGUMENT, as the reference's
+ * stoch_round raises, test_tlx.py:5291-5329); rbits holds one 32-bit word
+ * per element; the result always saturates (the reference lowers it to
+ * cvt.rs.satfinite, test_tlx.py:5182) and `saturate` is ignored.  Each
+ * element becomes its round-toward-zero value, moved one step away from
+ * zero iff rbits[i] + floor(frac * 2^32) >= 2^32, frac being the fraction of
+ * an ulp that truncation dropped: with uniform random bits the result rounds
+ * up with probability frac (to 2^-32) and is unbiased.  NaN stays NaN (as
+ * for tx_fp_to_fp); +-Inf and |x| above max give +-max.
+ */
+TX_API tx_status tx_fp_to_fp_with_rbits(const void *src, tx_dtype src_type, void *dst,
+                                        tx_dtype dst_type, const uint32_t *rbits,
+                                        int64_t n, tx_rounding rounding, int saturate,
+                                        tx_stream_t stream);
 
 /*
  * tt.atomic_rmw in scatter form: for every i < n with mask[i] != 0 (mask may

@@ -20,7 +20,10 @@ _LIB_PATH = os.path.join(_HERE, "libtxoracle.so")
 
 E4M3FN = 1
 E5M2 = 2
+BF16 = 3
+F16 = 6
 MAX_FINITE = {E4M3FN: 448.0, E5M2: 57344.0}
+CODE_DTYPE = {E4M3FN: np.uint8, E5M2: np.uint8, BF16: np.uint16, F16: np.uint16}
 
 _lib = None
 
@@ -62,6 +65,10 @@ def lib():
                                                I, I, I64, I64, P, P, I]
         L.txo_gemv_fp8_dequant.argtypes = [P, I64, P, I64, P, I64, I64, I64,
                                            I64, I64, I, P, P, I]
+        L.txo_encode_fmt.argtypes = [P, P, I64, I, I, I, I]
+        L.txo_encode_fmt.restype = I
+        L.txo_round_rs.argtypes = [P, P, P, I64, I, I]
+        L.txo_round_rs.restype = I
         L.txo_init()
         _lib = L
     return _lib
@@ -106,6 +113,30 @@ def encode1(x: float, fmt: int, sat: bool) -> int:
 
 def decode1(code: int, fmt: int) -> float:
     return float(lib().txo_decode1(fmt, code))
+
+
+# ------------------------------------------------- any format, rs rounding
+def encode_fmt(x, fmt: int, rtz: bool = False, sat: bool = False, nthreads: int = 0) -> np.ndarray:
+    """fp32 -> codes of format fmt (E4M3FN, E5M2: uint8; BF16, F16: uint16),
+    round to nearest even or toward zero, optionally saturating."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, CODE_DTYPE[fmt])
+    if lib().txo_encode_fmt(_p(x), _p(out), x.size, fmt, int(bool(rtz)), int(bool(sat)), nthreads):
+        raise ValueError(f"format {fmt}")
+    return out
+
+
+def round_rs(x, rbits, fmt: int, nthreads: int = 0) -> np.ndarray:
+    """fp32 -> codes of format fmt with stochastic rounding (one uint32 of
+    random bits per element; definition in tx_oracle.c)."""
+    x = _c(x, np.float32)
+    r = _c(rbits, np.uint32)
+    if r.shape != x.shape:
+        raise ValueError("rbits must match x")
+    out = np.empty(x.shape, CODE_DTYPE[fmt])
+    if lib().txo_round_rs(_p(x), _p(r), _p(out), x.size, fmt, nthreads):
+        raise ValueError(f"format {fmt}")
+    return out
 
 
 # ----------------------------------------------------------------- scatter

@@ -1,4 +1,5 @@
-// tt.fp_to_fp entry point (fp32 <-> fp8) and its table registration.
+// tt.fp_to_fp entry points (fp32 <-> fp8, fp32 -> fp16 / bf16, stochastic
+// rounding with random bits) and their table registration.
 //
 // Reference: tt.fp_to_fp is emitted by semantic.cast (semantic.py:807-827,
 // default rounding RTNE at :809), passed through the plugin's conversion
@@ -19,12 +20,22 @@ constexpr unsigned kBlock = 256;
 constexpr int64_t kChunk = 4096;  // elements per block step of the vector kernels
 
 const char *fmt_name(tx_dtype t) {
-  return t == TX_FP8E4M3FN ? "e4m3fn" : "e5m2";
+  switch (t) {
+    case TX_FP8E4M3FN: return "e4m3fn";
+    case TX_FP8E5M2: return "e5m2";
+    case TX_BF16: return "bf16";
+    case TX_F16: return "f16";
+    default: return nullptr;
+  }
 }
 
+bool is_fp8(tx_dtype t) { return t == TX_FP8E4M3FN || t == TX_FP8E5M2; }
+bool is_16(tx_dtype t) { return t == TX_BF16 || t == TX_F16; }
+
 tx_status run(const char *vec_name, const char *tail_name, const void *src,
-              void *dst, int64_t n, bool vec_ok, hipStream_t stream) {
-  tx_fp8_codec_args args{src, dst, 0, n};
+              void *dst, int64_t n, bool vec_ok, hipStream_t stream,
+              const uint32_t *rbits = nullptr) {
+  tx_fp8_codec_args args{src, dst, 0, n, rbits};
   int64_t n_vec = vec_ok ? (n / kChunk) * kChunk : 0;
   const int cus = cu_count();
   if (n_vec > 0) {
@@ -56,11 +67,11 @@ static tx_status fp_to_fp(const void *src, tx_dtype src_type, void *dst,
   if (n < 0) return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: n = %lld < 0", (long long)n);
   if (n == 0) return TX_SUCCESS;
   if (!src || !dst) return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: NULL buffer");
-  const bool src_fp8 = src_type == TX_FP8E4M3FN || src_type == TX_FP8E5M2;
-  const bool dst_fp8 = dst_type == TX_FP8E4M3FN || dst_type == TX_FP8E5M2;
+  const bool src_fp8 = is_fp8(src_type);
+  const bool dst_fp8 = is_fp8(dst_type);
   hipStream_t s = static_cast<hipStream_t>(stream);
   char vec[64], tail[64];
-  if (src_type == TX_F32 && dst_fp8) {
+  if (src_type == TX_F32 && (dst_fp8 || is_16(dst_type))) {
     if (rounding == TX_RS)
       return fail(TX_UNSUPPORTED,
                   "tx_fp_to_fp: stochastic rounding needs random bits "
@@ -69,9 +80,10 @@ static tx_status fp_to_fp(const void *src, tx_dtype src_type, void *dst,
       return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: rounding %d", int(rounding));
     const char *r = rounding == TX_RTZ ? "rtz" : "rtne";
     const char *sat = saturate ? "_sat" : "";
-    std::snprintf(vec, sizeof vec, "tx_fp8_encode_%s_%s%s_vec", fmt_name(dst_type), r, sat);
-    std::snprintf(tail, sizeof tail, "tx_fp8_encode_%s_%s%s_tail", fmt_name(dst_type), r, sat);
-    const bool vec_ok = aligned(src, 16) && aligned(dst, 4);
+    const char *kind = dst_fp8 ? "fp8_encode" : "cvt_f32";
+    std::snprintf(vec, sizeof vec, "tx_%s_%s_%s%s_vec", kind, fmt_name(dst_type), r, sat);
+    std::snprintf(tail, sizeof tail, "tx_%s_%s_%s%s_tail", kind, fmt_name(dst_type), r, sat);
+    const bool vec_ok = aligned(src, 16) && aligned(dst, dst_fp8 ? 4 : 8);
     return run(vec, tail, src, dst, n, vec_ok, s);
   }
   if (src_fp8 && dst_type == TX_F32) {
@@ -84,12 +96,42 @@ static tx_status fp_to_fp(const void *src, tx_dtype src_type, void *dst,
               int(src_type), int(dst_type));
 }
 
+// Stochastic rounding takes a float32 source and an fp16, bf16, e5m2 or
+// e4m3fn destination (the reference's stoch_round accepts exactly these and
+// raises otherwise, test_tlx.py:5291-5329) and one 32-bit word of random
+// bits per element; it always saturates (the reference lowers it to
+// cvt.rs.satfinite, test_tlx.py:5182).  Other roundings ignore rbits.
+static tx_status fp_to_fp_rbits(const void *src, tx_dtype src_type, void *dst,
+                                tx_dtype dst_type, const uint32_t *rbits, int64_t n,
+                                tx_rounding rounding, int saturate, tx_stream_t stream) {
+  if (rounding != TX_RS)
+    return fp_to_fp(src, src_type, dst, dst_type, n, rounding, saturate, stream);
+  if (n < 0) return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp_with_rbits: n = %lld < 0", (long long)n);
+  if (src_type != TX_F32)
+    return fail(TX_INVALID_ARGUMENT,
+                "tx_fp_to_fp_with_rbits: stochastic rounding takes a float32 source (got %d)",
+                int(src_type));
+  if (!is_fp8(dst_type) && !is_16(dst_type))
+    return fail(TX_INVALID_ARGUMENT,
+                "tx_fp_to_fp_with_rbits: stochastic rounding is supported to fp16, bf16, e5m2 "
+                "and e4m3fn only (got %d)", int(dst_type));
+  if (n == 0) return TX_SUCCESS;
+  if (!src || !dst || !rbits)
+    return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp_with_rbits: NULL buffer");
+  char vec[64], tail[64];
+  std::snprintf(vec, sizeof vec, "tx_cvt_f32_%s_rs_vec", fmt_name(dst_type));
+  std::snprintf(tail, sizeof tail, "tx_cvt_f32_%s_rs_tail", fmt_name(dst_type));
+  const bool vec_ok = aligned(src, 16) && aligned(rbits, 16) && aligned(dst, is_fp8(dst_type) ? 4 : 8);
+  return run(vec, tail, src, dst, n, vec_ok, static_cast<hipStream_t>(stream), rbits);
+}
+
 // Table form: operands = {dst (result slot), src, n, src_type, dst_type,
-// rounding, saturate}.
+// rounding, saturate[, rbits]}; rbits as in createFpToFpWithRbits, an
+// optional operand (ops/NewOps.cpp:253-257).
 static tx_status fp_to_fp_op(tx_value *v, size_t count, tx_stream_t stream) {
   Operands o{v, count, "tt.fp_to_fp"};
-  TX_TRY(o.need(7));
-  void *dst, *src;
+  if (count != 8) TX_TRY(o.need(7));
+  void *dst, *src, *rbits = nullptr;
   int64_t n, st, dt, rnd, sat;
   TX_TRY(o.ptr(0, &dst));
   TX_TRY(o.ptr(1, &src));
@@ -98,15 +140,26 @@ static tx_status fp_to_fp_op(tx_value *v, size_t count, tx_stream_t stream) {
   TX_TRY(o.integer(4, &dt));
   TX_TRY(o.integer(5, &rnd));
   TX_TRY(o.integer(6, &sat));
-  return fp_to_fp(src, tx_dtype(st), dst, tx_dtype(dt), n, tx_rounding(rnd),
-                  int(sat), stream);
+  if (count == 8) TX_TRY(o.ptr(7, &rbits));
+  return fp_to_fp_rbits(src, tx_dtype(st), dst, tx_dtype(dt), static_cast<const uint32_t *>(rbits),
+                        n, tx_rounding(rnd), int(sat), stream);
 }
 
 static const bool registered = register_op(
     "tt.fp_to_fp", fp_to_fp_op,
-    "dst(result), src, n:i64, src_type:i32, dst_type:i32, rounding:i32, saturate:i32");
+    "dst(result), src, n:i64, src_type:i32, dst_type:i32, rounding:i32, saturate:i32"
+    "[, rbits:u32*]");
 
 }  // namespace tx
+
+extern "C" TX_API tx_status tx_fp_to_fp_with_rbits(const void *src, tx_dtype src_type,
+                                                   void *dst, tx_dtype dst_type,
+                                                   const uint32_t *rbits, int64_t n,
+                                                   tx_rounding rounding, int saturate,
+                                                   tx_stream_t stream) {
+  tx::clear_error();
+  return tx::fp_to_fp_rbits(src, src_type, dst, dst_type, rbits, n, rounding, saturate, stream);
+}
 
 extern "C" TX_API tx_status tx_fp_to_fp(const void *src, tx_dtype src_type,
                                         void *dst, tx_dtype dst_type, int64_t n,

@@ -26,25 +26,45 @@
 //  int->float conversion times a power of two; NaN codes give 0x7FC00000
 //  and e5m2 Inf codes give Inf, each with the code's sign.
 //
-// Semantics follow tt.fp_to_fp (semantic.py:807-827, default RTNE at :809)
-// and the reference's saturating idiom clamp-then-convert
-// (mxfp8_utils.py:17-21, 36-38).
+// The same integer encoders, with the format's parameters, also produce
+// fp16 and bf16 (fp16: quantum 2^-24 below 2^-14; bf16: fp32's exponent
+// range, so only fp32 denormals take the subnormal path).  fp16 / bf16 NaN
+// outputs are the canonical quiet NaN (0x7E00 / 0x7FC0) with the input's
+// sign.
+//
+//  stochastic rounding (rounding "rs", fp32 source, one 32-bit word r of
+//  random bits per element, always saturating): the round-toward-zero code,
+//  moved one step away from zero iff r + floor(frac * 2^32) carries out of
+//  32 bits, frac being the dropped fraction of an ulp.  frac * 2^32 is read
+//  straight off the dropped bits: in the normal range they are the low
+//  23 - m bits of the fp32 encoding, in the subnormal range the low s bits
+//  of the 24-bit significand (s bits below the quantum).  Codes at max,
+//  +-Inf and |x| above max give +-max; NaN gives NaN.
+//
+// Semantics follow tt.fp_to_fp (semantic.py:807-827, default RTNE at :809;
+// rounding operand 0 rtne, 1 rtz, 2 rs with random bits,
+// createFpToFpWithRbits at ops/NewOps.cpp:249-303) and the reference's
+// saturating idiom clamp-then-convert (mxfp8_utils.py:17-21, 36-38).
 #include "tx_device.h"
 
 namespace {
 
-enum { E4M3FN = 1, E5M2 = 2 };
+// Format ids as tx_dtype.
+enum { E4M3FN = 1, E5M2 = 2, BF16 = 3, F16 = 6 };
 
 template <int FMT>
 struct Fp8Format {
-  static constexpr int M = (FMT == E4M3FN) ? 3 : 2;           // mantissa bits
-  static constexpr int BIAS = (FMT == E4M3FN) ? 7 : 15;
-  static constexpr uint32_t MAXC = (FMT == E4M3FN) ? 0x7Eu : 0x7Bu;
-  static constexpr uint32_t OVF = (FMT == E4M3FN) ? 0x7Fu : 0x7Cu;
+  static constexpr int M = FMT == E4M3FN ? 3 : FMT == E5M2 ? 2 : FMT == BF16 ? 7 : 10;  // mantissa bits
+  static constexpr int BIAS = FMT == E4M3FN ? 7 : FMT == BF16 ? 127 : 15;
+  static constexpr int W = (FMT == BF16 || FMT == F16) ? 16 : 8;                    // code bits
+  static constexpr uint32_t MAXC = FMT == E4M3FN ? 0x7Eu : FMT == E5M2 ? 0x7Bu : FMT == BF16 ? 0x7F7Fu : 0x7BFFu;
+  static constexpr uint32_t OVF = FMT == E4M3FN ? 0x7Fu : FMT == E5M2 ? 0x7Cu : FMT == BF16 ? 0x7F80u : 0x7C00u;
+  static constexpr uint32_t NANC = W == 8 ? 0x7Fu : FMT == BF16 ? 0x7FC0u : 0x7E00u;
   static constexpr int SH = 23 - M;                           // dropped bits
   static constexpr uint32_t MIN_NORM_BITS = uint32_t(128 - BIAS) << 23;
   static constexpr uint32_t REBIAS = uint32_t(127 - BIAS) << 23;
   static constexpr uint32_t MAGIC_BITS = uint32_t(127 + 24 - BIAS - M) << 23;
+  static __device__ __forceinline__ uint32_t sign(uint32_t u) { return (u >> (32 - W)) & (1u << (W - 1)); }
 };
 
 // fp32 bits -> fp8 code, round to nearest even.
@@ -58,8 +78,8 @@ __device__ __forceinline__ uint32_t encode_rtne(uint32_t u) {
   const uint32_t sub = __float_as_uint(f) - F::MAGIC_BITS;
   uint32_t code = (a < F::MIN_NORM_BITS) ? sub : nrm;
   code = min(code, SAT ? F::MAXC : F::OVF);
-  if (SAT || FMT == E5M2) code = (a > 0x7F800000u) ? 0x7Fu : code;
-  return code | ((u >> 24) & 0x80u);
+  code = (a > 0x7F800000u) ? F::NANC : code;
+  return code | F::sign(u);
 }
 
 // fp32 bits -> fp8 code, round toward zero.
@@ -75,8 +95,29 @@ __device__ __forceinline__ uint32_t encode_rtz(uint32_t u) {
   uint32_t code = (a < F::MIN_NORM_BITS) ? sub : nrm;
   code = min(code, F::MAXC);  // finite values never round away from zero
   if (a == 0x7F800000u) code = SAT ? F::MAXC : F::OVF;
-  if (a > 0x7F800000u) code = 0x7Fu;
-  return code | ((u >> 24) & 0x80u);
+  if (a > 0x7F800000u) code = F::NANC;
+  return code | F::sign(u);
+}
+
+// fp32 bits -> code, stochastic rounding with random word r (saturating).
+template <int FMT>
+__device__ __forceinline__ uint32_t round_rs(uint32_t u, uint32_t r) {
+  using F = Fp8Format<FMT>;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  const uint32_t code = encode_rtz<FMT, true>(u) & ~(1u << (F::W - 1));
+  // floor(frac * 2^32) from the dropped bits
+  uint32_t thr;
+  if (a >= F::MIN_NORM_BITS) {
+    thr = (a & ((1u << F::SH) - 1u)) << (32 - F::SH);
+  } else {
+    const uint32_t e = a >> 23;
+    const uint64_t sig = (a & 0x7FFFFFu) | (e ? 0x800000u : 0u);
+    const uint32_t s = uint32_t(151 - F::BIAS - F::M) - (e ? e : 1u);  // >= 24 - M
+    thr = s <= 32u ? uint32_t((sig & ((uint64_t(1) << s) - 1u)) << (32u - s))
+                   : (s - 32u < 24u ? uint32_t(sig >> (s - 32u)) : 0u);
+  }
+  const bool up = (uint64_t(r) + thr) >> 32 != 0 && code < F::MAXC && a < 0x7F800000u;
+  return (code + (up ? 1u : 0u)) | F::sign(u);
 }
 
 template <int FMT, bool SAT, bool RTZ>
@@ -175,7 +216,85 @@ __device__ __forceinline__ void decode_tail(const tx_fp8_codec_args &a) {
     dst[i] = decode<FMT>(src[i]);
 }
 
+// fp32 bits -> code of format FMT; MODE 0 rtne, 1 rtz, 2 rs (r random bits).
+template <int FMT, int MODE, bool SAT>
+__device__ __forceinline__ uint32_t convert(uint32_t u, uint32_t r) {
+  if constexpr (MODE == 2) return round_rs<FMT>(u, r);
+  else if constexpr (MODE == 1) return encode_rtz<FMT, SAT>(u);
+  else return encode_rtne<FMT, SAT>(u);
+}
+
+// Vector conversion: [start, n) with (n - start) a multiple of kChunk, src
+// (and for rs the random bits) 16-byte aligned, dst 4-byte (8-bit codes) or
+// 8-byte (16-bit codes) aligned, start a multiple of 4.
+template <int FMT, int MODE, bool SAT>
+__device__ __forceinline__ void cvt_vec(const tx_fp8_codec_args &a) {
+  using F = Fp8Format<FMT>;
+  const txd::u32x4 *src = reinterpret_cast<const txd::u32x4 *>(a.src) + a.start / 4;
+  const txd::u32x4 *rb = reinterpret_cast<const txd::u32x4 *>(a.rbits) + a.start / 4;
+  const int64_t nchunks = (a.n - a.start) / kChunk;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t w0 = c * (kChunk / 4) + threadIdx.x;
+    txd::u32x4 v[kVecPerThread], r[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      v[j] = __builtin_nontemporal_load(src + w0 + j * kBlock);
+      if constexpr (MODE == 2) r[j] = __builtin_nontemporal_load(rb + w0 + j * kBlock);
+      else r[j] = txd::u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      const uint32_t c0 = convert<FMT, MODE, SAT>(v[j].x, r[j].x);
+      const uint32_t c1 = convert<FMT, MODE, SAT>(v[j].y, r[j].y);
+      const uint32_t c2 = convert<FMT, MODE, SAT>(v[j].z, r[j].z);
+      const uint32_t c3 = convert<FMT, MODE, SAT>(v[j].w, r[j].w);
+      if constexpr (F::W == 8) {
+        uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst) + a.start / 4;
+        __builtin_nontemporal_store(c0 | (c1 << 8) | (c2 << 16) | (c3 << 24), dst + w0 + j * kBlock);
+      } else {
+        txd::u32x2 *dst = reinterpret_cast<txd::u32x2 *>(a.dst) + a.start / 4;
+        __builtin_nontemporal_store(txd::u32x2{c0 | (c1 << 16), c2 | (c3 << 16)}, dst + w0 + j * kBlock);
+      }
+    }
+  }
+}
+
+template <int FMT, int MODE, bool SAT>
+__device__ __forceinline__ void cvt_tail(const tx_fp8_codec_args &a) {
+  using F = Fp8Format<FMT>;
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(a.src);
+  for (int64_t i = a.start + int64_t(blockIdx.x) * kBlock + threadIdx.x; i < a.n;
+       i += int64_t(gridDim.x) * kBlock) {
+    const uint32_t code = convert<FMT, MODE, SAT>(src[i], MODE == 2 ? a.rbits[i] : 0u);
+    if constexpr (F::W == 8) reinterpret_cast<uint8_t *>(a.dst)[i] = uint8_t(code);
+    else reinterpret_cast<uint16_t *>(a.dst)[i] = uint16_t(code);
+  }
+}
+
 }  // namespace
+
+// fp32 -> fp16 / bf16 (rtne, rtz, saturating or not) and fp32 -> any of the
+// four formats with stochastic rounding.
+#define TX_CVT_KERNELS(NAME, FMT, MODE, SAT)                                                    \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_cvt_f32_##NAME##_vec(const tx_fp8_codec_args a) {  \
+    cvt_vec<FMT, MODE, SAT>(a);                                                                 \
+  }                                                                                             \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_cvt_f32_##NAME##_tail(const tx_fp8_codec_args a) { \
+    cvt_tail<FMT, MODE, SAT>(a);                                                                \
+  }
+
+TX_CVT_KERNELS(bf16_rtne, BF16, 0, false)
+TX_CVT_KERNELS(bf16_rtne_sat, BF16, 0, true)
+TX_CVT_KERNELS(bf16_rtz, BF16, 1, false)
+TX_CVT_KERNELS(bf16_rtz_sat, BF16, 1, true)
+TX_CVT_KERNELS(f16_rtne, F16, 0, false)
+TX_CVT_KERNELS(f16_rtne_sat, F16, 0, true)
+TX_CVT_KERNELS(f16_rtz, F16, 1, false)
+TX_CVT_KERNELS(f16_rtz_sat, F16, 1, true)
+TX_CVT_KERNELS(e4m3fn_rs, E4M3FN, 2, true)
+TX_CVT_KERNELS(e5m2_rs, E5M2, 2, true)
+TX_CVT_KERNELS(bf16_rs, BF16, 2, true)
+TX_CVT_KERNELS(f16_rs, F16, 2, true)
 
 #define TX_ENCODE_KERNELS(NAME, FMT, SAT, RTZ)                                      \
   TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_encode_##NAME##_vec(              \

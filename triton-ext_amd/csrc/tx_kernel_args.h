@@ -16,6 +16,7 @@ typedef struct tx_fp8_codec_args {
   void *dst;
   int64_t start; /* first element this launch handles */
   int64_t n;     /* one past the last element this launch handles */
+  const uint32_t *rbits; /* stochastic rounding: one random word per element */
 } tx_fp8_codec_args;
 
 /* scatter-reduce */

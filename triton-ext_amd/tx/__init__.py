@@ -26,7 +26,7 @@ from . import _lib
 from ._lib import TxError, check, lib
 
 __all__ = [
-    "TxError", "fp_to_fp", "atomic_rmw", "dot", "matmul", "dot_scaled_rowcol",
+    "TxError", "fp_to_fp", "stoch_round", "atomic_rmw", "dot", "matmul", "dot_scaled_rowcol",
     "gemv_fp8_dequant", "plugin_info", "invoke", "get_fp8_format_name",
     "version", "init", "RTNE", "RTZ", "RS",
 ]
@@ -39,6 +39,7 @@ _TX_DTYPE = {
     torch.float8_e4m3fn: _lib.FP8E4M3FN,
     torch.float8_e5m2: _lib.FP8E5M2,
     torch.bfloat16: _lib.BF16,
+    torch.float16: _lib.F16,
     torch.int32: _lib.I32,
     torch.uint32: _lib.U32,
 }
@@ -88,14 +89,18 @@ def _on_gpu(*ts):
 
 # --------------------------------------------------------------------------
 def fp_to_fp(x: torch.Tensor, dtype, rounding="rtne", saturate: bool = False,
-             out: torch.Tensor | None = None) -> torch.Tensor:
-    """tt.fp_to_fp: fp32 -> fp8 (e4m3fn / e5m2) or fp8 -> fp32, elementwise.
+             out: torch.Tensor | None = None, rbits: torch.Tensor | None = None) -> torch.Tensor:
+    """tt.fp_to_fp, elementwise: fp32 -> fp8 (e4m3fn / e5m2), fp16 or bf16, or
+    fp8 -> fp32.
 
-    rounding: "rtne" (Triton's default downcast, semantic.py:809) or "rtz".
+    rounding: "rtne" (Triton's default downcast, semantic.py:809), "rtz", or
+    "rs" (stochastic, fp32 source only, needs rbits: one int32/uint32 of random
+    bits per element, as utlx_fp_to_fp_with_rbits, ops/NewOps.cpp:249-303;
+    always saturating).
     saturate: the reference's clamp(x, -max, max)-then-convert idiom
-    (mxfp8_utils.py:36-38); without it overflow gives NaN (e4m3fn) / Inf (e5m2).
+    (mxfp8_utils.py:36-38); without it overflow gives NaN (e4m3fn) / Inf.
     """
-    _on_gpu(x, out)
+    _on_gpu(x, out, rbits)
     if not x.is_contiguous():
         raise ValueError("fp_to_fp needs a contiguous input")
     if x.dtype not in _TX_DTYPE or dtype not in _TX_DTYPE:
@@ -104,9 +109,25 @@ def fp_to_fp(x: torch.Tensor, dtype, rounding="rtne", saturate: bool = False,
         out = torch.empty(x.shape, dtype=dtype, device=x.device)
     elif out.dtype != dtype or out.numel() != x.numel() or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor of the target dtype and size")
-    check(lib.tx_fp_to_fp(_ptr(x), _TX_DTYPE[x.dtype], _ptr(out), _TX_DTYPE[dtype],
-                          x.numel(), _ROUNDING[rounding], int(bool(saturate)), _stream(x)))
+    if rbits is None:
+        check(lib.tx_fp_to_fp(_ptr(x), _TX_DTYPE[x.dtype], _ptr(out), _TX_DTYPE[dtype],
+                              x.numel(), _ROUNDING[rounding], int(bool(saturate)), _stream(x)))
+        return out
+    if rbits.dtype not in (torch.int32, torch.uint32) or rbits.numel() != x.numel() \
+            or not rbits.is_contiguous():
+        raise ValueError("rbits must be a contiguous int32/uint32 tensor, one word per element")
+    check(lib.tx_fp_to_fp_with_rbits(_ptr(x), _TX_DTYPE[x.dtype], _ptr(out), _TX_DTYPE[dtype],
+                                     _ptr(rbits), x.numel(), _ROUNDING[rounding],
+                                     int(bool(saturate)), _stream(x)))
     return out
+
+
+def stoch_round(x: torch.Tensor, dtype, rbits: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Stochastic rounding of fp32 x to dtype (float16, bfloat16, float8_e5m2,
+    float8_e4m3fn) with one 32-bit random word per element, as the
+    reference's tlx.stoch_round(x, dtype, rbits) (test_tlx.py:5138-5153)."""
+    return fp_to_fp(x, dtype, rounding="rs", saturate=True, out=out, rbits=rbits)
 
 
 def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor,

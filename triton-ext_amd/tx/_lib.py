@@ -26,7 +26,7 @@ STATUS_NAMES = {
 }
 
 # tx_dtype
-F32, FP8E4M3FN, FP8E5M2, BF16, I32, U32 = 0, 1, 2, 3, 4, 5
+F32, FP8E4M3FN, FP8E5M2, BF16, I32, U32, F16 = 0, 1, 2, 3, 4, 5, 6
 # tx_rounding (ops/NewOps.cpp:270-286 numbering)
 RTNE, RTZ, RS = 0, 1, 2
 # tx_rmw_op
@@ -39,7 +39,7 @@ VALUE_PTR, VALUE_INT = 0, 1
 EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
-    "tx_fp_to_fp", "tx_atomic_rmw_scatter", "tx_dot_bf16",
+    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
     "tx_dot_fp8_scaled", "tx_gemv_fp8_dequant",
 ]
 
@@ -111,6 +111,8 @@ def _load():
     L.txVersion.argtypes = []
     L.tx_fp_to_fp.argtypes = [P, I, P, I, I64, I, I, VP]
     L.tx_fp_to_fp.restype = I
+    L.tx_fp_to_fp_with_rbits.argtypes = [P, I, P, I, P, I64, I, I, VP]
+    L.tx_fp_to_fp_with_rbits.restype = I
     L.tx_atomic_rmw_scatter.argtypes = [P, I, I64, P, P, P, I64, I, P, VP]
     L.tx_atomic_rmw_scatter.restype = I
     L.tx_dot_bf16.argtypes = [P, I64, P, I64, P, I64, I64, I64, I64, VP]
