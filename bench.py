@@ -22,7 +22,13 @@ Infinity Cache for the memory-bound ops.
 cpu_baseline: the CPU oracle (oracle/, a C port of the path's semantics,
 OpenMP over all host cores) timed on bounded samples of the same workloads:
 rows of the 8192^3 GEMM for CPU_GEMM_S seconds and whole 16 Mi-value
-encodes for CPU_CONVERT_S seconds.
+encodes for CPU_CONVERT_S seconds.  Under "triton_interpreter" it also
+carries the reference's own CPU path: plain-Triton kernels of each op run by
+Triton's interpreter (TRITON_INTERPRET=1, one Python thread plus NumPy's
+BLAS threads) at full size, the GEMMs on their first 64 rows of C with the
+time scaled to the whole problem (oracle/triton_cpu.py).
+
+Progress lines ("bench: ... done") go to stderr; stdout holds the JSON line.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -42,6 +48,13 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
 MALL_BYTES = 256 << 20
+
+
+def progress(step):
+    print(f"bench: {step} done ({time.perf_counter() - T_START:.1f} s)", file=sys.stderr, flush=True)
+
+
+T_START = time.perf_counter()
 
 
 def parse():
@@ -219,12 +232,17 @@ def cpu_baseline():
         oracle.encode(x, 1, False, nthreads=cores)
         reps += 1
     dt_conv = (time.perf_counter() - t0) / reps
+    from triton_cpu import baseline as interpreter_baseline
+    progress("cpu baseline: oracle")
+    interp = interpreter_baseline(progress=progress)
+    progress("cpu baseline: triton interpreter")
     return {
         "value": gemm_tflops, "unit": "TFLOP/s", "cores": cores, "kind": "port",
         "sample": f"oracle fp8 scaled GEMM, {rows} of 8192 rows of M=N=K=8192 "
                   f"({2.0 * rows * N * K / 1e9:.0f} GFLOP in {dt:.1f} s, fp64 accumulate)",
         "fp8_convert": {"value": 5.0 * x.size / dt_conv / 1e9, "unit": "GB/s",
                         "sample": f"oracle encode e4m3fn RNE of 16,777,216 values x {reps}"},
+        "triton_interpreter": interp,
     }
 
 
@@ -316,7 +334,9 @@ def main():
     K, W = args.steps, args.warmup
 
     gemm = bench_fp8_gemm(tx, torch, 8192, 8192, 8192, K, W)
+    progress("fp8 GEMM 8192^3")
     conv = bench_fp8_convert(tx, torch, max(K, 50), W)
+    progress("fp8 convert 16Mi")
     secondary = []
     if not args.quick:
         for (m, n, k) in [(16, 14336, 4096), (512, 14336, 4096), (8192, 14336, 4096),
@@ -328,19 +348,23 @@ def main():
                               "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
                               "gbs": r["bytes"] / (r["ms"] * 1e-3) / 1e9})
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
         for (m, n, k) in [(4096, 4096, 4096), (4095, 4097, 4100)]:
             r = bench_bf16_gemm(tx, torch, m, n, k, K, W)
             secondary.append({"op": "bf16 GEMM", "shape": [m, n, k], "ms": r["ms"],
                               "tflops": r["tflops"], "frac_mfma": r["tflops"] / BF16_PEAK_TFLOPS})
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
         for kind in ("i32", "f32"):
             r = bench_scatter(tx, torch, kind, K, W)
             secondary.append({"op": f"scatter-reduce {kind} 64Mi->65536 Zipf(1.1)", "ms": r["ms"],
                               "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS,
                               "gupdates_per_s": r["updates_per_s"] / 1e9})
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
         for m in (1, 4, 16):
             r = bench_gemv(tx, torch, m, max(K, 50), W)
             secondary.append({"op": "fp8 e5m2 dequant GEMV", "shape": [m, 14336, 4096],
                               "ms": r["ms"], "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS})
+            progress(f"fp8 e5m2 dequant GEMV M={m}")
         secondary.append({"op": "fp8 decode e4m3fn->fp32 16Mi", "ms": conv["decode_ms"],
                           "gbs": conv["decode_gbs"], "frac_hbm": conv["decode_gbs"] / HBM_PEAK_GBS})
 
