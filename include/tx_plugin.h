@@ -19,16 +19,19 @@
  *     and a stream.  The table's fn pointers unpack operands and call these.
  *
  * Conventions (all entry points):
- *  - The caller owns every input and output buffer.  tx_dot_bf16 and
- *    tx_dot_fp8_scaled may use device scratch that the library keeps per
- *    (device, stream): fp32 split-K partial planes (at most 8 x M x N x 4
- *    bytes) when the output tiles leave CUs idle, and zero-padded copies of
- *    A and B when rows are not 16-byte aligned in a product of at least
- *    2^30 multiply-adds.  The scratch is allocated stream-ordered
- *    (hipMallocAsync on `stream`) the first time a stream needs it, grown
- *    the same way, and reused by later calls, so steady-state calls
- *    allocate nothing; requests above 512 MiB get a buffer per call.  If
- *    the allocation fails they run without it.  No other entry point
+ *  - The caller owns every input and output buffer.  tx_dot_bf16,
+ *    tx_dot_fp8_scaled and tx_dot_scaled_mx may use device scratch that
+ *    the library keeps per (device, stream): fp32 split-K partial planes
+ *    (at most 8 x M x N x 4 bytes) when the output tiles leave CUs idle,
+ *    zero-padded copies of A and B when rows are not 16-byte aligned in a
+ *    product of at least 2^30 multiply-adds (tx_dot_scaled_mx: in any
+ *    product), and repacked MX scale rows.  The scratch is allocated
+ *    stream-ordered (hipMallocAsync on `stream`) the first time a stream
+ *    needs it, grown the same way, and reused by later calls, so
+ *    steady-state calls allocate nothing; requests above 512 MiB get a
+ *    buffer per call.  If the allocation fails, tx_dot_bf16 and
+ *    tx_dot_fp8_scaled run without it and tx_dot_scaled_mx returns the
+ *    error.  No other entry point
  *    allocates device memory.  txShutdown frees the kept scratch.  The
  *    library owns its code-object handles, loaded once per device on first
  *    use (or by txInit) and unloaded by txShutdown.
@@ -265,6 +268,35 @@ TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
                                    const float *scale_b, void *C, int64_t ldc,
                                    int64_t M, int64_t N, int64_t K,
                                    tx_stream_t stream);
+
+/*
+ * tt.dot_scaled with MX block scales (OCP Microscaling: one e8m0 scale per
+ * 32 consecutive K elements of each row of A and each column of B), fp32
+ * accumulation:
+ * C[m,n] = out(sum_k A[m,k] * 2^(sa[m][k/32] - 127) * B[k,n] * 2^(sb[n][k/32] - 127)).
+ * e8m0 code e in 0..254 is 2^(e - 127) (0 is 2^-127, not zero); 255 is NaN.
+ * Replaces the scaled MMA of the reference's TLX ops (async_dot_scaled,
+ * tlx/mma_ops.py:163-237, lowered through GenericOpPattern<DotScaledOp>,
+ * uTLXConversionPatterns.cpp:616); closed form of its check at
+ * test_tlx.py:2271-2292, whose `bits << 23` scale decode agrees for codes
+ * 1..254.  a_type/b_type are TX_FP8E4M3FN or TX_FP8E5M2 (the "e4m3" / "e5m2"
+ * formats of async_dot_scaled).
+ * A: row-major M x K bytes (lda); B: column-major, N rows of K bytes (ldb).
+ * scale_a: e8m0 bytes, row-major M x ceil(K/32) (row stride ld_scale_a);
+ * scale_b: N x ceil(K/32) (ld_scale_b).  Past K inside the last block the
+ * operands count as zero.
+ * C: row-major M x N (ldc elements) of c_type TX_F32, TX_BF16 or TX_F16
+ * (round to nearest even; fp16 overflows to Inf).
+ * Uses the library's per-stream scratch (see the conventions above) for
+ * zero-padded operand rows when rows are not 16-byte aligned or K is not a
+ * multiple of 16, and for repacked scale rows unless K is a multiple of 128
+ * and the scale rows are 4-byte aligned (ld_scale_* a multiple of 4).
+ */
+TX_API tx_status tx_dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda,
+                                  const uint8_t *scale_a, int64_t ld_scale_a, const void *B,
+                                  tx_dtype b_type, int64_t ldb, const uint8_t *scale_b,
+                                  int64_t ld_scale_b, void *C, tx_dtype c_type, int64_t ldc,
+                                  int64_t M, int64_t N, int64_t K, tx_stream_t stream);
 
 /*
  * fp8 weight-only dequant GEMV / skinny GEMM:

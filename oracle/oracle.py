@@ -29,10 +29,9 @@ _lib = None
 
 
 def build(force: bool = False) -> str:
-    """Compile the oracle with its Makefile (gcc + OpenMP)."""
-    if force or not os.path.exists(_LIB_PATH):
-        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"],
-                       check=True)
+    """Compile the oracle with its Makefile (gcc + OpenMP); make rebuilds it
+    when the source is newer than the library."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"], check=True)
     return _LIB_PATH
 
 
@@ -65,6 +64,8 @@ def lib():
                                                I, I, I64, I64, P, P, I]
         L.txo_gemv_fp8_dequant.argtypes = [P, I64, P, I64, P, I64, I64, I64,
                                            I64, I64, I, P, P, I]
+        L.txo_gemm_mx_rows.argtypes = [P, I64, P, I64, P, I64, P, I64, I64, I64, I, I, I64, I64,
+                                       P, P, P, I]
         L.txo_encode_fmt.argtypes = [P, P, I64, I, I, I, I]
         L.txo_encode_fmt.restype = I
         L.txo_round_rs.argtypes = [P, P, P, I64, I, I]
@@ -227,6 +228,26 @@ def gemm_fp8_scaled_rows(A, B, sa, sb, r0: int, r1: int, fmt_a=E4M3FN,
                                    fmt_a, fmt_b, r0, r1, _p(o32), _p(o16),
                                    nthreads)
     return o32, o16
+
+
+def gemm_mx_rows(A, sa, B, sb, r0: int, r1: int, fmt_a=E4M3FN, fmt_b=E4M3FN, nthreads: int = 0,
+                 block_max: bool = False):
+    """Rows [r0, r1) of the MX-scaled dot: Aq M x K and Bq N x K fp8 codes,
+    sa M x ceil(K/32) and sb N x ceil(K/32) e8m0 codes.  Returns (fp32 of
+    the fp64 sum, fp32 of the sum of |terms|), and with block_max also the
+    sum over K blocks of the block's largest |term|."""
+    A = _c(A, np.uint8)
+    B = _c(B, np.uint8)
+    sa = _c(sa, np.uint8)
+    sb = _c(sb, np.uint8)
+    K = A.shape[1]
+    N = B.shape[0]
+    o32 = np.empty((r1 - r0, N), np.float32)
+    oab = np.empty((r1 - r0, N), np.float32)
+    obm = np.empty((r1 - r0, N), np.float32) if block_max else None
+    lib().txo_gemm_mx_rows(_p(A), K, _p(sa), sa.shape[1], _p(B), K, _p(sb), sb.shape[1], N, K,
+                           fmt_a, fmt_b, r0, r1, _p(o32), _p(oab), _p(obm), nthreads)
+    return (o32, oab, obm) if block_max else (o32, oab)
 
 
 def gemv_fp8_dequant(x, W, s, group: int = 128, fmt_w=E5M2, nthreads: int = 0):

@@ -35,6 +35,10 @@
  *   scatter      : brute-force loops on tiny inputs; int32 wrap mod 2^32;
  *                  conservation of the total.
  *   gemm / gemv  : brute force on tiny shapes vs. numpy float64; linearity.
+ *   MX dot       : numpy float64 matmul of the operands with each e8m0 scale
+ *                  repeated over its 32 K values (the reference check's
+ *                  form); scale exponent shifts double or halve rows and
+ *                  columns; e8m0 255 gives NaN, 0 gives 2^-127; ragged K.
  */
 #include <math.h>
 #include <stdint.h>
@@ -565,6 +569,68 @@ TXO_API void txo_gemm_fp8_scaled_rows(const uint8_t *A, int64_t lda,
       int64_t o = (m - r0) * N + n;
       if (out_f32) out_f32[o] = (float)v;
       if (out_bf16) out_bf16[o] = f32_to_bf16_rne((float)v);
+    }
+  }
+  (void)nthreads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MX-scaled dot (tt.dot_scaled with e8m0 block scales), rows [r0, r1):     */
+/*   C[m,n] = sum_k dec(A[m,k]) 2^(sa[m][k/32]-127) dec(B[n,k]) 2^(sb[n][k/32]-127) */
+/* as the closed form of the reference's scaled-dot check (test_tlx.py:     */
+/* 2271-2292: decode fp8 operands and e8m0 scales, repeat each scale over   */
+/* its 32 K values, fp32 matmul), with the e8m0 decode of the OCP          */
+/* Microscaling spec v1.0: code e in 0..254 is 2^(e-127), 255 is NaN (the   */
+/* check's `bits << 23` gives 0 for code 0 and +Inf for 255; it only uses   */
+/* 124..129).  Accumulated in fp64 block by block.  out_f32: the fp32 of the */
+/* sum; out_abs: sum of |terms|; out_bmax: sum over blocks of the largest   */
+/* |term| of the block (the last two for error bounds; either may be NULL). */
+/* Aq row-major (lda bytes), Bq N rows of K bytes (ldb), scales row-major   */
+/* (ld_sa / ld_sb).                                                         */
+/* ------------------------------------------------------------------------ */
+TXO_API void txo_gemm_mx_rows(const uint8_t *A, int64_t lda, const uint8_t *sa,
+                              int64_t ld_sa, const uint8_t *B, int64_t ldb,
+                              const uint8_t *sb, int64_t ld_sb, int64_t N,
+                              int64_t K, int fmt_a, int fmt_b, int64_t r0,
+                              int64_t r1, float *out_f32, float *out_abs,
+                              float *out_bmax, int nthreads) {
+  init_tables();
+  double lut_a[256], lut_b[256], e8[256];
+  for (int c = 0; c < 256; ++c) {
+    lut_a[c] = (double)txo_decode1(fmt_a, (uint8_t)c);
+    lut_b[c] = (double)txo_decode1(fmt_b, (uint8_t)c);
+    e8[c] = c == 255 ? NAN : ldexp(1.0, c - 127);
+  }
+  const int64_t nblk = (K + 31) / 32;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+  for (int64_t m = r0; m < r1; ++m) {
+    const uint8_t *arow = A + m * lda;
+    const uint8_t *sarow = sa + m * ld_sa;
+    for (int64_t n = 0; n < N; ++n) {
+      const uint8_t *bcol = B + n * ldb;
+      const uint8_t *sbrow = sb + n * ld_sb;
+      double acc = 0.0, mag = 0.0, bmax = 0.0;
+      for (int64_t b = 0; b < nblk; ++b) {
+        double blk = 0.0, blk_abs = 0.0, blk_max = 0.0;
+        const int64_t k1 = (b + 1) * 32 < K ? (b + 1) * 32 : K;
+        for (int64_t k = b * 32; k < k1; ++k) {
+          const double t = lut_a[arow[k]] * lut_b[bcol[k]];
+          blk += t;
+          blk_abs += fabs(t);
+          if (fabs(t) > blk_max) blk_max = fabs(t);
+        }
+        const double sc = e8[sarow[b]] * e8[sbrow[b]];
+        acc += blk * sc;
+        mag += blk_abs * sc;
+        bmax += blk_max * sc;
+      }
+      const int64_t o = (m - r0) * N + n;
+      if (out_f32) out_f32[o] = (float)acc;
+      if (out_abs) out_abs[o] = (float)mag;
+      if (out_bmax) out_bmax[o] = (float)bmax;
     }
   }
   (void)nthreads;

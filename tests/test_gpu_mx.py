@@ -1,0 +1,198 @@
+"""GPU parity: tt.dot_scaled with MX block scales (tx_dot_scaled_mx) vs the
+oracle's fp64 accumulation.
+
+Tolerances: fp8 class, max|gpu - ref| / max|ref| <= 2e-2 (and Frobenius);
+on top of that, element by element,
+  |gpu - ref| <= 32 * 2^-13 * sum_b max_{k in b} |term_k|
+                 + (K/64 + 2) * 2^-24 * sum|terms| + half an ulp of the output
+(bf16 2^-8, fp16 2^-11 relative; fp16 subnormal spacing 2^-24).  The first
+part is the scaled fp8 MFMA's own arithmetic: it sums the 32 products of a
+block in fixed point aligned to the block's largest product and drops what
+lies more than 13 bits below it (measured on the device: 1 + 2^-14 inside one
+block gives 1, while blocks are combined exactly in fp32).  A wrong scale
+block, lane, byte select or transposed scale is off by a factor of 2 or more
+on whole blocks, far above the bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+FP8_TOL = 2e-2
+TD = {1: torch.float8_e4m3fn, 2: torch.float8_e5m2}
+OUT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _codes(g, shape, fmt):
+    top = 0x7F if fmt == 1 else 0x7C
+    return g.integers(0, top, shape, dtype=np.uint8) | (g.integers(0, 2, shape, dtype=np.uint8) << 7)
+
+
+def _run(tx, dev, aq, sa, bq, sb, fa=1, fb=1, out="bf16", lda=None, ld_s=None):
+    """Operands and scales to the GPU (optionally as views into wider rows)."""
+    M, K = aq.shape
+    N = bq.shape[0]
+
+    def put(x, ld, dtype=None):
+        if ld is None or ld == x.shape[1]:
+            t = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+        else:
+            w = np.zeros((x.shape[0], ld), np.uint8)
+            w[:, :x.shape[1]] = x
+            t = torch.from_numpy(w).to(dev)[:, :x.shape[1]]
+        return t if dtype is None else t.view(dtype)
+
+    A = put(aq, lda, TD[fa])
+    B = put(bq, lda, TD[fb])
+    SA = put(sa, ld_s)
+    SB = put(sb, ld_s)
+    C = tx.dot_scaled(A, SA, B, SB, out_dtype=OUT[out])
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy()
+
+
+def check_mx(got, ref, mag, bmax, K, out):
+    got = got.astype(np.float64)
+    ref = ref.astype(np.float64)
+    mag = mag.astype(np.float64)
+    bmax = bmax.astype(np.float64)
+    scale = np.abs(ref).max()
+    if scale > 0:
+        assert np.abs(got - ref).max() / scale <= FP8_TOL
+        assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= FP8_TOL
+    ulp = {"f32": 2.0 ** -24, "bf16": 2.0 ** -8, "f16": 2.0 ** -11}[out]
+    floor = {"f32": 0.0, "bf16": 0.0, "f16": 2.0 ** -25}[out]
+    bound = 32 * 2.0 ** -13 * bmax + (K / 64 + 2) * 2.0 ** -24 * mag + ulp * np.abs(ref) * (1 + 1e-6) + floor
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:5], got[bad][:5], ref[bad][:5])
+
+
+@pytest.mark.parametrize("M,N,K,fa,fb,out", [
+    (256, 256, 256, 1, 1, "f32"), (256, 256, 256, 1, 1, "bf16"), (256, 256, 256, 1, 1, "f16"),
+    (300, 500, 4096, 1, 1, "bf16"), (257, 501, 2048, 2, 1, "f32"), (64, 96, 96, 1, 2, "f32"),
+    (130, 260, 1000, 2, 2, "bf16"), (77, 33, 33, 1, 1, "f32"), (1, 1, 32, 1, 1, "f32"),
+    (600, 1000, 640, 1, 1, "f16")])
+def test_mx_shapes(tx, oracle, dev, M, N, K, fa, fb, out):
+    """256x256 and 256x128 tiles; K a multiple of 128 (scales read in place),
+    of 32 (scale rows repacked), or ragged (operands zero-padded)."""
+    g = np.random.default_rng(M * 7 + N * 3 + K)
+    aq, bq = _codes(g, (M, K), fa), _codes(g, (N, K), fb)
+    nb = (K + 31) // 32
+    lo, hi = (108, 118) if out == "f16" else (118, 134)   # keep fp16 outputs finite
+    sa = g.integers(lo, hi, (M, nb), dtype=np.uint8)
+    sb = g.integers(lo, hi, (N, nb), dtype=np.uint8)
+    got = _run(tx, dev, aq, sa, bq, sb, fa, fb, out)
+    ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, 0, M, fa, fb, block_max=True)
+    check_mx(got, ref, mag, bmax, K, out)
+
+
+def test_mx_strided_operands_and_scales(tx, oracle, dev):
+    """Operand rows wider than K (lda 16-aligned, then not) and scale rows
+    wider than ceil(K/32) (4-aligned, then not)."""
+    g = np.random.default_rng(11)
+    M, N, K = 200, 300, 512
+    aq, bq = _codes(g, (M, K), 1), _codes(g, (N, K), 1)
+    sa = g.integers(120, 132, (M, K // 32), dtype=np.uint8)
+    sb = g.integers(120, 132, (N, K // 32), dtype=np.uint8)
+    ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, 0, M, block_max=True)
+    for lda, ld_s in ((K + 64, K // 32 + 4), (K + 3, K // 32 + 5)):
+        got = _run(tx, dev, aq, sa, bq, sb, lda=lda, ld_s=ld_s, out="f32")
+        check_mx(got, ref, mag, bmax, K, "f32")
+
+
+def test_mx_special_scales(tx, oracle, dev):
+    """e8m0 255 is NaN for every output it scales; code 0 is 2^-127 (0 on A
+    against 254 on B gives the same bits as 127 against 127); exponents far
+    from 127 (2^103 and 2^-87 on whole rows) stay within the fp32 bound."""
+    g = np.random.default_rng(12)
+    M, N, K = 256, 256, 256
+    aq, bq = _codes(g, (M, K), 1), _codes(g, (N, K), 1)
+    ones_a = np.full((M, K // 32), 127, np.uint8)
+    ones_b = np.full((N, K // 32), 127, np.uint8)
+    c11 = _run(tx, dev, aq, ones_a, bq, ones_b, out="f32")
+    c0 = _run(tx, dev, aq, np.zeros_like(ones_a), bq, np.full_like(ones_b, 254), out="f32")
+    assert np.array_equal(c0.view(np.uint32), c11.view(np.uint32))
+
+    sa = g.integers(120, 134, (M, K // 32), dtype=np.uint8)
+    sb = g.integers(100, 110, (N, K // 32), dtype=np.uint8)
+    sa[5, 3] = 255
+    sb[7, 0] = 255
+    sa[10, :] = 230
+    sa[11, :] = 40
+    got = _run(tx, dev, aq, sa, bq, sb, out="f32")
+    ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, 0, M, block_max=True)
+    assert np.all(np.isnan(got[5])) and np.all(np.isnan(got[:, 7]))
+    keep = np.ones((M, N), bool)
+    keep[5] = False
+    keep[:, 7] = False
+    assert np.all(np.isfinite(got[keep])) and np.all(np.isfinite(ref[keep]))
+    d = np.abs(got.astype(np.float64) - ref)[keep]
+    bound = 32 * 2.0 ** -13 * bmax.astype(np.float64) + (K / 64 + 2) * 2.0 ** -24 * mag.astype(np.float64)
+    assert np.all(d <= bound[keep])
+    assert np.abs(np.delete(got[10], 7)).max() > 2.0 ** 80
+    assert 0 < np.abs(np.delete(got[11], 7)).max() < 2.0 ** -60
+
+
+def test_mx_reference_check_form(tx, dev):
+    """The reference's own check (test_tlx.py:2271-2292): operands are the
+    values 20..39 cast to fp8, scales 124..129, fp16 output compared with a
+    float32 matmul of the scale-expanded operands, atol 1e-2 * sqrt(K / 32),
+    at its shape M = N = 256, K = 128."""
+    M, N, K = 256, 256, 128
+    torch.manual_seed(0)
+    for fa, fb in ((1, 1), (2, 2), (1, 2), (2, 1)):
+        a = torch.randint(20, 40, (M, K), dtype=torch.uint8).to(TD[fa])
+        b = torch.randint(20, 40, (K, N), dtype=torch.uint8).to(TD[fb])
+        sa = torch.randint(124, 130, (M, K // 32), dtype=torch.uint8)
+        sb = torch.randint(124, 130, (N, K // 32), dtype=torch.uint8)
+        c = tx.dot_scaled(a.to(dev), sa.to(dev), b.t().contiguous().to(dev), sb.to(dev),
+                          out_dtype=torch.float16)
+        sa_f = (sa.to(torch.int32) << 23).view(torch.float32).repeat_interleave(32, dim=1)[:M, :K]
+        sb_f = (sb.to(torch.int32) << 23).view(torch.float32).repeat_interleave(32, dim=1).T.contiguous()[:K, :N]
+        ref = torch.matmul(a.to(torch.float32) * sa_f, b.to(torch.float32) * sb_f).to(torch.float16)
+        torch.testing.assert_close(ref, c.cpu(), atol=1e-2 * (K / 32) ** 0.5, rtol=0)
+
+
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 8192), (512, 14336, 4096)])
+def test_mx_quantised_config(tx, oracle, dev, M, N, K):
+    """MX-quantised N(0,1) operands (the reference's quantiser idiom) at full
+    size: sampled rows against the oracle, and the full-size scale property
+    C(sa + 1) == 2 C bit-exactly."""
+    from tx import workloads
+    aq, sa, bq, sb = workloads.mx_gemm_input(M, N, K)
+    got = _run(tx, dev, aq, sa, bq, sb, out="bf16")
+    g = np.random.default_rng(1)
+    rows = sorted(set([0, M - 1] + list(g.integers(0, M, 6))))
+    for r in rows:
+        ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, r, r + 1, block_max=True)
+        check_mx(got[r:r + 1], ref, mag, bmax, K, "bf16")
+    got2 = _run(tx, dev, aq, sa + 1, bq, sb, out="bf16")
+    assert np.array_equal(got2, 2 * got)
+
+
+def test_mx_table_op_and_errors(tx, oracle, dev):
+    from tx import _lib
+    g = np.random.default_rng(3)
+    M, N, K = 64, 64, 128
+    aq, bq = _codes(g, (M, K), 1), _codes(g, (N, K), 1)
+    sa = g.integers(124, 130, (M, K // 32), dtype=np.uint8)
+    sb = g.integers(124, 130, (N, K // 32), dtype=np.uint8)
+    A = torch.from_numpy(aq).to(dev)
+    B = torch.from_numpy(bq).to(dev)
+    SA = torch.from_numpy(sa).to(dev)
+    SB = torch.from_numpy(sb).to(dev)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    tx.invoke("tt.dot_scaled", [C, A, B, SA, SB, M, N, K, K, K, N, K // 32, K // 32,
+                                _lib.FP8E4M3FN, _lib.FP8E4M3FN, _lib.F32])
+    torch.cuda.synchronize()
+    ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, 0, M, block_max=True)
+    check_mx(C.cpu().numpy(), ref, mag, bmax, K, "f32")
+    with pytest.raises(ValueError):
+        tx.dot_scaled(A.view(torch.float8_e4m3fn), SA[:, :3], B.view(torch.float8_e4m3fn), SB)
+    with pytest.raises(tx.TxError):
+        tx.invoke("tt.dot_scaled", [C, A, B, SA, SB, M, N, K, K, K, N, 2, K // 32,
+                                    _lib.FP8E4M3FN, _lib.FP8E4M3FN, _lib.F32])
+    with pytest.raises(tx.TxError):
+        tx.invoke("tt.dot_scaled", [C, A, B, SA, SB, M, N, K, K, K, N, K // 32, K // 32,
+                                    _lib.FP8E4M3FN, _lib.BF16, _lib.F32])

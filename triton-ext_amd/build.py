@@ -29,7 +29,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 # Code objects in the order of tx::CodeObject (csrc/host/tx_runtime.h).
-KERNEL_SOURCES = ["fp8_codec", "scatter", "gemm_bf16", "gemm_fp8", "gemv"]
+KERNEL_SOURCES = ["fp8_codec", "scatter", "gemm_bf16", "gemm_fp8", "gemv", "gemm_mx"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "--genco",

@@ -1,5 +1,5 @@
-// tt.dot entry points (bf16, and fp8 with row/column scales), the fp8
-// dequant GEMV, and their table registrations.
+// tt.dot entry points (bf16, fp8 with row/column scales, fp8 with MX block
+// scales), the fp8 dequant GEMV, and their table registrations.
 //
 // Reference: tt.dot is converted by TritonDotPattern
 // (uTLXConversionPatterns.cpp:227-296) and lowered to MFMA by Triton's AMD
@@ -285,6 +285,108 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   return launch_gemm(kname, CodeObject::GemmFp8, args, tile, tile, s);
 }
 
+// tt.dot_scaled with MX block scales (fp8 operands, e8m0 scales per 32 K
+// elements).  The kernel reads its operands through the fast path's LDS-DMA
+// pipeline, so rows that are not 16-byte aligned (or K not a multiple of 16)
+// are first copied into zero-padded rows (stream scratch slot 0, K rounded up
+// to a 128-byte step), and scale rows that are not whole dwords covering
+// exactly the kernel's K steps are copied into such rows, padded with 127
+// (2^0, against zero operands), in slot 2.
+static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, const uint8_t *sa,
+                               int64_t ld_sa, const void *B, tx_dtype b_type, int64_t ldb,
+                               const uint8_t *sb, int64_t ld_sb, void *C, tx_dtype c_type,
+                               int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  const char *what = "tx_dot_scaled_mx";
+  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, K));
+  const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
+  if (!fa || !fb)
+    return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 (got %d, %d)", what,
+                int(a_type), int(b_type));
+  const char *fo = c_type == TX_BF16 ? "bf16" : c_type == TX_F16 ? "f16" : c_type == TX_F32 ? "f32" : nullptr;
+  if (!fo)
+    return fail(TX_INVALID_ARGUMENT, "%s: output type must be bf16, fp16 or fp32 (got %d)", what,
+                int(c_type));
+  if (c_type == TX_F32 && !aligned(C, 4))
+    return fail(TX_INVALID_ARGUMENT, "%s: fp32 C must be 4-byte aligned", what);
+  if (M == 0 || N == 0) return TX_SUCCESS;
+  const int64_t nblk = (K + 31) / 32;
+  if (K > 0 && (!sa || !sb)) return fail(TX_INVALID_ARGUMENT, "%s: NULL scale matrix", what);
+  if (ld_sa < nblk || ld_sb < nblk)
+    return fail(TX_INVALID_ARGUMENT, "%s: scale stride smaller than ceil(K / 32) (ld_sa=%lld ld_sb=%lld)",
+                what, (long long)ld_sa, (long long)ld_sb);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t cus = cu_count();
+  tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+
+  // operands: as given, or zero-padded to whole 128-byte steps
+  ScratchLease ws, wsc;  // held until every launch using them is enqueued
+  int64_t kk = K;        // K the kernel runs over
+  if (!fast_ok(A, lda, B, ldb, K, M, N)) {
+    const int64_t kp = (K + 127) / 128 * 128;
+    if (std::max(M, N) * kp >= (int64_t(1) << 31))
+      return fail(TX_UNSUPPORTED, "%s: padded operands exceed 32-bit offsets", what);
+    const size_t a_bytes = size_t(M) * size_t(kp), b_bytes = size_t(N) * size_t(kp);
+    TX_TRY(ws.acquire(s, 0, a_bytes + b_bytes));
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pad_rows", &fn));
+    uint8_t *wa = static_cast<uint8_t *>(ws.ptr()), *wb = wa + a_bytes;
+    tx_pad_args pa{A, wa, lda, kp, int32_t(M), int32_t(K), int32_t(kp), pad_load_bytes(A, lda, K)};
+    TX_TRY(launch(fn, unsigned(std::min<int64_t>((M * kp / 16 + 255) / 256, cus * 16)), 1, 256, s,
+                  &pa, sizeof pa, "tx_gemm_mx_pad_rows"));
+    tx_pad_args pb{B, wb, ldb, kp, int32_t(N), int32_t(K), int32_t(kp), pad_load_bytes(B, ldb, K)};
+    TX_TRY(launch(fn, unsigned(std::min<int64_t>((N * kp / 16 + 255) / 256, cus * 16)), 1, 256, s,
+                  &pb, sizeof pb, "tx_gemm_mx_pad_rows"));
+    args.A = wa;
+    args.lda = kp;
+    args.B = wb;
+    args.ldb = kp;
+    args.K = int32_t(kp);
+    kk = kp;
+  }
+  // scales: each row must hold exactly one dword per K step of the kernel
+  const int64_t sw = (kk + 127) / 128 * 4;  // scale bytes per row the kernel reads
+  // (K = 0: the kernel reads no scale)
+  const bool direct_a = K == 0 || (sw == nblk && aligned(sa, 4) && ld_sa % 4 == 0);
+  const bool direct_b = K == 0 || (sw == nblk && aligned(sb, 4) && ld_sb % 4 == 0);
+  args.mx_a = sa;
+  args.ld_mxa = ld_sa;
+  args.mx_b = sb;
+  args.ld_mxb = ld_sb;
+  if (!direct_a || !direct_b) {
+    const size_t pa_bytes = direct_a ? 0 : size_t(M) * size_t(sw);
+    const size_t pb_bytes = direct_b ? 0 : size_t(N) * size_t(sw);
+    TX_TRY(wsc.acquire(s, 2, pa_bytes + pb_bytes));
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pack_scales", &fn));
+    uint8_t *p = static_cast<uint8_t *>(wsc.ptr());
+    if (!direct_a) {
+      tx_mx_pack_args pk{sa, p, ld_sa, sw, int32_t(M), int32_t(nblk), int32_t(sw), 0};
+      TX_TRY(launch(fn, unsigned(std::min<int64_t>((M * sw / 4 + 255) / 256, cus * 16)), 1, 256, s,
+                    &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
+      args.mx_a = p;
+      args.ld_mxa = sw;
+      p += pa_bytes;
+    }
+    if (!direct_b) {
+      tx_mx_pack_args pk{sb, p, ld_sb, sw, int32_t(N), int32_t(nblk), int32_t(sw), 0};
+      TX_TRY(launch(fn, unsigned(std::min<int64_t>((N * sw / 4 + 255) / 256, cus * 16)), 1, 256, s,
+                    &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
+      args.mx_b = p;
+      args.ld_mxb = sw;
+    }
+  }
+  // lanes address scale rows up to the last tile's end with 32-bit offsets
+  const int64_t lim = int64_t(1) << 31;
+  if ((M + 256) * args.ld_mxa + sw >= lim || (N + 256) * args.ld_mxb + sw >= lim)
+    return fail(TX_UNSUPPORTED, "%s: scale matrices exceed 32-bit offsets", what);
+
+  // 256x256 tiles while they give every CU one, else 256x128
+  const bool big = ((M + 255) / 256) * ((N + 255) / 256) >= cus;
+  char kname[80];
+  std::snprintf(kname, sizeof kname, "tx_gemm_mx_%s_%s_%s%s", fa, fb, fo, big ? "" : "_n128");
+  return launch_gemm(kname, CodeObject::GemmMx, args, 256, big ? 256 : 128, s, 256);
+}
+
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,
                                   int64_t ldw, const float *scales, int64_t ld_scales,
                                   int64_t group, void *y, int64_t ldy, int64_t M, int64_t N,
@@ -398,12 +500,45 @@ static tx_status gemv_op(tx_value *v, size_t count, tx_stream_t stream) {
                           y, ldy, M, N, K, stream);
 }
 
+// tt.dot_scaled: {C (result), A, B, scale_a, scale_b, M, N, K, lda, ldb, ldc,
+// ld_scale_a, ld_scale_b, a_type, b_type, c_type}
+static tx_status dot_mx_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.dot_scaled"};
+  TX_TRY(o.need(16));
+  void *C, *A, *B, *sa, *sb;
+  int64_t M, N, K, lda, ldb, ldc, ldsa, ldsb, at, bt, ct;
+  TX_TRY(o.ptr(0, &C));
+  TX_TRY(o.ptr(1, &A));
+  TX_TRY(o.ptr(2, &B));
+  TX_TRY(o.ptr(3, &sa));
+  TX_TRY(o.ptr(4, &sb));
+  TX_TRY(o.integer(5, &M));
+  TX_TRY(o.integer(6, &N));
+  TX_TRY(o.integer(7, &K));
+  TX_TRY(o.integer(8, &lda));
+  TX_TRY(o.integer(9, &ldb));
+  TX_TRY(o.integer(10, &ldc));
+  TX_TRY(o.integer(11, &ldsa));
+  TX_TRY(o.integer(12, &ldsb));
+  TX_TRY(o.integer(13, &at));
+  TX_TRY(o.integer(14, &bt));
+  TX_TRY(o.integer(15, &ct));
+  return dot_scaled_mx(A, tx_dtype(at), lda, static_cast<const uint8_t *>(sa), ldsa, B, tx_dtype(bt),
+                       ldb, static_cast<const uint8_t *>(sb), ldsb, C, tx_dtype(ct), ldc, M, N, K,
+                       stream);
+}
+
 static const bool reg_dot = register_op(
     "tt.dot", dot_op, "C:bf16*(result), A:bf16*, B:bf16* (N x K), M, N, K, lda, ldb, ldc");
 static const bool reg_dot_fp8 = register_op(
     "tt.dot_scaled.rowcol", dot_fp8_op,
     "C:bf16*(result), A:fp8*, B:fp8* (N x K), scale_a:f32*, scale_b:f32*, M, N, K, lda, ldb, "
     "ldc, a_type:i32, b_type:i32");
+static const bool reg_dot_mx = register_op(
+    "tt.dot_scaled", dot_mx_op,
+    "C:bf16|f16|f32*(result), A:fp8*, B:fp8* (N x K), scale_a:e8m0* (M x ceil(K/32)), "
+    "scale_b:e8m0* (N x ceil(K/32)), M, N, K, lda, ldb, ldc, ld_scale_a, ld_scale_b, a_type:i32, "
+    "b_type:i32, c_type:i32");
 static const bool reg_gemv = register_op(
     "tx.gemv_fp8_dequant", gemv_op,
     "y:bf16*(result), x:bf16*, W:fp8* (N x K), scales:f32* (N x K/group), M, N, K, group, ldx, "
@@ -426,6 +561,16 @@ TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
   tx::clear_error();
   return tx::dot_fp8_scaled(A, a_type, lda, scale_a, B, b_type, ldb, scale_b, C, ldc, M, N, K,
                             stream);
+}
+
+TX_API tx_status tx_dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda,
+                                  const uint8_t *scale_a, int64_t ld_scale_a, const void *B,
+                                  tx_dtype b_type, int64_t ldb, const uint8_t *scale_b,
+                                  int64_t ld_scale_b, void *C, tx_dtype c_type, int64_t ldc,
+                                  int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot_scaled_mx(A, a_type, lda, scale_a, ld_scale_a, B, b_type, ldb, scale_b, ld_scale_b,
+                           C, c_type, ldc, M, N, K, stream);
 }
 
 TX_API tx_status tx_gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,

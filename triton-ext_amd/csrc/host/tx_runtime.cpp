@@ -24,6 +24,7 @@ extern const unsigned char tx_co_scatter_begin[], tx_co_scatter_end[];
 extern const unsigned char tx_co_gemm_bf16_begin[], tx_co_gemm_bf16_end[];
 extern const unsigned char tx_co_gemm_fp8_begin[], tx_co_gemm_fp8_end[];
 extern const unsigned char tx_co_gemv_begin[], tx_co_gemv_end[];
+extern const unsigned char tx_co_gemm_mx_begin[], tx_co_gemm_mx_end[];
 }
 
 namespace tx {
@@ -43,6 +44,7 @@ const CodeObjectImage kImages[static_cast<int>(CodeObject::Count)] = {
     {"gemm_bf16", tx_co_gemm_bf16_begin, tx_co_gemm_bf16_end},
     {"gemm_fp8", tx_co_gemm_fp8_begin, tx_co_gemm_fp8_end},
     {"gemv", tx_co_gemv_begin, tx_co_gemv_end},
+    {"gemm_mx", tx_co_gemm_mx_begin, tx_co_gemm_mx_end},
 };
 
 constexpr int kMaxDevices = 64;

@@ -18,7 +18,8 @@ enum class CodeObject : int {
   GemmBf16 = 2,
   GemmFp8 = 3,
   Gemv = 4,
-  Count = 5
+  GemmMx = 5,
+  Count = 6
 };
 
 // Record `status` and a printf-style message as the calling thread's last
@@ -62,7 +63,7 @@ class ScratchLease {
   ScratchLease(const ScratchLease &) = delete;
   ScratchLease &operator=(const ScratchLease &) = delete;
   ~ScratchLease();
-  // `slot` (0 or 1) separates the buffers one call needs at the same time.
+  // `slot` (0, 1 or 2) separates the buffers one call needs at the same time.
   tx_status acquire(hipStream_t stream, int slot, size_t bytes);
   void *ptr() const { return ptr_; }
 

@@ -34,6 +34,19 @@
 //    next half consumes them) and, in the second half, one of the loads.
 //  * MFMA roles: the B tile feeds the MFMA A operand, so lane l, accumulator
 //    register j holds C[m0 + l % 32][n0 + 8 * (j / 4) + 4 * (l / 32) + j % 4].
+//  * The 32x32x64 fp8 MFMA takes a lane's 32 operand bytes as two 16-byte
+//    pieces: bytes 0-15 are K 16g .. 16g+15 of the 64, bytes 16-31 are
+//    K 32+16g .. 32+16g+15 (g = lane / 32).  Lane g therefore reads chunks g
+//    and g + 2 of a 64-byte K half, so that K block b (bytes 32b .. 32b+31 of
+//    the half) is piece b of both lane halves: the block an MX scale of lane
+//    32b + row covers.  (bf16 reads chunks 2g and 2g + 1; the order of K
+//    inside a product does not change an unscaled sum.)
+//  * MX (block-scaled) variant: one e8m0 scale per 32 K elements of each row
+//    of A and B.  A 128-byte step holds blocks 4s .. 4s+3 of a row, one
+//    dword; each lane loads the dword of its row for each of its fragments,
+//    one step ahead, and shifts it right by 8g so that byte 2h is the block
+//    of K half h it multiplies (op_sel picks the byte).  Only 4 wavefronts
+//    (one per SIMD) leave the registers for this.
 #pragma once
 
 #include <type_traits>
@@ -99,6 +112,15 @@ __device__ __forceinline__ void mfma32(txd::f32x16 &acc, const i32x8 &mb, const 
   }
 }
 
+// The same product with MX block scales: byte OPSEL of scale_b (scale_a)
+// scales the 32 K values of this lane's row of the B (A) block.
+template <class C, int OPSEL>
+__device__ __forceinline__ void mfma32_mx(txd::f32x16 &acc, const i32x8 &mb, const i32x8 &ma,
+                                          uint32_t scale_b, uint32_t scale_a) {
+  acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(mb, ma, acc, F8Code<C::EL_B_>::v, F8Code<C::EL_A_>::v,
+                                                        OPSEL, int(scale_b), OPSEL, int(scale_a));
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding and
 // all its LDS operations are done, then meet the workgroup at a barrier.
 // (A plain __syncthreads() would also wait for every outstanding load, which
@@ -112,11 +134,16 @@ __device__ __forceinline__ void wait_and_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <class C, int BN, int NW = fast::kWaves>
+// Output element types of the fast tile.
+enum FastOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
+
+template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16>
 __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
+  static_assert(!MX || (C::FP8 && NW == 4), "MX scales: fp8 operands, 4 wavefronts");
+  static_assert(OUT == OUT_BF16 || MX, "fp16 / fp32 output: MX variant only");
   // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per
   // wave): LDS reads per step are then (64 + 64) x 8 rows instead of
   // (128 + 32) x 8, which matters because narrow tiles are LDS-bound.
@@ -151,8 +178,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   const int ksteps = splits > 1 ? min(a.ksteps_split, ksteps_all - kfirst) : ksteps_all;
   const uint32_t kbase = uint32_t(kfirst) * kStep;
   const uint32_t lda_b = uint32_t(a.lda) * ES, ldb_b = uint32_t(a.ldb) * ES;
-  const __amdgpu_buffer_rsrc_t rsrc[2] = {make_rsrc(a.A, uint32_t(a.M - 1) * lda_b + kb_end),
-                                          make_rsrc(a.B, uint32_t(a.N - 1) * ldb_b + kb_end)};
+  // (K = 0: empty ranges, so the prologue's loads read nothing at all)
+  const __amdgpu_buffer_rsrc_t rsrc[2] = {make_rsrc(a.A, kb_end ? uint32_t(a.M - 1) * lda_b + kb_end : 0u),
+                                          make_rsrc(a.B, kb_end ? uint32_t(a.N - 1) * ldb_b + kb_end : 0u)};
 
   // DMA assignment: wave w fills blocks BLKA*w .. of A and BLKB*w .. of B.
   // Lane i of block q covers row 8q + i/8 and logical chunk
@@ -201,18 +229,47 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   };
 
   // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
-  // h, chunks 4h + 2g and 4h + 2g + 1 (g = l / 32).  Blocks 32 rows apart
-  // share the swizzle ((row >> 1) & 7 does not change by 32 rows), so they
-  // are one base plus 4 KiB steps.
+  // h, chunks 4h + g and 4h + g + 2 (fp8) or 4h + 2g and 4h + 2g + 1 (bf16),
+  // g = l / 32.  Blocks 32 rows apart share the swizzle ((row >> 1) & 7 does
+  // not change by 32 rows), so they are one base plus 4 KiB steps.
   const int frow = lane & 31, fg = lane >> 5;
   int ro[2][2][2];  // [operand][K half][piece]
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      ro[0][h][e] = off(wm * TM + frow, 4 * h + 2 * fg + e);
-      ro[1][h][e] = off(wn * TN + frow, 4 * h + 2 * fg + e);
+      const int chunk = 4 * h + (C::FP8 ? fg + 2 * e : 2 * fg + e);
+      ro[0][h][e] = off(wm * TM + frow, chunk);
+      ro[1][h][e] = off(wn * TN + frow, chunk);
     }
+
+  // MX scales: dword s of a scale row holds the blocks of K step s.  Lanes
+  // of rows past M / N read past the buffer's range and get 0 (2^-127, times
+  // zero operands).  scc: this step's dwords (shifted by 8g once landed),
+  // scn: the next step's, in flight.
+  constexpr int NS = MX ? NF : 1;
+  uint32_t scc[NS], scn[NS];
+  __amdgpu_buffer_rsrc_t srs[2];
+  uint32_t svb[2] = {0u, 0u};
+  if constexpr (MX) {
+    const uint32_t sbytes = uint32_t(ksteps_all) * 4u;
+    srs[0] = make_rsrc(a.mx_a, sbytes ? uint32_t(a.M - 1) * uint32_t(a.ld_mxa) + sbytes : 0u);
+    srs[1] = make_rsrc(a.mx_b, sbytes ? uint32_t(a.N - 1) * uint32_t(a.ld_mxb) + sbytes : 0u);
+    svb[0] = uint32_t(m0 + wm * TM + frow) * uint32_t(a.ld_mxa);
+    svb[1] = uint32_t(n0 + wn * TN + frow) * uint32_t(a.ld_mxb);
+  }
+  auto load_scales = [&](int ks, uint32_t(&dst)[NS]) {
+    if constexpr (MX) {
+      const int so = 4 * (kfirst + ks);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int op = f < FM ? 0 : 1;
+        const int fb = f < FM ? f : f - FM;
+        const int soff = fb * 32 * int(op == 0 ? a.ld_mxa : a.ld_mxb) + so;
+        dst[f] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(srs[op], int(svb[op]), soff, 0));
+      }
+    }
+  };
   txd::i32x4 fr[2][NF][2];  // [K half][fragment][16-byte piece]
   // Read r of a K half: fragments in the order the MFMAs consume them
   // (A0, B0, A1 .. A(FM-1), B1 .., two 16-byte pieces each.
@@ -236,7 +293,8 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     constexpr int h = decltype(h_tag)::value, i = decltype(i_tag)::value, fn = i / FM, fm = i % FM;
     const i32x8 va = __builtin_shufflevector(fr[h][fm][0], fr[h][fm][1], 0, 1, 2, 3, 4, 5, 6, 7);
     const i32x8 vb = __builtin_shufflevector(fr[h][FM + fn][0], fr[h][FM + fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
-    mfma32<C>(acc[fn][fm], vb, va);
+    if constexpr (MX) mfma32_mx<C, 2 * h>(acc[fn][fm], vb, va, scc[FM + fn], scc[fm]);
+    else mfma32<C>(acc[fn][fm], vb, va);
   };
   using H0 = std::integral_constant<int, 0>;
   using H1 = std::integral_constant<int, 1>;
@@ -245,7 +303,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   // The prologue and the K loop, with or without the K-tail zero fill.
   auto pipeline = [&](auto tail) {
     // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
-    // step 0 landed, half 0 of step 0 in registers.
+    // step 0 landed, half 0 of step 0 in registers.  The MX scales of step 0
+    // go first, so the same wait covers them.
+    load_scales(0, scc);
     static_for<BLKA>([&](auto j) { load_op(0, 0, OpA{}, j, tail); });
     static_for<BLKB>([&](auto j) { load_op(0, 1, OpB{}, j, tail); });
     static_for<BLKA>([&](auto j) { load_op(1, 2, OpA{}, j, tail); });
@@ -257,6 +317,13 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
     for (int ks = 0; ks < ksteps; ++ks) {
       const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;  // step ks+1
+      if constexpr (MX) {
+        // next step's scales first (the mid-step wait below lets them fly),
+        // then this step's into place
+        load_scales(ks + 1, scn);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) scc[f] >>= 8 * fg;
+      }
       static_for<NM>([&](auto I) {
         constexpr int i = decltype(I)::value;
         mma(H0{}, I);
@@ -268,8 +335,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
         __builtin_amdgcn_sched_barrier(0);
       });
       // A and B of step ks+1 landed for every wave (the BLKA loads of A of step
-      // ks+2, issued last, may still be in flight); the slots of step ks are free.
-      wait_and_barrier<BLKA>();
+      // ks+2 and the MX scales of step ks+1, issued last, may still be in
+      // flight); the slots of step ks are free.
+      wait_and_barrier<BLKA + (MX ? NF : 0)>();
       __builtin_amdgcn_sched_barrier(0);
       static_for<NM>([&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -287,6 +355,10 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       });
       sa = na;
       sb = nb;
+      if constexpr (MX) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f) scc[f] = scn[f];
+      }
     }
   };
   if (kb_end % kStep == 0) pipeline(std::false_type{});
@@ -297,10 +369,14 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   // Epilogue: lane owns, per (fm, fn, jj), C[m][n .. n+3] with
   // m = m0 + wm*TM + fm*32 + l%32, n = n0 + wn*TN + fn*32 + 8*jj + 4*(l/32).
   // With K split, the unscaled fp32 sums go to the split's partial plane
-  // (row-major M x N); a reduction kernel combines the planes.
-  if (splits > 1) {
-    float *P = a.part + int64_t(split) * a.M * a.N;
-    const bool pvec = (a.N & 3) == 0;
+  // (row-major M x N); a reduction kernel combines the planes.  An fp32
+  // output (MX variant) is stored the same way, straight into C.
+  if (splits > 1 || OUT == OUT_F32) {
+    float *P = OUT == OUT_F32 ? static_cast<float *>(a.C) : a.part + int64_t(split) * a.M * a.N;
+    const int64_t ldp = OUT == OUT_F32 ? a.ldc : a.N;
+    const bool pvec = OUT == OUT_F32
+                          ? ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0 && (a.ldc & 3) == 0)
+                          : (a.N & 3) == 0;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int m = m0 + wm * TM + fm * 32 + frow;
@@ -310,7 +386,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int n = n0 + wn * TN + fn * 32 + 8 * jj + 4 * fg;
-          float *dst = P + int64_t(m) * a.N + n;
+          float *dst = P + int64_t(m) * ldp + n;
           if (pvec && n + 3 < a.N) {
             *reinterpret_cast<txd::f32x4 *>(dst) =
                 txd::f32x4{acc[fn][fm][4 * jj], acc[fn][fm][4 * jj + 1], acc[fn][fm][4 * jj + 2], acc[fn][fm][4 * jj + 3]};
@@ -323,9 +399,10 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     }
     return;
   }
-  // Epilogue: scale (fp8), round to bf16 and stage the whole tile in LDS (the
-  // ring is free after the drain above), then write whole row segments of C
-  // with 16-byte stores.  Staged 16-byte chunk c of tile row r sits at chunk
+  // Epilogue: scale (fp8 with row / column scales), round to bf16 (fp16)
+  // and stage the whole tile in LDS (the ring is free after the drain
+  // above), then write whole row segments of C with 16-byte stores.
+  // Staged 16-byte chunk c of tile row r sits at chunk
   // c ^ (r % CH): the 32 rows of a fragment column write 32 (BN 256) or 16
   // twice-used (BN 128) different chunks, the minimum two passes for 512
   // bytes, and the CH lanes reading one row cover every chunk once.
@@ -333,8 +410,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   constexpr int ROWB = BN * 2;      // staged row bytes
   constexpr int RPI = 64 / CH;      // rows per store instruction
   static_assert(256 * ROWB <= kSlots * kSlotBytes, "staged tile fits in LDS");
+  constexpr bool ROWCOL = C::FP8 && !MX;  // per-row / per-column fp32 scales
   float sav[FM], sbv[FN][4][4];
-  if constexpr (C::FP8) {
+  if constexpr (ROWCOL) {
     // all scale loads in one batch ahead of their use
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
@@ -362,11 +440,12 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           v[t] = acc[fn][fm][4 * jj + t];
-          if constexpr (C::FP8) v[t] = v[t] * sav[fm] * sbv[fn][jj][t];
+          if constexpr (ROWCOL) v[t] = v[t] * sav[fm] * sbv[fn][jj][t];
         }
         const int c = (wn * TN + fn * 32 + 8 * jj) / 8;
         *reinterpret_cast<txd::u32x2 *>(lds + row * ROWB + ((c ^ (row & (CH - 1))) << 4) + 8 * fg) =
-            txd::u32x2{txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
+            OUT == OUT_F16 ? txd::u32x2{txd::pack_f16x2(v[0], v[1]), txd::pack_f16x2(v[2], v[3])}
+                           : txd::u32x2{txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
       }
   }
   __syncthreads();

@@ -29,6 +29,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// Two fp32 -> packed fp16x2 (low half = a), round to nearest even, fp16
+// subnormals kept, overflow to +-Inf.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
 // fp32 -> bf16 bits, as pack_bf16x2.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return pack_bf16x2(f, 0.0f) & 0xFFFFu;

@@ -27,6 +27,7 @@ from ._lib import TxError, check, lib
 
 __all__ = [
     "TxError", "fp_to_fp", "stoch_round", "atomic_rmw", "dot", "matmul", "dot_scaled_rowcol",
+    "dot_scaled",
     "gemv_fp8_dequant", "plugin_info", "invoke", "get_fp8_format_name",
     "version", "init", "RTNE", "RTZ", "RS",
 ]
@@ -217,6 +218,50 @@ def dot_scaled_rowcol(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Te
     check(lib.tx_dot_fp8_scaled(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
                                 _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0),
                                 _ptr(scale_b), _ptr(out), out.stride(0), M, N, K, _stream(a_q)))
+    return out
+
+
+def _e8m0_bytes(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype == torch.uint8:
+        return t
+    if t.dtype == getattr(torch, "float8_e8m0fnu", None):
+        return t.view(torch.uint8)
+    raise ValueError("MX scales must be uint8 (e8m0 codes) or float8_e8m0fnu")
+
+
+def dot_scaled(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
+               scale_b: torch.Tensor, out_dtype: torch.dtype = torch.float32,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """tt.dot_scaled with MX block scales: one e8m0 scale per 32 K elements,
+    out[m,n] = sum_k a_q[m,k] 2^(scale_a[m,k//32]-127) * b[k,n] 2^(scale_b[n,k//32]-127),
+    fp32 accumulation, rounded to ``out_dtype`` (fp32, bf16 or fp16).
+    a_q: fp8 M x K; b_q_nk: fp8 N x K (the column-major K x N operand);
+    scale_a: M x ceil(K/32), scale_b: N x ceil(K/32), uint8 codes or
+    float8_e8m0fnu."""
+    _on_gpu(a_q, scale_a, b_q_nk, scale_b, out)
+    if a_q.dtype not in _FP8 or b_q_nk.dtype not in _FP8:
+        raise ValueError("dot_scaled takes fp8 operands")
+    if a_q.dim() != 2 or b_q_nk.dim() != 2 or a_q.shape[1] != b_q_nk.shape[1]:
+        raise ValueError("incompatible shapes")
+    if a_q.stride(1) != 1 or b_q_nk.stride(1) != 1:
+        raise ValueError("operands must be K-contiguous")
+    M, K = a_q.shape
+    N = b_q_nk.shape[0]
+    sa, sb = _e8m0_bytes(scale_a), _e8m0_bytes(scale_b)
+    nblk = (K + 31) // 32
+    if sa.dim() != 2 or sb.dim() != 2 or tuple(sa.shape) != (M, nblk) or \
+            tuple(sb.shape) != (N, nblk) or sa.stride(1) != 1 or sb.stride(1) != 1:
+        raise ValueError(f"scales must be row-major {M} x {nblk} and {N} x {nblk}")
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError("out_dtype must be fp32, bf16 or fp16")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
+    if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major M x N tensor of out_dtype")
+    check(lib.tx_dot_scaled_mx(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(sa), sa.stride(0),
+                               _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0), _ptr(sb),
+                               sb.stride(0), _ptr(out), _TX_DTYPE[out_dtype], out.stride(0), M, N, K,
+                               _stream(a_q)))
     return out
 
 

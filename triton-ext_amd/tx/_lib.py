@@ -40,7 +40,7 @@ EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
-    "tx_dot_fp8_scaled", "tx_gemv_fp8_dequant",
+    "tx_dot_fp8_scaled", "tx_dot_scaled_mx", "tx_gemv_fp8_dequant",
 ]
 
 
@@ -119,6 +119,8 @@ def _load():
     L.tx_dot_bf16.restype = I
     L.tx_dot_fp8_scaled.argtypes = [P, I, I64, P, P, I, I64, P, P, I64, I64, I64, I64, VP]
     L.tx_dot_fp8_scaled.restype = I
+    L.tx_dot_scaled_mx.argtypes = [P, I, I64, P, I64, P, I, I64, P, I64, P, I, I64, I64, I64, I64, VP]
+    L.tx_dot_scaled_mx.restype = I
     L.tx_gemv_fp8_dequant.argtypes = [P, I64, P, I, I64, P, I64, I64, P, I64, I64, I64, I64, VP]
     L.tx_gemv_fp8_dequant.restype = I
     return L

@@ -13,6 +13,9 @@ the GPU.  Base seed 20261201; config c uses seed ``BASE ^ (c << 32)``.
       e4m3fn RNE with saturation of x * (448 / absmax).
   c=5 dequant GEMV: x bf16 N(0, 1) M x K; W ~ N(0, 0.02) N x K quantised to
       e5m2 with one fp32 scale per 128 consecutive k (absmax / 57344).
+  c=6 MX-scaled dot: A, B ~ N(0, 1); one e8m0 scale per 32 consecutive k of
+      each row, absmax / fmax rounded up to a power of two, then fp8 RNE with
+      saturation (the reference's MX quantiser, mxfp8_utils.py:17-38).
 """
 from __future__ import annotations
 
@@ -137,3 +140,32 @@ def gemv_input(M: int, N: int = 14336, K: int = 4096, group: int = 128, seed_str
     q = np.clip(wg / s[:, :, None], -57344.0, 57344.0).astype(np.float32).reshape(N, K)
     wq = torch.from_numpy(q).to(torch.float8_e5m2).view(torch.uint8).numpy()
     return x, wq, s
+
+
+# ----------------------------------------------------------------- MX (c=6)
+def quant_mx(x: np.ndarray, fmt: str = "e4m3fn"):
+    """MX quantisation of x (rows x K, K a multiple of 32), following the
+    reference's _compute_scale_and_quantize (mxfp8_utils.py:17-38): per block
+    of 32, descale = absmax / fmax rounded up to a power of two (adding
+    0x007FFFFF to the fp32 bits and keeping the exponent field), e8m0 code =
+    that exponent field, data = clamp(x / descale, +-fmax) cast to fp8 RNE.
+    Returns (codes uint8 rows x K, e8m0 uint8 rows x K/32)."""
+    fmax, dt = (448.0, torch.float8_e4m3fn) if fmt == "e4m3fn" else (57344.0, torch.float8_e5m2)
+    R, K = x.shape
+    xb = x.reshape(R, K // 32, 32).astype(np.float32)
+    descale = (np.abs(xb).max(axis=2) / np.float32(fmax)).astype(np.float32)
+    e = ((descale.view(np.uint32) + np.uint32(0x007FFFFF)) & np.uint32(0x7F800000))
+    rounded = e.view(np.float32)
+    quant = np.where(rounded == 0, np.float32(0), np.float32(1) / np.where(rounded == 0, 1, rounded))
+    q = np.clip(xb * quant[:, :, None].astype(np.float32), -fmax, fmax).astype(np.float32)
+    codes = torch.from_numpy(q.reshape(R, K)).to(dt).view(torch.uint8).numpy()
+    return codes, (e >> np.uint32(23)).astype(np.uint8)
+
+
+def mx_gemm_input(M: int, N: int, K: int, seed_stream: int = 0, fa: str = "e4m3fn",
+                  fb: str = "e4m3fn"):
+    """Returns (Aq uint8[M,K], sa e8m0 uint8[M,K/32], Bq uint8[N,K], sb e8m0 uint8[N,K/32])."""
+    g = rng(6, seed_stream)
+    aq, sa = quant_mx(g.standard_normal((M, K), dtype=np.float32), fa)
+    bq, sb = quant_mx(g.standard_normal((N, K), dtype=np.float32), fb)
+    return aq, sa, bq, sb
