@@ -130,6 +130,29 @@ def bench_fp8_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
             "bytes": M * K + N * K + 4 * (M + N) + 2 * M * N}
 
 
+def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
+    """tt.dot_scaled with MX block scales (e8m0 per 32 K), e4m3fn operands, bf16 out."""
+    from tx import workloads
+    dev = torch.device("cuda:0")
+    aq, sa, bq, sb = workloads.mx_gemm_input(M, N, K)
+    bufs = []
+    for s in range(sets):
+        A = torch.from_numpy(aq).to(dev).view(torch.float8_e4m3fn)
+        B = torch.from_numpy(bq).to(dev).view(torch.float8_e4m3fn)
+        bufs.append((A, torch.from_numpy(sa).to(dev), B, torch.from_numpy(sb).to(dev),
+                     torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
+    del aq, bq
+
+    def step(i):
+        A, a_s, B, b_s, C = bufs[i % sets]
+        tx.dot_scaled(A, a_s, B, b_s, out_dtype=torch.bfloat16, out=C)
+
+    ms = timed(step, steps, warmup)
+    flops = 2.0 * M * N * K
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops,
+            "bytes": M * K + N * K + (M + N) * K // 32 + 2 * M * N}
+
+
 def bench_bf16_gemm(tx, torch, M, N, K, steps, warmup):
     from tx import workloads
     import numpy as np
@@ -348,6 +371,12 @@ def main():
                               "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
                               "gbs": r["bytes"] / (r["ms"] * 1e-3) / 1e9})
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+        for (m, n, k) in [(8192, 8192, 8192), (512, 14336, 4096)]:
+            r = bench_mx_gemm(tx, torch, m, n, k, K, W)
+            secondary.append({"op": "MX-scaled fp8 GEMM (e8m0 per 32 K)", "shape": [m, n, k],
+                              "ms": r["ms"], "tflops": r["tflops"],
+                              "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
             progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
         for (m, n, k) in [(4096, 4096, 4096), (4095, 4097, 4100)]:
             r = bench_bf16_gemm(tx, torch, m, n, k, K, W)

@@ -288,9 +288,9 @@ TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
  * C: row-major M x N (ldc elements) of c_type TX_F32, TX_BF16 or TX_F16
  * (round to nearest even; fp16 overflows to Inf).
  * Uses the library's per-stream scratch (see the conventions above) for
- * zero-padded operand rows when rows are not 16-byte aligned or K is not a
- * multiple of 16, and for repacked scale rows unless K is a multiple of 128
- * and the scale rows are 4-byte aligned (ld_scale_* a multiple of 4).
+ * the scales, repacked into the layout the kernel reads (about
+ * 4 * ceil(K/128) * (M + N) bytes), and for zero-padded operand rows when
+ * rows are not 16-byte aligned or K is not a multiple of 16.
  */
 TX_API tx_status tx_dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda,
                                   const uint8_t *scale_a, int64_t ld_scale_a, const void *B,

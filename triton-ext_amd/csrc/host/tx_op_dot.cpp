@@ -289,9 +289,8 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
 // elements).  The kernel reads its operands through the fast path's LDS-DMA
 // pipeline, so rows that are not 16-byte aligned (or K not a multiple of 16)
 // are first copied into zero-padded rows (stream scratch slot 0, K rounded up
-// to a 128-byte step), and scale rows that are not whole dwords covering
-// exactly the kernel's K steps are copied into such rows, padded with 127
-// (2^0, against zero operands), in slot 2.
+// to a 128-byte step).  The scales are always repacked step-major (slot 2),
+// the layout in which a fragment's scales for one K step are one cache line.
 static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, const uint8_t *sa,
                                int64_t ld_sa, const void *B, tx_dtype b_type, int64_t ldb,
                                const uint8_t *sb, int64_t ld_sb, void *C, tx_dtype c_type,
@@ -343,42 +342,29 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
     args.K = int32_t(kp);
     kk = kp;
   }
-  // scales: each row must hold exactly one dword per K step of the kernel
-  const int64_t sw = (kk + 127) / 128 * 4;  // scale bytes per row the kernel reads
-  // (K = 0: the kernel reads no scale)
-  const bool direct_a = K == 0 || (sw == nblk && aligned(sa, 4) && ld_sa % 4 == 0);
-  const bool direct_b = K == 0 || (sw == nblk && aligned(sb, 4) && ld_sb % 4 == 0);
-  args.mx_a = sa;
-  args.ld_mxa = ld_sa;
-  args.mx_b = sb;
-  args.ld_mxb = ld_sb;
-  if (!direct_a || !direct_b) {
-    const size_t pa_bytes = direct_a ? 0 : size_t(M) * size_t(sw);
-    const size_t pb_bytes = direct_b ? 0 : size_t(N) * size_t(sw);
+  // scales: repacked step-major (one 128-byte line per fragment and step),
+  // rows padded to whole tiles, blocks past ceil(K / 32) set to 2^0
+  const int64_t steps = (kk + 127) / 128;
+  const int64_t rows_a = (M + 255) / 256 * 256, rows_b = (N + 255) / 256 * 256;
+  if (steps * 4 * std::max(rows_a, rows_b) >= (int64_t(1) << 31))
+    return fail(TX_UNSUPPORTED, "%s: scale matrices exceed 32-bit offsets", what);
+  if (steps > 0) {
+    const size_t pa_bytes = size_t(steps) * size_t(rows_a) * 4, pb_bytes = size_t(steps) * size_t(rows_b) * 4;
     TX_TRY(wsc.acquire(s, 2, pa_bytes + pb_bytes));
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pack_scales", &fn));
     uint8_t *p = static_cast<uint8_t *>(wsc.ptr());
-    if (!direct_a) {
-      tx_mx_pack_args pk{sa, p, ld_sa, sw, int32_t(M), int32_t(nblk), int32_t(sw), 0};
-      TX_TRY(launch(fn, unsigned(std::min<int64_t>((M * sw / 4 + 255) / 256, cus * 16)), 1, 256, s,
-                    &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
-      args.mx_a = p;
-      args.ld_mxa = sw;
-      p += pa_bytes;
-    }
-    if (!direct_b) {
-      tx_mx_pack_args pk{sb, p, ld_sb, sw, int32_t(N), int32_t(nblk), int32_t(sw), 0};
-      TX_TRY(launch(fn, unsigned(std::min<int64_t>((N * sw / 4 + 255) / 256, cus * 16)), 1, 256, s,
-                    &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
-      args.mx_b = p;
-      args.ld_mxb = sw;
-    }
+    tx_mx_pack_args pk{sa, p, ld_sa, int32_t(M), int32_t(nblk), int32_t(steps), int32_t(rows_a)};
+    TX_TRY(launch(fn, unsigned(std::min<int64_t>((steps * rows_a + 255) / 256, cus * 16)), 1, 256, s,
+                  &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
+    tx_mx_pack_args pkb{sb, p + pa_bytes, ld_sb, int32_t(N), int32_t(nblk), int32_t(steps), int32_t(rows_b)};
+    TX_TRY(launch(fn, unsigned(std::min<int64_t>((steps * rows_b + 255) / 256, cus * 16)), 1, 256, s,
+                  &pkb, sizeof pkb, "tx_gemm_mx_pack_scales"));
+    args.mx_a = p;
+    args.ld_mxa = rows_a * 4;
+    args.mx_b = p + pa_bytes;
+    args.ld_mxb = rows_b * 4;
   }
-  // lanes address scale rows up to the last tile's end with 32-bit offsets
-  const int64_t lim = int64_t(1) << 31;
-  if ((M + 256) * args.ld_mxa + sw >= lim || (N + 256) * args.ld_mxb + sw >= lim)
-    return fail(TX_UNSUPPORTED, "%s: scale matrices exceed 32-bit offsets", what);
 
   // 256x256 tiles while they give every CU one, else 256x128
   const bool big = ((M + 255) / 256) * ((N + 255) / 256) >= cus;

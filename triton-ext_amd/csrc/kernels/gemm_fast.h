@@ -43,10 +43,16 @@
 //    inside a product does not change an unscaled sum.)
 //  * MX (block-scaled) variant: one e8m0 scale per 32 K elements of each row
 //    of A and B.  A 128-byte step holds blocks 4s .. 4s+3 of a row, one
-//    dword; each lane loads the dword of its row for each of its fragments,
-//    one step ahead, and shifts it right by 8g so that byte 2h is the block
-//    of K half h it multiplies (op_sel picks the byte).  Only 4 wavefronts
-//    (one per SIMD) leave the registers for this.
+//    dword; the host repacks the scales step-major (dword [s][row]), so the
+//    32 rows of a fragment are one 128-byte line per step.  Each lane loads
+//    the dword of its row for each of its fragments and, when the step
+//    begins, shifts it right by 8g so that byte 2h is the block of K half h
+//    it multiplies (op_sel picks the byte).  The loads of step k+1 are issued
+//    at the start of the second half of step k, ahead of that half's LDS-DMA
+//    loads: loads complete in issue order, so a scale load issued behind the
+//    DMA loads would make its first use wait for operand loads that the
+//    pipeline otherwise gives two steps.  Only 4 wavefronts (one per SIMD)
+//    leave the registers for this.
 #pragma once
 
 #include <type_traits>
@@ -243,29 +249,29 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       ro[1][h][e] = off(wn * TN + frow, chunk);
     }
 
-  // MX scales: dword s of a scale row holds the blocks of K step s.  Lanes
-  // of rows past M / N read past the buffer's range and get 0 (2^-127, times
-  // zero operands).  scc: this step's dwords (shifted by 8g once landed),
-  // scn: the next step's, in flight.
+  // MX scales, step-major: the dword of row r for K step s (blocks 4s ..
+  // 4s+3) at byte s * ld_mx + 4r; rows are padded to whole tiles (with
+  // finite codes), and the load one step past the end reads past the
+  // buffer's range (zeros, never used).  scn: the raw dwords of the next
+  // step, in flight; scc: this step's, shifted by 8g.
   constexpr int NS = MX ? NF : 1;
   uint32_t scc[NS], scn[NS];
   __amdgpu_buffer_rsrc_t srs[2];
   uint32_t svb[2] = {0u, 0u};
   if constexpr (MX) {
-    const uint32_t sbytes = uint32_t(ksteps_all) * 4u;
-    srs[0] = make_rsrc(a.mx_a, sbytes ? uint32_t(a.M - 1) * uint32_t(a.ld_mxa) + sbytes : 0u);
-    srs[1] = make_rsrc(a.mx_b, sbytes ? uint32_t(a.N - 1) * uint32_t(a.ld_mxb) + sbytes : 0u);
-    svb[0] = uint32_t(m0 + wm * TM + frow) * uint32_t(a.ld_mxa);
-    svb[1] = uint32_t(n0 + wn * TN + frow) * uint32_t(a.ld_mxb);
+    srs[0] = make_rsrc(a.mx_a, uint32_t(ksteps_all) * uint32_t(a.ld_mxa));
+    srs[1] = make_rsrc(a.mx_b, uint32_t(ksteps_all) * uint32_t(a.ld_mxb));
+    svb[0] = 4u * uint32_t(m0 + wm * TM + frow);
+    svb[1] = 4u * uint32_t(n0 + wn * TN + frow);
   }
   auto load_scales = [&](int ks, uint32_t(&dst)[NS]) {
     if constexpr (MX) {
-      const int so = 4 * (kfirst + ks);
+      const int s = kfirst + ks;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const int op = f < FM ? 0 : 1;
         const int fb = f < FM ? f : f - FM;
-        const int soff = fb * 32 * int(op == 0 ? a.ld_mxa : a.ld_mxb) + so;
+        const int soff = s * int(op == 0 ? a.ld_mxa : a.ld_mxb) + 128 * fb;
         dst[f] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(srs[op], int(svb[op]), soff, 0));
       }
     }
@@ -305,7 +311,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
     // step 0 landed, half 0 of step 0 in registers.  The MX scales of step 0
     // go first, so the same wait covers them.
-    load_scales(0, scc);
+    load_scales(0, scn);
     static_for<BLKA>([&](auto j) { load_op(0, 0, OpA{}, j, tail); });
     static_for<BLKB>([&](auto j) { load_op(0, 1, OpB{}, j, tail); });
     static_for<BLKA>([&](auto j) { load_op(1, 2, OpA{}, j, tail); });
@@ -318,11 +324,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     for (int ks = 0; ks < ksteps; ++ks) {
       const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;  // step ks+1
       if constexpr (MX) {
-        // next step's scales first (the mid-step wait below lets them fly),
-        // then this step's into place
-        load_scales(ks + 1, scn);
+        // this step's scales (loaded during the previous half) into place
 #pragma unroll
-        for (int f = 0; f < NF; ++f) scc[f] >>= 8 * fg;
+        for (int f = 0; f < NF; ++f) scc[f] = scn[f] >> (8 * fg);
       }
       static_for<NM>([&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -335,10 +339,10 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
         __builtin_amdgcn_sched_barrier(0);
       });
       // A and B of step ks+1 landed for every wave (the BLKA loads of A of step
-      // ks+2 and the MX scales of step ks+1, issued last, may still be in
-      // flight); the slots of step ks are free.
-      wait_and_barrier<BLKA + (MX ? NF : 0)>();
+      // ks+2, issued last, may still be in flight); the slots of step ks are free.
+      wait_and_barrier<BLKA>();
       __builtin_amdgcn_sched_barrier(0);
+      load_scales(ks + 1, scn);  // MX: ahead of this half's DMA loads
       static_for<NM>([&](auto I) {
         constexpr int i = decltype(I)::value;
         mma(H1{}, I);
@@ -355,10 +359,6 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       });
       sa = na;
       sb = nb;
-      if constexpr (MX) {
-#pragma unroll
-        for (int f = 0; f < NF; ++f) scc[f] = scn[f];
-      }
     }
   };
   if (kb_end % kStep == 0) pipeline(std::false_type{});

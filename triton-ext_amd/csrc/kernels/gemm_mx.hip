@@ -29,22 +29,26 @@ TX_GEMM_MX_OUTS(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 // Operand rows into zero-padded, 16-byte aligned rows (as the fp8 GEMM's).
 TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pad_rows(const tx_pad_args a) { pad_rows<1>(a); }
 
-// Scale rows into rows of a whole number of dwords, padded with 127 (2^0):
-// one thread per output dword.
+// Scales into the step-major layout the tile reads (see tx_mx_pack_args):
+// one thread per output dword, consecutive threads on consecutive rows.
 TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pack_scales(const tx_mx_pack_args a) {
-  const int64_t words_per_row = a.dst_cols / 4;
-  const int64_t total = int64_t(a.rows) * words_per_row;
+  const int64_t total = int64_t(a.steps) * a.rows_pad;
+  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst);
   for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
        t += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t r = t / words_per_row;
-    const int c0 = int(t % words_per_row) * 4;
-    const uint8_t *src = a.src + r * a.src_ld;
-    uint32_t w = 0;
+    const int s = int(t / a.rows_pad);
+    const int r = int(t % a.rows_pad);
+    uint32_t w = 0x7F7F7F7Fu;
+    if (r < a.rows) {
+      const uint8_t *src = a.src + int64_t(r) * a.src_ld;
+      w = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t b = c0 + i < a.cols ? uint32_t(src[c0 + i]) : 127u;
-      w |= b << (8 * i);
+      for (int i = 0; i < 4; ++i) {
+        const int c = 4 * s + i;
+        const uint32_t b = c < a.cols ? uint32_t(src[c]) : 127u;
+        w |= b << (8 * i);
+      }
     }
-    *reinterpret_cast<uint32_t *>(a.dst + r * a.dst_ld + c0) = w;
+    dst[t] = w;
   }
 }

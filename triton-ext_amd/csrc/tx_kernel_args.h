@@ -53,26 +53,27 @@ typedef struct tx_gemm_args {
   int32_t splits;    /* fast path: K splits (<= 1: none) */
   int32_t ksteps_split; /* fast path: 128-byte K steps per split */
   float *part;       /* fast path with splits > 1: splits x M x N fp32 partial sums */
-  /* MX-scaled dot: e8m0 block scales, one byte per 32 K elements; row r of A
-   * (of B) at mx_a + r * ld_mxa (mx_b + r * ld_mxb).  Every row holds at least
-   * ceil(K / 128) * 4 readable bytes, and ld_mx* is a multiple of 4. */
+  /* MX-scaled dot: e8m0 block scales (one byte per 32 K elements), packed
+   * step-major: the 4 scales of row r for 128-element K step s (blocks
+   * 4s .. 4s+3, low byte first) are the dword at byte s * ld_mx* + 4r, for
+   * every row of every tile (rows past M / N hold finite codes). */
   const uint8_t *mx_a;
   const uint8_t *mx_b;
   int64_t ld_mxa;
   int64_t ld_mxb;
 } tx_gemm_args;
 
-/* Scale-row copy for the MX-scaled dot: dst[r][c] = c < cols ? src[r][c] : 127
- * (2^0) for c < dst_cols (dst_cols a multiple of 4, dst_ld of 4). */
+/* Step-major repack of MX scales: dst dword [s][r] (byte s * 4 * rows_pad +
+ * 4r) = bytes src[r][4s .. 4s+3], with 127 (2^0) for r >= rows or a block
+ * >= cols. */
 typedef struct tx_mx_pack_args {
   const uint8_t *src;
   uint8_t *dst;
-  int64_t src_ld;
-  int64_t dst_ld;
+  int64_t src_ld;   /* bytes between source rows */
   int32_t rows;
-  int32_t cols;
-  int32_t dst_cols;
-  int32_t reserved;
+  int32_t cols;     /* scale blocks per source row, ceil(K / 32) */
+  int32_t steps;    /* K steps of the kernel */
+  int32_t rows_pad; /* rows of the packed matrix (whole tiles) */
 } tx_mx_pack_args;
 
 /* Row copy into a zero-padded buffer: dst[r][c] = c < cols ? src[r][c] : 0
