@@ -72,10 +72,12 @@ def check_mx(got, ref, mag, bmax, K, out):
     (256, 256, 256, 1, 1, "f32"), (256, 256, 256, 1, 1, "bf16"), (256, 256, 256, 1, 1, "f16"),
     (300, 500, 4096, 1, 1, "bf16"), (257, 501, 2048, 2, 1, "f32"), (64, 96, 96, 1, 2, "f32"),
     (130, 260, 1000, 2, 2, "bf16"), (77, 33, 33, 1, 1, "f32"), (1, 1, 32, 1, 1, "f32"),
-    (600, 1000, 640, 1, 1, "f16")])
+    (600, 1000, 640, 1, 1, "f16"), (512, 2048, 4096, 1, 1, "f32"), (300, 1000, 2048, 2, 1, "bf16"),
+    (256, 512, 8192, 1, 1, "f16")])
 def test_mx_shapes(tx, oracle, dev, M, N, K, fa, fb, out):
-    """256x256 and 256x128 tiles; K a multiple of 128 (scales read in place),
-    of 32 (scale rows repacked), or ragged (operands zero-padded)."""
+    """256x256 tiles, 256x128 tiles with and without K split into fp32
+    planes (the last three shapes split 4, 2 and 8 ways); K a multiple of
+    128, of 32, or ragged (operands zero-padded)."""
     g = np.random.default_rng(M * 7 + N * 3 + K)
     aq, bq = _codes(g, (M, K), fa), _codes(g, (N, K), fb)
     nb = (K + 31) // 32

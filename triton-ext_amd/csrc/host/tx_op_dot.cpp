@@ -354,23 +354,49 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pack_scales", &fn));
     uint8_t *p = static_cast<uint8_t *>(wsc.ptr());
-    tx_mx_pack_args pk{sa, p, ld_sa, int32_t(M), int32_t(nblk), int32_t(steps), int32_t(rows_a)};
-    TX_TRY(launch(fn, unsigned(std::min<int64_t>((steps * rows_a + 255) / 256, cus * 16)), 1, 256, s,
-                  &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
-    tx_mx_pack_args pkb{sb, p + pa_bytes, ld_sb, int32_t(N), int32_t(nblk), int32_t(steps), int32_t(rows_b)};
-    TX_TRY(launch(fn, unsigned(std::min<int64_t>((steps * rows_b + 255) / 256, cus * 16)), 1, 256, s,
-                  &pkb, sizeof pkb, "tx_gemm_mx_pack_scales"));
+    // one workgroup per 64 rows x 32 K steps
+    const int64_t ga = (rows_a / 64) * ((steps + 31) / 32), gb = (rows_b / 64) * ((steps + 31) / 32);
+    if (ga + gb > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: scale repack grid too large", what);
+    tx_mx_pack2_args pk{{{sa, p, ld_sa, int32_t(M), int32_t(nblk), int32_t(steps), int32_t(rows_a)},
+                         {sb, p + pa_bytes, ld_sb, int32_t(N), int32_t(nblk), int32_t(steps), int32_t(rows_b)}},
+                        int32_t(ga), 0};
+    TX_TRY(launch(fn, unsigned(ga + gb), 1, 256, s, &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
     args.mx_a = p;
     args.ld_mxa = rows_a * 4;
     args.mx_b = p + pa_bytes;
     args.ld_mxb = rows_b * 4;
   }
 
-  // 256x256 tiles while they give every CU one, else 256x128
+  // 256x256 tiles while they give every CU one, else 256x128, with K split
+  // into fp32 partial planes (slot 1) while tiles still leave CUs idle
   const bool big = ((M + 255) / 256) * ((N + 255) / 256) >= cus;
   char kname[80];
   std::snprintf(kname, sizeof kname, "tx_gemm_mx_%s_%s_%s%s", fa, fb, fo, big ? "" : "_n128");
-  return launch_gemm(kname, CodeObject::GemmMx, args, 256, big ? 256 : 128, s, 256);
+  if (big) return launch_gemm(kname, CodeObject::GemmMx, args, 256, 256, s, 256);
+  const int64_t tiles = ((M + 255) / 256) * ((N + 127) / 128);
+  int64_t splits = std::min({kMaxSplits, cus / tiles, steps / kMinStepsPerSplit});
+  ScratchLease part;
+  if (splits >= 2) {
+    const int64_t per = (steps + splits - 1) / splits;
+    splits = (steps + per - 1) / per;  // no empty split
+    const size_t bytes = size_t(splits) * size_t(M) * size_t(N) * sizeof(float);
+    if (part.acquire(s, 1, bytes) != TX_SUCCESS) {
+      clear_error();  // no workspace: run unsplit
+    } else {
+      args.splits = int32_t(splits);
+      args.ksteps_split = int32_t(per);
+      args.part = static_cast<float *>(part.ptr());
+    }
+  }
+  if (!part.ptr()) return launch_gemm(kname, CodeObject::GemmMx, args, 256, 128, s, 512);
+  TX_TRY(launch_gemm(kname, CodeObject::GemmMx, args, 256, 128, s, 512, int(args.splits)));
+  char rname[64];
+  std::snprintf(rname, sizeof rname, "tx_gemm_mx_splitk_reduce_%s", fo);
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::GemmMx, rname, &fn));
+  const int64_t quads = M * ((N + 3) / 4);
+  const int64_t grid = std::min<int64_t>((quads + 255) / 256, cus * 16);
+  return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, rname);
 }
 
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,

@@ -51,8 +51,9 @@
 //    at the start of the second half of step k, ahead of that half's LDS-DMA
 //    loads: loads complete in issue order, so a scale load issued behind the
 //    DMA loads would make its first use wait for operand loads that the
-//    pipeline otherwise gives two steps.  Only 4 wavefronts (one per SIMD)
-//    leave the registers for this.
+//    pipeline otherwise gives two steps.  In the 256 x 256 tile only 4
+//    wavefronts (one per SIMD) leave the registers for this; the 256 x 128
+//    tile keeps 8.
 #pragma once
 
 #include <type_traits>
@@ -148,7 +149,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
-  static_assert(!MX || (C::FP8 && NW == 4), "MX scales: fp8 operands, 4 wavefronts");
+  static_assert(!MX || (C::FP8 && (NW == 4 || BN == 128)), "MX scales: fp8 operands; 256x256: 4 wavefronts");
   static_assert(OUT == OUT_BF16 || MX, "fp16 / fp32 output: MX variant only");
   // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per
   // wave): LDS reads per step are then (64 + 64) x 8 rows instead of
@@ -372,11 +373,10 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   // (row-major M x N); a reduction kernel combines the planes.  An fp32
   // output (MX variant) is stored the same way, straight into C.
   if (splits > 1 || OUT == OUT_F32) {
-    float *P = OUT == OUT_F32 ? static_cast<float *>(a.C) : a.part + int64_t(split) * a.M * a.N;
-    const int64_t ldp = OUT == OUT_F32 ? a.ldc : a.N;
-    const bool pvec = OUT == OUT_F32
-                          ? ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0 && (a.ldc & 3) == 0)
-                          : (a.N & 3) == 0;
+    float *P = splits > 1 ? a.part + int64_t(split) * a.M * a.N : static_cast<float *>(a.C);
+    const int64_t ldp = splits > 1 ? a.N : a.ldc;
+    const bool pvec = splits > 1 ? (a.N & 3) == 0
+                                 : ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0 && (a.ldc & 3) == 0);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int m = m0 + wm * TM + fm * 32 + frow;
@@ -472,9 +472,10 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   }
 }
 
-// Split-K reduction: C[m, n] = bf16_rne(scale_a[m] * scale_b[n] * sum_s P[s][m][n])
-// (scales for fp8 only), four consecutive n per thread.
-template <bool FP8>
+// Split-K reduction: C[m, n] = out(scale_a[m] * scale_b[n] * sum_s P[s][m][n])
+// (ROWCOL: the fp8 row / column scales; out: bf16 or fp16 round to nearest
+// even, or fp32), four consecutive n per thread.
+template <bool ROWCOL, int OUT = OUT_BF16>
 __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
   const int64_t quads_per_row = (a.N + 3) / 4;
   const int64_t total = int64_t(a.M) * quads_per_row;
@@ -498,13 +499,15 @@ __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
           if (n + i < a.N) v[i] += p[s * plane + i];
     }
     float sa = 1.0f;
-    if constexpr (FP8) sa = a.scale_a[m];
+    if constexpr (ROWCOL) sa = a.scale_a[m];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (n + i >= a.N) break;
       float r = v[i];
-      if constexpr (FP8) r = r * sa * a.scale_b[n + i];
-      Cb[int64_t(m) * a.ldc + n + i] = uint16_t(txd::f32_to_bf16_bits(r));
+      if constexpr (ROWCOL) r = r * sa * a.scale_b[n + i];
+      if constexpr (OUT == OUT_F32) static_cast<float *>(a.C)[int64_t(m) * a.ldc + n + i] = r;
+      else if constexpr (OUT == OUT_F16) Cb[int64_t(m) * a.ldc + n + i] = uint16_t(txd::pack_f16x2(r, 0.0f));
+      else Cb[int64_t(m) * a.ldc + n + i] = uint16_t(txd::f32_to_bf16_bits(r));
     }
   }
 }

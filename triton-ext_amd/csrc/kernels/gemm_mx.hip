@@ -2,8 +2,8 @@
 // operands, one e8m0 scale per 32 K elements of each row of A and each
 // column of B, fp32 accumulation in v_mfma_scale_f32_32x32x64_f8f6f4 (the
 // scales enter the MFMA itself), output bf16, fp16 or fp32.  The tile is the
-// fast path's 256 x 256 (or 256 x 128) LDS-DMA pipeline with 4 wavefronts;
-// see gemm_fast.h.
+// fast path's LDS-DMA pipeline: 256 x 256 with 4 wavefronts, 256 x 128 with
+// 8; see gemm_fast.h.
 #include "gemm_common.h"
 #include "gemm_fast.h"
 
@@ -13,8 +13,8 @@ using namespace txg;
   TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_##FA##_##FB##_##ON(const tx_gemm_args a) {      \
     gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256, 4, true, OUT>(a);                    \
   }                                                                                                \
-  TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_##FA##_##FB##_##ON##_n128(const tx_gemm_args a) { \
-    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128, 4, true, OUT>(a);                    \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_mx_##FA##_##FB##_##ON##_n128(const tx_gemm_args a) { \
+    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128, 8, true, OUT>(a);                    \
   }
 #define TX_GEMM_MX_OUTS(FA, FB, ELA, ELB)      \
   TX_GEMM_MX(FA, FB, ELA, ELB, bf16, OUT_BF16) \
@@ -26,29 +26,67 @@ TX_GEMM_MX_OUTS(e5m2, e5m2, EL_E5M2, EL_E5M2)
 TX_GEMM_MX_OUTS(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
 TX_GEMM_MX_OUTS(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 
+// Split-K: sums of the K splits' fp32 planes, rounded to the output type.
+TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_splitk_reduce_bf16(const tx_gemm_args a) {
+  splitk_reduce<false, OUT_BF16>(a);
+}
+TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_splitk_reduce_f16(const tx_gemm_args a) {
+  splitk_reduce<false, OUT_F16>(a);
+}
+TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_splitk_reduce_f32(const tx_gemm_args a) {
+  splitk_reduce<false, OUT_F32>(a);
+}
+
 // Operand rows into zero-padded, 16-byte aligned rows (as the fp8 GEMM's).
 TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pad_rows(const tx_pad_args a) { pad_rows<1>(a); }
 
-// Scales into the step-major layout the tile reads (see tx_mx_pack_args):
-// one thread per output dword, consecutive threads on consecutive rows.
-TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pack_scales(const tx_mx_pack_args a) {
-  const int64_t total = int64_t(a.steps) * a.rows_pad;
-  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst);
-  for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
-       t += int64_t(gridDim.x) * blockDim.x) {
-    const int s = int(t / a.rows_pad);
-    const int r = int(t % a.rows_pad);
-    uint32_t w = 0x7F7F7F7Fu;
-    if (r < a.rows) {
-      const uint8_t *src = a.src + int64_t(r) * a.src_ld;
-      w = 0;
+// Scales of A and B into the step-major layout the tile reads (see
+// tx_mx_pack_args), through LDS: workgroup b of an operand transposes rows
+// 64 * (b % R) .. +63 (R = rows_pad / 64) for K steps 32 * (b / R) .. +31
+// (128 blocks), reading each source
+// row's bytes contiguously (dwords when the rows are 4-byte aligned, every
+// load issued before the first is used) and writing 256-byte runs of each
+// step's dwords.
+TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pack_scales(const tx_mx_pack2_args both) {
+  __shared__ uint32_t t[64][33];  // [row][dword of 4 blocks], odd pitch against bank conflicts
+  const bool second = int(blockIdx.x) >= both.blocks0;
+  const tx_mx_pack_args &a = both.op[second ? 1 : 0];
+  const int b = int(blockIdx.x) - (second ? both.blocks0 : 0);
+  const int nrb = a.rows_pad / 64;
+  const int r0 = (b % nrb) * 64;
+  const int s0 = (b / nrb) * 32;
+  const int c0 = 4 * s0;
+  const int tid = threadIdx.x;
+  const bool words = (reinterpret_cast<uintptr_t>(a.src) & 3) == 0 && (a.src_ld & 3) == 0;
+  uint32_t w[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = 4 * s + i;
-        const uint32_t b = c < a.cols ? uint32_t(src[c]) : 127u;
-        w |= b << (8 * i);
+  for (int j = 0; j < 8; ++j) {
+    const int i = tid + 256 * j;  // tile dword: row i / 32, blocks 4 (i % 32) .. +3
+    const int r = i >> 5, c = c0 + 4 * (i & 31);
+    uint32_t v = 0x7F7F7F7Fu;
+    if (r0 + r < a.rows) {
+      const uint8_t *row = a.src + int64_t(r0 + r) * a.src_ld;
+      if (words && c + 3 < a.cols) {
+        v = *reinterpret_cast<const uint32_t *>(row + c);
+      } else {
+        v = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v |= (c + k < a.cols ? uint32_t(row[c + k]) : 127u) << (8 * k);
       }
     }
-    dst[t] = w;
+    w[j] = v;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = tid + 256 * j;
+    t[i >> 5][i & 31] = w[j];
+  }
+  __syncthreads();
+  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst);
+  const int r = tid & 63;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int sl = (tid >> 6) + 4 * j;  // step within the tile
+    if (s0 + sl < a.steps) dst[int64_t(s0 + sl) * a.rows_pad + r0 + r] = t[r][sl];
   }
 }

@@ -76,6 +76,14 @@ typedef struct tx_mx_pack_args {
   int32_t rows_pad; /* rows of the packed matrix (whole tiles) */
 } tx_mx_pack_args;
 
+/* Both operands' repacks in one launch: workgroups [0, blocks0) pack op[0],
+ * the rest op[1]. */
+typedef struct tx_mx_pack2_args {
+  tx_mx_pack_args op[2];
+  int32_t blocks0;
+  int32_t reserved;
+} tx_mx_pack2_args;
+
 /* Row copy into a zero-padded buffer: dst[r][c] = c < cols ? src[r][c] : 0
  * for c < dst_cols (elements of elem_bytes bytes; dst rows 16-byte aligned,
  * dst_cols a multiple of 16 / elem_bytes). */
