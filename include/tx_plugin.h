@@ -299,6 +299,41 @@ TX_API tx_status tx_dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda,
                                   int64_t M, int64_t N, int64_t K, tx_stream_t stream);
 
 /*
+ * absmax + fp8 quantiser with MX block scales, the producer in front of
+ * tx_dot_scaled_mx.  Follows the reference's _compute_scale_and_quantize /
+ * _to_mxfp8_block (extensions/utlx/python/utlx_plugin/mxfp8_utils.py:10-56)
+ * for each block of 32 consecutive elements of a row:
+ *   amax  = max |x| over the block (NaN ignored, as tl.max),
+ *   e     = ((bits(amax / fmax) + 0x007FFFFF) & 0x7F800000) >> 23   (fp32
+ *           division, round to nearest; the e8m0 scale written to scales),
+ *   q     = fp8_rne(clamp(x * (1 / 2^(e - 127)), +-fmax))   (x * 0 when e = 0),
+ * fmax = 448 (TX_FP8E4M3FN) or 57344 (TX_FP8E5M2).  NaN inputs give the NaN
+ * code; an infinite amax gives e = 255 and zeros (NaN for the infinities).
+ * x: fp32 or bf16 (x_type), row-major rows x K (ldx elements), K a multiple
+ * of 32; q: fp8 row-major (ldq bytes); scales: e8m0 bytes rows x K/32
+ * (ld_scales bytes).
+ */
+TX_API tx_status tx_quantize_mx(const void *x, tx_dtype x_type, int64_t ldx, void *q,
+                                tx_dtype q_type, int64_t ldq, uint8_t *scales,
+                                int64_t ld_scales, int64_t rows, int64_t K,
+                                tx_stream_t stream);
+
+/*
+ * absmax + fp8 quantiser with one fp32 scale per row, the producer of
+ * tx_dot_fp8_scaled's operands (rows of A, and rows of the N x K storage of
+ * B, i.e. its columns).  No reference kernel exists; the form is the
+ * reference's saturating idiom (clamp, then convert: mxfp8_utils.py:36-38)
+ * with a per-row scale:
+ *   amax = max |x| over the row (NaN ignored; 1 if it is 0),
+ *   q = fp8_rne(clamp(x * (fmax / amax), +-fmax)),  scales[r] = amax / fmax
+ * in fp32.  x: fp32 or bf16 rows x K (ldx elements); q: fp8 (ldq bytes);
+ * scales: fp32[rows].
+ */
+TX_API tx_status tx_quantize_rowwise(const void *x, tx_dtype x_type, int64_t ldx, void *q,
+                                     tx_dtype q_type, int64_t ldq, float *scales,
+                                     int64_t rows, int64_t K, tx_stream_t stream);
+
+/*
  * fp8 weight-only dequant GEMV / skinny GEMM:
  * y[m,n] = bf16_rne(sum_g scales[n,g] * sum_{k in group g} x[m,k] * f32(W[n,k])).
  * No reference kernel exists (the nearest is the fp8 tt.dot of

@@ -66,6 +66,8 @@ def lib():
                                            I64, I64, I, P, P, I]
         L.txo_gemm_mx_rows.argtypes = [P, I64, P, I64, P, I64, P, I64, I64, I64, I, I, I64, I64,
                                        P, P, P, I]
+        L.txo_quant_mx.argtypes = [P, I64, I64, I64, I, P, P, I]
+        L.txo_quant_row.argtypes = [P, I64, I64, I64, I, P, P, I]
         L.txo_encode_fmt.argtypes = [P, P, I64, I, I, I, I]
         L.txo_encode_fmt.restype = I
         L.txo_round_rs.argtypes = [P, P, P, I64, I, I]
@@ -248,6 +250,35 @@ def gemm_mx_rows(A, sa, B, sb, r0: int, r1: int, fmt_a=E4M3FN, fmt_b=E4M3FN, nth
     lib().txo_gemm_mx_rows(_p(A), K, _p(sa), sa.shape[1], _p(B), K, _p(sb), sb.shape[1], N, K,
                            fmt_a, fmt_b, r0, r1, _p(o32), _p(oab), _p(obm), nthreads)
     return (o32, oab, obm) if block_max else (o32, oab)
+
+
+def _widen(x):
+    """fp32 values of x (fp32, or bf16 given as uint16 bits)."""
+    x = np.asarray(x)
+    if x.dtype == np.uint16:
+        return (x.astype(np.uint32) << 16).view(np.float32)
+    return np.ascontiguousarray(x, np.float32)
+
+
+def quant_mx(x, fmt: int = E4M3FN, nthreads: int = 0):
+    """MX quantisation of the rows of x (fp32, or bf16 bits as uint16), K a
+    multiple of 32.  Returns (codes uint8 rows x K, e8m0 uint8 rows x K/32)."""
+    xf = np.ascontiguousarray(_widen(x))
+    rows, K = xf.shape
+    q = np.empty((rows, K), np.uint8)
+    s = np.empty((rows, K // 32), np.uint8)
+    lib().txo_quant_mx(_p(xf), K, rows, K, fmt, _p(q), _p(s), nthreads)
+    return q, s
+
+
+def quant_rowwise(x, fmt: int = E4M3FN, nthreads: int = 0):
+    """Row-wise absmax quantisation.  Returns (codes uint8 rows x K, fp32 scales[rows])."""
+    xf = np.ascontiguousarray(_widen(x))
+    rows, K = xf.shape
+    q = np.empty((rows, K), np.uint8)
+    s = np.empty((rows,), np.float32)
+    lib().txo_quant_row(_p(xf), K, rows, K, fmt, _p(q), _p(s), nthreads)
+    return q, s
 
 
 def gemv_fp8_dequant(x, W, s, group: int = 128, fmt_w=E5M2, nthreads: int = 0):

@@ -35,6 +35,11 @@
  *   scatter      : brute-force loops on tiny inputs; int32 wrap mod 2^32;
  *                  conservation of the total.
  *   gemm / gemv  : brute force on tiny shapes vs. numpy float64; linearity.
+ *   quantisers   : the scale is the smallest power of two >= amax / fmax
+ *                  (MX) or amax / fmax (row-wise), checked in exact
+ *                  arithmetic; codes vs PyTorch's fp8 cast of the clamped,
+ *                  scaled values; the dequantised error bound; NaN / Inf /
+ *                  zero / denormal blocks.
  *   MX dot       : numpy float64 matmul of the operands with each e8m0 scale
  *                  repeated over its 32 K values (the reference check's
  *                  form); scale exponent shifts double or halve rows and
@@ -632,6 +637,78 @@ TXO_API void txo_gemm_mx_rows(const uint8_t *A, int64_t lda, const uint8_t *sa,
       if (out_abs) out_abs[o] = (float)mag;
       if (out_bmax) out_bmax[o] = (float)bmax;
     }
+  }
+  (void)nthreads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* absmax + fp8 quantisers (fp32 input; bf16 input is widened exactly by    */
+/* the caller).                                                             */
+/* MX (the reference's _compute_scale_and_quantize, mxfp8_utils.py:17-38),   */
+/* per 32-element block of a row: amax = max |x| ignoring NaN (tl.max's      */
+/* combine, tl.maximum, defaults to propagate_nan NONE); descale = amax /   */
+/* fmax in fp32; exponent field e of descale rounded up to a power of two   */
+/* by adding 0x007FFFFF to its bits; scale code e; quant = 0 when the       */
+/* rounded descale is 0, else 1 / rounded (0 for e = 255, Inf);            */
+/* q = fp8_rne(clamp(x * quant, +-fmax)) with NaN kept.                     */
+/* Row-wise: amax over the row (1 if 0), q = fp8_rne(clamp(x * (fmax /     */
+/* amax))), scale = amax / fmax, all fp32.                                  */
+/* ------------------------------------------------------------------------ */
+static float q_clamp(float v, float fmax) {
+  return v > fmax ? fmax : (v < -fmax ? -fmax : v);
+}
+
+TXO_API void txo_quant_mx(const float *x, int64_t ldx, int64_t rows, int64_t K,
+                          int fmt, uint8_t *q, uint8_t *scales, int nthreads) {
+  init_tables();
+  const fp8_fmt *F = fmt_of(fmt);
+  const int fid = fmt == TXO_E5M2 ? 2 : 1;
+  const float fmax = fmt == TXO_E5M2 ? 57344.0f : 448.0f;
+  const int64_t nb = K / 32;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t b = 0; b < nb; ++b) {
+      const float *xb = x + r * ldx + 32 * b;
+      float amax = 0.0f;
+      for (int i = 0; i < 32; ++i)
+        if (fabsf(xb[i]) > amax) amax = fabsf(xb[i]);
+      const float descale = amax / fmax;
+      uint32_t bits;
+      memcpy(&bits, &descale, 4);
+      const uint32_t e = ((bits + 0x007FFFFFu) & 0x7F800000u) >> 23;
+      float quant = 0.0f;
+      if (e != 0 && e != 255) quant = ldexpf(1.0f, 127 - (int)e);
+      scales[r * nb + b] = (uint8_t)e;
+      for (int i = 0; i < 32; ++i)
+        q[r * K + 32 * b + i] = encode_one(F, fid, q_clamp(xb[i] * quant, fmax), 0, 0);
+    }
+  }
+  (void)nthreads;
+}
+
+TXO_API void txo_quant_row(const float *x, int64_t ldx, int64_t rows, int64_t K,
+                           int fmt, uint8_t *q, float *scales, int nthreads) {
+  init_tables();
+  const fp8_fmt *F = fmt_of(fmt);
+  const int fid = fmt == TXO_E5M2 ? 2 : 1;
+  const float fmax = fmt == TXO_E5M2 ? 57344.0f : 448.0f;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *xr = x + r * ldx;
+    float amax = 0.0f;
+    for (int64_t k = 0; k < K; ++k)
+      if (fabsf(xr[k]) > amax) amax = fabsf(xr[k]);
+    if (amax == 0.0f) amax = 1.0f;
+    const float mult = fmax / amax;
+    scales[r] = amax / fmax;
+    for (int64_t k = 0; k < K; ++k)
+      q[r * K + k] = encode_one(F, fid, q_clamp(xr[k] * mult, fmax), 0, 0);
   }
   (void)nthreads;
 }

@@ -19,6 +19,23 @@ typedef struct tx_fp8_codec_args {
   const uint32_t *rbits; /* stochastic rounding: one random word per element */
 } tx_fp8_codec_args;
 
+/* absmax + fp8 quantisers: x (fp32 or bf16) rows x K (ldx elements) ->
+ * q fp8 rows x K (ldq bytes) and scales (MX: e8m0 bytes rows x K/32, ld_s
+ * bytes; row-wise: fp32[rows]).  vec: rows and pitches allow the 16-byte
+ * loads / 8-byte stores of the vector path. */
+typedef struct tx_quant_args {
+  const void *x;
+  uint8_t *q;
+  void *scales;
+  int64_t ldx;
+  int64_t ldq;
+  int64_t ld_s;
+  int64_t rows;
+  int64_t K;
+  int32_t vec;
+  int32_t reserved;
+} tx_quant_args;
+
 /* scatter-reduce */
 typedef struct tx_scatter_args {
   void *bins;

@@ -27,7 +27,7 @@ from ._lib import TxError, check, lib
 
 __all__ = [
     "TxError", "fp_to_fp", "stoch_round", "atomic_rmw", "dot", "matmul", "dot_scaled_rowcol",
-    "dot_scaled",
+    "dot_scaled", "quantize_mx", "quantize_rowwise",
     "gemv_fp8_dequant", "plugin_info", "invoke", "get_fp8_format_name",
     "version", "init", "RTNE", "RTZ", "RS",
 ]
@@ -263,6 +263,41 @@ def dot_scaled(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
                                sb.stride(0), _ptr(out), _TX_DTYPE[out_dtype], out.stride(0), M, N, K,
                                _stream(a_q)))
     return out
+
+
+def _quant_checks(x, dtype):
+    _on_gpu(x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("x must be fp32 or bf16")
+    if dtype not in _FP8:
+        raise ValueError("dtype must be torch.float8_e4m3fn or torch.float8_e5m2")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D tensor with contiguous rows")
+
+
+def quantize_mx(x: torch.Tensor, dtype: torch.dtype = torch.float8_e4m3fn):
+    """MX quantisation of x's rows (the reference's _compute_scale_and_quantize,
+    mxfp8_utils.py:17-38): returns (q fp8 rows x K, e8m0 scales uint8 rows x K/32)."""
+    _quant_checks(x, dtype)
+    rows, K = x.shape
+    q = torch.empty((rows, K), dtype=dtype, device=x.device)
+    s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
+    check(lib.tx_quantize_mx(_ptr(x), _TX_DTYPE[x.dtype], x.stride(0), _ptr(q), _TX_DTYPE[dtype],
+                             q.stride(0), _ptr(s), s.stride(0) if s.numel() else max(1, K // 32),
+                             rows, K, _stream(x)))
+    return q, s
+
+
+def quantize_rowwise(x: torch.Tensor, dtype: torch.dtype = torch.float8_e4m3fn):
+    """Per-row absmax quantisation: returns (q fp8 rows x K, fp32 scales[rows]) with
+    x ~= q * scales[:, None] -- the operands of dot_scaled_rowcol (pass B as N x K)."""
+    _quant_checks(x, dtype)
+    rows, K = x.shape
+    q = torch.empty((rows, K), dtype=dtype, device=x.device)
+    s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    check(lib.tx_quantize_rowwise(_ptr(x), _TX_DTYPE[x.dtype], x.stride(0), _ptr(q),
+                                  _TX_DTYPE[dtype], q.stride(0), _ptr(s), rows, K, _stream(x)))
+    return q, s
 
 
 def gemv_fp8_dequant(x: torch.Tensor, w_q: torch.Tensor, scales: torch.Tensor, group: int = 128,

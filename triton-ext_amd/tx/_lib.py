@@ -40,7 +40,8 @@ EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
-    "tx_dot_fp8_scaled", "tx_dot_scaled_mx", "tx_gemv_fp8_dequant",
+    "tx_dot_fp8_scaled", "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
+    "tx_gemv_fp8_dequant",
 ]
 
 
@@ -121,6 +122,10 @@ def _load():
     L.tx_dot_fp8_scaled.restype = I
     L.tx_dot_scaled_mx.argtypes = [P, I, I64, P, I64, P, I, I64, P, I64, P, I, I64, I64, I64, I64, VP]
     L.tx_dot_scaled_mx.restype = I
+    L.tx_quantize_mx.argtypes = [P, I, I64, P, I, I64, P, I64, I64, I64, VP]
+    L.tx_quantize_mx.restype = I
+    L.tx_quantize_rowwise.argtypes = [P, I, I64, P, I, I64, P, I64, I64, VP]
+    L.tx_quantize_rowwise.restype = I
     L.tx_gemv_fp8_dequant.argtypes = [P, I64, P, I, I64, P, I64, I64, P, I64, I64, I64, I64, VP]
     L.tx_gemv_fp8_dequant.restype = I
     return L
