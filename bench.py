@@ -153,6 +153,28 @@ def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
             "bytes": M * K + N * K + (M + N) * K // 32 + 2 * M * N}
 
 
+def bench_quant(tx, torch, kind, xdt, steps, warmup, rows=8192, K=8192):
+    """absmax + fp8 quantiser over a rows x K fp32 / bf16 matrix (MX or row-wise)."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    g = np.random.default_rng(6)
+    x0 = torch.from_numpy(g.standard_normal((rows, K), dtype=np.float32)).to(dev)
+    if xdt == "bf16":
+        x0 = x0.to(torch.bfloat16)
+    es = x0.element_size()
+    per_set = rows * K * (es + 1)
+    sets = ring_count(per_set)
+    xs = [x0] + [x0.clone() for _ in range(sets - 1)]
+    fn = tx.quantize_mx if kind == "mx" else tx.quantize_rowwise
+
+    def step(i):
+        fn(xs[i % sets])
+
+    ms = timed(step, steps, warmup)
+    nbytes = rows * K * (es + 1) + (rows * K // 32 if kind == "mx" else 4 * rows)
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "sets": sets}
+
+
 def bench_bf16_gemm(tx, torch, M, N, K, steps, warmup):
     from tx import workloads
     import numpy as np
@@ -378,6 +400,11 @@ def main():
                               "ms": r["ms"], "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
             progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+        for kind, xdt in (("mx", "f32"), ("mx", "bf16"), ("rowwise", "f32"), ("rowwise", "bf16")):
+            r = bench_quant(tx, torch, kind, xdt, max(K, 50), W)
+            secondary.append({"op": f"absmax+fp8 quantise ({kind}) {xdt} 8192x8192 -> e4m3fn",
+                              "ms": r["ms"], "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS})
+            progress(secondary[-1]["op"])
         for (m, n, k) in [(4096, 4096, 4096), (4095, 4097, 4100)]:
             r = bench_bf16_gemm(tx, torch, m, n, k, K, W)
             secondary.append({"op": "bf16 GEMM", "shape": [m, n, k], "ms": r["ms"],
