@@ -20,7 +20,7 @@
  *
  * Conventions (all entry points):
  *  - The caller owns every input and output buffer.  tx_dot_bf16,
- *    tx_dot_fp8_scaled and tx_dot_scaled_mx may use device scratch that
+ *    tx_dot_fp8_scaled[_ex] and tx_dot_scaled_mx may use device scratch that
  *    the library keeps per (device, stream): fp32 split-K partial planes
  *    (at most 8 x M x N x 4 bytes) when the output tiles leave CUs idle,
  *    zero-padded copies of A and B when rows are not 16-byte aligned in a
@@ -103,6 +103,14 @@ typedef enum tx_rmw_op {
   TX_RMW_OR = 7,
   TX_RMW_XOR = 8
 } tx_rmw_op;
+
+/* Activations of the fp8 GEMM's fused epilogue (tx_dot_fp8_scaled_ex). */
+typedef enum tx_activation {
+  TX_ACT_NONE = 0,
+  TX_ACT_RELU = 1,      /* y < 0 ? 0 : y (NaN kept) */
+  TX_ACT_GELU_TANH = 2, /* 0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3))) */
+  TX_ACT_SILU = 3       /* y / (1 + exp(-y)) */
+} tx_activation;
 
 /* ----------------------------------------------------------------------- */
 /* Registration surface                                                     */
@@ -268,6 +276,26 @@ TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
                                    const float *scale_b, void *C, int64_t ldc,
                                    int64_t M, int64_t N, int64_t K,
                                    tx_stream_t stream);
+
+/*
+ * tx_dot_fp8_scaled with a fused epilogue, the adjacent caller in serving
+ * stacks (a GEMM followed by bias, activation and a cast, often back to
+ * fp8).  No reference kernel exists; the product is tx_dot_fp8_scaled's:
+ *   y[m,n] = act(scale_a[m] * scale_b[n] * sum_k f32(A[m,k]) * f32(B[k,n]) + bias[n])
+ * in fp32 (bias may be NULL; activation a tx_activation), then C[m,n] =
+ *   bf16 / fp16 (round to nearest even) or fp32 of y (c_type TX_BF16,
+ *   TX_F16, TX_F32), or fp8 (TX_FP8E4M3FN / TX_FP8E5M2) of y * (1 / c_scale)
+ *   rounded to nearest even with saturation (c_scale > 0; NaN stays NaN).
+ * Layouts as tx_dot_fp8_scaled; C row-major with ldc elements of c_type,
+ * aligned to its element size.  Skinny (M <= 64) and misaligned products
+ * stage the scaled sums in the library's per-stream scratch (M x N x 4 bytes).
+ */
+TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t lda,
+                                      const float *scale_a, const void *B, tx_dtype b_type,
+                                      int64_t ldb, const float *scale_b, const float *bias,
+                                      int activation, void *C, tx_dtype c_type, float c_scale,
+                                      int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                      tx_stream_t stream);
 
 /*
  * tt.dot_scaled with MX block scales (OCP Microscaling: one e8m0 scale per

@@ -252,6 +252,30 @@ def gemm_mx_rows(A, sa, B, sb, r0: int, r1: int, fmt_a=E4M3FN, fmt_b=E4M3FN, nth
     return (o32, oab, obm) if block_max else (o32, oab)
 
 
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
+
+
+def activation(y, act: int):
+    """The fp8 GEMM epilogue's activations in float64: relu (NaN kept), the
+    tanh form of gelu (Hendrycks & Gimpel), silu."""
+    y = np.asarray(y, np.float64)
+    if act == ACT_RELU:
+        return np.where(y < 0, 0.0, y)
+    if act == ACT_GELU_TANH:
+        return 0.5 * y * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (y + 0.044715 * y ** 3)))
+    if act == ACT_SILU:
+        return y / (1.0 + np.exp(-y))
+    return y
+
+
+def gemm_fp8_epilogue(acc, bias, act: int):
+    """y = act(acc + bias) in float64 for acc = the scaled fp8 GEMM sums (rows x N)."""
+    y = np.asarray(acc, np.float64)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)[None, :]
+    return activation(y, act)
+
+
 def _widen(x):
     """fp32 values of x (fp32, or bf16 given as uint16 bits)."""
     x = np.asarray(x)

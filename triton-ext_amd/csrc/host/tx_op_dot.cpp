@@ -9,7 +9,9 @@
 // (:204-212), fp32 accumulation (:259-292), cast and masked store (:294-300).
 #include <algorithm>
 #include <climits>
+#include <cmath>
 #include <cstdio>
+#include <cstring>
 
 #include "tx_kernel_args.h"
 #include "tx_ops.h"
@@ -32,7 +34,8 @@ int pick_vec(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 }
 
 tx_status check_gemm(const char *what, const void *A, int64_t lda, const void *B, int64_t ldb,
-                     const void *C, int64_t ldc, int64_t M, int64_t N, int64_t K) {
+                     const void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                     size_t c_align = 2) {
   if (M < 0 || N < 0 || K < 0)
     return fail(TX_INVALID_ARGUMENT, "%s: negative size (M=%lld N=%lld K=%lld)", what,
                 (long long)M, (long long)N, (long long)K);
@@ -43,7 +46,8 @@ tx_status check_gemm(const char *what, const void *A, int64_t lda, const void *B
   if (lda < K || ldb < K || ldc < N)
     return fail(TX_INVALID_ARGUMENT, "%s: stride smaller than row length (lda=%lld ldb=%lld ldc=%lld)",
                 what, (long long)lda, (long long)ldb, (long long)ldc);
-  if (!aligned(C, 2)) return fail(TX_INVALID_ARGUMENT, "%s: C must be 2-byte aligned", what);
+  if (!aligned(C, c_align))
+    return fail(TX_INVALID_ARGUMENT, "%s: C must be %zu-byte aligned", what, c_align);
   return TX_SUCCESS;
 }
 
@@ -110,8 +114,10 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
       tx_gemm_args strip_args = args;
       const int64_t n0 = full * 256;
       strip_args.B = static_cast<const uint8_t *>(args.B) + n0 * args.ldb * es;
-      strip_args.C = static_cast<uint16_t *>(args.C) + n0;
+      const int64_t ce = !args.epi ? 2 : args.out_kind == EPI_OUT_F32 ? 4 : args.out_kind >= EPI_OUT_E4M3FN ? 1 : 2;
+      strip_args.C = static_cast<uint8_t *>(args.C) + n0 * ce;
       if (args.scale_b) strip_args.scale_b = args.scale_b + n0;
+      if (args.bias) strip_args.bias = args.bias + n0;
       strip_args.N = int32_t(tail);
       args.N = int32_t(n0);
       TX_TRY(launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves));
@@ -236,20 +242,57 @@ static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb
   return launch_gemm(kname, CodeObject::GemmBf16, args, tile, tile, s);
 }
 
-static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
-                                const void *B, tx_dtype b_type, int64_t ldb, const float *sb,
-                                void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
-                                tx_stream_t stream) {
-  TX_TRY(check_gemm("tx_dot_fp8_scaled", A, lda, B, ldb, C, ldc, M, N, K));
+// The fp8 GEMM's optional epilogue (tx_dot_fp8_scaled_ex).
+struct Epilogue {
+  const float *bias = nullptr;
+  int act = EPI_ACT_NONE;
+  int out_kind = EPI_OUT_BF16;
+  float out_mul = 1.0f;
+  bool on() const { return bias || act != EPI_ACT_NONE || out_kind != EPI_OUT_BF16; }
+};
+
+// Skinny and generic kernels write scaled fp32 sums to a.part (stream
+// scratch slot 1) when an epilogue is requested; this pass finishes them.
+tx_status epilogue_pass(tx_gemm_args &args, hipStream_t s) {
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::GemmFp8, "tx_gemm_fp8_epilogue", &fn));
+  const int64_t total = int64_t(args.M) * args.N;
+  const int64_t grid = std::min<int64_t>((total + 255) / 256, int64_t(cu_count()) * 16);
+  return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, "tx_gemm_fp8_epilogue");
+}
+
+static tx_status dot_fp8_impl(const char *what, const void *A, tx_dtype a_type, int64_t lda,
+                              const float *sa, const void *B, tx_dtype b_type, int64_t ldb,
+                              const float *sb, void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                              const Epilogue &epi, tx_stream_t stream) {
+  const size_t ce = epi.out_kind == EPI_OUT_F32 ? 4 : epi.out_kind >= EPI_OUT_E4M3FN ? 1 : 2;
+  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, K, ce));
   const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
   if (!fa || !fb)
-    return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: operand types must be fp8 (got %d, %d)",
+    return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 (got %d, %d)", what,
                 int(a_type), int(b_type));
   if (M == 0 || N == 0) return TX_SUCCESS;
-  if (!sa || !sb) return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: NULL scale vector");
-  if (!aligned(sa, 4) || !aligned(sb, 4))
-    return fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled: scales must be 4-byte aligned");
-  char kname[80];
+  if (!sa || !sb) return fail(TX_INVALID_ARGUMENT, "%s: NULL scale vector", what);
+  if (!aligned(sa, 4) || !aligned(sb, 4) || !aligned(epi.bias, 4))
+    return fail(TX_INVALID_ARGUMENT, "%s: scales and bias must be 4-byte aligned", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+  const bool with_epi = epi.on();
+  if (with_epi) {
+    args.bias = epi.bias;
+    args.act = epi.act;
+    args.out_kind = epi.out_kind;
+    args.out_mul = epi.out_mul;
+    args.epi = 1;
+  }
+  // skinny / generic kernels with an epilogue: scaled sums into scratch first
+  ScratchLease sums;
+  auto with_sums = [&]() -> tx_status {
+    TX_TRY(sums.acquire(s, 1, size_t(M) * size_t(N) * sizeof(float)));
+    args.part = static_cast<float *>(sums.ptr());
+    return TX_SUCCESS;
+  };
+  char kname[96];
   // Decode-sized M: stream B once with the skinny kernel (16 columns per
   // workgroup, K split over its wavefronts).
   if (M <= kSkinnyMaxM && K % 128 == 0 && aligned(A, 16) && aligned(B, 16) && lda % 16 == 0 &&
@@ -262,13 +305,11 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
     std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_skinny_w%d_m%d", fa, fb, waves, mb);
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
-    tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
-    return launch(fn, unsigned(grid), 1, unsigned(64 * waves), static_cast<hipStream_t>(stream),
-                  &args, sizeof args, kname);
+    if (with_epi) TX_TRY(with_sums());
+    TX_TRY(launch(fn, unsigned(grid), 1, unsigned(64 * waves), s, &args, sizeof args, kname));
+    return with_epi ? epilogue_pass(args, s) : TX_SUCCESS;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  tx_gemm_args args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
-  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast", fa, fb);
+  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast%s", fa, fb, with_epi ? "_epi" : "");
   if (fast_ok(A, lda, B, ldb, K, M, N))
     return launch_fast(kname, "tx_gemm_fp8_splitk_reduce", CodeObject::GemmFp8, args, K, 1, s);
   {
@@ -282,7 +323,47 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
   const int vec = pick_vec(A, lda, B, ldb, K, widths, 3);
   const int tile = (vec != 1 && use_big_tile(M, N)) ? 256 : 128;
   std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_%dx%d_v%d", fa, fb, tile, tile, vec);
-  return launch_gemm(kname, CodeObject::GemmFp8, args, tile, tile, s);
+  if (with_epi) TX_TRY(with_sums());
+  TX_TRY(launch_gemm(kname, CodeObject::GemmFp8, args, tile, tile, s));
+  return with_epi ? epilogue_pass(args, s) : TX_SUCCESS;
+}
+
+static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
+                                const void *B, tx_dtype b_type, int64_t ldb, const float *sb,
+                                void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                tx_stream_t stream) {
+  return dot_fp8_impl("tx_dot_fp8_scaled", A, a_type, lda, sa, B, b_type, ldb, sb, C, ldc, M, N, K,
+                      Epilogue{}, stream);
+}
+
+static tx_status dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
+                                   const void *B, tx_dtype b_type, int64_t ldb, const float *sb,
+                                   const float *bias, int activation, void *C, tx_dtype c_type,
+                                   float c_scale, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                   tx_stream_t stream) {
+  const char *what = "tx_dot_fp8_scaled_ex";
+  Epilogue e;
+  e.bias = bias;
+  if (activation < TX_ACT_NONE || activation > TX_ACT_SILU)
+    return fail(TX_INVALID_ARGUMENT, "%s: unknown activation %d", what, activation);
+  e.act = activation;
+  size_t es;
+  switch (c_type) {
+    case TX_BF16: e.out_kind = EPI_OUT_BF16; es = 2; break;
+    case TX_F16: e.out_kind = EPI_OUT_F16; es = 2; break;
+    case TX_F32: e.out_kind = EPI_OUT_F32; es = 4; break;
+    case TX_FP8E4M3FN: e.out_kind = EPI_OUT_E4M3FN; es = 1; break;
+    case TX_FP8E5M2: e.out_kind = EPI_OUT_E5M2; es = 1; break;
+    default:
+      return fail(TX_INVALID_ARGUMENT, "%s: output type must be bf16, fp16, fp32 or fp8 (got %d)", what,
+                  int(c_type));
+  }
+  if (es == 1) {
+    if (!(c_scale > 0.0f) || !std::isfinite(c_scale))
+      return fail(TX_INVALID_ARGUMENT, "%s: fp8 output needs a positive finite c_scale", what);
+    e.out_mul = 1.0f / c_scale;
+  }
+  return dot_fp8_impl(what, A, a_type, lda, sa, B, b_type, ldb, sb, C, ldc, M, N, K, e, stream);
 }
 
 // tt.dot_scaled with MX block scales (fp8 operands, e8m0 scales per 32 K
@@ -540,12 +621,49 @@ static tx_status dot_mx_op(tx_value *v, size_t count, tx_stream_t stream) {
                        stream);
 }
 
+// tx.dot_fp8_scaled_ex: {C (result), A, B, scale_a, scale_b, bias (may be NULL), M, N, K,
+// lda, ldb, ldc, a_type, b_type, c_type, activation, c_scale_bits (fp32 bits of c_scale)}
+static tx_status dot_fp8_ex_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tx.dot_fp8_scaled_ex"};
+  TX_TRY(o.need(17));
+  void *C, *A, *B, *sa, *sb, *bias;
+  int64_t M, N, K, lda, ldb, ldc, at, bt, ct, act, csb;
+  TX_TRY(o.ptr(0, &C));
+  TX_TRY(o.ptr(1, &A));
+  TX_TRY(o.ptr(2, &B));
+  TX_TRY(o.ptr(3, &sa));
+  TX_TRY(o.ptr(4, &sb));
+  TX_TRY(o.ptr(5, &bias));
+  TX_TRY(o.integer(6, &M));
+  TX_TRY(o.integer(7, &N));
+  TX_TRY(o.integer(8, &K));
+  TX_TRY(o.integer(9, &lda));
+  TX_TRY(o.integer(10, &ldb));
+  TX_TRY(o.integer(11, &ldc));
+  TX_TRY(o.integer(12, &at));
+  TX_TRY(o.integer(13, &bt));
+  TX_TRY(o.integer(14, &ct));
+  TX_TRY(o.integer(15, &act));
+  TX_TRY(o.integer(16, &csb));
+  const uint32_t bits = uint32_t(csb);
+  float c_scale;
+  std::memcpy(&c_scale, &bits, sizeof c_scale);
+  return dot_fp8_scaled_ex(A, tx_dtype(at), lda, static_cast<const float *>(sa), B, tx_dtype(bt), ldb,
+                           static_cast<const float *>(sb), static_cast<const float *>(bias), int(act),
+                           C, tx_dtype(ct), c_scale, ldc, M, N, K, stream);
+}
+
 static const bool reg_dot = register_op(
     "tt.dot", dot_op, "C:bf16*(result), A:bf16*, B:bf16* (N x K), M, N, K, lda, ldb, ldc");
 static const bool reg_dot_fp8 = register_op(
     "tt.dot_scaled.rowcol", dot_fp8_op,
     "C:bf16*(result), A:fp8*, B:fp8* (N x K), scale_a:f32*, scale_b:f32*, M, N, K, lda, ldb, "
     "ldc, a_type:i32, b_type:i32");
+static const bool reg_dot_fp8_ex = register_op(
+    "tx.dot_fp8_scaled_ex", dot_fp8_ex_op,
+    "C:bf16|f16|f32|fp8*(result), A:fp8*, B:fp8* (N x K), scale_a:f32*, scale_b:f32*, "
+    "bias:f32*|NULL, M, N, K, lda, ldb, ldc, a_type:i32, b_type:i32, c_type:i32, activation:i32, "
+    "c_scale:f32 bits");
 static const bool reg_dot_mx = register_op(
     "tt.dot_scaled", dot_mx_op,
     "C:bf16|f16|f32*(result), A:fp8*, B:fp8* (N x K), scale_a:e8m0* (M x ceil(K/32)), "
@@ -573,6 +691,17 @@ TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
   tx::clear_error();
   return tx::dot_fp8_scaled(A, a_type, lda, scale_a, B, b_type, ldb, scale_b, C, ldc, M, N, K,
                             stream);
+}
+
+TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t lda,
+                                      const float *scale_a, const void *B, tx_dtype b_type,
+                                      int64_t ldb, const float *scale_b, const float *bias,
+                                      int activation, void *C, tx_dtype c_type, float c_scale,
+                                      int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                      tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot_fp8_scaled_ex(A, a_type, lda, scale_a, B, b_type, ldb, scale_b, bias, activation,
+                               C, c_type, c_scale, ldc, M, N, K, stream);
 }
 
 TX_API tx_status tx_dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda,

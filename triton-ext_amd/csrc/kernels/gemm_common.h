@@ -29,9 +29,81 @@
 
 #include <type_traits>
 
+#include "fp8_encode.h"
 #include "tx_device.h"
 
 namespace txg {
+
+// ------------------------------------------------------------ epilogues
+// y = act(v + bias[n]) for the fp8 GEMMs' fused epilogue (v already carries
+// the row / column scales).  relu keeps NaN; gelu is the tanh form
+// 0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3))) (Hendrycks & Gimpel);
+// silu is y / (1 + e^-y).
+__device__ __forceinline__ float epi_value(const tx_gemm_args &a, float v, int n) {
+  if (a.bias) v += a.bias[n];
+  switch (a.act) {
+    case EPI_ACT_RELU: return v < 0.0f ? 0.0f : v;
+    case EPI_ACT_GELU_TANH: return 0.5f * v * (1.0f + tanhf(0.7978845608f * (v + 0.044715f * v * v * v)));
+    case EPI_ACT_SILU: return v / (1.0f + expf(-v));
+    default: return v;
+  }
+}
+
+// One output element of C (row-major, ldc elements) in the epilogue's type.
+__device__ __forceinline__ void epi_store1(const tx_gemm_args &a, int64_t m, int64_t n, float y) {
+  const int64_t i = m * a.ldc + n;
+  switch (a.out_kind) {
+    case EPI_OUT_F16: static_cast<uint16_t *>(a.C)[i] = uint16_t(txd::pack_f16x2(y, 0.0f)); break;
+    case EPI_OUT_F32: static_cast<float *>(a.C)[i] = y; break;
+    case EPI_OUT_E4M3FN:
+      static_cast<uint8_t *>(a.C)[i] = uint8_t(txf::encode_rtne<txf::E4M3FN, true>(__float_as_uint(y * a.out_mul)));
+      break;
+    case EPI_OUT_E5M2:
+      static_cast<uint8_t *>(a.C)[i] = uint8_t(txf::encode_rtne<txf::E5M2, true>(__float_as_uint(y * a.out_mul)));
+      break;
+    default: static_cast<uint16_t *>(a.C)[i] = uint16_t(txd::f32_to_bf16_bits(y)); break;
+  }
+}
+
+// Four consecutive outputs C[m][n .. n+3] (n + 3 < N), one vector store when
+// the row and pitch allow it.
+__device__ __forceinline__ void epi_store4(const tx_gemm_args &a, int64_t m, int64_t n, const float (&y)[4]) {
+  const int64_t i = m * a.ldc + n;
+  const uintptr_t base = reinterpret_cast<uintptr_t>(a.C);
+  switch (a.out_kind) {
+    case EPI_OUT_F32:
+      if (((base | uintptr_t(4 * i)) & 15) == 0) {
+        *reinterpret_cast<txd::f32x4 *>(static_cast<float *>(a.C) + i) = txd::f32x4{y[0], y[1], y[2], y[3]};
+        return;
+      }
+      break;
+    case EPI_OUT_E4M3FN:
+    case EPI_OUT_E5M2:
+      if (((base | uintptr_t(i)) & 3) == 0) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t u = __float_as_uint(y[t] * a.out_mul);
+          w |= (a.out_kind == EPI_OUT_E4M3FN ? txf::encode_rtne<txf::E4M3FN, true>(u)
+                                             : txf::encode_rtne<txf::E5M2, true>(u)) << (8 * t);
+        }
+        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(a.C) + i) = w;
+        return;
+      }
+      break;
+    default:
+      if (((base | uintptr_t(2 * i)) & 7) == 0) {
+        const bool h = a.out_kind == EPI_OUT_F16;
+        *reinterpret_cast<txd::u32x2 *>(static_cast<uint16_t *>(a.C) + i) =
+            h ? txd::u32x2{txd::pack_f16x2(y[0], y[1]), txd::pack_f16x2(y[2], y[3])}
+              : txd::u32x2{txd::pack_bf16x2(y[0], y[1]), txd::pack_bf16x2(y[2], y[3])};
+        return;
+      }
+      break;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) epi_store1(a, m, n + t, y[t]);
+}
 
 using txd::f32x4;
 using txd::i32x8;

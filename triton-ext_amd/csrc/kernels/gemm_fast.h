@@ -144,13 +144,14 @@ __device__ __forceinline__ void wait_and_barrier() {
 // Output element types of the fast tile.
 enum FastOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
 
-template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16>
+template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16, bool EPI = false>
 __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
   static_assert(!MX || (C::FP8 && (NW == 4 || BN == 128)), "MX scales: fp8 operands; 256x256: 4 wavefronts");
   static_assert(OUT == OUT_BF16 || MX, "fp16 / fp32 output: MX variant only");
+  static_assert(!EPI || (C::FP8 && !MX && OUT == OUT_BF16), "fused epilogue: row/column-scaled fp8");
   // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per
   // wave): LDS reads per step are then (64 + 64) x 8 rows instead of
   // (128 + 32) x 8, which matters because narrow tiles are LDS-bound.
@@ -399,6 +400,34 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     }
     return;
   }
+  // Fused epilogue (bias, activation, output type): per 32-row block of its
+  // tile, each wave stages its raw sums in LDS (rows padded by 16 bytes
+  // against bank conflicts), then walks them with consecutive lanes on
+  // consecutive columns, applying scales, bias and activation and storing
+  // one element per lane (one copy of the epilogue code, coalesced rows).
+  if constexpr (EPI) {
+    constexpr int SP = TN + 4;  // staged row pitch, floats
+    float *ws = reinterpret_cast<float *>(lds) + wave * 32 * SP;
+    static_assert(NW * 32 * SP * 4 <= kSlots * kSlotBytes, "epilogue staging fits in LDS");
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          *reinterpret_cast<txd::f32x4 *>(ws + frow * SP + fn * 32 + 8 * jj + 4 * fg) =
+              txd::f32x4{acc[fn][fm][4 * jj], acc[fn][fm][4 * jj + 1], acc[fn][fm][4 * jj + 2],
+                         acc[fn][fm][4 * jj + 3]};
+      __syncthreads();
+      for (int e = lane; e < 32 * TN; e += 64) {
+        const int r = e / TN, c = e % TN;
+        const int m = m0 + wm * TM + fm * 32 + r, n = n0 + wn * TN + c;
+        if (m < a.M && n < a.N) epi_store1(a, m, n, epi_value(a, ws[r * SP + c] * a.scale_a[m] * a.scale_b[n], n));
+      }
+      __syncthreads();
+    }
+    return;
+  }
   // Epilogue: scale (fp8 with row / column scales), round to bf16 (fp16)
   // and stage the whole tile in LDS (the ring is free after the drain
   // above), then write whole row segments of C with 16-byte stores.
@@ -505,6 +534,10 @@ __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
       if (n + i >= a.N) break;
       float r = v[i];
       if constexpr (ROWCOL) r = r * sa * a.scale_b[n + i];
+      if (a.epi) {  // fused epilogue of the fp8 GEMM (uniform branch)
+        epi_store1(a, m, n + i, epi_value(a, r, n + i));
+        continue;
+      }
       if constexpr (OUT == OUT_F32) static_cast<float *>(a.C)[int64_t(m) * a.ldc + n + i] = r;
       else if constexpr (OUT == OUT_F16) Cb[int64_t(m) * a.ldc + n + i] = uint16_t(txd::pack_f16x2(r, 0.0f));
       else Cb[int64_t(m) * a.ldc + n + i] = uint16_t(txd::f32_to_bf16_bits(r));

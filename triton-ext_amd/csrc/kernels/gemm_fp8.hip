@@ -44,6 +44,20 @@ TX_GEMM_FP8_FAST(e5m2, e5m2, EL_E5M2, EL_E5M2)
 TX_GEMM_FP8_FAST(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
 TX_GEMM_FP8_FAST(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 
+// The same tiles with the fused epilogue (bias, activation, output type).
+#define TX_GEMM_FP8_FAST_EPI(FA, FB, ELA, ELB)                                                        \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast_epi(const tx_gemm_args a) {      \
+    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256, fast::kWaves, false, OUT_BF16, true>(a);  \
+  }                                                                                                     \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast_epi_n128(const tx_gemm_args a) { \
+    gemm_fast_tile<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128, fast::kWaves, false, OUT_BF16, true>(a);  \
+  }
+
+TX_GEMM_FP8_FAST_EPI(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
+TX_GEMM_FP8_FAST_EPI(e5m2, e5m2, EL_E5M2, EL_E5M2)
+TX_GEMM_FP8_FAST_EPI(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
+TX_GEMM_FP8_FAST_EPI(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
+
 #include "gemm_skinny.h"
 
 // Kernel names: tx_gemm_fp8_<a>_<b>_skinny_w<waves>_m<16-row blocks of M>
@@ -65,3 +79,15 @@ TX_GEMM_FP8_SKINNY_ALL(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
 TX_GEMM_FP8_SKINNY_ALL(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 
 TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_pad_rows(const tx_pad_args a) { pad_rows<1>(a); }
+
+// Epilogue pass of the skinny and generic kernels: their scaled fp32 sums
+// (a.part, M x N) through bias, activation and the output conversion into C.
+TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_epilogue(const tx_gemm_args a) {
+  const int64_t total = int64_t(a.M) * a.N;
+  for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t m = t / a.N;
+    const int n = int(t % a.N);
+    epi_store1(a, m, n, epi_value(a, a.part[t], n));
+  }
+}

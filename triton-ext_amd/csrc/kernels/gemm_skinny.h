@@ -160,7 +160,9 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = mb * 16 + 4 * g + i;
-        if (m < a.M) Cb[int64_t(m) * a.ldc + n] = uint16_t(txd::f32_to_bf16_bits(v[i] * a.scale_a[m] * sb));
+        if (m >= a.M) continue;
+        if (a.epi) a.part[int64_t(m) * a.N + n] = v[i] * a.scale_a[m] * sb;  // epilogue pass follows
+        else Cb[int64_t(m) * a.ldc + n] = uint16_t(txd::f32_to_bf16_bits(v[i] * a.scale_a[m] * sb));
       }
     }
   }

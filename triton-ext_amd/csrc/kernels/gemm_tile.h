@@ -154,14 +154,20 @@ __device__ __forceinline__ void gemm_tile(const tx_gemm_args &a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = v[j] * sa * (n + j < a.N ? a.scale_b[n + j] : 0.0f);
       }
-      uint16_t *dst = Cb + int64_t(m) * a.ldc + n;
-      if (cvec && n + 3 < a.N) {
-        txd::u32x2 p = {txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
-        *reinterpret_cast<txd::u32x2 *>(dst) = p;
-      } else {
+      if (C::FP8 && a.epi) {  // epilogue requested: scaled fp32 sums to a.part (M x N)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (n + j < a.N) dst[j] = uint16_t(txd::f32_to_bf16_bits(v[j]));
+          if (n + j < a.N) a.part[int64_t(m) * a.N + n + j] = v[j];
+      } else {
+        uint16_t *dst = Cb + int64_t(m) * a.ldc + n;
+        if (cvec && n + 3 < a.N) {
+          txd::u32x2 p = {txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
+          *reinterpret_cast<txd::u32x2 *>(dst) = p;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (n + j < a.N) dst[j] = uint16_t(txd::f32_to_bf16_bits(v[j]));
+        }
       }
     }
   }

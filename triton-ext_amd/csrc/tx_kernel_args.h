@@ -78,7 +78,18 @@ typedef struct tx_gemm_args {
   const uint8_t *mx_b;
   int64_t ld_mxa;
   int64_t ld_mxb;
+  /* fp8 GEMM epilogue (used when epi != 0): y = act(scaled sum + bias[n]),
+   * written as out_kind (EPI_OUT_*); fp8 outputs are y * out_mul, rounded to
+   * nearest even with saturation. */
+  const float *bias;   /* NULL: none */
+  int32_t act;         /* EPI_ACT_* */
+  int32_t out_kind;    /* EPI_OUT_* */
+  float out_mul;
+  int32_t epi;
 } tx_gemm_args;
+
+enum { EPI_ACT_NONE = 0, EPI_ACT_RELU = 1, EPI_ACT_GELU_TANH = 2, EPI_ACT_SILU = 3 };
+enum { EPI_OUT_BF16 = 0, EPI_OUT_F16 = 1, EPI_OUT_F32 = 2, EPI_OUT_E4M3FN = 3, EPI_OUT_E5M2 = 4 };
 
 /* Step-major repack of MX scales: dst dword [s][r] (byte s * 4 * rows_pad +
  * 4r) = bytes src[r][4s .. 4s+3], with 127 (2^0) for r >= rows or a block

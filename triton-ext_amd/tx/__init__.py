@@ -194,10 +194,21 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return dot(a, b.t())
 
 
+_ACT = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "relu": _lib.ACT_RELU,
+        "gelu_tanh": _lib.ACT_GELU_TANH, "silu": _lib.ACT_SILU}
+
+
 def dot_scaled_rowcol(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
-                      scale_b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+                      scale_b: torch.Tensor, out: torch.Tensor | None = None,
+                      bias: torch.Tensor | None = None, activation: str | None = None,
+                      out_dtype: torch.dtype = torch.bfloat16, out_scale: float = 1.0) -> torch.Tensor:
     """fp8 tt.dot with fp32 per-row (scale_a[M]) and per-column (scale_b[N])
-    scales: out = bf16(scale_a[:,None] * scale_b[None,:] * (a_q @ b_q))."""
+    scales: out = bf16(scale_a[:,None] * scale_b[None,:] * (a_q @ b_q)).
+    With bias (fp32[N]), activation ("relu", "gelu_tanh", "silu") or another
+    out_dtype (fp16, fp32, or fp8 holding y / out_scale with saturation) the
+    fused epilogue is applied: out = cast(act(that + bias))."""
+    if bias is not None or activation not in (None, "none") or out_dtype != torch.bfloat16:
+        return _dot_fp8_ex(a_q, scale_a, b_q_nk, scale_b, out, bias, activation, out_dtype, out_scale)
     _on_gpu(a_q, scale_a, b_q_nk, scale_b, out)
     if a_q.dtype not in _FP8 or b_q_nk.dtype not in _FP8:
         raise ValueError("dot_scaled_rowcol takes fp8 operands")
@@ -218,6 +229,32 @@ def dot_scaled_rowcol(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Te
     check(lib.tx_dot_fp8_scaled(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
                                 _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0),
                                 _ptr(scale_b), _ptr(out), out.stride(0), M, N, K, _stream(a_q)))
+    return out
+
+
+def _dot_fp8_ex(a_q, scale_a, b_q_nk, scale_b, out, bias, activation, out_dtype, out_scale):
+    _on_gpu(a_q, scale_a, b_q_nk, scale_b, out, bias)
+    if a_q.dtype not in _FP8 or b_q_nk.dtype not in _FP8:
+        raise ValueError("dot_scaled_rowcol takes fp8 operands")
+    if a_q.dim() != 2 or b_q_nk.dim() != 2 or a_q.shape[1] != b_q_nk.shape[1]:
+        raise ValueError("incompatible shapes")
+    if a_q.stride(1) != 1 or b_q_nk.stride(1) != 1:
+        raise ValueError("operands must be K-contiguous")
+    if activation not in _ACT:
+        raise ValueError(f"unknown activation {activation!r}")
+    M, K = a_q.shape
+    N = b_q_nk.shape[0]
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous fp32 vector of length N")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
+    if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major M x N tensor of out_dtype")
+    check(lib.tx_dot_fp8_scaled_ex(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
+                                   _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0),
+                                   _ptr(scale_b), _ptr(bias), _ACT[activation], _ptr(out),
+                                   _TX_DTYPE[out_dtype], float(out_scale), out.stride(0), M, N, K,
+                                   _stream(a_q)))
     return out
 
 

@@ -27,6 +27,7 @@ STATUS_NAMES = {
 
 # tx_dtype
 F32, FP8E4M3FN, FP8E5M2, BF16, I32, U32, F16 = 0, 1, 2, 3, 4, 5, 6
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 # tx_rounding (ops/NewOps.cpp:270-286 numbering)
 RTNE, RTZ, RS = 0, 1, 2
 # tx_rmw_op
@@ -40,7 +41,7 @@ EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
-    "tx_dot_fp8_scaled", "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
+    "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
     "tx_gemv_fp8_dequant",
 ]
 
@@ -120,6 +121,9 @@ def _load():
     L.tx_dot_bf16.restype = I
     L.tx_dot_fp8_scaled.argtypes = [P, I, I64, P, P, I, I64, P, P, I64, I64, I64, I64, VP]
     L.tx_dot_fp8_scaled.restype = I
+    L.tx_dot_fp8_scaled_ex.argtypes = [P, I, I64, P, P, I, I64, P, P, I, P, I, ctypes.c_float,
+                                       I64, I64, I64, I64, VP]
+    L.tx_dot_fp8_scaled_ex.restype = I
     L.tx_dot_scaled_mx.argtypes = [P, I, I64, P, I64, P, I, I64, P, I64, P, I, I64, I64, I64, I64, VP]
     L.tx_dot_scaled_mx.restype = I
     L.tx_quantize_mx.argtypes = [P, I, I64, P, I, I64, P, I64, I64, I64, VP]
