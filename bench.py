@@ -130,6 +130,30 @@ def bench_fp8_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
             "bytes": M * K + N * K + 4 * (M + N) + 2 * M * N}
 
 
+def bench_fp8_gemm_epilogue(tx, torch, M, N, K, steps, warmup, act, out_dtype, sets=2):
+    """fp8 scaled GEMM with the fused epilogue (bias, activation, output cast)."""
+    from tx import workloads
+    import numpy as np
+    dev = torch.device("cuda:0")
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
+    bias = torch.from_numpy(np.random.default_rng(2).standard_normal(N).astype(np.float32)).to(dev)
+    bufs = []
+    for s in range(sets):
+        A = torch.from_numpy(aq).to(dev).view(torch.float8_e4m3fn)
+        B = torch.from_numpy(bq).to(dev).view(torch.float8_e4m3fn)
+        bufs.append((A, torch.from_numpy(sa).to(dev), B, torch.from_numpy(sb).to(dev),
+                     torch.empty((M, N), dtype=out_dtype, device=dev)))
+    del aq, bq
+
+    def step(i):
+        A, a_s, B, b_s, C = bufs[i % sets]
+        tx.dot_scaled_rowcol(A, a_s, B, b_s, out=C, bias=bias, activation=act, out_dtype=out_dtype,
+                             out_scale=0.5)
+
+    ms = timed(step, steps, warmup)
+    return {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+
+
 def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
     """tt.dot_scaled with MX block scales (e8m0 per 32 K), e4m3fn operands, bf16 out."""
     from tx import workloads
@@ -394,6 +418,12 @@ def main():
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
                               "gbs": r["bytes"] / (r["ms"] * 1e-3) / 1e9})
             progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+        for act, odt, oname in (("gelu_tanh", torch.float8_e4m3fn, "e4m3fn"), ("silu", torch.bfloat16, "bf16")):
+            r = bench_fp8_gemm_epilogue(tx, torch, 8192, 8192, 8192, K, W, act, odt)
+            secondary.append({"op": f"fp8 scaled GEMM + bias + {act} -> {oname} (fused)",
+                              "shape": [8192, 8192, 8192], "ms": r["ms"], "tflops": r["tflops"],
+                              "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
+            progress(secondary[-1]["op"])
         for (m, n, k) in [(8192, 8192, 8192), (512, 14336, 4096)]:
             r = bench_mx_gemm(tx, torch, m, n, k, K, W)
             secondary.append({"op": "MX-scaled fp8 GEMM (e8m0 per 32 K)", "shape": [m, n, k],

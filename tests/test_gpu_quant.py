@@ -158,3 +158,29 @@ def test_quantise_table_ops_and_errors(tx, oracle, dev):
         tx.invoke("tx.quantize_rowwise", [q, sf, X, rows, K, K, K, _lib.F16, _lib.FP8E5M2])
     with pytest.raises(ValueError):
         tx.quantize_rowwise(X.cpu())
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_hardware_conversion_matches_the_software_encoder(tx, dev, fmt):
+    """The quantisers convert with gfx950's packed fp8 instructions after the
+    clamp; the codec's tt.fp_to_fp encoder (saturating RNE, integer method,
+    pinned to the oracle elsewhere) is the reference.  Rows whose absmax is
+    exactly fmax quantise with multiplier 1, so the codes must equal the
+    saturating conversion of x itself: 2^28 fp32 patterns spread over all
+    2^32 (every exponent, sign and low-bit mix, NaNs and infinities)."""
+    K, rows = 1 << 20, 256
+    i = torch.arange(rows * K, dtype=torch.int64, device=dev)
+    bits = (i * 16 + (i % 13)).to(torch.int64) & 0xFFFFFFFF
+    x = bits.to(torch.int32).view(torch.float32).reshape(rows, K).clone()
+    del i, bits
+    # amax must be exactly fmax: values beyond it (and infinities) would set
+    # the row's scale, so they become +-fmax-sized NaN-free entries here, and
+    # two entries pin amax
+    big = ~torch.isnan(x) & (x.abs() > FMAX[fmt])
+    x[big] = torch.where(x[big] > 0, FMAX[fmt], -FMAX[fmt])
+    x[:, 0] = FMAX[fmt]
+    x[:, 1] = -FMAX[fmt]
+    q, s = tx.quantize_rowwise(x, TD[fmt])
+    assert torch.all(s == 1.0)
+    ref = tx.fp_to_fp(x.reshape(-1), TD[fmt], saturate=True).reshape(rows, K)
+    assert torch.equal(q.view(torch.uint8), ref.view(torch.uint8))

@@ -56,4 +56,31 @@ __device__ __forceinline__ uint32_t encode_rtz(uint32_t u) {
   return code | F::sign(u);
 }
 
+// Four fp32 values already clamped to +-max (NaN allowed) -> four fp8 codes
+// (byte i = value i), round to nearest even, with gfx950's packed convert
+// instructions.  Over all 2^32 fp32 patterns clamped to +-max they return
+// encode_rtne's codes (checked exhaustively on the device); NaN inputs are
+// set to encode_rtne's NaN code (0x7F with the input's sign) explicitly.
+template <int FMT>
+__device__ __forceinline__ uint32_t encode_clamped4_hw(const float (&x)[4]) {
+  static_assert(FMT == E4M3FN || FMT == E5M2, "fp8 formats");
+  int w;
+  if constexpr (FMT == E4M3FN) {
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], w, true);
+  } else {
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(x[0], x[1], 0, false);
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(x[2], x[3], w, true);
+  }
+  uint32_t c = uint32_t(w);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (x[i] != x[i]) {
+      const uint32_t nanc = 0x7Fu | ((__float_as_uint(x[i]) >> 24) & 0x80u);
+      c = (c & ~(0xFFu << (8 * i))) | (nanc << (8 * i));
+    }
+  }
+  return c;
+}
+
 }  // namespace txf

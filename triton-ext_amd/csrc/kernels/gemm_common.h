@@ -37,16 +37,43 @@ namespace txg {
 // ------------------------------------------------------------ epilogues
 // y = act(v + bias[n]) for the fp8 GEMMs' fused epilogue (v already carries
 // the row / column scales).  relu keeps NaN; gelu is the tanh form
-// 0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3))) (Hendrycks & Gimpel);
-// silu is y / (1 + e^-y).
-__device__ __forceinline__ float epi_value(const tx_gemm_args &a, float v, int n) {
-  if (a.bias) v += a.bias[n];
-  switch (a.act) {
-    case EPI_ACT_RELU: return v < 0.0f ? 0.0f : v;
-    case EPI_ACT_GELU_TANH: return 0.5f * v * (1.0f + tanhf(0.7978845608f * (v + 0.044715f * v * v * v)));
-    case EPI_ACT_SILU: return v / (1.0f + expf(-v));
+// 0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3))) (Hendrycks & Gimpel),
+// evaluated as y / (1 + e^(-2u)) with u the tanh argument (the identity
+// 0.5 (1 + tanh u) = 1 / (1 + e^(-2u))); silu is y / (1 + e^-y).  Both use
+// the hardware exp and reciprocal (a few ulp in fp32: the outputs are
+// bf16 / fp16 / fp8 or an fp8 product's fp32 sum).
+template <int ACT>
+__device__ __forceinline__ float epi_act_t(float v) {
+  if constexpr (ACT == EPI_ACT_RELU) return v < 0.0f ? 0.0f : v;
+  else if constexpr (ACT == EPI_ACT_GELU_TANH)
+    return __fdividef(v, 1.0f + __expf(-1.5957691216f * (v + 0.044715f * v * v * v)));
+  else if constexpr (ACT == EPI_ACT_SILU) return __fdividef(v, 1.0f + __expf(-v));
+  else return v;
+}
+
+__device__ __forceinline__ float epi_act(int act, float v) {
+  switch (act) {
+    case EPI_ACT_RELU: return epi_act_t<EPI_ACT_RELU>(v);
+    case EPI_ACT_GELU_TANH: return epi_act_t<EPI_ACT_GELU_TANH>(v);
+    case EPI_ACT_SILU: return epi_act_t<EPI_ACT_SILU>(v);
     default: return v;
   }
+}
+
+// f(integral_constant<int, ACT>) for the runtime activation `act`.
+template <class F>
+__device__ __forceinline__ void with_act(int act, F &&f) {
+  switch (act) {
+    case EPI_ACT_RELU: f(std::integral_constant<int, EPI_ACT_RELU>{}); break;
+    case EPI_ACT_GELU_TANH: f(std::integral_constant<int, EPI_ACT_GELU_TANH>{}); break;
+    case EPI_ACT_SILU: f(std::integral_constant<int, EPI_ACT_SILU>{}); break;
+    default: f(std::integral_constant<int, EPI_ACT_NONE>{}); break;
+  }
+}
+
+__device__ __forceinline__ float epi_value(const tx_gemm_args &a, float v, int n) {
+  if (a.bias) v += a.bias[n];
+  return epi_act(a.act, v);
 }
 
 // One output element of C (row-major, ldc elements) in the epilogue's type.
@@ -80,14 +107,17 @@ __device__ __forceinline__ void epi_store4(const tx_gemm_args &a, int64_t m, int
     case EPI_OUT_E4M3FN:
     case EPI_OUT_E5M2:
       if (((base | uintptr_t(i)) & 3) == 0) {
-        uint32_t w = 0;
+        // saturate (NaN kept), then the hardware's round-to-nearest-even
+        const float fmax = a.out_kind == EPI_OUT_E4M3FN ? 448.0f : 57344.0f;
+        float c[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const uint32_t u = __float_as_uint(y[t] * a.out_mul);
-          w |= (a.out_kind == EPI_OUT_E4M3FN ? txf::encode_rtne<txf::E4M3FN, true>(u)
-                                             : txf::encode_rtne<txf::E5M2, true>(u)) << (8 * t);
+          const float v = y[t] * a.out_mul;
+          c[t] = v > fmax ? fmax : (v < -fmax ? -fmax : v);
         }
-        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(a.C) + i) = w;
+        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(a.C) + i) =
+            a.out_kind == EPI_OUT_E4M3FN ? txf::encode_clamped4_hw<txf::E4M3FN>(c)
+                                         : txf::encode_clamped4_hw<txf::E5M2>(c);
         return;
       }
       break;

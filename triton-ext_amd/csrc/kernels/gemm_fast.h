@@ -400,32 +400,77 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     }
     return;
   }
-  // Fused epilogue (bias, activation, output type): per 32-row block of its
-  // tile, each wave stages its raw sums in LDS (rows padded by 16 bytes
-  // against bank conflicts), then walks them with consecutive lanes on
-  // consecutive columns, applying scales, bias and activation and storing
-  // one element per lane (one copy of the epilogue code, coalesced rows).
+  // Fused epilogue (bias, activation, output type): two 32-row blocks of its
+  // tile at a time, each wave stages its raw sums in LDS (rows padded by 16
+  // bytes against bank conflicts), then walks a block four rows at a time
+  // with lane l on row l / 16 and columns 4 (l % 16) .. +3 of the wave's 64:
+  // the columns' scales and bias stay in registers, the row's scale comes
+  // from lane r by a lane shuffle, and each lane stores its four outputs at
+  // once (8-, 16- or 4-byte stores).  Staging is expanded at compile time
+  // (the accumulators need constant indices); the walk is a plain loop with
+  // one copy of the epilogue code per activation.
   if constexpr (EPI) {
-    constexpr int SP = TN + 4;  // staged row pitch, floats
-    float *ws = reinterpret_cast<float *>(lds) + wave * 32 * SP;
-    static_assert(NW * 32 * SP * 4 <= kSlots * kSlotBytes, "epilogue staging fits in LDS");
+    static_assert(TN == 64, "16 lanes x 4 columns per row of the wave tile");
+    constexpr int SP = TN + 4;     // staged row pitch, floats
+    constexpr int NB = FM < 2 ? FM : 2;  // blocks staged at once
+    static_assert(FM % NB == 0, "whole groups of staged blocks");
+    static_assert(NW * NB * 32 * SP * 4 <= kSlots * kSlotBytes, "epilogue staging fits in LDS");
+    float *ws = reinterpret_cast<float *>(lds) + wave * NB * 32 * SP;
+    const int c4 = 4 * (lane & 15), rq = lane >> 4;
+    const int n = n0 + wn * TN + c4;
+    float sb4[4], bias4[4];
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          *reinterpret_cast<txd::f32x4 *>(ws + frow * SP + fn * 32 + 8 * jj + 4 * fg) =
-              txd::f32x4{acc[fn][fm][4 * jj], acc[fn][fm][4 * jj + 1], acc[fn][fm][4 * jj + 2],
-                         acc[fn][fm][4 * jj + 3]};
-      __syncthreads();
-      for (int e = lane; e < 32 * TN; e += 64) {
-        const int r = e / TN, c = e % TN;
-        const int m = m0 + wm * TM + fm * 32 + r, n = n0 + wn * TN + c;
-        if (m < a.M && n < a.N) epi_store1(a, m, n, epi_value(a, ws[r * SP + c] * a.scale_a[m] * a.scale_b[n], n));
-      }
-      __syncthreads();
+    for (int t = 0; t < 4; ++t) {
+      sb4[t] = n + t < a.N ? a.scale_b[n + t] : 0.0f;
+      bias4[t] = (n + t < a.N && a.bias) ? a.bias[n + t] : 0.0f;
     }
+    static_for<FM / NB>([&](auto g_tag) {
+      constexpr int G = decltype(g_tag)::value;
+      static_for<NB>([&](auto q_tag) {
+        constexpr int q = decltype(q_tag)::value, fm = G * NB + q;
+        static_for<FN>([&](auto fn_tag) {
+          constexpr int fn = decltype(fn_tag)::value;
+          static_for<4>([&](auto jj_tag) {
+            constexpr int jj = decltype(jj_tag)::value;
+            *reinterpret_cast<txd::f32x4 *>(ws + (q * 32 + frow) * SP + fn * 32 + 8 * jj + 4 * fg) =
+                txd::f32x4{acc[fn][fm][4 * jj], acc[fn][fm][4 * jj + 1], acc[fn][fm][4 * jj + 2],
+                           acc[fn][fm][4 * jj + 3]};
+          });
+        });
+      });
+      __syncthreads();
+      with_act(a.act, [&](auto act_tag) {
+        constexpr int ACT = decltype(act_tag)::value;
+        for (int q = 0; q < NB; ++q) {
+          const int mb = m0 + wm * TM + (G * NB + q) * 32;
+          const float sa_lane = mb + frow < a.M ? a.scale_a[mb + frow] : 0.0f;  // lanes 0..31: rows
+          const float *wq = ws + q * 32 * SP;
+          txd::f32x4 v[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const txd::f32x4 *>(wq + (4 * i + rq) * SP + c4);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int r = 4 * i + rq;
+            const float sa_r = __shfl(sa_lane, r);
+            const int m = mb + r;
+            const float x[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            float y[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) y[t] = epi_act_t<ACT>(x[t] * sa_r * sb4[t] + bias4[t]);
+            if (m < a.M) {
+              if (n + 3 < a.N) {
+                epi_store4(a, m, n, y);
+              } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                  if (n + t < a.N) epi_store1(a, m, n + t, y[t]);
+              }
+            }
+          }
+        }
+      });
+      __syncthreads();
+    });
     return;
   }
   // Epilogue: scale (fp8 with row / column scales), round to bf16 (fp16)
