@@ -46,6 +46,7 @@ sys.path.insert(0, os.path.join(REPO, "triton-ext_amd"))
 METRIC = "fp8 GEMM TFLOP/s + % MFMA peak @8192^3; fp8 convert GB/s + % HBM peak"
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA
+FP4_PEAK_TFLOPS = 10100.0    # dense fp4 MFMA
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
 MALL_BYTES = 256 << 20
 
@@ -154,27 +155,34 @@ def bench_fp8_gemm_epilogue(tx, torch, M, N, K, steps, warmup, act, out_dtype, s
     return {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
 
 
-def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
-    """tt.dot_scaled with MX block scales (e8m0 per 32 K), e4m3fn operands, bf16 out."""
+def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2, fp4=False):
+    """tt.dot_scaled with MX block scales (e8m0 per 32 K), bf16 out; e4m3fn
+    operands, or fp4 (e2m1, two per byte) with ``fp4``."""
     from tx import workloads
     dev = torch.device("cuda:0")
-    aq, sa, bq, sb = workloads.mx_gemm_input(M, N, K)
+    if fp4:
+        aq, sa, bq, sb = workloads.mx_fp4_gemm_input(M, N, K)
+        dt, fmt = torch.uint8, "e2m1"
+    else:
+        aq, sa, bq, sb = workloads.mx_gemm_input(M, N, K)
+        dt, fmt = torch.float8_e4m3fn, None
     bufs = []
     for s in range(sets):
-        A = torch.from_numpy(aq).to(dev).view(torch.float8_e4m3fn)
-        B = torch.from_numpy(bq).to(dev).view(torch.float8_e4m3fn)
+        A = torch.from_numpy(aq).to(dev).view(dt)
+        B = torch.from_numpy(bq).to(dev).view(dt)
         bufs.append((A, torch.from_numpy(sa).to(dev), B, torch.from_numpy(sb).to(dev),
                      torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
     del aq, bq
 
     def step(i):
         A, a_s, B, b_s, C = bufs[i % sets]
-        tx.dot_scaled(A, a_s, B, b_s, out_dtype=torch.bfloat16, out=C)
+        tx.dot_scaled(A, a_s, B, b_s, out_dtype=torch.bfloat16, out=C, a_format=fmt, b_format=fmt)
 
     ms = timed(step, steps, warmup)
     flops = 2.0 * M * N * K
+    ob = K // 2 if fp4 else K
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops,
-            "bytes": M * K + N * K + (M + N) * K // 32 + 2 * M * N}
+            "bytes": M * ob + N * ob + (M + N) * K // 32 + 2 * M * N}
 
 
 def bench_quant(tx, torch, kind, xdt, steps, warmup, rows=8192, K=8192):
@@ -430,6 +438,10 @@ def main():
                               "ms": r["ms"], "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
             progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+        r = bench_mx_gemm(tx, torch, 8192, 8192, 8192, K, W, fp4=True)
+        secondary.append({"op": "MX-scaled fp4 GEMM (e2m1, e8m0 per 32 K)", "shape": [8192, 8192, 8192],
+                          "ms": r["ms"], "tflops": r["tflops"], "frac_mfma": r["tflops"] / FP4_PEAK_TFLOPS})
+        progress(secondary[-1]["op"])
         for kind, xdt in (("mx", "f32"), ("mx", "bf16"), ("rowwise", "f32"), ("rowwise", "bf16")):
             r = bench_quant(tx, torch, kind, xdt, max(K, 50), W)
             secondary.append({"op": f"absmax+fp8 quantise ({kind}) {xdt} 8192x8192 -> e4m3fn",

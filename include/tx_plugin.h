@@ -84,7 +84,9 @@ typedef enum tx_dtype {
   TX_BF16 = 3,
   TX_I32 = 4,
   TX_U32 = 5,
-  TX_F16 = 6
+  TX_F16 = 6,
+  TX_FP4E2M1 = 7 /* OCP MX fp4: 1 sign, 2 exponent (bias 1), 1 mantissa bit; two per byte,
+                    the lower K index in the low nibble (tx_dot_scaled_mx operands) */
 } tx_dtype;
 
 /* Rounding modes, numbered as the rounding operand of
@@ -307,9 +309,11 @@ TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t ld
  * tlx/mma_ops.py:163-237, lowered through GenericOpPattern<DotScaledOp>,
  * uTLXConversionPatterns.cpp:616); closed form of its check at
  * test_tlx.py:2271-2292, whose `bits << 23` scale decode agrees for codes
- * 1..254.  a_type/b_type are TX_FP8E4M3FN or TX_FP8E5M2 (the "e4m3" / "e5m2"
- * formats of async_dot_scaled).
- * A: row-major M x K bytes (lda); B: column-major, N rows of K bytes (ldb).
+ * 1..254.  a_type/b_type are TX_FP8E4M3FN or TX_FP8E5M2 in any pairing, or
+ * both TX_FP4E2M1 (the "e4m3" / "e5m2" / "e2m1" formats of async_dot_scaled;
+ * mixed fp8 x fp4 returns TX_UNSUPPORTED).
+ * A: row-major M rows of K bytes (fp8) or K/2 bytes (fp4, K even), row
+ * stride lda in bytes; B: column-major, N rows likewise (ldb bytes).
  * scale_a: e8m0 bytes, row-major M x ceil(K/32) (row stride ld_scale_a);
  * scale_b: N x ceil(K/32) (ld_scale_b).  Past K inside the last block the
  * operands count as zero.

@@ -20,6 +20,7 @@ _LIB_PATH = os.path.join(_HERE, "libtxoracle.so")
 
 E4M3FN = 1
 E5M2 = 2
+E2M1 = 4    # OCP MX fp4, two per byte (MX dot operands only)
 BF16 = 3
 F16 = 6
 MAX_FINITE = {E4M3FN: 448.0, E5M2: 57344.0}
@@ -66,6 +67,8 @@ def lib():
                                            I64, I64, I, P, P, I]
         L.txo_gemm_mx_rows.argtypes = [P, I64, P, I64, P, I64, P, I64, I64, I64, I, I, I64, I64,
                                        P, P, P, I]
+        L.txo_e2m1_value.argtypes = [I]
+        L.txo_e2m1_value.restype = ctypes.c_double
         L.txo_quant_mx.argtypes = [P, I64, I64, I64, I, P, P, I]
         L.txo_quant_row.argtypes = [P, I64, I64, I64, I, P, P, I]
         L.txo_encode_fmt.argtypes = [P, P, I64, I, I, I, I]
@@ -242,14 +245,22 @@ def gemm_mx_rows(A, sa, B, sb, r0: int, r1: int, fmt_a=E4M3FN, fmt_b=E4M3FN, nth
     B = _c(B, np.uint8)
     sa = _c(sa, np.uint8)
     sb = _c(sb, np.uint8)
-    K = A.shape[1]
+    # fp4 (format 4) rows hold two K values per byte
+    K = A.shape[1] * (2 if fmt_a == E2M1 else 1)
+    if K != B.shape[1] * (2 if fmt_b == E2M1 else 1):
+        raise ValueError("A and B disagree on K")
     N = B.shape[0]
     o32 = np.empty((r1 - r0, N), np.float32)
     oab = np.empty((r1 - r0, N), np.float32)
     obm = np.empty((r1 - r0, N), np.float32) if block_max else None
-    lib().txo_gemm_mx_rows(_p(A), K, _p(sa), sa.shape[1], _p(B), K, _p(sb), sb.shape[1], N, K,
-                           fmt_a, fmt_b, r0, r1, _p(o32), _p(oab), _p(obm), nthreads)
+    lib().txo_gemm_mx_rows(_p(A), A.shape[1], _p(sa), sa.shape[1], _p(B), B.shape[1], _p(sb), sb.shape[1],
+                           N, K, fmt_a, fmt_b, r0, r1, _p(o32), _p(oab), _p(obm), nthreads)
     return (o32, oab, obm) if block_max else (o32, oab)
+
+
+def e2m1_value(nib: int) -> float:
+    """The oracle's decode of one fp4 (e2m1) nibble."""
+    return lib().txo_e2m1_value(nib)
 
 
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3

@@ -44,6 +44,11 @@
  *                  repeated over its 32 K values (the reference check's
  *                  form); scale exponent shifts double or halve rows and
  *                  columns; e8m0 255 gives NaN, 0 gives 2^-127; ragged K.
+ *                  fp4 (e2m1) operands: the 16 nibble values against the
+ *                  OCP table and triton's MXFP4Tensor decode, the packing
+ *                  (even K in the low nibble) against MXFP4Tensor's
+ *                  to_packed_tensor, and the product against a float64
+ *                  matmul of the unpacked values.
  */
 #include <math.h>
 #include <stdint.h>
@@ -64,7 +69,7 @@
 /* Format ids match the library's tx_dtype values: 1 = e4m3fn, 2 = e5m2.     */
 /* ------------------------------------------------------------------------ */
 
-enum { TXO_E4M3FN = 1, TXO_E5M2 = 2 };
+enum { TXO_E4M3FN = 1, TXO_E5M2 = 2, TXO_E2M1 = 4 };
 
 typedef struct {
   int mbits;
@@ -591,8 +596,24 @@ TXO_API void txo_gemm_fp8_scaled_rows(const uint8_t *A, int64_t lda,
 /* sum; out_abs: sum of |terms|; out_bmax: sum over blocks of the largest   */
 /* |term| of the block (the last two for error bounds; either may be NULL). */
 /* Aq row-major (lda bytes), Bq N rows of K bytes (ldb), scales row-major   */
-/* (ld_sa / ld_sb).                                                         */
+/* (ld_sa / ld_sb).  Format 4 is OCP e2m1 (fp4: sign, 2 exponent bits with  */
+/* bias 1, 1 mantissa bit; values 0, 0.5, 1, 1.5, 2, 3, 4, 6), two to a      */
+/* byte with the even K index in the low nibble (the packing of triton's    */
+/* MXFP4Tensor.to_packed_tensor that the reference's mxfp4 test feeds,      */
+/* test_tlx.py:4783-4786); rows then hold ceil(K/2) bytes.                  */
 /* ------------------------------------------------------------------------ */
+static double e2m1_value(unsigned nib) {
+  const unsigned e = (nib >> 1) & 3, m = nib & 1;
+  const double mag = e == 0 ? 0.5 * m : ldexp(1.0 + 0.5 * m, (int)e - 1);
+  return (nib & 8) ? -mag : mag;
+}
+
+static inline double mx_elem(const double *lut, const uint8_t *row, int64_t k, int fp4) {
+  return fp4 ? lut[(row[k >> 1] >> ((k & 1) * 4)) & 15] : lut[row[k]];
+}
+
+TXO_API double txo_e2m1_value(int nib) { return e2m1_value((unsigned)nib & 15); }
+
 TXO_API void txo_gemm_mx_rows(const uint8_t *A, int64_t lda, const uint8_t *sa,
                               int64_t ld_sa, const uint8_t *B, int64_t ldb,
                               const uint8_t *sb, int64_t ld_sb, int64_t N,
@@ -601,9 +622,10 @@ TXO_API void txo_gemm_mx_rows(const uint8_t *A, int64_t lda, const uint8_t *sa,
                               float *out_bmax, int nthreads) {
   init_tables();
   double lut_a[256], lut_b[256], e8[256];
+  const int fp4_a = fmt_a == TXO_E2M1, fp4_b = fmt_b == TXO_E2M1;
   for (int c = 0; c < 256; ++c) {
-    lut_a[c] = (double)txo_decode1(fmt_a, (uint8_t)c);
-    lut_b[c] = (double)txo_decode1(fmt_b, (uint8_t)c);
+    lut_a[c] = fp4_a ? e2m1_value(c & 15) : (double)txo_decode1(fmt_a, (uint8_t)c);
+    lut_b[c] = fp4_b ? e2m1_value(c & 15) : (double)txo_decode1(fmt_b, (uint8_t)c);
     e8[c] = c == 255 ? NAN : ldexp(1.0, c - 127);
   }
   const int64_t nblk = (K + 31) / 32;
@@ -622,7 +644,7 @@ TXO_API void txo_gemm_mx_rows(const uint8_t *A, int64_t lda, const uint8_t *sa,
         double blk = 0.0, blk_abs = 0.0, blk_max = 0.0;
         const int64_t k1 = (b + 1) * 32 < K ? (b + 1) * 32 : K;
         for (int64_t k = b * 32; k < k1; ++k) {
-          const double t = lut_a[arow[k]] * lut_b[bcol[k]];
+          const double t = mx_elem(lut_a, arow, k, fp4_a) * mx_elem(lut_b, bcol, k, fp4_b);
           blk += t;
           blk_abs += fabs(t);
           if (fabs(t) > blk_max) blk_max = fabs(t);

@@ -198,3 +198,111 @@ def test_mx_table_op_and_errors(tx, oracle, dev):
     with pytest.raises(tx.TxError):
         tx.invoke("tt.dot_scaled", [C, A, B, SA, SB, M, N, K, K, K, N, K // 32, K // 32,
                                     _lib.FP8E4M3FN, _lib.BF16, _lib.F32])
+
+
+# ---------------------------------------------------------------- fp4 (e2m1)
+def _run_fp4(tx, dev, pa, sa, pb, sb, out="bf16", lda=None, dtype_form=False):
+    """Packed fp4 operands (M x K/2 bytes) to the GPU as uint8 with format
+    'e2m1' (or as float4_e2m1fn_x2), optionally as views into wider rows."""
+    def put(x, ld):
+        if ld is None or ld == x.shape[1]:
+            return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+        w = np.zeros((x.shape[0], ld), np.uint8)
+        w[:, :x.shape[1]] = x
+        return torch.from_numpy(w).to(dev)[:, :x.shape[1]]
+
+    A, B = put(pa, lda), put(pb, lda)
+    SA, SB = put(sa, None), put(sb, None)
+    if dtype_form:
+        C = tx.dot_scaled(A.view(torch.float4_e2m1fn_x2), SA, B.view(torch.float4_e2m1fn_x2), SB,
+                          out_dtype=OUT[out])
+    else:
+        C = tx.dot_scaled(A, SA, B, SB, out_dtype=OUT[out], a_format="e2m1", b_format="e2m1")
+    torch.cuda.synchronize()
+    return C.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K,out", [
+    (256, 256, 256, "f32"), (256, 256, 512, "bf16"), (1024, 1280, 2048, "bf16"),
+    (300, 500, 4096, "f32"), (77, 33, 64, "f32"), (130, 260, 1000, "f16"), (1, 1, 2, "f32"),
+    (512, 2048, 8192, "f32"), (256, 512, 16384, "bf16")])
+def test_mx_fp4_shapes(tx, oracle, dev, M, N, K, out):
+    """fp4 x fp4 (two values a byte, the even K index in the low nibble):
+    256x256 tiles, 256x128 tiles unsplit and split over K, K a multiple of
+    256 (whole 128-byte steps), of 32, and ragged (rows zero-padded)."""
+    g = np.random.default_rng(M * 5 + N + K)
+    pa = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    pb = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    nb = (K + 31) // 32
+    lo, hi = (112, 122) if out == "f16" else (118, 136)
+    sa = g.integers(lo, hi, (M, nb), dtype=np.uint8)
+    sb = g.integers(lo, hi, (N, nb), dtype=np.uint8)
+    got = _run_fp4(tx, dev, pa, sa, pb, sb, out)
+    ref, mag, bmax = oracle.gemm_mx_rows(pa, sa, pb, sb, 0, M, fmt_a=4, fmt_b=4, block_max=True)
+    check_mx(got, ref, mag, bmax, K, out)
+
+
+def test_mx_fp4_strided_and_dtype_form(tx, oracle, dev):
+    """Operand rows wider than K/2 bytes (16-aligned, then not) and the
+    float4_e2m1fn_x2 dtype in place of uint8 + format."""
+    g = np.random.default_rng(31)
+    M, N, K = 200, 300, 1024
+    pa = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    pb = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sa = g.integers(120, 132, (M, K // 32), dtype=np.uint8)
+    sb = g.integers(120, 132, (N, K // 32), dtype=np.uint8)
+    ref, mag, bmax = oracle.gemm_mx_rows(pa, sa, pb, sb, 0, M, fmt_a=4, fmt_b=4, block_max=True)
+    for lda in (K // 2 + 64, K // 2 + 3):
+        check_mx(_run_fp4(tx, dev, pa, sa, pb, sb, "f32", lda=lda), ref, mag, bmax, K, "f32")
+    check_mx(_run_fp4(tx, dev, pa, sa, pb, sb, "f32", dtype_form=True), ref, mag, bmax, K, "f32")
+
+
+def test_mx_fp4_reference_check_form(tx, dev):
+    """The reference's mxfp4 check (test_tlx.py:4774-4856): M = N = K = 128,
+    operands of 2.0 packed by triton's MXFP4Tensor, scales 127, fp16 output
+    against a float32 matmul of the scale-expanded values, atol
+    1e-2 * sqrt(K / 32); then the same with random values and scales
+    124..129."""
+    mxfp = pytest.importorskip("triton.tools.mxfp")
+    M = N = K = 128
+    torch.manual_seed(0)
+    for rand in (False, True):
+        if rand:
+            a = torch.randint(0, 16, (M, K), dtype=torch.uint8)
+            b = torch.randint(0, 16, (N, K), dtype=torch.uint8)
+            ta, tb = mxfp.MXFP4Tensor(size=(M, K), device="cpu"), mxfp.MXFP4Tensor(size=(N, K), device="cpu")
+            ta.data, tb.data = a, b
+            sa = torch.randint(124, 130, (M, K // 32), dtype=torch.uint8)
+            sb = torch.randint(124, 130, (N, K // 32), dtype=torch.uint8)
+        else:
+            ta = mxfp.MXFP4Tensor(data=torch.full((M, K), 2.0), device="cpu")
+            tb = mxfp.MXFP4Tensor(data=torch.full((N, K), 2.0), device="cpu")
+            sa = torch.full((M, K // 32), 127, dtype=torch.uint8)
+            sb = torch.full((N, K // 32), 127, dtype=torch.uint8)
+        c = tx.dot_scaled(ta.to_packed_tensor(dim=1).to(dev), sa.to(dev), tb.to_packed_tensor(dim=1).to(dev),
+                          sb.to(dev), out_dtype=torch.float16, a_format="e2m1", b_format="e2m1")
+        sa_f = (sa.to(torch.int32) << 23).view(torch.float32).repeat_interleave(32, dim=1)[:M, :K]
+        sb_f = (sb.to(torch.int32) << 23).view(torch.float32).repeat_interleave(32, dim=1).T.contiguous()[:K, :N]
+        ref = torch.matmul(ta.to(torch.float32) * sa_f, tb.to(torch.float32).T * sb_f).to(torch.float16)
+        torch.testing.assert_close(ref, c.cpu(), atol=1e-2 * (K / 32) ** 0.5, rtol=0)
+
+
+def test_mx_fp4_errors(tx, dev):
+    from tx import _lib
+    M, N, K = 64, 64, 128
+    A = torch.zeros((M, K // 2), dtype=torch.uint8, device=dev)
+    A8 = torch.zeros((M, K), dtype=torch.uint8, device=dev)
+    S = torch.full((M, K // 32), 127, dtype=torch.uint8, device=dev)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    with pytest.raises(tx.TxError):   # fp4 x fp8 is not served
+        tx.invoke("tt.dot_scaled", [C, A, A8, S, S, M, N, K, K // 2, K, N, K // 32, K // 32,
+                                    _lib.FP4E2M1, _lib.FP8E4M3FN, _lib.F32])
+    with pytest.raises(tx.TxError):   # odd K
+        tx.invoke("tt.dot_scaled", [C, A, A, S, S, M, N, K - 1, K // 2, K // 2, N, K // 32, K // 32,
+                                    _lib.FP4E2M1, _lib.FP4E2M1, _lib.F32])
+    with pytest.raises(ValueError):   # uint8 without a format
+        tx.dot_scaled(A, S, A, S)
+    with pytest.raises(ValueError):   # K of A (128) and B (64) disagree
+        tx.dot_scaled(A, S, A8[:, :64].view(torch.float8_e4m3fn), S[:, :2], a_format="e2m1")
+    with pytest.raises(tx.TxError):   # same K, fp4 x fp8
+        tx.dot_scaled(A, S, A8.view(torch.float8_e4m3fn), S, a_format="e2m1")

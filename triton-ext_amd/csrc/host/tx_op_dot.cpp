@@ -366,8 +366,10 @@ static tx_status dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t lda, 
   return dot_fp8_impl(what, A, a_type, lda, sa, B, b_type, ldb, sb, C, ldc, M, N, K, e, stream);
 }
 
-// tt.dot_scaled with MX block scales (fp8 operands, e8m0 scales per 32 K
-// elements).  The kernel reads its operands through the fast path's LDS-DMA
+// tt.dot_scaled with MX block scales (fp8 operands, or fp4 (e2m1) packed two
+// per byte, e8m0 scales per 32 K elements).  The kernel walks operand bytes
+// (fp4: a 128-byte step is 256 K values and 8 scale blocks, two scale dwords
+// per row), and reads its operands through the fast path's LDS-DMA
 // pipeline, so rows that are not 16-byte aligned (or K not a multiple of 16)
 // are first copied into zero-padded rows (stream scratch slot 0, K rounded up
 // to a 128-byte step).  The scales are always repacked step-major (slot 2),
@@ -377,10 +379,16 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
                                const uint8_t *sb, int64_t ld_sb, void *C, tx_dtype c_type,
                                int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
   const char *what = "tx_dot_scaled_mx";
-  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, K));
-  const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
+  const bool fp4 = a_type == TX_FP4E2M1 || b_type == TX_FP4E2M1;
+  if (fp4 && a_type != b_type)
+    return fail(TX_UNSUPPORTED, "%s: mixed fp4 x fp8 operands are not served (both fp4 or both fp8)", what);
+  if (fp4 && K % 2)
+    return fail(TX_INVALID_ARGUMENT, "%s: fp4 operands need an even K (two values per byte)", what);
+  const int64_t kb = fp4 ? K / 2 : K;  // operand row bytes
+  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, kb));
+  const char *fa = fp4 ? "e2m1" : fp8_name(a_type), *fb = fp4 ? "e2m1" : fp8_name(b_type);
   if (!fa || !fb)
-    return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 (got %d, %d)", what,
+    return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 or fp4 (got %d, %d)", what,
                 int(a_type), int(b_type));
   const char *fo = c_type == TX_BF16 ? "bf16" : c_type == TX_F16 ? "f16" : c_type == TX_F32 ? "f32" : nullptr;
   if (!fo)
@@ -396,13 +404,14 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
                 what, (long long)ld_sa, (long long)ld_sb);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t cus = cu_count();
-  tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+  // the kernel walks operand bytes (fp4: K / 2 of them per row)
+  tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(kb), 0, 0, 0};
 
   // operands: as given, or zero-padded to whole 128-byte steps
   ScratchLease ws, wsc;  // held until every launch using them is enqueued
-  int64_t kk = K;        // K the kernel runs over
-  if (!fast_ok(A, lda, B, ldb, K, M, N)) {
-    const int64_t kp = (K + 127) / 128 * 128;
+  int64_t kk = kb;       // row bytes the kernel runs over
+  if (!fast_ok(A, lda, B, ldb, kb, M, N)) {
+    const int64_t kp = (kb + 127) / 128 * 128;
     if (std::max(M, N) * kp >= (int64_t(1) << 31))
       return fail(TX_UNSUPPORTED, "%s: padded operands exceed 32-bit offsets", what);
     const size_t a_bytes = size_t(M) * size_t(kp), b_bytes = size_t(N) * size_t(kp);
@@ -410,10 +419,10 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pad_rows", &fn));
     uint8_t *wa = static_cast<uint8_t *>(ws.ptr()), *wb = wa + a_bytes;
-    tx_pad_args pa{A, wa, lda, kp, int32_t(M), int32_t(K), int32_t(kp), pad_load_bytes(A, lda, K)};
+    tx_pad_args pa{A, wa, lda, kp, int32_t(M), int32_t(kb), int32_t(kp), pad_load_bytes(A, lda, kb)};
     TX_TRY(launch(fn, unsigned(std::min<int64_t>((M * kp / 16 + 255) / 256, cus * 16)), 1, 256, s,
                   &pa, sizeof pa, "tx_gemm_mx_pad_rows"));
-    tx_pad_args pb{B, wb, ldb, kp, int32_t(N), int32_t(K), int32_t(kp), pad_load_bytes(B, ldb, K)};
+    tx_pad_args pb{B, wb, ldb, kp, int32_t(N), int32_t(kb), int32_t(kp), pad_load_bytes(B, ldb, kb)};
     TX_TRY(launch(fn, unsigned(std::min<int64_t>((N * kp / 16 + 255) / 256, cus * 16)), 1, 256, s,
                   &pb, sizeof pb, "tx_gemm_mx_pad_rows"));
     args.A = wa;
@@ -423,29 +432,33 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
     args.K = int32_t(kp);
     kk = kp;
   }
-  // scales: repacked step-major (one 128-byte line per fragment and step),
-  // rows padded to whole tiles, blocks past ceil(K / 32) set to 2^0
+  // scales: repacked step-major (one or two 128-byte lines per fragment and
+  // step: a 128-byte step holds 4 blocks of fp8, 8 of fp4), rows padded to
+  // whole tiles, blocks past ceil(K / 32) set to 2^0
   const int64_t steps = (kk + 127) / 128;
+  const int64_t sd = fp4 ? 2 : 1;  // scale dwords per row and step
   const int64_t rows_a = (M + 255) / 256 * 256, rows_b = (N + 255) / 256 * 256;
-  if (steps * 4 * std::max(rows_a, rows_b) >= (int64_t(1) << 31))
+  if (steps * 4 * sd * std::max(rows_a, rows_b) >= (int64_t(1) << 31))
     return fail(TX_UNSUPPORTED, "%s: scale matrices exceed 32-bit offsets", what);
   if (steps > 0) {
-    const size_t pa_bytes = size_t(steps) * size_t(rows_a) * 4, pb_bytes = size_t(steps) * size_t(rows_b) * 4;
+    const size_t pa_bytes = size_t(steps * sd) * size_t(rows_a) * 4, pb_bytes = size_t(steps * sd) * size_t(rows_b) * 4;
     TX_TRY(wsc.acquire(s, 2, pa_bytes + pb_bytes));
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pack_scales", &fn));
     uint8_t *p = static_cast<uint8_t *>(wsc.ptr());
-    // one workgroup per 64 rows x 32 K steps
-    const int64_t ga = (rows_a / 64) * ((steps + 31) / 32), gb = (rows_b / 64) * ((steps + 31) / 32);
+    // one workgroup per 64 rows x 32 scale dwords (128 blocks)
+    const int64_t dcols = (steps * sd + 31) / 32;
+    const int64_t ga = (rows_a / 64) * dcols, gb = (rows_b / 64) * dcols;
     if (ga + gb > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: scale repack grid too large", what);
-    tx_mx_pack2_args pk{{{sa, p, ld_sa, int32_t(M), int32_t(nblk), int32_t(steps), int32_t(rows_a)},
-                         {sb, p + pa_bytes, ld_sb, int32_t(N), int32_t(nblk), int32_t(steps), int32_t(rows_b)}},
+    tx_mx_pack2_args pk{{{sa, p, ld_sa, int32_t(M), int32_t(nblk), int32_t(steps), int32_t(rows_a), int32_t(sd), 0},
+                         {sb, p + pa_bytes, ld_sb, int32_t(N), int32_t(nblk), int32_t(steps), int32_t(rows_b),
+                          int32_t(sd), 0}},
                         int32_t(ga), 0};
     TX_TRY(launch(fn, unsigned(ga + gb), 1, 256, s, &pk, sizeof pk, "tx_gemm_mx_pack_scales"));
     args.mx_a = p;
-    args.ld_mxa = rows_a * 4;
+    args.ld_mxa = rows_a * 4 * sd;
     args.mx_b = p + pa_bytes;
-    args.ld_mxb = rows_b * 4;
+    args.ld_mxb = rows_b * 4 * sd;
   }
 
   // 256x256 tiles while they give every CU one, else 256x128, with K split
@@ -666,7 +679,7 @@ static const bool reg_dot_fp8_ex = register_op(
     "c_scale:f32 bits");
 static const bool reg_dot_mx = register_op(
     "tt.dot_scaled", dot_mx_op,
-    "C:bf16|f16|f32*(result), A:fp8*, B:fp8* (N x K), scale_a:e8m0* (M x ceil(K/32)), "
+    "C:bf16|f16|f32*(result), A:fp8|fp4x2*, B:fp8|fp4x2* (N x K), scale_a:e8m0* (M x ceil(K/32)), "
     "scale_b:e8m0* (N x ceil(K/32)), M, N, K, lda, ldb, ldc, ld_scale_a, ld_scale_b, a_type:i32, "
     "b_type:i32, c_type:i32");
 static const bool reg_gemv = register_op(

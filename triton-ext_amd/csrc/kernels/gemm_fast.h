@@ -128,6 +128,18 @@ __device__ __forceinline__ void mfma32_mx(txd::f32x16 &acc, const i32x8 &mb, con
                                                         OPSEL, int(scale_b), OPSEL, int(scale_a));
 }
 
+// fp4 (e2m1) operands: one 16-byte piece per lane is 32 K values, so a
+// 64-byte K half is two MFMAs of K = 64 (the instruction reads the first 4
+// registers of each operand).
+template <class C, int OPSEL>
+__device__ __forceinline__ void mfma32_mx_fp4(txd::f32x16 &acc, const txd::i32x4 &pb, const txd::i32x4 &pa,
+                                              uint32_t scale_b, uint32_t scale_a) {
+  const i32x8 mb = __builtin_shufflevector(pb, pb, 0, 1, 2, 3, 0, 1, 2, 3);
+  const i32x8 ma = __builtin_shufflevector(pa, pa, 0, 1, 2, 3, 0, 1, 2, 3);
+  acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(mb, ma, acc, 4, 4, OPSEL, int(scale_b), OPSEL,
+                                                        int(scale_a));
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding and
 // all its LDS operations are done, then meet the workgroup at a barrier.
 // (A plain __syncthreads() would also wait for every outstanding load, which
@@ -150,6 +162,9 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
   static_assert(!MX || (C::FP8 && (NW == 4 || BN == 128)), "MX scales: fp8 operands; 256x256: 4 wavefronts");
+  constexpr bool FP4 = C::EL_A_ == EL_E2M1;
+  static_assert(!FP4 || (MX && C::EL_B_ == EL_E2M1), "fp4: MX-scaled, both operands");
+  constexpr int SD = FP4 ? 2 : 1;  // MX scale dwords per row and K step (4 blocks each)
   static_assert(OUT == OUT_BF16 || MX, "fp16 / fp32 output: MX variant only");
   static_assert(!EPI || (C::FP8 && !MX && OUT == OUT_BF16), "fused epilogue: row/column-scaled fp8");
   // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per
@@ -251,20 +266,21 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       ro[1][h][e] = off(wn * TN + frow, chunk);
     }
 
-  // MX scales, step-major: the dword of row r for K step s (blocks 4s ..
-  // 4s+3) at byte s * ld_mx + 4r; rows are padded to whole tiles (with
-  // finite codes), and the load one step past the end reads past the
-  // buffer's range (zeros, never used).  scn: the raw dwords of the next
-  // step, in flight; scc: this step's, shifted by 8g.
-  constexpr int NS = MX ? NF : 1;
+  // MX scales, step-major: the SD dwords of row r for K step s (blocks
+  // 4 SD s .. +4 SD - 1; fp8: 4 blocks of 32 bytes, fp4: 8 blocks of 16) at
+  // byte s * ld_mx + 4 SD r; rows are padded to whole tiles (with finite
+  // codes), and the load one step past the end reads past the buffer's
+  // range (zeros, never used).  scn: the raw dwords of the next step, in
+  // flight; scc: this step's, shifted by 8g.
+  constexpr int NS = MX ? NF * SD : 1;
   uint32_t scc[NS], scn[NS];
   __amdgpu_buffer_rsrc_t srs[2];
   uint32_t svb[2] = {0u, 0u};
   if constexpr (MX) {
     srs[0] = make_rsrc(a.mx_a, uint32_t(ksteps_all) * uint32_t(a.ld_mxa));
     srs[1] = make_rsrc(a.mx_b, uint32_t(ksteps_all) * uint32_t(a.ld_mxb));
-    svb[0] = 4u * uint32_t(m0 + wm * TM + frow);
-    svb[1] = 4u * uint32_t(n0 + wn * TN + frow);
+    svb[0] = 4u * SD * uint32_t(m0 + wm * TM + frow);
+    svb[1] = 4u * SD * uint32_t(n0 + wn * TN + frow);
   }
   auto load_scales = [&](int ks, uint32_t(&dst)[NS]) {
     if constexpr (MX) {
@@ -273,8 +289,15 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       for (int f = 0; f < NF; ++f) {
         const int op = f < FM ? 0 : 1;
         const int fb = f < FM ? f : f - FM;
-        const int soff = s * int(op == 0 ? a.ld_mxa : a.ld_mxb) + 128 * fb;
-        dst[f] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(srs[op], int(svb[op]), soff, 0));
+        const int soff = s * int(op == 0 ? a.ld_mxa : a.ld_mxb) + 128 * SD * fb;
+        if constexpr (SD == 1) {
+          dst[f] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(srs[op], int(svb[op]), soff, 0));
+        } else {
+          const txd::u32x2 d = __builtin_bit_cast(
+              txd::u32x2, __builtin_amdgcn_raw_buffer_load_b64(srs[op], int(svb[op]), soff, 0));
+          dst[2 * f] = d.x;
+          dst[2 * f + 1] = d.y;
+        }
       }
     }
   };
@@ -301,8 +324,16 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
     constexpr int h = decltype(h_tag)::value, i = decltype(i_tag)::value, fn = i / FM, fm = i % FM;
     const i32x8 va = __builtin_shufflevector(fr[h][fm][0], fr[h][fm][1], 0, 1, 2, 3, 4, 5, 6, 7);
     const i32x8 vb = __builtin_shufflevector(fr[h][FM + fn][0], fr[h][FM + fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
-    if constexpr (MX) mfma32_mx<C, 2 * h>(acc[fn][fm], vb, va, scc[FM + fn], scc[fm]);
-    else mfma32<C>(acc[fn][fm], vb, va);
+    if constexpr (FP4) {
+      // K half h holds blocks 4h .. 4h + 3 (dword h of the step's two):
+      // piece e is blocks 4h + 2e + g, byte 2e after the 8g shift
+      mfma32_mx_fp4<C, 0>(acc[fn][fm], fr[h][FM + fn][0], fr[h][fm][0], scc[2 * (FM + fn) + h], scc[2 * fm + h]);
+      mfma32_mx_fp4<C, 2>(acc[fn][fm], fr[h][FM + fn][1], fr[h][fm][1], scc[2 * (FM + fn) + h], scc[2 * fm + h]);
+    } else if constexpr (MX) {
+      mfma32_mx<C, 2 * h>(acc[fn][fm], vb, va, scc[FM + fn], scc[fm]);
+    } else {
+      mfma32<C>(acc[fn][fm], vb, va);
+    }
   };
   using H0 = std::integral_constant<int, 0>;
   using H1 = std::integral_constant<int, 1>;
@@ -328,7 +359,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
       if constexpr (MX) {
         // this step's scales (loaded during the previous half) into place
 #pragma unroll
-        for (int f = 0; f < NF; ++f) scc[f] = scn[f] >> (8 * fg);
+        for (int f = 0; f < NS; ++f) scc[f] = scn[f] >> (8 * fg);
       }
       static_for<NM>([&](auto I) {
         constexpr int i = decltype(I)::value;

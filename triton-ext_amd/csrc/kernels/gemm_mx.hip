@@ -1,5 +1,5 @@
-// tt.dot_scaled with MX block scales on gfx950: fp8 (e4m3fn / e5m2)
-// operands, one e8m0 scale per 32 K elements of each row of A and each
+// tt.dot_scaled with MX block scales on gfx950: fp8 (e4m3fn / e5m2) or
+// fp4 (e2m1, two per byte along K) operands, one e8m0 scale per 32 K elements of each row of A and each
 // column of B, fp32 accumulation in v_mfma_scale_f32_32x32x64_f8f6f4 (the
 // scales enter the MFMA itself), output bf16, fp16 or fp32.  The tile is the
 // fast path's LDS-DMA pipeline: 256 x 256 with 4 wavefronts, 256 x 128 with
@@ -25,6 +25,7 @@ TX_GEMM_MX_OUTS(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
 TX_GEMM_MX_OUTS(e5m2, e5m2, EL_E5M2, EL_E5M2)
 TX_GEMM_MX_OUTS(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
 TX_GEMM_MX_OUTS(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
+TX_GEMM_MX_OUTS(e2m1, e2m1, EL_E2M1, EL_E2M1)
 
 // Split-K: sums of the K splits' fp32 planes, rounded to the output type.
 TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_splitk_reduce_bf16(const tx_gemm_args a) {
@@ -42,11 +43,10 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pad_rows(const tx_pad_args a) {
 
 // Scales of A and B into the step-major layout the tile reads (see
 // tx_mx_pack_args), through LDS: workgroup b of an operand transposes rows
-// 64 * (b % R) .. +63 (R = rows_pad / 64) for K steps 32 * (b / R) .. +31
-// (128 blocks), reading each source
-// row's bytes contiguously (dwords when the rows are 4-byte aligned, every
-// load issued before the first is used) and writing 256-byte runs of each
-// step's dwords.
+// 64 * (b % R) .. +63 (R = rows_pad / 64) for source dword columns
+// 32 * (b / R) .. +31 (128 blocks), reading each source row's bytes
+// contiguously (dwords when the rows are 4-byte aligned, every load issued
+// before the first is used) and writing runs of consecutive rows' dwords.
 TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pack_scales(const tx_mx_pack2_args both) {
   __shared__ uint32_t t[64][33];  // [row][dword of 4 blocks], odd pitch against bank conflicts
   const bool second = int(blockIdx.x) >= both.blocks0;
@@ -54,8 +54,8 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pack_scales(const tx_mx_pack2_a
   const int b = int(blockIdx.x) - (second ? both.blocks0 : 0);
   const int nrb = a.rows_pad / 64;
   const int r0 = (b % nrb) * 64;
-  const int s0 = (b / nrb) * 32;
-  const int c0 = 4 * s0;
+  const int d0 = (b / nrb) * 32;  // first dword column (4 blocks each)
+  const int c0 = 4 * d0;
   const int tid = threadIdx.x;
   const bool words = (reinterpret_cast<uintptr_t>(a.src) & 3) == 0 && (a.src_ld & 3) == 0;
   uint32_t w[8];
@@ -84,9 +84,14 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pack_scales(const tx_mx_pack2_a
   __syncthreads();
   uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst);
   const int r = tid & 63;
+  const int ndw = a.steps * a.sd;  // dword columns in all
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int sl = (tid >> 6) + 4 * j;  // step within the tile
-    if (s0 + sl < a.steps) dst[int64_t(s0 + sl) * a.rows_pad + r0 + r] = t[r][sl];
+    const int cl = (tid >> 6) + 4 * j;  // dword column within the tile
+    const int d = d0 + cl;
+    if (d < ndw) {
+      const int s = d / a.sd, q = d % a.sd;
+      dst[(int64_t(s) * a.rows_pad + r0 + r) * a.sd + q] = t[r][cl];
+    }
   }
 }

@@ -7,7 +7,7 @@
 namespace txg {
 
 // Operand element kinds for the MFMA selection.
-enum { EL_BF16 = 0, EL_E4M3 = 1, EL_E5M2 = 2 };
+enum { EL_BF16 = 0, EL_E4M3 = 1, EL_E5M2 = 2, EL_E2M1 = 4 };  // e2m1: fp4, two per byte along K
 
 template <int EL_A, int EL_B, int BM_, int BN_, int WM_, int WN_, int VEC_>
 struct GemmCfg {
@@ -23,8 +23,9 @@ struct GemmCfg {
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile");
 };
 
-// f8f6f4 operand format codes of the gfx950 MFMA (0 = fp8 e4m3, 1 = bf8 e5m2).
-template <int EL> struct F8Code { static constexpr int v = EL == EL_E5M2 ? 1 : 0; };
+// f8f6f4 operand format codes of the gfx950 MFMA (0 = fp8 e4m3, 1 = bf8 e5m2,
+// 4 = fp4 e2m1).
+template <int EL> struct F8Code { static constexpr int v = EL == EL_E5M2 ? 1 : EL == EL_E2M1 ? 4 : 0; };
 
 template <class C>
 __device__ __forceinline__ f32x4 mfma_step(f32x4 acc, const u32x4 (&mfa)[2], const u32x4 (&mfb)[2]) {

@@ -91,9 +91,10 @@ typedef struct tx_gemm_args {
 enum { EPI_ACT_NONE = 0, EPI_ACT_RELU = 1, EPI_ACT_GELU_TANH = 2, EPI_ACT_SILU = 3 };
 enum { EPI_OUT_BF16 = 0, EPI_OUT_F16 = 1, EPI_OUT_F32 = 2, EPI_OUT_E4M3FN = 3, EPI_OUT_E5M2 = 4 };
 
-/* Step-major repack of MX scales: dst dword [s][r] (byte s * 4 * rows_pad +
- * 4r) = bytes src[r][4s .. 4s+3], with 127 (2^0) for r >= rows or a block
- * >= cols. */
+/* Step-major repack of MX scales: with sd dwords per row and K step (1 for
+ * fp8, 2 for fp4), dword j of row r for step s sits at byte
+ * s * 4 * sd * rows_pad + 4 * (sd * r + j) and holds src[r][4 (sd s + j) .. +3],
+ * with 127 (2^0) for r >= rows or a block >= cols. */
 typedef struct tx_mx_pack_args {
   const uint8_t *src;
   uint8_t *dst;
@@ -102,6 +103,8 @@ typedef struct tx_mx_pack_args {
   int32_t cols;     /* scale blocks per source row, ceil(K / 32) */
   int32_t steps;    /* K steps of the kernel */
   int32_t rows_pad; /* rows of the packed matrix (whole tiles) */
+  int32_t sd;       /* dwords per row and step */
+  int32_t reserved;
 } tx_mx_pack_args;
 
 /* Both operands' repacks in one launch: workgroups [0, blocks0) pack op[0],

@@ -266,23 +266,48 @@ def _e8m0_bytes(t: torch.Tensor) -> torch.Tensor:
     raise ValueError("MX scales must be uint8 (e8m0 codes) or float8_e8m0fnu")
 
 
+_FP4 = getattr(torch, "float4_e2m1fn_x2", None)
+
+
+def _mx_operand(t, fmt):
+    """(tx dtype, logical K) of an MX operand: fp8 by dtype, or fp4 (e2m1)
+    packed two per byte (even K in the low nibble) as float4_e2m1fn_x2 or as
+    uint8 with format "e2m1"."""
+    if fmt not in (None, "e4m3", "e5m2", "e2m1"):
+        raise ValueError(f"unknown MX format {fmt!r}")
+    if t.dtype in _FP8:
+        if fmt is not None and fmt != {torch.float8_e4m3fn: "e4m3", torch.float8_e5m2: "e5m2"}[t.dtype]:
+            raise ValueError(f"format {fmt!r} does not match dtype {t.dtype}")
+        return _TX_DTYPE[t.dtype], t.shape[1]
+    if (_FP4 is not None and t.dtype == _FP4 and fmt in (None, "e2m1")) or \
+            (t.dtype == torch.uint8 and fmt == "e2m1"):
+        return _lib.FP4E2M1, 2 * t.shape[1]
+    raise ValueError("MX operands are fp8 tensors, or fp4 packed as float4_e2m1fn_x2 / uint8 with format 'e2m1'")
+
+
 def dot_scaled(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
                scale_b: torch.Tensor, out_dtype: torch.dtype = torch.float32,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, a_format: str | None = None,
+               b_format: str | None = None) -> torch.Tensor:
     """tt.dot_scaled with MX block scales: one e8m0 scale per 32 K elements,
     out[m,n] = sum_k a_q[m,k] 2^(scale_a[m,k//32]-127) * b[k,n] 2^(scale_b[n,k//32]-127),
     fp32 accumulation, rounded to ``out_dtype`` (fp32, bf16 or fp16).
-    a_q: fp8 M x K; b_q_nk: fp8 N x K (the column-major K x N operand);
-    scale_a: M x ceil(K/32), scale_b: N x ceil(K/32), uint8 codes or
-    float8_e8m0fnu."""
+    a_q: M x K fp8, or fp4 (e2m1) M x K/2 bytes; b_q_nk: N x K likewise (the
+    column-major K x N operand).  fp4 is packed two per byte with the even K
+    index in the low nibble (triton's MXFP4Tensor.to_packed_tensor), given
+    as float4_e2m1fn_x2 or as uint8 with ``a_format`` / ``b_format`` "e2m1";
+    both operands fp4 or both fp8.  scale_a: M x ceil(K/32), scale_b:
+    N x ceil(K/32), uint8 codes or float8_e8m0fnu."""
     _on_gpu(a_q, scale_a, b_q_nk, scale_b, out)
-    if a_q.dtype not in _FP8 or b_q_nk.dtype not in _FP8:
-        raise ValueError("dot_scaled takes fp8 operands")
-    if a_q.dim() != 2 or b_q_nk.dim() != 2 or a_q.shape[1] != b_q_nk.shape[1]:
+    if a_q.dim() != 2 or b_q_nk.dim() != 2:
+        raise ValueError("incompatible shapes")
+    ta, K = _mx_operand(a_q, a_format)
+    tb, Kb = _mx_operand(b_q_nk, b_format)
+    if K != Kb:
         raise ValueError("incompatible shapes")
     if a_q.stride(1) != 1 or b_q_nk.stride(1) != 1:
         raise ValueError("operands must be K-contiguous")
-    M, K = a_q.shape
+    M = a_q.shape[0]
     N = b_q_nk.shape[0]
     sa, sb = _e8m0_bytes(scale_a), _e8m0_bytes(scale_b)
     nblk = (K + 31) // 32
@@ -295,8 +320,8 @@ def dot_scaled(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
         out = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
     if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:
         raise ValueError("out must be a row-major M x N tensor of out_dtype")
-    check(lib.tx_dot_scaled_mx(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(sa), sa.stride(0),
-                               _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0), _ptr(sb),
+    check(lib.tx_dot_scaled_mx(_ptr(a_q), ta, a_q.stride(0), _ptr(sa), sa.stride(0),
+                               _ptr(b_q_nk), tb, b_q_nk.stride(0), _ptr(sb),
                                sb.stride(0), _ptr(out), _TX_DTYPE[out_dtype], out.stride(0), M, N, K,
                                _stream(a_q)))
     return out

@@ -162,6 +162,42 @@ def quant_mx(x: np.ndarray, fmt: str = "e4m3fn"):
     return codes, (e >> np.uint32(23)).astype(np.uint8)
 
 
+E2M1_GRID = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float32)
+
+
+def quant_mx_fp4(x: np.ndarray):
+    """MX fp4 (e2m1) quantisation of x (rows x K, K a multiple of 32) by the
+    OCP Microscaling spec v1.0 rule: shared exponent floor(log2(absmax)) - 2
+    (e2m1's largest exponent), clamped to the e8m0 range; elements
+    x / 2^shared rounded to the nearest e2m1 value (ties to the even code),
+    saturating at 6, the sign kept on zeros (as triton's MXFP4Tensor
+    rounds).  Returns (packed uint8 rows x K/2, the even K index in the low
+    nibble; e8m0 uint8 rows x K/32); all-zero blocks get scale 2^0."""
+    R, K = x.shape
+    xb = x.reshape(R, K // 32, 32).astype(np.float32)
+    amax = np.abs(xb).max(axis=2)
+    with np.errstate(divide="ignore"):
+        shared = np.where(amax > 0, np.floor(np.log2(np.where(amax > 0, amax, 1))) - 2, 0)
+    shared = np.clip(shared, -127, 127).astype(np.int32)
+    v = np.abs(xb) * np.exp2(-shared.astype(np.float32))[:, :, None]
+    mid = (E2M1_GRID[1:] + E2M1_GRID[:-1]) / 2
+    code = np.searchsorted(mid, v, side="left").astype(np.uint8)         # v <= mid[i] -> i
+    tie = (code < 7) & (v == mid[np.minimum(code, 6)])
+    code = np.where(tie & (code % 2 == 1), code + 1, code).astype(np.uint8)  # ties to even
+    code |= np.signbit(xb).astype(np.uint8) << 3                          # -0 kept
+    code = code.reshape(R, K)
+    packed = (code[:, 0::2] | (code[:, 1::2] << 4)).astype(np.uint8)
+    return packed, (shared + 127).astype(np.uint8)
+
+
+def mx_fp4_gemm_input(M: int, N: int, K: int, seed_stream: int = 0):
+    """Returns (Aq packed fp4 uint8[M,K/2], sa e8m0 uint8[M,K/32], Bq uint8[N,K/2], sb)."""
+    g = rng(6, seed_stream + 1)
+    aq, sa = quant_mx_fp4(g.standard_normal((M, K), dtype=np.float32))
+    bq, sb = quant_mx_fp4(g.standard_normal((N, K), dtype=np.float32))
+    return aq, sa, bq, sb
+
+
 def mx_gemm_input(M: int, N: int, K: int, seed_stream: int = 0, fa: str = "e4m3fn",
                   fb: str = "e4m3fn"):
     """Returns (Aq uint8[M,K], sa e8m0 uint8[M,K/32], Bq uint8[N,K], sb e8m0 uint8[N,K/32])."""
