@@ -25,7 +25,8 @@
  *    (at most 8 x M x N x 4 bytes) when the output tiles leave CUs idle,
  *    zero-padded copies of A and B when rows are not 16-byte aligned in a
  *    product of at least 2^30 multiply-adds (tx_dot_scaled_mx: in any
- *    product), and repacked MX scale rows.  The scratch is allocated
+ *    product), the e4m3fn expansion of an fp4 operand that meets an fp8
+ *    one (tx_dot_scaled_mx), and repacked MX scale rows.  The scratch is allocated
  *    stream-ordered (hipMallocAsync on `stream`) the first time a stream
  *    needs it, grown the same way, and reused by later calls, so
  *    steady-state calls allocate nothing; requests above 512 MiB get a
@@ -309,9 +310,10 @@ TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t ld
  * tlx/mma_ops.py:163-237, lowered through GenericOpPattern<DotScaledOp>,
  * uTLXConversionPatterns.cpp:616); closed form of its check at
  * test_tlx.py:2271-2292, whose `bits << 23` scale decode agrees for codes
- * 1..254.  a_type/b_type are TX_FP8E4M3FN or TX_FP8E5M2 in any pairing, or
- * both TX_FP4E2M1 (the "e4m3" / "e5m2" / "e2m1" formats of async_dot_scaled;
- * mixed fp8 x fp4 returns TX_UNSUPPORTED).
+ * 1..254.  a_type/b_type are TX_FP8E4M3FN, TX_FP8E5M2 or TX_FP4E2M1 in any
+ * pairing (the "e4m3" / "e5m2" / "e2m1" formats of async_dot_scaled; an
+ * fp4 operand that meets an fp8 one is first expanded to e4m3fn, exactly,
+ * in the library's scratch).
  * A: row-major M rows of K bytes (fp8) or K/2 bytes (fp4, K even), row
  * stride lda in bytes; B: column-major, N rows likewise (ldb bytes).
  * scale_a: e8m0 bytes, row-major M x ceil(K/32) (row stride ld_scale_a);

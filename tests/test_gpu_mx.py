@@ -287,6 +287,66 @@ def test_mx_fp4_reference_check_form(tx, dev):
         torch.testing.assert_close(ref, c.cpu(), atol=1e-2 * (K / 32) ** 0.5, rtol=0)
 
 
+@pytest.mark.parametrize("M,N,K,a4,f8,out", [
+    (256, 256, 256, True, 1, "f32"), (256, 256, 256, False, 1, "bf16"), (1024, 1280, 2048, True, 2, "bf16"),
+    (300, 500, 4096, False, 2, "f32"), (77, 33, 64, True, 1, "f32"), (130, 260, 1000, False, 1, "f16"),
+    (64, 96, 200, True, 2, "f32"), (512, 2048, 8192, False, 1, "f32")])
+def test_mx_mixed_fp4_fp8(tx, oracle, dev, M, N, K, a4, f8, out):
+    """fp4 x fp8 and fp8 x fp4 (the reference's mixed mxfp8 / mxfp4 pairs):
+    the fp4 operand is expanded to e4m3fn, exactly, then meets the fp8 one in
+    the fp8 tile; K a multiple of 128, ragged with the fp8 rows read in
+    place (K % 16 == 0), and ragged with them padded (1000, 200)."""
+    g = np.random.default_rng(M * 3 + N * 7 + K + a4)
+    nb = (K + 31) // 32
+    p4 = g.integers(0, 256, ((M if a4 else N), K // 2), dtype=np.uint8)
+    c8 = _codes(g, ((N if a4 else M), K), f8)
+    lo, hi = (112, 120) if out == "f16" else (118, 134)
+    sa = g.integers(lo, hi, (M, nb), dtype=np.uint8)
+    sb = g.integers(lo, hi, (N, nb), dtype=np.uint8)
+    aq, bq = (p4, c8) if a4 else (c8, p4)
+    fa, fb = (4, f8) if a4 else (f8, 4)
+    A = torch.from_numpy(aq).to(dev)
+    B = torch.from_numpy(bq).to(dev)
+    if not a4:
+        A = A.view(TD[f8])
+    else:
+        B = B.view(TD[f8])
+    C = tx.dot_scaled(A, torch.from_numpy(sa).to(dev), B, torch.from_numpy(sb).to(dev), out_dtype=OUT[out],
+                      a_format="e2m1" if a4 else None, b_format=None if a4 else "e2m1")
+    torch.cuda.synchronize()
+    ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, 0, M, fmt_a=fa, fmt_b=fb, block_max=True)
+    check_mx(C.float().cpu().numpy(), ref, mag, bmax, K, out)
+
+
+@pytest.mark.parametrize("a_fmt,b_fmt", [("e4m3", "e2m1"), ("e2m1", "e4m3")])
+def test_mx_mixed_reference_check_form(tx, dev, a_fmt, b_fmt):
+    """The reference's mixed check (test_tlx.py:4866-5080): M = N = K = 128,
+    the fp4 operand 2.0 packed by triton's MXFP4Tensor, the fp8 one the
+    values 20..39 cast to e4m3fn, scales 127, fp16 output against a float32
+    matmul, atol 1e-2 * sqrt(K / 32)."""
+    mxfp = pytest.importorskip("triton.tools.mxfp")
+    M = N = K = 128
+    torch.manual_seed(0)
+    if a_fmt == "e2m1":
+        t = mxfp.MXFP4Tensor(data=torch.full((M, K), 2.0), device="cpu")
+        a, a_ref = t.to_packed_tensor(dim=1), t.to(torch.float32)
+    else:
+        a = torch.randint(20, 40, (M, K), dtype=torch.uint8).to(torch.float8_e4m3fn)
+        a_ref = a.to(torch.float32)
+    if b_fmt == "e2m1":
+        t = mxfp.MXFP4Tensor(data=torch.full((N, K), 2.0), device="cpu")
+        b_nk, b_ref = t.to_packed_tensor(dim=1), t.to(torch.float32).T
+    else:
+        b = torch.randint(20, 40, (K, N), dtype=torch.uint8).to(torch.float8_e4m3fn)
+        b_nk, b_ref = b.t().contiguous(), b.to(torch.float32)
+    sa = torch.full((M, K // 32), 127, dtype=torch.uint8)
+    sb = torch.full((N, K // 32), 127, dtype=torch.uint8)
+    c = tx.dot_scaled(a.to(dev), sa.to(dev), b_nk.to(dev), sb.to(dev), out_dtype=torch.float16,
+                      a_format=a_fmt, b_format=b_fmt)
+    ref = torch.matmul(a_ref, b_ref).to(torch.float16)
+    torch.testing.assert_close(ref, c.cpu(), atol=1e-2 * (K / 32) ** 0.5, rtol=0)
+
+
 def test_mx_fp4_errors(tx, dev):
     from tx import _lib
     M, N, K = 64, 64, 128
@@ -294,8 +354,8 @@ def test_mx_fp4_errors(tx, dev):
     A8 = torch.zeros((M, K), dtype=torch.uint8, device=dev)
     S = torch.full((M, K // 32), 127, dtype=torch.uint8, device=dev)
     C = torch.empty((M, N), dtype=torch.float32, device=dev)
-    with pytest.raises(tx.TxError):   # fp4 x fp8 is not served
-        tx.invoke("tt.dot_scaled", [C, A, A8, S, S, M, N, K, K // 2, K, N, K // 32, K // 32,
+    with pytest.raises(tx.TxError):   # fp8 B rows shorter than K bytes
+        tx.invoke("tt.dot_scaled", [C, A, A8, S, S, M, N, K, K // 2, K // 2, N, K // 32, K // 32,
                                     _lib.FP4E2M1, _lib.FP8E4M3FN, _lib.F32])
     with pytest.raises(tx.TxError):   # odd K
         tx.invoke("tt.dot_scaled", [C, A, A, S, S, M, N, K - 1, K // 2, K // 2, N, K // 32, K // 32,
@@ -304,5 +364,6 @@ def test_mx_fp4_errors(tx, dev):
         tx.dot_scaled(A, S, A, S)
     with pytest.raises(ValueError):   # K of A (128) and B (64) disagree
         tx.dot_scaled(A, S, A8[:, :64].view(torch.float8_e4m3fn), S[:, :2], a_format="e2m1")
-    with pytest.raises(tx.TxError):   # same K, fp4 x fp8
-        tx.dot_scaled(A, S, A8.view(torch.float8_e4m3fn), S, a_format="e2m1")
+    # same K, fp4 x fp8: served (zeros in, zeros out)
+    z = tx.dot_scaled(A, S, A8.view(torch.float8_e4m3fn), S, a_format="e2m1")
+    assert torch.count_nonzero(z).item() == 0

@@ -379,14 +379,19 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
                                const uint8_t *sb, int64_t ld_sb, void *C, tx_dtype c_type,
                                int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
   const char *what = "tx_dot_scaled_mx";
-  const bool fp4 = a_type == TX_FP4E2M1 || b_type == TX_FP4E2M1;
-  if (fp4 && a_type != b_type)
-    return fail(TX_UNSUPPORTED, "%s: mixed fp4 x fp8 operands are not served (both fp4 or both fp8)", what);
-  if (fp4 && K % 2)
+  const bool fa4 = a_type == TX_FP4E2M1, fb4 = b_type == TX_FP4E2M1;
+  const bool fp4 = fa4 && fb4;    // the fp4 x fp4 tile
+  const bool mixed = fa4 != fb4;  // fp4 operand expanded to e4m3fn, then the fp8 tile
+  if ((fa4 || fb4) && K % 2)
     return fail(TX_INVALID_ARGUMENT, "%s: fp4 operands need an even K (two values per byte)", what);
-  const int64_t kb = fp4 ? K / 2 : K;  // operand row bytes
+  const int64_t ka = fa4 ? K / 2 : K, kbb = fb4 ? K / 2 : K;  // operand row bytes
+  const int64_t kb = std::min(ka, kbb);
   TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, kb));
-  const char *fa = fp4 ? "e2m1" : fp8_name(a_type), *fb = fp4 ? "e2m1" : fp8_name(b_type);
+  if (M > 0 && N > 0 && (lda < ka || ldb < kbb))
+    return fail(TX_INVALID_ARGUMENT, "%s: stride smaller than row length (lda=%lld ldb=%lld)", what,
+                (long long)lda, (long long)ldb);
+  const char *fa = fp4 ? "e2m1" : fa4 ? "e4m3fn" : fp8_name(a_type);
+  const char *fb = fp4 ? "e2m1" : fb4 ? "e4m3fn" : fp8_name(b_type);
   if (!fa || !fb)
     return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 or fp4 (got %d, %d)", what,
                 int(a_type), int(b_type));
@@ -410,7 +415,40 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
   // operands: as given, or zero-padded to whole 128-byte steps
   ScratchLease ws, wsc;  // held until every launch using them is enqueued
   int64_t kk = kb;       // row bytes the kernel runs over
-  if (!fast_ok(A, lda, B, ldb, kb, M, N)) {
+  if (mixed && K > 0) {
+    // the fp4 operand into e4m3fn rows of kp bytes (zeros past K); the fp8
+    // one as given when the fast path can read it, else padded likewise
+    const int64_t kp = (K + 127) / 128 * 128;
+    const void *src4 = fa4 ? A : B, *src8 = fa4 ? B : A;
+    const int64_t ld4 = fa4 ? lda : ldb, ld8 = fa4 ? ldb : lda;
+    const int64_t rows4 = fa4 ? M : N, rows8 = fa4 ? N : M;
+    const bool direct8 = aligned(src8, 16) && ld8 % 16 == 0 && K % 16 == 0 &&
+                         (rows8 - 1) * ld8 + K < (int64_t(1) << 31);
+    if (std::max(rows4, direct8 ? int64_t(0) : rows8) * kp >= (int64_t(1) << 31))
+      return fail(TX_UNSUPPORTED, "%s: expanded operands exceed 32-bit offsets", what);
+    const size_t b4 = size_t(rows4) * size_t(kp), b8 = direct8 ? 0 : size_t(rows8) * size_t(kp);
+    TX_TRY(ws.acquire(s, 0, b4 + b8));
+    uint8_t *w4 = static_cast<uint8_t *>(ws.ptr()), *w8 = w4 + b4;
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_fp4_to_e4m3", &fn));
+    tx_pad_args px{src4, w4, ld4, kp, int32_t(rows4), int32_t(K / 2), int32_t(kp), 0};
+    TX_TRY(launch(fn, unsigned(std::min<int64_t>((rows4 * kp / 8 + 255) / 256, cus * 16)), 1, 256, s,
+                  &px, sizeof px, "tx_gemm_mx_fp4_to_e4m3"));
+    if (!direct8) {
+      TX_TRY(get_kernel(CodeObject::GemmMx, "tx_gemm_mx_pad_rows", &fn));
+      tx_pad_args pp{src8, w8, ld8, kp, int32_t(rows8), int32_t(K), int32_t(kp), pad_load_bytes(src8, ld8, K)};
+      TX_TRY(launch(fn, unsigned(std::min<int64_t>((rows8 * kp / 16 + 255) / 256, cus * 16)), 1, 256, s,
+                    &pp, sizeof pp, "tx_gemm_mx_pad_rows"));
+    }
+    const void *d8 = direct8 ? src8 : w8;
+    const int64_t l8 = direct8 ? ld8 : kp;
+    args.A = fa4 ? static_cast<const void *>(w4) : d8;
+    args.lda = fa4 ? kp : l8;
+    args.B = fa4 ? d8 : static_cast<const void *>(w4);
+    args.ldb = fa4 ? l8 : kp;
+    kk = direct8 ? K : kp;
+    args.K = int32_t(kk);
+  } else if (!fast_ok(A, lda, B, ldb, kb, M, N)) {
     const int64_t kp = (kb + 127) / 128 * 128;
     if (std::max(M, N) * kp >= (int64_t(1) << 31))
       return fail(TX_UNSUPPORTED, "%s: padded operands exceed 32-bit offsets", what);

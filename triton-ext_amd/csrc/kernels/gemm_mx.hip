@@ -41,6 +41,50 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_splitk_reduce_f32(const tx_gemm
 // Operand rows into zero-padded, 16-byte aligned rows (as the fp8 GEMM's).
 TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_pad_rows(const tx_pad_args a) { pad_rows<1>(a); }
 
+// fp4 (e2m1) operand rows, two values a byte with the even K index in the
+// low nibble, into e4m3fn rows of dst_ld bytes (cols = source bytes, i.e.
+// K / 2; dst_cols = the zero-filled destination row length), so that an fp4
+// operand can meet an fp8 one in the fp8 x fp8 tile.  Every e2m1 value is
+// exact in e4m3fn: magnitude nibble (e, m) = (bits 2:1, bit 0) is 0.5 m for
+// e = 0 and 2^(e-1) (1 + m/2) otherwise, i.e. code ((e + 6) << 3) | (m << 2)
+// (0x30 for 0.5, 0 for 0), sign to bit 7.  Thread unit: 4 source bytes ->
+// 8 destination bytes.
+__device__ __forceinline__ uint32_t e2m1x4_to_e4m3(uint32_t nibs16) {  // 4 nibbles in bits 0..15
+  uint32_t out = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t n = (nibs16 >> (4 * i)) & 15u, mag = n & 7u, e = mag >> 1, m = mag & 1u;
+    const uint32_t code = e ? (((e + 6u) << 3) | (m << 2)) : (m ? 0x30u : 0u);
+    out |= (code | ((n & 8u) << 4)) << (8 * i);
+  }
+  return out;
+}
+
+TX_KERNEL void __launch_bounds__(256) tx_gemm_mx_fp4_to_e4m3(const tx_pad_args a) {
+  const uint8_t *src = static_cast<const uint8_t *>(a.src);
+  uint8_t *dst = static_cast<uint8_t *>(a.dst);
+  const int64_t units_row = (int64_t(a.dst_cols) + 7) / 8;  // 8 destination bytes each
+  const int64_t total = int64_t(a.rows) * units_row;
+  const bool words = (reinterpret_cast<uintptr_t>(src) & 3) == 0 && (a.src_ld & 3) == 0;
+  for (int64_t u = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
+       u += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = u / units_row;
+    const int c = int(u - r * units_row) * 4;  // first source byte
+    const uint8_t *row = src + r * a.src_ld;
+    uint32_t v = 0;
+    if (words && c + 3 < a.cols) {
+      v = *reinterpret_cast<const uint32_t *>(row + c);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (c + k < a.cols) v |= uint32_t(row[c + k]) << (8 * k);
+    }
+    const txd::u32x2 o = {e2m1x4_to_e4m3(v & 0xFFFFu), e2m1x4_to_e4m3(v >> 16)};
+    // dst rows are whole 8-byte units (dst_ld and dst_cols multiples of 8)
+    *reinterpret_cast<txd::u32x2 *>(dst + r * a.dst_ld + 2 * c) = o;
+  }
+}
+
 // Scales of A and B into the step-major layout the tile reads (see
 // tx_mx_pack_args), through LDS: workgroup b of an operand transposes rows
 // 64 * (b % R) .. +63 (R = rows_pad / 64) for source dword columns

@@ -296,7 +296,7 @@ def dot_scaled(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Tensor,
     column-major K x N operand).  fp4 is packed two per byte with the even K
     index in the low nibble (triton's MXFP4Tensor.to_packed_tensor), given
     as float4_e2m1fn_x2 or as uint8 with ``a_format`` / ``b_format`` "e2m1";
-    both operands fp4 or both fp8.  scale_a: M x ceil(K/32), scale_b:
+    any pairing of fp4 and fp8 operands.  scale_a: M x ceil(K/32), scale_b:
     N x ceil(K/32), uint8 codes or float8_e8m0fnu."""
     _on_gpu(a_q, scale_a, b_q_nk, scale_b, out)
     if a_q.dim() != 2 or b_q_nk.dim() != 2:
