@@ -155,6 +155,43 @@ def bench_fp8_gemm_epilogue(tx, torch, M, N, K, steps, warmup, act, out_dtype, s
     return {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
 
 
+def bench_fp8_grouped(tx, torch, G, total, N, K, steps, warmup):
+    """Grouped fp8 scaled GEMM (mixture-of-experts layer): `total` routed
+    rows split unevenly over G experts (tx.workloads.moe_group_sizes), each
+    expert's N x K weights; one grouped launch, and the same products as a
+    loop of G plain calls for comparison.  Random finite e4m3fn codes."""
+    import numpy as np
+    from tx import workloads
+    dev = torch.device("cuda:0")
+    sizes = workloads.moe_group_sizes(total, G)
+    off_np = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+
+    def codes(*shape):
+        c = torch.randint(0, 127, shape, dtype=torch.uint8, device=dev, generator=gen)
+        return (c | (torch.randint(0, 2, shape, dtype=torch.uint8, device=dev, generator=gen) << 7)).view(
+            torch.float8_e4m3fn)
+
+    A, B = codes(total, K), codes(G, N, K)
+    sa = torch.rand(total, device=dev, generator=gen) + 0.5
+    sb = torch.rand(G, N, device=dev, generator=gen) + 0.5
+    off = torch.from_numpy(off_np).to(dev)
+    C = torch.empty((total, N), dtype=torch.bfloat16, device=dev)
+    ms = timed(lambda i: tx.dot_scaled_rowcol_grouped(A, sa, B, sb, off, out=C), steps, warmup)
+
+    def loop(i):
+        for p in range(G):
+            r0, r1 = int(off_np[p]), int(off_np[p + 1])
+            if r1 > r0:
+                tx.dot_scaled_rowcol(A[r0:r1], sa[r0:r1], B[p], sb[p], out=C[r0:r1])
+
+    ms_loop = timed(loop, steps, warmup)
+    flops = 2.0 * total * N * K
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "ms_loop": ms_loop,
+            "tflops_loop": flops / (ms_loop * 1e-3) / 1e12, "sizes": sizes.tolist()}
+
+
 def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2, fp4=False):
     """tt.dot_scaled with MX block scales (e8m0 per 32 K), bf16 out; e4m3fn
     operands, or fp4 (e2m1, two per byte) with ``fp4``."""
@@ -438,6 +475,13 @@ def main():
                               "ms": r["ms"], "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
             progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+        for (G, total, n, k) in [(8, 16384, 14336, 4096), (64, 8192, 2048, 4096)]:
+            r = bench_fp8_grouped(tx, torch, G, total, n, k, K, W)
+            secondary.append({"op": f"grouped fp8 scaled GEMM, {G} experts (one launch)",
+                              "shape": [total, n, k], "ms": r["ms"], "tflops": r["tflops"],
+                              "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
+                              "loop_of_plain_ms": r["ms_loop"], "group_rows": r["sizes"]})
+            progress(secondary[-1]["op"])
         r = bench_mx_gemm(tx, torch, 8192, 8192, 8192, K, W, fp4=True)
         secondary.append({"op": "MX-scaled fp4 GEMM (e2m1, e8m0 per 32 K)", "shape": [8192, 8192, 8192],
                           "ms": r["ms"], "tflops": r["tflops"], "frac_mfma": r["tflops"] / FP4_PEAK_TFLOPS})

@@ -301,6 +301,47 @@ TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t ld
                                       tx_stream_t stream);
 
 /*
+ * Grouped tx_dot_fp8_scaled (the grouped variant serving stacks call for
+ * mixture-of-experts layers): one launch computes, for every group p,
+ *   C[r, n] = bf16_rne(scale_a[r] * scale_b[p * stride_scale_b + n] *
+ *                      sum_k f32(A[r, k]) * f32(B_p[k, n]))
+ * for the rows r of A in group_offsets[p] .. group_offsets[p + 1], where
+ * B_p is the column-major N x K operand at B + p * stride_b bytes.  No
+ * reference kernel exists; each group's product is tx_dot_fp8_scaled's.
+ * group_offsets: groups + 1 int32 row offsets on the device, nondecreasing,
+ * within 0 .. M (M = rows of A and C in all; values outside are clamped);
+ * they are read by the device only, so the call never waits for them.
+ * A row-major (lda bytes), C row-major bf16 (ldc), scale_a M floats.
+ * Operands as the fast path reads them in place: A and B 16-byte aligned,
+ * lda, ldb, K and stride_b multiples of 16 (else TX_UNSUPPORTED).  Uses
+ * (groups + 1) x 4 bytes of the library's per-stream scratch.
+ */
+TX_API tx_status tx_dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64_t lda,
+                                           const float *scale_a, const void *B,
+                                           tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                           const float *scale_b, int64_t stride_scale_b,
+                                           void *C, int64_t ldc,
+                                           const int32_t *group_offsets, int64_t groups,
+                                           int64_t M, int64_t N, int64_t K,
+                                           tx_stream_t stream);
+
+/*
+ * Batched tx_dot_fp8_scaled: `batch` products of one shape in one launch,
+ * product p on A + p * stride_a bytes, scale_a + p * stride_scale_a,
+ * B + p * stride_b bytes, scale_b + p * stride_scale_b and C + p * stride_c
+ * elements (M x N each).  No reference kernel exists.  Alignment as
+ * tx_dot_fp8_scaled_grouped (stride_a too a multiple of 16).
+ */
+TX_API tx_status tx_dot_fp8_scaled_batched(const void *A, tx_dtype a_type, int64_t lda,
+                                           int64_t stride_a, const float *scale_a,
+                                           int64_t stride_scale_a, const void *B,
+                                           tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                           const float *scale_b, int64_t stride_scale_b,
+                                           void *C, int64_t ldc, int64_t stride_c,
+                                           int64_t batch, int64_t M, int64_t N, int64_t K,
+                                           tx_stream_t stream);
+
+/*
  * tt.dot_scaled with MX block scales (OCP Microscaling: one e8m0 scale per
  * 32 consecutive K elements of each row of A and each column of B), fp32
  * accumulation:

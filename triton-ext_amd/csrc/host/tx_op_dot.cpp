@@ -531,6 +531,75 @@ static tx_status dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda, cons
   return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, rname);
 }
 
+// Grouped (offsets != NULL) or batched fp8 scaled dot, bf16 out: the fast
+// tile over every (problem, tile) pair in one launch (tx_grouped_args).  The
+// group sizes stay on the device: a one-workgroup scan turns the offsets
+// into m-tile prefix sums (stream scratch slot 1), and the grid covers
+// ceil(M / 256) + groups m tiles, of which the ones past the last problem
+// exit at once.  Operands must be what the fast path reads in place
+// (16-byte aligned rows, K a multiple of 16 bytes).
+static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype a_type, int64_t lda,
+                                      int64_t stride_a, const float *sa, int64_t stride_sa,
+                                      const void *B, tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                      const float *sb, int64_t stride_sb, void *C, int64_t ldc,
+                                      int64_t stride_c, const int32_t *offsets, int64_t groups,
+                                      int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
+  if (!fa || !fb)
+    return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 (got %d, %d)", what, int(a_type),
+                int(b_type));
+  if (groups < 0) return fail(TX_INVALID_ARGUMENT, "%s: negative group count", what);
+  if (groups > INT32_MAX / 2) return fail(TX_UNSUPPORTED, "%s: too many groups", what);
+  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, K));
+  if (groups == 0 || M == 0 || N == 0) return TX_SUCCESS;
+  if (!sa || !sb) return fail(TX_INVALID_ARGUMENT, "%s: NULL scale vector", what);
+  if (!aligned(sa, 4) || !aligned(sb, 4))
+    return fail(TX_INVALID_ARGUMENT, "%s: scales must be 4-byte aligned", what);
+  const bool grouped = offsets != nullptr;
+  if (stride_b < 0 || stride_sb < 0 || (!grouped && (stride_a < 0 || stride_sa < 0 || stride_c < 0)))
+    return fail(TX_INVALID_ARGUMENT, "%s: negative stride", what);
+  if (K > 0 && (!aligned(A, 16) || !aligned(B, 16) || lda % 16 || ldb % 16 || K % 16 || stride_b % 16 ||
+                (!grouped && stride_a % 16)))
+    return fail(TX_UNSUPPORTED,
+                "%s: needs 16-byte aligned operand rows and problems (A, B, lda, ldb, K, strides)", what);
+  if ((M - 1) * lda + K >= (int64_t(1) << 31) || (N - 1) * ldb + K >= (int64_t(1) << 31))
+    return fail(TX_UNSUPPORTED, "%s: a problem's operands exceed 32-bit offsets", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t cus = cu_count();
+  const int64_t rt = (M + 255) / 256;
+  const int64_t mtiles = grouped ? rt + groups : groups * rt;
+  const bool big = (grouped ? rt : mtiles) * ((N + 255) / 256) >= cus;
+  const int64_t bn = big ? 256 : 128;
+  const int64_t tiles_n = (N + bn - 1) / bn;
+  if (mtiles * tiles_n > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: too many tiles", what);
+
+  tx_grouped_args q{};
+  q.g = tx_gemm_args{A, B, C, sa, sb, lda, ldb, ldc, int32_t(M), int32_t(N), int32_t(K),
+                     int32_t(mtiles), int32_t(tiles_n), int32_t(std::min<int64_t>(kGroupM, mtiles)), 1, 0,
+                     nullptr};
+  q.offsets = offsets;
+  q.stride_a = stride_a;
+  q.stride_sa = stride_sa;
+  q.stride_c = stride_c;
+  q.stride_b = stride_b;
+  q.stride_sb = stride_sb;
+  q.groups = int32_t(groups);
+  q.mtiles = int32_t(mtiles);
+  q.tiles_per = int32_t(rt);
+  ScratchLease pre;  // held until the product is enqueued
+  hipFunction_t fn;
+  if (grouped) {
+    TX_TRY(pre.acquire(s, 1, size_t(groups + 1) * sizeof(int32_t)));
+    q.tile_prefix = static_cast<int32_t *>(pre.ptr());
+    TX_TRY(get_kernel(CodeObject::GemmFp8, "tx_gemm_fp8_grouped_prefix", &fn));
+    TX_TRY(launch(fn, 1, 1, 256, s, &q, sizeof q, "tx_gemm_fp8_grouped_prefix"));
+  }
+  char kname[80];
+  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped%s", fa, fb, big ? "" : "_n128");
+  TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
+  return launch(fn, unsigned(mtiles * tiles_n), 1, 64 * kFastWaves, s, &q, sizeof q, kname);
+}
+
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,
                                   int64_t ldw, const float *scales, int64_t ld_scales,
                                   int64_t group, void *y, int64_t ldy, int64_t M, int64_t N,
@@ -618,6 +687,68 @@ static tx_status dot_fp8_op(tx_value *v, size_t count, tx_stream_t stream) {
   TX_TRY(o.integer(12, &bt));
   return dot_fp8_scaled(A, tx_dtype(at), lda, static_cast<const float *>(sa), B, tx_dtype(bt), ldb,
                         static_cast<const float *>(sb), C, ldc, M, N, K, stream);
+}
+
+// tx.dot_fp8_scaled_grouped: {C (result), A, B, scale_a, scale_b, offsets,
+// groups, M, N, K, lda, ldb, ldc, stride_b, stride_scale_b, a_type, b_type}
+static tx_status dot_fp8_grouped_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tx.dot_fp8_scaled_grouped"};
+  TX_TRY(o.need(17));
+  void *C, *A, *B, *sa, *sb, *off;
+  int64_t G, M, N, K, lda, ldb, ldc, stb, stsb, at, bt;
+  TX_TRY(o.ptr(0, &C));
+  TX_TRY(o.ptr(1, &A));
+  TX_TRY(o.ptr(2, &B));
+  TX_TRY(o.ptr(3, &sa));
+  TX_TRY(o.ptr(4, &sb));
+  TX_TRY(o.ptr(5, &off));
+  TX_TRY(o.integer(6, &G));
+  TX_TRY(o.integer(7, &M));
+  TX_TRY(o.integer(8, &N));
+  TX_TRY(o.integer(9, &K));
+  TX_TRY(o.integer(10, &lda));
+  TX_TRY(o.integer(11, &ldb));
+  TX_TRY(o.integer(12, &ldc));
+  TX_TRY(o.integer(13, &stb));
+  TX_TRY(o.integer(14, &stsb));
+  TX_TRY(o.integer(15, &at));
+  TX_TRY(o.integer(16, &bt));
+  if (!off) return fail(TX_INVALID_ARGUMENT, "tx.dot_fp8_scaled_grouped: NULL offsets");
+  return dot_fp8_grouped_impl("tx_dot_fp8_scaled_grouped", A, tx_dtype(at), lda, 0, static_cast<const float *>(sa),
+                              0, B, tx_dtype(bt), ldb, stb, static_cast<const float *>(sb), stsb, C, ldc, 0,
+                              static_cast<const int32_t *>(off), G, M, N, K, stream);
+}
+
+// tx.dot_fp8_scaled_batched: {C (result), A, B, scale_a, scale_b, batch, M,
+// N, K, lda, ldb, ldc, stride_a, stride_scale_a, stride_b, stride_scale_b,
+// stride_c, a_type, b_type}
+static tx_status dot_fp8_batched_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tx.dot_fp8_scaled_batched"};
+  TX_TRY(o.need(19));
+  void *C, *A, *B, *sa, *sb;
+  int64_t G, M, N, K, lda, ldb, ldc, sta, stsa, stb, stsb, stc, at, bt;
+  TX_TRY(o.ptr(0, &C));
+  TX_TRY(o.ptr(1, &A));
+  TX_TRY(o.ptr(2, &B));
+  TX_TRY(o.ptr(3, &sa));
+  TX_TRY(o.ptr(4, &sb));
+  TX_TRY(o.integer(5, &G));
+  TX_TRY(o.integer(6, &M));
+  TX_TRY(o.integer(7, &N));
+  TX_TRY(o.integer(8, &K));
+  TX_TRY(o.integer(9, &lda));
+  TX_TRY(o.integer(10, &ldb));
+  TX_TRY(o.integer(11, &ldc));
+  TX_TRY(o.integer(12, &sta));
+  TX_TRY(o.integer(13, &stsa));
+  TX_TRY(o.integer(14, &stb));
+  TX_TRY(o.integer(15, &stsb));
+  TX_TRY(o.integer(16, &stc));
+  TX_TRY(o.integer(17, &at));
+  TX_TRY(o.integer(18, &bt));
+  return dot_fp8_grouped_impl("tx_dot_fp8_scaled_batched", A, tx_dtype(at), lda, sta,
+                              static_cast<const float *>(sa), stsa, B, tx_dtype(bt), ldb, stb,
+                              static_cast<const float *>(sb), stsb, C, ldc, stc, nullptr, G, M, N, K, stream);
 }
 
 // tx.gemv_fp8_dequant: {y (result), x, W, scales, M, N, K, group, ldx, ldw,
@@ -720,6 +851,16 @@ static const bool reg_dot_mx = register_op(
     "C:bf16|f16|f32*(result), A:fp8|fp4x2*, B:fp8|fp4x2* (N x K), scale_a:e8m0* (M x ceil(K/32)), "
     "scale_b:e8m0* (N x ceil(K/32)), M, N, K, lda, ldb, ldc, ld_scale_a, ld_scale_b, a_type:i32, "
     "b_type:i32, c_type:i32");
+static const bool reg_dot_fp8_grouped = register_op(
+    "tx.dot_fp8_scaled_grouped", dot_fp8_grouped_op,
+    "C:bf16*(result, M x N), A:fp8* (M x K), B:fp8* (groups x N x K), scale_a:f32* (M), "
+    "scale_b:f32* (groups x N), offsets:i32* (groups + 1 rows of A), groups, M, N, K, lda, ldb, ldc, "
+    "stride_b, stride_scale_b, a_type:i32, b_type:i32");
+static const bool reg_dot_fp8_batched = register_op(
+    "tx.dot_fp8_scaled_batched", dot_fp8_batched_op,
+    "C:bf16*(result, batch x M x N), A:fp8*, B:fp8* (N x K each), scale_a:f32*, scale_b:f32*, batch, "
+    "M, N, K, lda, ldb, ldc, stride_a, stride_scale_a, stride_b, stride_scale_b, stride_c, a_type:i32, "
+    "b_type:i32");
 static const bool reg_gemv = register_op(
     "tx.gemv_fp8_dequant", gemv_op,
     "y:bf16*(result), x:bf16*, W:fp8* (N x K), scales:f32* (N x K/group), M, N, K, group, ldx, "
@@ -753,6 +894,32 @@ TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t ld
   tx::clear_error();
   return tx::dot_fp8_scaled_ex(A, a_type, lda, scale_a, B, b_type, ldb, scale_b, bias, activation,
                                C, c_type, c_scale, ldc, M, N, K, stream);
+}
+
+TX_API tx_status tx_dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64_t lda,
+                                           const float *scale_a, const void *B, tx_dtype b_type,
+                                           int64_t ldb, int64_t stride_b, const float *scale_b,
+                                           int64_t stride_scale_b, void *C, int64_t ldc,
+                                           const int32_t *group_offsets, int64_t groups, int64_t M,
+                                           int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  if (!group_offsets && groups > 0 && M > 0 && N > 0)
+    return tx::fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled_grouped: NULL group offsets");
+  return tx::dot_fp8_grouped_impl("tx_dot_fp8_scaled_grouped", A, a_type, lda, 0, scale_a, 0, B, b_type,
+                                  ldb, stride_b, scale_b, stride_scale_b, C, ldc, 0, group_offsets, groups,
+                                  M, N, K, stream);
+}
+
+TX_API tx_status tx_dot_fp8_scaled_batched(const void *A, tx_dtype a_type, int64_t lda, int64_t stride_a,
+                                           const float *scale_a, int64_t stride_scale_a, const void *B,
+                                           tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                           const float *scale_b, int64_t stride_scale_b, void *C,
+                                           int64_t ldc, int64_t stride_c, int64_t batch, int64_t M,
+                                           int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot_fp8_grouped_impl("tx_dot_fp8_scaled_batched", A, a_type, lda, stride_a, scale_a,
+                                  stride_scale_a, B, b_type, ldb, stride_b, scale_b, stride_scale_b, C, ldc,
+                                  stride_c, nullptr, batch, M, N, K, stream);
 }
 
 TX_API tx_status tx_dot_scaled_mx(const void *A, tx_dtype a_type, int64_t lda,

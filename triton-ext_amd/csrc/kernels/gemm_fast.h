@@ -156,8 +156,10 @@ __device__ __forceinline__ void wait_and_barrier() {
 // Output element types of the fast tile.
 enum FastOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
 
+// The tile (tm, tn) of C (256 x BN elements at row 256 tm, column BN tn),
+// split `split` of a.splits along K.
 template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16, bool EPI = false>
-__device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
+__device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm, int tn, int split) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
   static_assert(NW == 8 || NW == 4, "8 or 4 wavefronts");
@@ -185,11 +187,7 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   static_assert(BLKA % 2 == 0 && BLKB % 2 == 0, "a wave's first block must have an even index");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
-  // Split K: workgroup b computes split b % splits of tile b / splits.
   const int splits = a.splits > 1 ? a.splits : 1;
-  const int split = int(blockIdx.x) % splits;
-  int tm, tn;
-  tile_coords(int(blockIdx.x) / splits, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
   const int m0 = tm * 256, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps LDS addresses scalar
@@ -580,6 +578,16 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 // Split-K reduction: C[m, n] = out(scale_a[m] * scale_b[n] * sum_s P[s][m][n])
 // (ROWCOL: the fp8 row / column scales; out: bf16 or fp16 round to nearest
 // even, or fp32), four consecutive n per thread.
+// One workgroup per tile of a single product: with K split, workgroup b
+// computes split b % splits of tile b / splits.
+template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16, bool EPI = false>
+__device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
+  const int splits = a.splits > 1 ? a.splits : 1;
+  int tm, tn;
+  tile_coords(int(blockIdx.x) / splits, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
+  gemm_fast_tile_at<C, BN, NW, MX, OUT, EPI>(a, tm, tn, int(blockIdx.x) % splits);
+}
+
 template <bool ROWCOL, int OUT = OUT_BF16>
 __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
   const int64_t quads_per_row = (a.N + 3) / 4;

@@ -91,3 +91,86 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_epilogue(const tx_gemm_args a)
     epi_store1(a, m, n, epi_value(a, a.part[t], n));
   }
 }
+
+// ---------------------------------------------------------------------------
+// Grouped / batched fp8 GEMM (see tx_grouped_args): the fast tile, one
+// workgroup per (problem, tile), no K split.
+//
+// Tile prefix of a grouped product: one workgroup scans the groups' m-tile
+// counts ceil(rows / 256) in chunks of 256 (rows from the clamped offsets).
+TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_grouped_prefix(const tx_grouped_args q) {
+  __shared__ int sc[256];
+  const int t = threadIdx.x;
+  const int total = q.g.M;
+  int carry = 0;
+  if (t == 0) q.tile_prefix[0] = 0;
+  for (int base = 0; base < q.groups; base += 256) {
+    const int p = base + t;
+    int c = 0;
+    if (p < q.groups) {
+      const int r1 = min(max(q.offsets[p + 1], 0), total);
+      const int r0 = min(max(q.offsets[p], 0), r1);
+      c = (r1 - r0 + 255) / 256;
+    }
+    sc[t] = c;
+    __syncthreads();
+    for (int d = 1; d < 256; d *= 2) {  // inclusive scan
+      const int v = t >= d ? sc[t - d] : 0;
+      __syncthreads();
+      sc[t] += v;
+      __syncthreads();
+    }
+    if (p < q.groups) q.tile_prefix[p + 1] = carry + sc[t];
+    carry += sc[255];
+    __syncthreads();
+  }
+}
+
+template <class C, int BN>
+__device__ __forceinline__ void gemm_fp8_grouped(const tx_grouped_args &q) {
+  int vm, tn;
+  tile_coords(int(blockIdx.x), q.mtiles, q.g.tiles_n, q.g.group_m, &vm, &tn);
+  tx_gemm_args a = q.g;
+  int p, tm;
+  if (q.offsets) {
+    const int32_t *T = q.tile_prefix;
+    if (vm >= T[q.groups]) return;  // uniform: the whole workgroup leaves
+    int lo = 0, hi = q.groups - 1;  // the last problem p with T[p] <= vm
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (T[mid] <= vm) lo = mid;
+      else hi = mid - 1;
+    }
+    p = lo;
+    tm = vm - T[p];
+    const int r1 = min(max(q.offsets[p + 1], 0), q.g.M);
+    const int r0 = min(max(q.offsets[p], 0), r1);
+    a.M = r1 - r0;
+    a.A = static_cast<const uint8_t *>(q.g.A) + int64_t(r0) * q.g.lda;
+    a.C = static_cast<uint16_t *>(q.g.C) + int64_t(r0) * q.g.ldc;
+    a.scale_a = q.g.scale_a + r0;
+  } else {
+    p = vm / q.tiles_per;
+    tm = vm - p * q.tiles_per;
+    if (p >= q.groups) return;
+    a.A = static_cast<const uint8_t *>(q.g.A) + int64_t(p) * q.stride_a;
+    a.C = static_cast<uint16_t *>(q.g.C) + int64_t(p) * q.stride_c;
+    a.scale_a = q.g.scale_a + int64_t(p) * q.stride_sa;
+  }
+  a.B = static_cast<const uint8_t *>(q.g.B) + int64_t(p) * q.stride_b;
+  a.scale_b = q.g.scale_b + int64_t(p) * q.stride_sb;
+  gemm_fast_tile_at<C, BN>(a, tm, tn, 0);
+}
+
+#define TX_GEMM_FP8_GROUPED(FA, FB, ELA, ELB)                                                    \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped(const tx_grouped_args q) { \
+    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256>(q);                              \
+  }                                                                                              \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_n128(const tx_grouped_args q) { \
+    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128>(q);                              \
+  }
+
+TX_GEMM_FP8_GROUPED(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
+TX_GEMM_FP8_GROUPED(e5m2, e5m2, EL_E5M2, EL_E5M2)
+TX_GEMM_FP8_GROUPED(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
+TX_GEMM_FP8_GROUPED(e5m2, e4m3fn, EL_E5M2, EL_E4M3)

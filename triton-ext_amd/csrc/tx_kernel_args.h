@@ -71,9 +71,10 @@ typedef struct tx_gemm_args {
   int32_t ksteps_split; /* fast path: 128-byte K steps per split */
   float *part;       /* fast path with splits > 1: splits x M x N fp32 partial sums */
   /* MX-scaled dot: e8m0 block scales (one byte per 32 K elements), packed
-   * step-major: the 4 scales of row r for 128-element K step s (blocks
-   * 4s .. 4s+3, low byte first) are the dword at byte s * ld_mx* + 4r, for
-   * every row of every tile (rows past M / N hold finite codes). */
+   * step-major: the scales of row r for 128-byte K step s are sd dwords
+   * (low byte first) at byte s * ld_mx* + 4 sd r: blocks 4s .. 4s+3 for fp8
+   * (sd = 1), 8s .. 8s+7 for fp4 (sd = 2), for every row of every tile (rows
+   * past M / N hold finite codes). */
   const uint8_t *mx_a;
   const uint8_t *mx_b;
   int64_t ld_mxa;
@@ -87,6 +88,31 @@ typedef struct tx_gemm_args {
   float out_mul;
   int32_t epi;
 } tx_gemm_args;
+
+/* Grouped / batched fp8 GEMM (row/column scales, bf16 out) over the fast
+ * tile.  g holds the shared fields (B, C, scales, strides, N, K, tiles_n,
+ * group_m; A and C at problem 0).  Grouped (offsets != NULL): problem p is
+ * rows offsets[p] .. offsets[p + 1] of A, C and scale_a (g.M = the rows of
+ * A in all; offsets are clamped to 0 .. g.M), against B + p * stride_b and
+ * scale_b + p * stride_sb; tile_prefix[p] = sum over q < p of
+ * ceil(rows_q / 256) (written by tx_gemm_fp8_grouped_prefix).  Batched
+ * (offsets == NULL): problem p is g.M rows at A + p * stride_a (elements),
+ * scale_a + p * stride_sa, C + p * stride_c.  The grid covers mtiles x
+ * tiles_n tiles; m tiles past the last problem's exit at once. */
+typedef struct tx_grouped_args {
+  tx_gemm_args g;
+  const int32_t *offsets;
+  int32_t *tile_prefix;
+  int64_t stride_a;
+  int64_t stride_sa;
+  int64_t stride_c;
+  int64_t stride_b;
+  int64_t stride_sb;
+  int32_t groups;
+  int32_t mtiles;       /* m tiles the grid covers */
+  int32_t tiles_per;    /* batched: ceil(g.M / 256) */
+  int32_t reserved;
+} tx_grouped_args;
 
 enum { EPI_ACT_NONE = 0, EPI_ACT_RELU = 1, EPI_ACT_GELU_TANH = 2, EPI_ACT_SILU = 3 };
 enum { EPI_OUT_BF16 = 0, EPI_OUT_F16 = 1, EPI_OUT_F32 = 2, EPI_OUT_E4M3FN = 3, EPI_OUT_E5M2 = 4 };

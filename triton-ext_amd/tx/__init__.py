@@ -27,7 +27,7 @@ from ._lib import TxError, check, lib
 
 __all__ = [
     "TxError", "fp_to_fp", "stoch_round", "atomic_rmw", "dot", "matmul", "dot_scaled_rowcol",
-    "dot_scaled", "quantize_mx", "quantize_rowwise",
+    "dot_scaled_rowcol_grouped", "dot_scaled_rowcol_batched", "dot_scaled", "quantize_mx", "quantize_rowwise",
     "gemv_fp8_dequant", "plugin_info", "invoke", "get_fp8_format_name",
     "version", "init", "RTNE", "RTZ", "RS",
 ]
@@ -229,6 +229,71 @@ def dot_scaled_rowcol(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_nk: torch.Te
     check(lib.tx_dot_fp8_scaled(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
                                 _ptr(b_q_nk), _TX_DTYPE[b_q_nk.dtype], b_q_nk.stride(0),
                                 _ptr(scale_b), _ptr(out), out.stride(0), M, N, K, _stream(a_q)))
+    return out
+
+
+def _fp8_checks(*ts):
+    for t in ts:
+        if t.dtype not in _FP8:
+            raise ValueError("fp8 operands expected")
+        if t.stride(-1) != 1:
+            raise ValueError("operands must be K-contiguous")
+
+
+def dot_scaled_rowcol_grouped(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_gnk: torch.Tensor,
+                              scale_b: torch.Tensor, group_offsets: torch.Tensor,
+                              out: torch.Tensor | None = None) -> torch.Tensor:
+    """Grouped fp8 dot with row/column scales (mixture-of-experts layers):
+    rows group_offsets[p] .. group_offsets[p+1] of a_q (M x K) against
+    expert p's b_q_gnk[p] (N x K, the column-major K x N operand), scaled by
+    scale_a[r] and scale_b[p, n], bf16 out (M x N).  group_offsets: int32 on
+    the device, G + 1 nondecreasing row offsets within 0 .. M; the group
+    sizes are never read back to the host."""
+    _on_gpu(a_q, scale_a, b_q_gnk, scale_b, group_offsets, out)
+    _fp8_checks(a_q, b_q_gnk)
+    if a_q.dim() != 2 or b_q_gnk.dim() != 3 or a_q.shape[1] != b_q_gnk.shape[2]:
+        raise ValueError("a_q must be M x K and b_q_gnk G x N x K")
+    M, K = a_q.shape
+    G, N = b_q_gnk.shape[0], b_q_gnk.shape[1]
+    if group_offsets.dtype != torch.int32 or group_offsets.numel() != G + 1 or not group_offsets.is_contiguous():
+        raise ValueError("group_offsets must be G + 1 contiguous int32 values")
+    if scale_a.dtype != torch.float32 or scale_a.numel() != M or not scale_a.is_contiguous() or \
+            scale_b.dtype != torch.float32 or tuple(scale_b.shape) != (G, N) or scale_b.stride(1) != 1:
+        raise ValueError("scale_a must be fp32[M] and scale_b fp32[G, N]")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a_q.device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major bf16 M x N tensor")
+    check(lib.tx_dot_fp8_scaled_grouped(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
+                                        _ptr(b_q_gnk), _TX_DTYPE[b_q_gnk.dtype], b_q_gnk.stride(1),
+                                        b_q_gnk.stride(0), _ptr(scale_b), scale_b.stride(0), _ptr(out),
+                                        out.stride(0), _ptr(group_offsets), G, M, N, K, _stream(a_q)))
+    return out
+
+
+def dot_scaled_rowcol_batched(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_bnk: torch.Tensor,
+                              scale_b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Batched fp8 dot with row/column scales: out[p] = bf16(scale_a[p][:,None]
+    * scale_b[p][None,:] * (a_q[p] @ b_q_bnk[p].T)) for a_q B x M x K,
+    b_q_bnk B x N x K, scale_a B x M, scale_b B x N (any batch strides)."""
+    _on_gpu(a_q, scale_a, b_q_bnk, scale_b, out)
+    _fp8_checks(a_q, b_q_bnk)
+    if a_q.dim() != 3 or b_q_bnk.dim() != 3 or a_q.shape[0] != b_q_bnk.shape[0] or a_q.shape[2] != b_q_bnk.shape[2]:
+        raise ValueError("a_q must be B x M x K and b_q_bnk B x N x K")
+    Bt, M, K = a_q.shape
+    N = b_q_bnk.shape[1]
+    if scale_a.dtype != torch.float32 or tuple(scale_a.shape) != (Bt, M) or scale_a.stride(1) != 1 or \
+            scale_b.dtype != torch.float32 or tuple(scale_b.shape) != (Bt, N) or scale_b.stride(1) != 1:
+        raise ValueError("scales must be fp32 B x M and B x N")
+    if out is None:
+        out = torch.empty((Bt, M, N), dtype=torch.bfloat16, device=a_q.device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (Bt, M, N) or out.stride(2) != 1:
+        raise ValueError("out must be a bf16 B x M x N tensor with unit column stride")
+    check(lib.tx_dot_fp8_scaled_batched(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(1), a_q.stride(0),
+                                        _ptr(scale_a), scale_a.stride(0), _ptr(b_q_bnk),
+                                        _TX_DTYPE[b_q_bnk.dtype], b_q_bnk.stride(1), b_q_bnk.stride(0),
+                                        _ptr(scale_b), scale_b.stride(0), _ptr(out), out.stride(1),
+                                        out.stride(0), Bt, M, N, K, _stream(a_q)))
     return out
 
 

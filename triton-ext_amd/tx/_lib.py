@@ -41,7 +41,8 @@ EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
-    "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
+    "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped", "tx_dot_fp8_scaled_batched",
+    "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
     "tx_gemv_fp8_dequant",
 ]
 
@@ -124,6 +125,12 @@ def _load():
     L.tx_dot_fp8_scaled_ex.argtypes = [P, I, I64, P, P, I, I64, P, P, I, P, I, ctypes.c_float,
                                        I64, I64, I64, I64, VP]
     L.tx_dot_fp8_scaled_ex.restype = I
+    L.tx_dot_fp8_scaled_grouped.argtypes = [P, I, I64, P, P, I, I64, I64, P, I64, P, I64, P, I64, I64, I64,
+                                            I64, P]
+    L.tx_dot_fp8_scaled_grouped.restype = I
+    L.tx_dot_fp8_scaled_batched.argtypes = [P, I, I64, I64, P, I64, P, I, I64, I64, P, I64, P, I64, I64, I64,
+                                            I64, I64, I64, P]
+    L.tx_dot_fp8_scaled_batched.restype = I
     L.tx_dot_scaled_mx.argtypes = [P, I, I64, P, I64, P, I, I64, P, I64, P, I, I64, I64, I64, I64, VP]
     L.tx_dot_scaled_mx.restype = I
     L.tx_quantize_mx.argtypes = [P, I, I64, P, I, I64, P, I64, I64, I64, VP]

@@ -205,3 +205,13 @@ def mx_gemm_input(M: int, N: int, K: int, seed_stream: int = 0, fa: str = "e4m3f
     aq, sa = quant_mx(g.standard_normal((M, K), dtype=np.float32), fa)
     bq, sb = quant_mx(g.standard_normal((N, K), dtype=np.float32), fb)
     return aq, sa, bq, sb
+
+
+# ----------------------------------------------------- grouped (MoE) fp8 GEMM
+def moe_group_sizes(total: int, groups: int, seed_stream: int = 0) -> np.ndarray:
+    """Rows per expert for `total` routed rows: a multinomial draw with
+    expert weights proportional to 1 / (i + 1)^0.8 (a skewed router), so
+    groups are uneven and rarely multiples of the 256-row tile."""
+    g = rng(7, seed_stream)
+    w = 1.0 / np.arange(1, groups + 1) ** 0.8
+    return g.multinomial(total, w / w.sum()).astype(np.int64)
