@@ -301,17 +301,21 @@ TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t ld
                                       tx_stream_t stream);
 
 /*
- * Grouped tx_dot_fp8_scaled (the grouped variant serving stacks call for
+ * Grouped tx_dot_fp8_scaled_ex (the grouped variant serving stacks call for
  * mixture-of-experts layers): one launch computes, for every group p,
- *   C[r, n] = bf16_rne(scale_a[r] * scale_b[p * stride_scale_b + n] *
- *                      sum_k f32(A[r, k]) * f32(B_p[k, n]))
+ *   y[r, n] = act(scale_a[r] * scale_b[p * stride_scale_b + n] *
+ *                 sum_k f32(A[r, k]) * f32(B_p[k, n]) + bias[p * stride_bias + n])
  * for the rows r of A in group_offsets[p] .. group_offsets[p + 1], where
- * B_p is the column-major N x K operand at B + p * stride_b bytes.  No
- * reference kernel exists; each group's product is tx_dot_fp8_scaled's.
+ * B_p is the column-major N x K operand at B + p * stride_b bytes, and
+ * writes C[r, n] as tx_dot_fp8_scaled_ex does (c_type bf16 / fp16 / fp32,
+ * or fp8 of y / c_scale; bias may be NULL, activation a tx_activation; with
+ * no bias, no activation and bf16 it is tx_dot_fp8_scaled per group).  No
+ * reference kernel exists.
  * group_offsets: groups + 1 int32 row offsets on the device, nondecreasing,
  * within 0 .. M (M = rows of A and C in all; values outside are clamped);
  * they are read by the device only, so the call never waits for them.
- * A row-major (lda bytes), C row-major bf16 (ldc), scale_a M floats.
+ * A row-major (lda bytes), C row-major (ldc elements of c_type), scale_a M
+ * floats.
  * Operands as the fast path reads them in place: A and B 16-byte aligned,
  * lda, ldb, K and stride_b multiples of 16 (else TX_UNSUPPORTED).  Uses
  * (groups + 1) x 4 bytes of the library's per-stream scratch.
@@ -320,7 +324,9 @@ TX_API tx_status tx_dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64
                                            const float *scale_a, const void *B,
                                            tx_dtype b_type, int64_t ldb, int64_t stride_b,
                                            const float *scale_b, int64_t stride_scale_b,
-                                           void *C, int64_t ldc,
+                                           const float *bias, int64_t stride_bias,
+                                           int activation, void *C, tx_dtype c_type,
+                                           float c_scale, int64_t ldc,
                                            const int32_t *group_offsets, int64_t groups,
                                            int64_t M, int64_t N, int64_t K,
                                            tx_stream_t stream);

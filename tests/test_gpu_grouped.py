@@ -14,6 +14,7 @@ from test_gpu_gemm import FP8_TOL, check_close, sample_rows
 pytestmark = pytest.mark.gpu
 
 TD = {1: torch.float8_e4m3fn, 2: torch.float8_e5m2}
+ONE = 0x3F800000   # 1.0f as an fp32 bit pattern (the table ops' c_scale operand)
 
 
 def _codes(g, shape, fmt):
@@ -129,8 +130,8 @@ def test_grouped_table_ops_and_errors(tx, oracle, dev):
     SA, SB = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
     O = torch.from_numpy(off).to(dev)
     C = torch.empty((M, 64), dtype=torch.bfloat16, device=dev)
-    tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, O, 2, M, 64, 128, 128, 128, 64, 64 * 128, 64,
-                                            _lib.FP8E4M3FN, _lib.FP8E4M3FN])
+    tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, O, None, 2, M, 64, 128, 128, 128, 64, 64 * 128, 64,
+                                            0, _lib.FP8E4M3FN, _lib.FP8E4M3FN, _lib.BF16, 0, ONE])
     C2 = torch.empty((2, 64, 64), dtype=torch.bfloat16, device=dev)
     tx.invoke("tx.dot_fp8_scaled_batched", [C2, A, B, SA, SB, 2, 64, 64, 128, 128, 128, 64, 64 * 128, 64,
                                             64 * 128, 64, 64 * 64, _lib.FP8E4M3FN, _lib.FP8E4M3FN])
@@ -143,10 +144,66 @@ def test_grouped_table_ops_and_errors(tx, oracle, dev):
         r32, r16 = oracle.gemm_fp8_scaled_rows(aq[64 * p:64 * p + 64], bq[p], sa[64 * p:64 * p + 64], sb[p], 0, 64)
         check_close(_bits(C2[p]), r32, r16, FP8_TOL)
     with pytest.raises(tx.TxError):   # K not a multiple of 16 bytes
-        tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, O, 2, M, 64, 120, 128, 128, 64, 64 * 128, 64,
-                                                _lib.FP8E4M3FN, _lib.FP8E4M3FN])
+        tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, O, None, 2, M, 64, 120, 128, 128, 64, 64 * 128,
+                                                64, 0, _lib.FP8E4M3FN, _lib.FP8E4M3FN, _lib.BF16, 0, ONE])
     with pytest.raises(tx.TxError):   # NULL offsets
-        tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, None, 2, M, 64, 128, 128, 128, 64, 64 * 128, 64,
-                                                _lib.FP8E4M3FN, _lib.FP8E4M3FN])
+        tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, None, None, 2, M, 64, 128, 128, 128, 64,
+                                                64 * 128, 64, 0, _lib.FP8E4M3FN, _lib.FP8E4M3FN, _lib.BF16, 0, ONE])
+    with pytest.raises(tx.TxError):   # unknown activation
+        tx.invoke("tx.dot_fp8_scaled_grouped", [C, A, B, SA, SB, O, None, 2, M, 64, 128, 128, 128, 64, 64 * 128,
+                                                64, 0, _lib.FP8E4M3FN, _lib.FP8E4M3FN, _lib.BF16, 9, ONE])
     with pytest.raises(ValueError):   # offsets of the wrong length
         tx.dot_scaled_rowcol_grouped(A.view(TD[1]), SA, B.view(TD[1]), SB, O[:2])
+
+
+EPI_OUT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32, "e4m3fn": torch.float8_e4m3fn,
+           "e5m2": torch.float8_e5m2}
+EPI_REL = {"f32": 2.0 ** -23, "bf16": 2.0 ** -8, "f16": 2.0 ** -11, "e4m3fn": 2.0 ** -3, "e5m2": 2.0 ** -2}
+EPI_ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "silu": 3}
+
+
+@pytest.mark.parametrize("sizes,N,K,act,out,with_bias", [
+    ([300, 0, 17, 1024, 255], 384, 512, "silu", "bf16", True),
+    ([300, 0, 17, 1024, 255], 384, 512, "gelu_tanh", "e4m3fn", True),
+    ([1024] * 8, 2048, 512, "relu", "f32", True),
+    ([640, 5, 700], 1000, 256, "none", "e5m2", False),
+    ([129, 64], 96, 128, "gelu_tanh", "f16", True)])
+def test_grouped_fused_epilogue(tx, oracle, dev, sizes, N, K, act, out, with_bias):
+    """Per-expert bias, activation and output cast fused into the grouped
+    product (256x256 and 256x128 tiles), against the oracle's fp64 sums of
+    each group through the epilogue in float64: the fp8 GEMM bar plus, per
+    element, 5e-3 of the output scale and the output type's rounding.
+    Operands are absmax-quantised N(0,1) values (the fp8 GEMM workload), so
+    outputs are O(1) and fp32 accumulation error stays far below the bound;
+    raw random codes make near-cancelling sums of 1e5-sized terms whose fp32
+    error the bound, relative to the saturated output scale, cannot hold."""
+    from tx import workloads
+    g = np.random.default_rng(sum(sizes) + N + EPI_ACT[act])
+    M = sum(sizes)
+    off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    aq, sa, bq, sb = workloads.fp8_gemm_input(M, len(sizes) * N, K, seed_stream=M + N)
+    bq = bq.reshape(len(sizes), N, K)
+    sb = sb.reshape(len(sizes), N)
+    bias = (g.standard_normal((len(sizes), N)) * 3).astype(np.float32) if with_bias else None
+    out_scale = 0.25 if out in ("e4m3fn", "e5m2") else 1.0
+    C = tx.dot_scaled_rowcol_grouped(
+        torch.from_numpy(aq).to(dev).view(TD[1]), torch.from_numpy(sa).to(dev),
+        torch.from_numpy(bq).to(dev).view(TD[1]), torch.from_numpy(sb).to(dev), torch.from_numpy(off).to(dev),
+        bias=None if bias is None else torch.from_numpy(bias).to(dev), activation=act, out_dtype=EPI_OUT[out],
+        out_scale=out_scale)
+    torch.cuda.synchronize()
+    got = C.float().cpu().numpy().astype(np.float64) * (out_scale if out in ("e4m3fn", "e5m2") else 1.0)
+    fmax = {"e4m3fn": 448.0, "e5m2": 57344.0}.get(out)
+    for p in range(len(sizes)):
+        r0, r1 = int(off[p]), int(off[p + 1])
+        if r1 == r0:
+            continue
+        acc, _ = oracle.gemm_fp8_scaled_rows(aq[r0:r1], bq[p], sa[r0:r1], sb[p], 0, r1 - r0)
+        ref = oracle.gemm_fp8_epilogue(acc, None if bias is None else bias[p], EPI_ACT[act])
+        if fmax is not None:
+            ref = np.clip(ref, -fmax * out_scale, fmax * out_scale)
+        gg = got[r0:r1]
+        scale = np.abs(ref).max()
+        assert np.abs(gg - ref).max() <= (2e-2 + EPI_REL[out]) * scale
+        bad = np.abs(gg - ref) > 5e-3 * scale + EPI_REL[out] * np.abs(ref)
+        assert not bad.any(), (p, int(bad.sum()), gg[bad][:4], ref[bad][:4])

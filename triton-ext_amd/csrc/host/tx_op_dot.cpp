@@ -336,6 +336,33 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
                       Epilogue{}, stream);
 }
 
+// The fused epilogue's options (bias, tx_activation, output type and, for
+// fp8 outputs, the scale the output is divided by) into an Epilogue; *es =
+// bytes per output element.
+tx_status make_epilogue(const char *what, const float *bias, int activation, tx_dtype c_type,
+                        float c_scale, Epilogue *e, size_t *es) {
+  e->bias = bias;
+  if (activation < TX_ACT_NONE || activation > TX_ACT_SILU)
+    return fail(TX_INVALID_ARGUMENT, "%s: unknown activation %d", what, activation);
+  e->act = activation;
+  switch (c_type) {
+    case TX_BF16: e->out_kind = EPI_OUT_BF16; *es = 2; break;
+    case TX_F16: e->out_kind = EPI_OUT_F16; *es = 2; break;
+    case TX_F32: e->out_kind = EPI_OUT_F32; *es = 4; break;
+    case TX_FP8E4M3FN: e->out_kind = EPI_OUT_E4M3FN; *es = 1; break;
+    case TX_FP8E5M2: e->out_kind = EPI_OUT_E5M2; *es = 1; break;
+    default:
+      return fail(TX_INVALID_ARGUMENT, "%s: output type must be bf16, fp16, fp32 or fp8 (got %d)", what,
+                  int(c_type));
+  }
+  if (*es == 1) {
+    if (!(c_scale > 0.0f) || !std::isfinite(c_scale))
+      return fail(TX_INVALID_ARGUMENT, "%s: fp8 output needs a positive finite c_scale", what);
+    e->out_mul = 1.0f / c_scale;
+  }
+  return TX_SUCCESS;
+}
+
 static tx_status dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
                                    const void *B, tx_dtype b_type, int64_t ldb, const float *sb,
                                    const float *bias, int activation, void *C, tx_dtype c_type,
@@ -343,26 +370,8 @@ static tx_status dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t lda, 
                                    tx_stream_t stream) {
   const char *what = "tx_dot_fp8_scaled_ex";
   Epilogue e;
-  e.bias = bias;
-  if (activation < TX_ACT_NONE || activation > TX_ACT_SILU)
-    return fail(TX_INVALID_ARGUMENT, "%s: unknown activation %d", what, activation);
-  e.act = activation;
   size_t es;
-  switch (c_type) {
-    case TX_BF16: e.out_kind = EPI_OUT_BF16; es = 2; break;
-    case TX_F16: e.out_kind = EPI_OUT_F16; es = 2; break;
-    case TX_F32: e.out_kind = EPI_OUT_F32; es = 4; break;
-    case TX_FP8E4M3FN: e.out_kind = EPI_OUT_E4M3FN; es = 1; break;
-    case TX_FP8E5M2: e.out_kind = EPI_OUT_E5M2; es = 1; break;
-    default:
-      return fail(TX_INVALID_ARGUMENT, "%s: output type must be bf16, fp16, fp32 or fp8 (got %d)", what,
-                  int(c_type));
-  }
-  if (es == 1) {
-    if (!(c_scale > 0.0f) || !std::isfinite(c_scale))
-      return fail(TX_INVALID_ARGUMENT, "%s: fp8 output needs a positive finite c_scale", what);
-    e.out_mul = 1.0f / c_scale;
-  }
+  TX_TRY(make_epilogue(what, bias, activation, c_type, c_scale, &e, &es));
   return dot_fp8_impl(what, A, a_type, lda, sa, B, b_type, ldb, sb, C, ldc, M, N, K, e, stream);
 }
 
@@ -543,16 +552,20 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
                                       const void *B, tx_dtype b_type, int64_t ldb, int64_t stride_b,
                                       const float *sb, int64_t stride_sb, void *C, int64_t ldc,
                                       int64_t stride_c, const int32_t *offsets, int64_t groups,
-                                      int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+                                      int64_t M, int64_t N, int64_t K, tx_stream_t stream,
+                                      const Epilogue &e = Epilogue{}, size_t es = 2,
+                                      int64_t stride_bias = 0) {
   const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
   if (!fa || !fb)
     return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 (got %d, %d)", what, int(a_type),
                 int(b_type));
   if (groups < 0) return fail(TX_INVALID_ARGUMENT, "%s: negative group count", what);
   if (groups > INT32_MAX / 2) return fail(TX_UNSUPPORTED, "%s: too many groups", what);
-  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, K));
+  TX_TRY(check_gemm(what, A, lda, B, ldb, C, ldc, M, N, K, es));
   if (groups == 0 || M == 0 || N == 0) return TX_SUCCESS;
   if (!sa || !sb) return fail(TX_INVALID_ARGUMENT, "%s: NULL scale vector", what);
+  if (e.bias && (!aligned(e.bias, 4) || stride_bias < 0))
+    return fail(TX_INVALID_ARGUMENT, "%s: bias must be 4-byte aligned with a non-negative stride", what);
   if (!aligned(sa, 4) || !aligned(sb, 4))
     return fail(TX_INVALID_ARGUMENT, "%s: scales must be 4-byte aligned", what);
   const bool grouped = offsets != nullptr;
@@ -583,6 +596,14 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
   q.stride_c = stride_c;
   q.stride_b = stride_b;
   q.stride_sb = stride_sb;
+  q.stride_bias = stride_bias;
+  if (e.on()) {
+    q.g.bias = e.bias;
+    q.g.act = e.act;
+    q.g.out_kind = e.out_kind;
+    q.g.out_mul = e.out_mul;
+    q.g.epi = 1;
+  }
   q.groups = int32_t(groups);
   q.mtiles = int32_t(mtiles);
   q.tiles_per = int32_t(rt);
@@ -595,9 +616,26 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
     TX_TRY(launch(fn, 1, 1, 256, s, &q, sizeof q, "tx_gemm_fp8_grouped_prefix"));
   }
   char kname[80];
-  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped%s", fa, fb, big ? "" : "_n128");
+  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped%s%s", fa, fb, e.on() ? "_epi" : "",
+                big ? "" : "_n128");
   TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
   return launch(fn, unsigned(mtiles * tiles_n), 1, 64 * kFastWaves, s, &q, sizeof q, kname);
+}
+
+static tx_status dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
+                                        const void *B, tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                        const float *sb, int64_t stride_sb, const float *bias,
+                                        int64_t stride_bias, int activation, void *C, tx_dtype c_type,
+                                        float c_scale, int64_t ldc, const int32_t *offsets, int64_t groups,
+                                        int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  const char *what = "tx_dot_fp8_scaled_grouped";
+  if (!offsets && groups > 0 && M > 0 && N > 0)
+    return fail(TX_INVALID_ARGUMENT, "%s: NULL group offsets", what);
+  Epilogue e;
+  size_t es;
+  TX_TRY(make_epilogue(what, bias, activation, c_type, c_scale, &e, &es));
+  return dot_fp8_grouped_impl(what, A, a_type, lda, 0, sa, 0, B, b_type, ldb, stride_b, sb, stride_sb, C,
+                              ldc, 0, offsets, groups, M, N, K, stream, e, es, stride_bias);
 }
 
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,
@@ -690,33 +728,42 @@ static tx_status dot_fp8_op(tx_value *v, size_t count, tx_stream_t stream) {
 }
 
 // tx.dot_fp8_scaled_grouped: {C (result), A, B, scale_a, scale_b, offsets,
-// groups, M, N, K, lda, ldb, ldc, stride_b, stride_scale_b, a_type, b_type}
+// bias (or NULL), groups, M, N, K, lda, ldb, ldc, stride_b, stride_scale_b,
+// stride_bias, a_type, b_type, c_type, activation, c_scale (fp32 bits)}
 static tx_status dot_fp8_grouped_op(tx_value *v, size_t count, tx_stream_t stream) {
   Operands o{v, count, "tx.dot_fp8_scaled_grouped"};
-  TX_TRY(o.need(17));
-  void *C, *A, *B, *sa, *sb, *off;
-  int64_t G, M, N, K, lda, ldb, ldc, stb, stsb, at, bt;
+  TX_TRY(o.need(22));
+  void *C, *A, *B, *sa, *sb, *off, *bias;
+  int64_t G, M, N, K, lda, ldb, ldc, stb, stsb, stbias, at, bt, ct, act, cs;
   TX_TRY(o.ptr(0, &C));
   TX_TRY(o.ptr(1, &A));
   TX_TRY(o.ptr(2, &B));
   TX_TRY(o.ptr(3, &sa));
   TX_TRY(o.ptr(4, &sb));
   TX_TRY(o.ptr(5, &off));
-  TX_TRY(o.integer(6, &G));
-  TX_TRY(o.integer(7, &M));
-  TX_TRY(o.integer(8, &N));
-  TX_TRY(o.integer(9, &K));
-  TX_TRY(o.integer(10, &lda));
-  TX_TRY(o.integer(11, &ldb));
-  TX_TRY(o.integer(12, &ldc));
-  TX_TRY(o.integer(13, &stb));
-  TX_TRY(o.integer(14, &stsb));
-  TX_TRY(o.integer(15, &at));
-  TX_TRY(o.integer(16, &bt));
-  if (!off) return fail(TX_INVALID_ARGUMENT, "tx.dot_fp8_scaled_grouped: NULL offsets");
-  return dot_fp8_grouped_impl("tx_dot_fp8_scaled_grouped", A, tx_dtype(at), lda, 0, static_cast<const float *>(sa),
-                              0, B, tx_dtype(bt), ldb, stb, static_cast<const float *>(sb), stsb, C, ldc, 0,
-                              static_cast<const int32_t *>(off), G, M, N, K, stream);
+  TX_TRY(o.ptr(6, &bias));
+  TX_TRY(o.integer(7, &G));
+  TX_TRY(o.integer(8, &M));
+  TX_TRY(o.integer(9, &N));
+  TX_TRY(o.integer(10, &K));
+  TX_TRY(o.integer(11, &lda));
+  TX_TRY(o.integer(12, &ldb));
+  TX_TRY(o.integer(13, &ldc));
+  TX_TRY(o.integer(14, &stb));
+  TX_TRY(o.integer(15, &stsb));
+  TX_TRY(o.integer(16, &stbias));
+  TX_TRY(o.integer(17, &at));
+  TX_TRY(o.integer(18, &bt));
+  TX_TRY(o.integer(19, &ct));
+  TX_TRY(o.integer(20, &act));
+  TX_TRY(o.integer(21, &cs));
+  float c_scale;
+  const uint32_t bits = uint32_t(cs);
+  std::memcpy(&c_scale, &bits, sizeof c_scale);
+  return dot_fp8_scaled_grouped(A, tx_dtype(at), lda, static_cast<const float *>(sa), B, tx_dtype(bt), ldb,
+                                stb, static_cast<const float *>(sb), stsb, static_cast<const float *>(bias),
+                                stbias, int(act), C, tx_dtype(ct), c_scale, ldc,
+                                static_cast<const int32_t *>(off), G, M, N, K, stream);
 }
 
 // tx.dot_fp8_scaled_batched: {C (result), A, B, scale_a, scale_b, batch, M,
@@ -853,9 +900,10 @@ static const bool reg_dot_mx = register_op(
     "b_type:i32, c_type:i32");
 static const bool reg_dot_fp8_grouped = register_op(
     "tx.dot_fp8_scaled_grouped", dot_fp8_grouped_op,
-    "C:bf16*(result, M x N), A:fp8* (M x K), B:fp8* (groups x N x K), scale_a:f32* (M), "
-    "scale_b:f32* (groups x N), offsets:i32* (groups + 1 rows of A), groups, M, N, K, lda, ldb, ldc, "
-    "stride_b, stride_scale_b, a_type:i32, b_type:i32");
+    "C:bf16|f16|f32|fp8*(result, M x N), A:fp8* (M x K), B:fp8* (groups x N x K), scale_a:f32* (M), "
+    "scale_b:f32* (groups x N), offsets:i32* (groups + 1 rows of A), bias:f32*|NULL (groups x N), "
+    "groups, M, N, K, lda, ldb, ldc, stride_b, stride_scale_b, stride_bias, a_type:i32, b_type:i32, "
+    "c_type:i32, activation:i32, c_scale:f32 bits");
 static const bool reg_dot_fp8_batched = register_op(
     "tx.dot_fp8_scaled_batched", dot_fp8_batched_op,
     "C:bf16*(result, batch x M x N), A:fp8*, B:fp8* (N x K each), scale_a:f32*, scale_b:f32*, batch, "
@@ -899,15 +947,15 @@ TX_API tx_status tx_dot_fp8_scaled_ex(const void *A, tx_dtype a_type, int64_t ld
 TX_API tx_status tx_dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64_t lda,
                                            const float *scale_a, const void *B, tx_dtype b_type,
                                            int64_t ldb, int64_t stride_b, const float *scale_b,
-                                           int64_t stride_scale_b, void *C, int64_t ldc,
+                                           int64_t stride_scale_b, const float *bias,
+                                           int64_t stride_bias, int activation, void *C,
+                                           tx_dtype c_type, float c_scale, int64_t ldc,
                                            const int32_t *group_offsets, int64_t groups, int64_t M,
                                            int64_t N, int64_t K, tx_stream_t stream) {
   tx::clear_error();
-  if (!group_offsets && groups > 0 && M > 0 && N > 0)
-    return tx::fail(TX_INVALID_ARGUMENT, "tx_dot_fp8_scaled_grouped: NULL group offsets");
-  return tx::dot_fp8_grouped_impl("tx_dot_fp8_scaled_grouped", A, a_type, lda, 0, scale_a, 0, B, b_type,
-                                  ldb, stride_b, scale_b, stride_scale_b, C, ldc, 0, group_offsets, groups,
-                                  M, N, K, stream);
+  return tx::dot_fp8_scaled_grouped(A, a_type, lda, scale_a, B, b_type, ldb, stride_b, scale_b,
+                                    stride_scale_b, bias, stride_bias, activation, C, c_type, c_scale, ldc,
+                                    group_offsets, groups, M, N, K, stream);
 }
 
 TX_API tx_status tx_dot_fp8_scaled_batched(const void *A, tx_dtype a_type, int64_t lda, int64_t stride_a,

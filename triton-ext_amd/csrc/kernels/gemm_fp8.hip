@@ -126,8 +126,10 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_grouped_prefix(const tx_groupe
   }
 }
 
-template <class C, int BN>
+template <class C, int BN, bool EPI>
 __device__ __forceinline__ void gemm_fp8_grouped(const tx_grouped_args &q) {
+  // bytes per C element: bf16, or the fused epilogue's output type
+  const int ce = !EPI ? 2 : q.g.out_kind == EPI_OUT_F32 ? 4 : q.g.out_kind >= EPI_OUT_E4M3FN ? 1 : 2;
   int vm, tn;
   tile_coords(int(blockIdx.x), q.mtiles, q.g.tiles_n, q.g.group_m, &vm, &tn);
   tx_gemm_args a = q.g;
@@ -147,27 +149,34 @@ __device__ __forceinline__ void gemm_fp8_grouped(const tx_grouped_args &q) {
     const int r0 = min(max(q.offsets[p], 0), r1);
     a.M = r1 - r0;
     a.A = static_cast<const uint8_t *>(q.g.A) + int64_t(r0) * q.g.lda;
-    a.C = static_cast<uint16_t *>(q.g.C) + int64_t(r0) * q.g.ldc;
+    a.C = static_cast<uint8_t *>(q.g.C) + int64_t(r0) * q.g.ldc * ce;
     a.scale_a = q.g.scale_a + r0;
   } else {
     p = vm / q.tiles_per;
     tm = vm - p * q.tiles_per;
     if (p >= q.groups) return;
     a.A = static_cast<const uint8_t *>(q.g.A) + int64_t(p) * q.stride_a;
-    a.C = static_cast<uint16_t *>(q.g.C) + int64_t(p) * q.stride_c;
+    a.C = static_cast<uint8_t *>(q.g.C) + int64_t(p) * q.stride_c * ce;
     a.scale_a = q.g.scale_a + int64_t(p) * q.stride_sa;
   }
   a.B = static_cast<const uint8_t *>(q.g.B) + int64_t(p) * q.stride_b;
   a.scale_b = q.g.scale_b + int64_t(p) * q.stride_sb;
-  gemm_fast_tile_at<C, BN>(a, tm, tn, 0);
+  if (EPI && q.g.bias) a.bias = q.g.bias + int64_t(p) * q.stride_bias;
+  gemm_fast_tile_at<C, BN, fast::kWaves, false, OUT_BF16, EPI>(a, tm, tn, 0);
 }
 
 #define TX_GEMM_FP8_GROUPED(FA, FB, ELA, ELB)                                                    \
   TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped(const tx_grouped_args q) { \
-    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256>(q);                              \
+    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256, false>(q);                       \
   }                                                                                              \
   TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_n128(const tx_grouped_args q) { \
-    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128>(q);                              \
+    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128, false>(q);                       \
+  }                                                                                              \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_epi(const tx_grouped_args q) { \
+    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256, true>(q);                        \
+  }                                                                                              \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_epi_n128(const tx_grouped_args q) { \
+    gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128, true>(q);                        \
   }
 
 TX_GEMM_FP8_GROUPED(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)

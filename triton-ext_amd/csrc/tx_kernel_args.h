@@ -98,7 +98,9 @@ typedef struct tx_gemm_args {
  * ceil(rows_q / 256) (written by tx_gemm_fp8_grouped_prefix).  Batched
  * (offsets == NULL): problem p is g.M rows at A + p * stride_a (elements),
  * scale_a + p * stride_sa, C + p * stride_c.  The grid covers mtiles x
- * tiles_n tiles; m tiles past the last problem's exit at once. */
+ * tiles_n tiles; m tiles past the last problem's exit at once.  With g.epi
+ * the fast tile's fused epilogue writes C as g.out_kind (strides in
+ * elements of that type). */
 typedef struct tx_grouped_args {
   tx_gemm_args g;
   const int32_t *offsets;
@@ -108,6 +110,7 @@ typedef struct tx_grouped_args {
   int64_t stride_c;
   int64_t stride_b;
   int64_t stride_sb;
+  int64_t stride_bias;  /* fused epilogue (g.epi): bias of problem p at g.bias + p * stride_bias */
   int32_t groups;
   int32_t mtiles;       /* m tiles the grid covers */
   int32_t tiles_per;    /* batched: ceil(g.M / 256) */

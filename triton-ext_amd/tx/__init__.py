@@ -242,17 +242,25 @@ def _fp8_checks(*ts):
 
 def dot_scaled_rowcol_grouped(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_gnk: torch.Tensor,
                               scale_b: torch.Tensor, group_offsets: torch.Tensor,
-                              out: torch.Tensor | None = None) -> torch.Tensor:
+                              out: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                              activation: str | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                              out_scale: float = 1.0) -> torch.Tensor:
     """Grouped fp8 dot with row/column scales (mixture-of-experts layers):
     rows group_offsets[p] .. group_offsets[p+1] of a_q (M x K) against
     expert p's b_q_gnk[p] (N x K, the column-major K x N operand), scaled by
-    scale_a[r] and scale_b[p, n], bf16 out (M x N).  group_offsets: int32 on
-    the device, G + 1 nondecreasing row offsets within 0 .. M; the group
-    sizes are never read back to the host."""
-    _on_gpu(a_q, scale_a, b_q_gnk, scale_b, group_offsets, out)
+    scale_a[r] and scale_b[p, n], then the fused epilogue of
+    dot_scaled_rowcol (bias[p] of a G x N bias, activation, out_dtype, fp8
+    outputs holding y / out_scale); bf16 M x N by default.  group_offsets:
+    int32 on the device, G + 1 nondecreasing row offsets within 0 .. M; the
+    group sizes are never read back to the host."""
+    _on_gpu(a_q, scale_a, b_q_gnk, scale_b, group_offsets, out, bias)
     _fp8_checks(a_q, b_q_gnk)
     if a_q.dim() != 2 or b_q_gnk.dim() != 3 or a_q.shape[1] != b_q_gnk.shape[2]:
         raise ValueError("a_q must be M x K and b_q_gnk G x N x K")
+    if activation not in _ACT:
+        raise ValueError(f"unknown activation {activation!r}")
+    if out_dtype not in (torch.bfloat16, torch.float16, torch.float32) + _FP8:
+        raise ValueError("out_dtype must be bf16, fp16, fp32 or fp8")
     M, K = a_q.shape
     G, N = b_q_gnk.shape[0], b_q_gnk.shape[1]
     if group_offsets.dtype != torch.int32 or group_offsets.numel() != G + 1 or not group_offsets.is_contiguous():
@@ -260,14 +268,18 @@ def dot_scaled_rowcol_grouped(a_q: torch.Tensor, scale_a: torch.Tensor, b_q_gnk:
     if scale_a.dtype != torch.float32 or scale_a.numel() != M or not scale_a.is_contiguous() or \
             scale_b.dtype != torch.float32 or tuple(scale_b.shape) != (G, N) or scale_b.stride(1) != 1:
         raise ValueError("scale_a must be fp32[M] and scale_b fp32[G, N]")
+    if bias is not None and (bias.dtype != torch.float32 or tuple(bias.shape) != (G, N) or bias.stride(1) != 1):
+        raise ValueError("bias must be fp32[G, N]")
     if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=a_q.device)
-    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
-        raise ValueError("out must be a row-major bf16 M x N tensor")
+        out = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
+    if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a row-major M x N tensor of out_dtype")
     check(lib.tx_dot_fp8_scaled_grouped(_ptr(a_q), _TX_DTYPE[a_q.dtype], a_q.stride(0), _ptr(scale_a),
                                         _ptr(b_q_gnk), _TX_DTYPE[b_q_gnk.dtype], b_q_gnk.stride(1),
-                                        b_q_gnk.stride(0), _ptr(scale_b), scale_b.stride(0), _ptr(out),
-                                        out.stride(0), _ptr(group_offsets), G, M, N, K, _stream(a_q)))
+                                        b_q_gnk.stride(0), _ptr(scale_b), scale_b.stride(0), _ptr(bias),
+                                        0 if bias is None else bias.stride(0), _ACT[activation], _ptr(out),
+                                        _TX_DTYPE[out_dtype], float(out_scale), out.stride(0),
+                                        _ptr(group_offsets), G, M, N, K, _stream(a_q)))
     return out
 
 

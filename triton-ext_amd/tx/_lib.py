@@ -125,8 +125,8 @@ def _load():
     L.tx_dot_fp8_scaled_ex.argtypes = [P, I, I64, P, P, I, I64, P, P, I, P, I, ctypes.c_float,
                                        I64, I64, I64, I64, VP]
     L.tx_dot_fp8_scaled_ex.restype = I
-    L.tx_dot_fp8_scaled_grouped.argtypes = [P, I, I64, P, P, I, I64, I64, P, I64, P, I64, P, I64, I64, I64,
-                                            I64, P]
+    L.tx_dot_fp8_scaled_grouped.argtypes = [P, I, I64, P, P, I, I64, I64, P, I64, P, I64, I, P, I, ctypes.c_float,
+                                            I64, P, I64, I64, I64, I64, P]
     L.tx_dot_fp8_scaled_grouped.restype = I
     L.tx_dot_fp8_scaled_batched.argtypes = [P, I, I64, I64, P, I64, P, I, I64, I64, P, I64, P, I64, I64, I64,
                                             I64, I64, I64, P]
