@@ -76,6 +76,38 @@ def test_grouped_rows_outside_groups_untouched(tx, oracle, dev):
         check_close(got[r0:r1], r32, r16, FP8_TOL)
 
 
+@pytest.mark.parametrize("N,K,fa,fb", [(1000, 256, 1, 1), (2048, 512, 2, 1)])
+def test_grouped_many_small_experts(tx, oracle, dev, N, K, fa, fb):
+    """64 experts of 0..200 rows (under 192 on average): the transposed tile
+    (a group's rows along the tile's 128-wide side, C stored transposed),
+    including empty groups and a ragged N."""
+    g = np.random.default_rng(N + K)
+    sizes = list(g.integers(0, 200, 64))
+    sizes[5] = sizes[40] = 0
+    M, off, aq, bq, sa, sb = _grouped_case(g, sizes, N, K, fa, fb)
+    got = _bits(_run_grouped(tx, dev, aq, bq, sa, sb, off, fa, fb))
+    for p in range(64):
+        r0, r1 = int(off[p]), int(off[p + 1])
+        if r1 > r0:
+            r32, r16 = oracle.gemm_fp8_scaled_rows(aq[r0:r1], bq[p], sa[r0:r1], sb[p], 0, r1 - r0, fa, fb)
+            check_close(got[r0:r1], r32, r16, FP8_TOL)
+
+
+def test_grouped_small_rows_outside_groups_untouched(tx, oracle, dev):
+    """The transposed tile writes only the groups' rows."""
+    g = np.random.default_rng(5)
+    M, off, aq, bq, sa, sb = _grouped_case(g, [36, 20], 130, 256, 1, 1, lead=64, tail=100)
+    C = torch.full((M, 130), 7.0, dtype=torch.bfloat16, device=dev)
+    _run_grouped(tx, dev, aq, bq, sa, sb, off, 1, 1, out=C)
+    got = _bits(C)
+    seven = np.uint16(0x40E0)
+    assert np.all(got[:64] == seven) and np.all(got[120:] == seven)
+    for p in range(2):
+        r0, r1 = int(off[p]), int(off[p + 1])
+        r32, r16 = oracle.gemm_fp8_scaled_rows(aq[r0:r1], bq[p], sa[r0:r1], sb[p], 0, r1 - r0)
+        check_close(got[r0:r1], r32, r16, FP8_TOL)
+
+
 def test_grouped_large_big_tiles(tx, oracle, dev):
     """8 experts x 1024 rows, N = 4096, K = 1024: 256 x 256 tiles; sampled
     rows of every group against the oracle."""

@@ -579,10 +579,14 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
     return fail(TX_UNSUPPORTED, "%s: a problem's operands exceed 32-bit offsets", what);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t cus = cu_count();
-  const int64_t rt = (M + 255) / 256;
+  // Groups averaging under 192 rows: the transposed tile (a group's rows on
+  // the tile's 128-wide side, so a 100-row group wastes 28 rows, not 156).
+  const bool trans = grouped && !e.on() && M < 192 * groups;
+  const int64_t tile_rows = trans ? 128 : 256;
+  const int64_t rt = (M + tile_rows - 1) / tile_rows;
   const int64_t mtiles = grouped ? rt + groups : groups * rt;
-  const bool big = (grouped ? rt : mtiles) * ((N + 255) / 256) >= cus;
-  const int64_t bn = big ? 256 : 128;
+  const bool big = !trans && (grouped ? rt : mtiles) * ((N + 255) / 256) >= cus;
+  const int64_t bn = big || trans ? 256 : 128;  // C columns per tile
   const int64_t tiles_n = (N + bn - 1) / bn;
   if (mtiles * tiles_n > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: too many tiles", what);
 
@@ -607,6 +611,7 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
   q.groups = int32_t(groups);
   q.mtiles = int32_t(mtiles);
   q.tiles_per = int32_t(rt);
+  q.tile_rows = int32_t(tile_rows);
   ScratchLease pre;  // held until the product is enqueued
   hipFunction_t fn;
   if (grouped) {
@@ -616,8 +621,9 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
     TX_TRY(launch(fn, 1, 1, 256, s, &q, sizeof q, "tx_gemm_fp8_grouped_prefix"));
   }
   char kname[80];
-  std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped%s%s", fa, fb, e.on() ? "_epi" : "",
-                big ? "" : "_n128");
+  if (trans) std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped_t", fa, fb);
+  else std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped%s%s", fa, fb, e.on() ? "_epi" : "",
+                     big ? "" : "_n128");
   TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
   return launch(fn, unsigned(mtiles * tiles_n), 1, 64 * kFastWaves, s, &q, sizeof q, kname);
 }

@@ -157,8 +157,10 @@ __device__ __forceinline__ void wait_and_barrier() {
 enum FastOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
 
 // The tile (tm, tn) of C (256 x BN elements at row 256 tm, column BN tn),
-// split `split` of a.splits along K.
-template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16, bool EPI = false>
+// split `split` of a.splits along K.  TRANS (bf16 out, no split): the tile
+// is stored transposed, element (i, j) at C[j * ldc + i].
+template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16, bool EPI = false,
+          bool TRANS = false>
 __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm, int tn, int split) {
   using namespace fast;
   static_assert(BN == 256 || BN == 128, "tile 256 x 256 or 256 x 128");
@@ -169,6 +171,7 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   constexpr int SD = FP4 ? 2 : 1;  // MX scale dwords per row and K step (4 blocks each)
   static_assert(OUT == OUT_BF16 || MX, "fp16 / fp32 output: MX variant only");
   static_assert(!EPI || (C::FP8 && !MX && OUT == OUT_BF16), "fused epilogue: row/column-scaled fp8");
+  static_assert(!TRANS || (!EPI && OUT == OUT_BF16), "transposed store: plain bf16 output");
   // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per
   // wave): LDS reads per step are then (64 + 64) x 8 rows instead of
   // (128 + 32) x 8, which matters because narrow tiles are LDS-bound.
@@ -402,7 +405,7 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   // With K split, the unscaled fp32 sums go to the split's partial plane
   // (row-major M x N); a reduction kernel combines the planes.  An fp32
   // output (MX variant) is stored the same way, straight into C.
-  if (splits > 1 || OUT == OUT_F32) {
+  if (!TRANS && (splits > 1 || OUT == OUT_F32)) {
     float *P = splits > 1 ? a.part + int64_t(split) * a.M * a.N : static_cast<float *>(a.C);
     const int64_t ldp = splits > 1 ? a.N : a.ldc;
     const bool pvec = splits > 1 ? (a.N & 3) == 0
@@ -553,6 +556,38 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   }
   __syncthreads();
   uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
+  if constexpr (TRANS) {
+    // Unit u: staged column c = u % BN (C row n0 + c) and staged rows 8 s ..
+    // 8 s + 7 (C columns m0 + 8 s ..), s = u / BN: a wave reads one staged
+    // row segment of 64 columns at a time and each lane stores 16 bytes.
+    const bool tvec = ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0) && ((a.ldc & 7) == 0);
+#pragma unroll
+    for (int i = 0; i < 256 * BN / 8 / (64 * NW); ++i) {
+      const int u = tid + 64 * NW * i;
+      const int c = u % BN, s8 = 8 * (u / BN);
+      uint32_t h[4];
+#pragma unroll
+      for (int t = 0; t < 8; t += 2) {
+        const uint32_t lo = *reinterpret_cast<const uint16_t *>(
+            lds + (s8 + t) * ROWB + (((c >> 3) ^ ((s8 + t) & (CH - 1))) << 4) + 2 * (c & 7));
+        const uint32_t hi = *reinterpret_cast<const uint16_t *>(
+            lds + (s8 + t + 1) * ROWB + (((c >> 3) ^ ((s8 + t + 1) & (CH - 1))) << 4) + 2 * (c & 7));
+        h[t / 2] = lo | (hi << 16);
+      }
+      const int orow = n0 + c, ocol = m0 + s8;
+      if (orow < a.N && ocol < a.M) {
+        uint16_t *dst = Cb + int64_t(orow) * a.ldc + ocol;
+        if (tvec && ocol + 7 < a.M) {
+          *reinterpret_cast<txd::u32x4 *>(dst) = txd::u32x4{h[0], h[1], h[2], h[3]};
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            if (ocol + t < a.M) dst[t] = uint16_t(h[t / 2] >> (16 * (t % 2)));
+        }
+      }
+    }
+    return;
+  }
   const bool cvec = ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0) && ((a.ldc & 7) == 0);
   const int sc = lane % CH;
   const int n = n0 + 8 * sc;

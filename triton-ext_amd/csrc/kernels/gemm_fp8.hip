@@ -110,7 +110,7 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_grouped_prefix(const tx_groupe
     if (p < q.groups) {
       const int r1 = min(max(q.offsets[p + 1], 0), total);
       const int r0 = min(max(q.offsets[p], 0), r1);
-      c = (r1 - r0 + 255) / 256;
+      c = (r1 - r0 + q.tile_rows - 1) / q.tile_rows;
     }
     sc[t] = c;
     __syncthreads();
@@ -126,17 +126,40 @@ TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_grouped_prefix(const tx_groupe
   }
 }
 
+// Tile of workgroup wg among the real_m x tiles_n tiles of a grouped
+// product (real_m = the prefix total, known only on the device; the grid
+// is larger).  Workgroups reach the 8 XCDs round robin, so XCD x = wg % 8
+// takes the x-th eighth of the real tiles in its own dispatch order (the
+// same contiguous, L2-sharing ranges as tile_coords) and the rest of its
+// workgroups leave: every XCD gets an equal share of the real work, which
+// tile_coords over the padded grid would give mostly to the first XCDs.
+__device__ __forceinline__ bool grouped_tile(int wg, int real_m, int tiles_n, int *tm, int *tn) {
+  const int total = real_m * tiles_n;
+  const int per = total / 8, rem = total % 8;
+  const int x = wg % 8, i = wg / 8;
+  if (i >= per + (x < rem ? 1 : 0)) return false;
+  const int pid = x * per + (x < rem ? x : rem) + i;
+  const int group_m = real_m < 8 ? real_m : 8;
+  const int in_group = group_m * tiles_n;
+  const int first_m = (pid / in_group) * group_m;
+  const int gsz = (real_m - first_m) < group_m ? (real_m - first_m) : group_m;
+  const int r = pid % in_group;
+  *tm = first_m + r % gsz;
+  *tn = r / gsz;
+  return true;
+}
+
 template <class C, int BN, bool EPI>
 __device__ __forceinline__ void gemm_fp8_grouped(const tx_grouped_args &q) {
   // bytes per C element: bf16, or the fused epilogue's output type
   const int ce = !EPI ? 2 : q.g.out_kind == EPI_OUT_F32 ? 4 : q.g.out_kind >= EPI_OUT_E4M3FN ? 1 : 2;
   int vm, tn;
-  tile_coords(int(blockIdx.x), q.mtiles, q.g.tiles_n, q.g.group_m, &vm, &tn);
   tx_gemm_args a = q.g;
   int p, tm;
   if (q.offsets) {
     const int32_t *T = q.tile_prefix;
-    if (vm >= T[q.groups]) return;  // uniform: the whole workgroup leaves
+    // uniform: a workgroup without a real tile leaves as a whole
+    if (!grouped_tile(int(blockIdx.x), T[q.groups], q.g.tiles_n, &vm, &tn)) return;
     int lo = 0, hi = q.groups - 1;  // the last problem p with T[p] <= vm
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -152,6 +175,7 @@ __device__ __forceinline__ void gemm_fp8_grouped(const tx_grouped_args &q) {
     a.C = static_cast<uint8_t *>(q.g.C) + int64_t(r0) * q.g.ldc * ce;
     a.scale_a = q.g.scale_a + r0;
   } else {
+    tile_coords(int(blockIdx.x), q.mtiles, q.g.tiles_n, q.g.group_m, &vm, &tn);
     p = vm / q.tiles_per;
     tm = vm - p * q.tiles_per;
     if (p >= q.groups) return;
@@ -165,12 +189,47 @@ __device__ __forceinline__ void gemm_fp8_grouped(const tx_grouped_args &q) {
   gemm_fast_tile_at<C, BN, fast::kWaves, false, OUT_BF16, EPI>(a, tm, tn, 0);
 }
 
+// Groups of few rows: the roles swapped, so that a group's rows fill the
+// tile's 128-wide side instead of a fraction of its 256 rows.  The tile's A
+// operand is expert p's B (N rows), its B operand the group's rows of A
+// (m tiles of 128 rows in the prefix), and the bf16 tile is stored
+// transposed into C's rows.
+template <class C>
+__device__ __forceinline__ void gemm_fp8_grouped_t(const tx_grouped_args &q) {
+  int vt, tf;  // 128-row tile of A (over all groups), 256-column tile of C
+  const int32_t *T = q.tile_prefix;
+  if (!grouped_tile(int(blockIdx.x), T[q.groups], q.g.tiles_n, &vt, &tf)) return;
+  int lo = 0, hi = q.groups - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (T[mid] <= vt) lo = mid;
+    else hi = mid - 1;
+  }
+  const int p = lo;
+  const int r1 = min(max(q.offsets[p + 1], 0), q.g.M);
+  const int r0 = min(max(q.offsets[p], 0), r1);
+  tx_gemm_args a = q.g;
+  a.A = static_cast<const uint8_t *>(q.g.B) + int64_t(p) * q.stride_b;
+  a.lda = q.g.ldb;
+  a.scale_a = q.g.scale_b + int64_t(p) * q.stride_sb;
+  a.M = q.g.N;
+  a.B = static_cast<const uint8_t *>(q.g.A) + int64_t(r0) * q.g.lda;
+  a.ldb = q.g.lda;
+  a.scale_b = q.g.scale_a + r0;
+  a.N = r1 - r0;
+  a.C = static_cast<uint16_t *>(q.g.C) + int64_t(r0) * q.g.ldc;
+  gemm_fast_tile_at<C, 128, fast::kWaves, false, OUT_BF16, false, true>(a, tf, vt - T[p], 0);
+}
+
 #define TX_GEMM_FP8_GROUPED(FA, FB, ELA, ELB)                                                    \
   TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped(const tx_grouped_args q) { \
     gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256, false>(q);                       \
   }                                                                                              \
   TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_n128(const tx_grouped_args q) { \
     gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 128, 2, 2, 16>, 128, false>(q);                       \
+  }                                                                                              \
+  TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_t(const tx_grouped_args q) { \
+    gemm_fp8_grouped_t<GemmCfg<ELB, ELA, 256, 128, 2, 2, 16>>(q);                                 \
   }                                                                                              \
   TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_grouped_epi(const tx_grouped_args q) { \
     gemm_fp8_grouped<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, 256, true>(q);                        \

@@ -114,7 +114,7 @@ typedef struct tx_grouped_args {
   int32_t groups;
   int32_t mtiles;       /* m tiles the grid covers */
   int32_t tiles_per;    /* batched: ceil(g.M / 256) */
-  int32_t reserved;
+  int32_t tile_rows;    /* grouped: rows of A per m tile (256; 128 in the transposed tile) */
 } tx_grouped_args;
 
 enum { EPI_ACT_NONE = 0, EPI_ACT_RELU = 1, EPI_ACT_GELU_TANH = 2, EPI_ACT_SILU = 3 };
