@@ -363,10 +363,16 @@ def test_gemv_config_full(tx, oracle, dev, M):
 @pytest.mark.parametrize("M,N,K,group,fmt", [(8, 8200, 384, 128, 2), (20, 8200, 512, 128, 2),
                                              (40, 8208, 256, 256, 1),
                                              (3, 100, 256, 128, 2), (33, 77, 1024, 256, 2),
-                                             (64, 50, 384, 384, 1), (5, 1, 128, 128, 1)])
+                                             (64, 50, 384, 384, 1), (5, 1, 128, 128, 1),
+                                             (1, 8200, 384, 128, 2), (2, 8208, 256, 256, 1),
+                                             (1, 100, 1152, 384, 1), (2, 77, 3072, 128, 2),
+                                             (1, 1, 128, 128, 2), (2, 3, 5120, 640, 1), (1, 3, 5120, 640, 1),
+                                             (1, 14336, 4096, 128, 1)])
 def test_gemv_shapes(tx, oracle, dev, M, N, K, group, fmt):
     """Small and ragged shapes; N >= 8192 takes the wide variants (two W
-    blocks per wave when M > 4, with an odd number of 16-row blocks)."""
+    blocks per wave when M > 4, with an odd number of 16-row blocks); M = 1
+    the streaming kernel (1 KiB slices: K not a multiple of 1024, odd N,
+    groups of 384), M = 2 beside it on the MFMA kernel."""
     g = np.random.default_rng(M * N)
     x = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
     wq = g.integers(0, 256, size=(N, K), dtype=np.uint8)

@@ -670,6 +670,18 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
       !aligned(scales, 4) || !aligned(y, 2))
     return fail(TX_UNSUPPORTED,
                 "%s: needs 16-byte aligned x and W rows (ldx %% 8 == 0, ldw %% 16 == 0)", what);
+  tx_gemv_args args{static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(W), scales,
+                    static_cast<uint16_t *>(y), ldx, ldw, ld_scales, ldy, int32_t(M), int32_t(N),
+                    int32_t(K), int32_t(group)};
+  char kname[48];
+  hipFunction_t fn;
+  if (M == 1 && K * 2 <= 32768) {  // x fits the kernel's LDS stage
+    // streaming VALU kernel: two W rows per wavefront, 8 wavefronts
+    std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s_lin_m1", fw);
+    TX_TRY(get_kernel(CodeObject::Gemv, kname, &fn));
+    return launch(fn, unsigned((N + 15) / 16), 1, 512, static_cast<hipStream_t>(stream), &args, sizeof args,
+                  kname);
+  }
   // 16 or 32 W rows per workgroup, K split over its wavefronts.  Many column
   // blocks: 4 wavefronts, each with two 16-row W blocks sharing its x reads
   // once x has more than a few rows.  Few: one W block per workgroup and 16
@@ -679,13 +691,8 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
   const int waves = wide ? 4 : (mblocks == 1 ? 16 : 8);
   const int nb = (wide && M > 4) ? 2 : 1;
   const int64_t grid = (N + 16 * nb - 1) / (16 * nb);
-  char kname[48];
   std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s_w%d_m%d_b%d", fw, waves, mblocks, nb);
-  hipFunction_t fn;
   TX_TRY(get_kernel(CodeObject::Gemv, kname, &fn));
-  tx_gemv_args args{static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(W), scales,
-                    static_cast<uint16_t *>(y), ldx, ldw, ld_scales, ldy, int32_t(M), int32_t(N),
-                    int32_t(K), int32_t(group)};
   return launch(fn, unsigned(grid), 1, unsigned(64 * waves), static_cast<hipStream_t>(stream), &args,
                 sizeof args, kname);
 }
