@@ -439,8 +439,8 @@ def main():
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build measures one GPU only: every op runs on one "
-                                   "MI355X; multi-GPU sharding is described, not run"}))
+        print(json.dumps({"error": "bench.py measures one GPU only: every op runs on one "
+                                   "MI355X; multi-GPU sharding is not implemented"}))
         sys.exit(2)
     import torch
     import tx

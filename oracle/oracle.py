@@ -1,7 +1,7 @@
 """ctypes wrapper around oracle/libtxoracle.so -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may
-import this module, and only as the checker (or, for the baseline, as the timed
+import this module, and only as the parity reference (or, for the baseline, as the timed
 CPU port).  The product path never routes through it.
 
 Each wrapper mirrors one C function of ``tx_oracle.c``; the C file states which

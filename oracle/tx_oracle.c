@@ -3,8 +3,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product path (the HIP kernels,
  * the C-ABI library, the Python host mirror) may call, link or load this
- * file.  It is used by tests/ as the checker, by __graft_entry__.smoke() as
- * the checker, and by bench.py's cpu_baseline leg as the timed CPU port.
+ * file.  It is used by tests/ as the parity reference, by __graft_entry__.smoke() as
+ * the parity reference, and by bench.py's cpu_baseline leg as the timed CPU port.
  *
  * Every function restates, in plain C, the semantics of one op on the
  * reference's hot path.  The reference itself never spells out the

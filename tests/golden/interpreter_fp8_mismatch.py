@@ -16,7 +16,7 @@ _convert_float):
   other      : none of the above (expected to be empty)
 
 Usage: python tests/golden/interpreter_fp8_mismatch.py [--n N]  (prints markdown)
-Test infrastructure: it imports the oracle as the checker.
+Test infrastructure: it imports the oracle as the parity reference.
 """
 from __future__ import annotations
 
