@@ -110,3 +110,65 @@ def test_python_mirror_rejects_cpu_tensors(tx):
     assert tx.get_fp8_format_name(torch.float8_e4m3fn) == "e4m3"
     with pytest.raises(AssertionError):
         tx.get_fp8_format_name(torch.float16)
+
+
+_P = ctypes.c_void_p(256)   # a non-NULL, 256-byte aligned stand-in: these calls fail before any access
+
+
+@pytest.mark.parametrize("call,status,msg", [
+    # fused epilogue options: unknown activation, output type, fp8 output scale
+    (lambda L: L.tx_dot_fp8_scaled_ex(_P, 1, 16, _P, _P, 1, 16, _P, None, 9, _P, 3, 1.0, 16, 16, 16, 16, None),
+     "INVALID_ARGUMENT", "activation"),
+    (lambda L: L.tx_dot_fp8_scaled_ex(_P, 1, 16, _P, _P, 1, 16, _P, None, 0, _P, 4, 1.0, 16, 16, 16, 16, None),
+     "INVALID_ARGUMENT", "output type"),
+    (lambda L: L.tx_dot_fp8_scaled_ex(_P, 1, 16, _P, _P, 1, 16, _P, None, 0, _P, 1, 0.0, 16, 16, 16, 16, None),
+     "INVALID_ARGUMENT", "c_scale"),
+    # MX dot: fp4 needs an even K; operand and output types; scale strides
+    (lambda L: L.tx_dot_scaled_mx(_P, 7, 64, _P, 4, _P, 7, 64, _P, 4, _P, 0, 16, 16, 16, 127, None),
+     "INVALID_ARGUMENT", "even K"),
+    (lambda L: L.tx_dot_scaled_mx(_P, 3, 128, _P, 4, _P, 1, 128, _P, 4, _P, 0, 16, 16, 16, 128, None),
+     "INVALID_ARGUMENT", "fp8 or fp4"),
+    (lambda L: L.tx_dot_scaled_mx(_P, 1, 128, _P, 4, _P, 7, 64, _P, 4, _P, 4, 16, 16, 16, 128, None),
+     "INVALID_ARGUMENT", "output type"),
+    (lambda L: L.tx_dot_scaled_mx(_P, 1, 128, _P, 3, _P, 1, 128, _P, 4, _P, 0, 16, 16, 16, 128, None),
+     "INVALID_ARGUMENT", "scale stride"),
+    (lambda L: L.tx_dot_scaled_mx(_P, 1, 128, _P, 4, _P, 7, 32, _P, 4, _P, 0, 16, 16, 16, 128, None),
+     "INVALID_ARGUMENT", "stride smaller"),
+    # grouped / batched fp8 dot
+    (lambda L: L.tx_dot_fp8_scaled_grouped(_P, 1, 128, _P, _P, 1, 128, 128 * 64, _P, 64, None, 0, 0, _P, 3,
+                                          1.0, 64, None, 2, 100, 64, 128, None),
+     "INVALID_ARGUMENT", "offsets"),
+    (lambda L: L.tx_dot_fp8_scaled_grouped(_P, 1, 128, _P, _P, 1, 128, 128 * 64, _P, 64, None, 0, 0, _P, 3,
+                                          1.0, 64, _P, -1, 100, 64, 128, None),
+     "INVALID_ARGUMENT", "negative group"),
+    (lambda L: L.tx_dot_fp8_scaled_grouped(_P, 1, 128, _P, _P, 1, 128, 128 * 64, _P, 64, None, 0, 5, _P, 3,
+                                          1.0, 64, _P, 2, 100, 64, 128, None),
+     "INVALID_ARGUMENT", "activation"),
+    (lambda L: L.tx_dot_fp8_scaled_grouped(_P, 1, 120, _P, _P, 1, 120, 120 * 64, _P, 64, None, 0, 0, _P, 3,
+                                          1.0, 64, _P, 2, 100, 64, 120, None),
+     "UNSUPPORTED", "16-byte"),
+    (lambda L: L.tx_dot_fp8_scaled_batched(_P, 6, 128, 128 * 64, _P, 64, _P, 1, 128, 128 * 64, _P, 64, _P, 64,
+                                          64 * 64, 2, 64, 64, 128, None),
+     "INVALID_ARGUMENT", "fp8"),
+    # quantisers: K a multiple of the 32-element block; input and code types
+    (lambda L: L.tx_quantize_mx(_P, 0, 100, _P, 1, 100, _P, 4, 4, 100, None), "INVALID_ARGUMENT", "multiple"),
+    (lambda L: L.tx_quantize_mx(_P, 6, 128, _P, 1, 128, _P, 4, 4, 128, None), "INVALID_ARGUMENT", "fp32 or bf16"),
+    (lambda L: L.tx_quantize_rowwise(_P, 0, 128, _P, 3, 128, _P, 4, 128, None), "INVALID_ARGUMENT", "fp8"),
+])
+def test_new_entry_points_validate_arguments(tx, call, status, msg):
+    """Argument errors of the epilogue, MX, grouped / batched and quantiser
+    entry points come back as status codes with a message, before any device
+    access."""
+    st = call(tx.lib)
+    assert st == getattr(tx._lib, status), (st, tx._lib.last_error())
+    assert msg in tx._lib.last_error(), tx._lib.last_error()
+
+
+def test_new_entry_points_zero_sized(tx):
+    L = tx.lib
+    assert L.tx_dot_fp8_scaled_grouped(None, 1, 0, None, None, 1, 0, 0, None, 0, None, 0, 0, None, 3, 1.0, 0,
+                                       None, 0, 0, 0, 0, None) == 0
+    assert L.tx_dot_fp8_scaled_batched(None, 1, 0, 0, None, 0, None, 1, 0, 0, None, 0, None, 0, 0, 0, 0, 0, 0,
+                                       None) == 0
+    assert L.tx_dot_scaled_mx(None, 7, 0, None, 0, None, 7, 0, None, 0, None, 0, 0, 0, 0, 0, None) == 0
+    assert L.tx_quantize_mx(None, 0, 0, None, 1, 0, None, 0, 0, 0, None) == 0
