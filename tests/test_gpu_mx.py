@@ -367,3 +367,37 @@ def test_mx_fp4_errors(tx, dev):
     # same K, fp4 x fp8: served (zeros in, zeros out)
     z = tx.dot_scaled(A, S, A8.view(torch.float8_e4m3fn), S, a_format="e2m1")
     assert torch.count_nonzero(z).item() == 0
+
+
+def test_mx_fp4_special_scales(tx, oracle, dev):
+    """fp4 operands under e8m0 special codes: 255 is NaN for every output it
+    scales, code 0 (2^-127) against 254 gives the same bits as 127 against
+    127, and far exponents (2^103, 2^-87 on whole rows) stay within the
+    fp32 bound."""
+    g = np.random.default_rng(13)
+    M, N, K = 256, 256, 512
+    pa = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    pb = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    ones_a = np.full((M, K // 32), 127, np.uint8)
+    ones_b = np.full((N, K // 32), 127, np.uint8)
+    c11 = _run_fp4(tx, dev, pa, ones_a, pb, ones_b, "f32")
+    c0 = _run_fp4(tx, dev, pa, np.zeros_like(ones_a), pb, np.full_like(ones_b, 254), "f32")
+    assert np.array_equal(c0.view(np.uint32), c11.view(np.uint32))
+    sa = g.integers(120, 134, (M, K // 32), dtype=np.uint8)
+    sb = g.integers(100, 110, (N, K // 32), dtype=np.uint8)
+    sa[5, 3] = 255
+    sb[7, 0] = 255
+    sa[10, :] = 230
+    sa[11, :] = 40
+    got = _run_fp4(tx, dev, pa, sa, pb, sb, "f32")
+    ref, mag, bmax = oracle.gemm_mx_rows(pa, sa, pb, sb, 0, M, fmt_a=4, fmt_b=4, block_max=True)
+    assert np.all(np.isnan(got[5])) and np.all(np.isnan(got[:, 7]))
+    keep = np.ones((M, N), bool)
+    keep[5] = False
+    keep[:, 7] = False
+    assert np.all(np.isfinite(got[keep])) and np.all(np.isfinite(ref[keep]))
+    d = np.abs(got.astype(np.float64) - ref)[keep]
+    bound = 32 * 2.0 ** -13 * bmax.astype(np.float64) + (K / 64 + 2) * 2.0 ** -24 * mag.astype(np.float64)
+    assert np.all(d <= bound[keep])
+    assert np.abs(np.delete(got[10], 7)).max() > 2.0 ** 80
+    assert 0 < np.abs(np.delete(got[11], 7)).max() < 2.0 ** -60
