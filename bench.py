@@ -42,6 +42,7 @@ import time
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "triton-ext_amd"))
+sys.path.insert(0, os.path.join(REPO, "tests"))  # workloads: the seeded input generators
 
 METRIC = "fp8 GEMM TFLOP/s + % MFMA peak @8192^3; fp8 convert GB/s + % HBM peak"
 HBM_PEAK_GBS = 8000.0
@@ -109,7 +110,7 @@ def ring_count(set_bytes):
 
 # ------------------------------------------------------------------ ops
 def bench_fp8_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
-    from tx import workloads
+    import workloads
     dev = torch.device("cuda:0")
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
     bufs = []
@@ -133,7 +134,7 @@ def bench_fp8_gemm(tx, torch, M, N, K, steps, warmup, sets=2):
 
 def bench_fp8_gemm_epilogue(tx, torch, M, N, K, steps, warmup, act, out_dtype, sets=2):
     """fp8 scaled GEMM with the fused epilogue (bias, activation, output cast)."""
-    from tx import workloads
+    import workloads
     import numpy as np
     dev = torch.device("cuda:0")
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
@@ -157,11 +158,11 @@ def bench_fp8_gemm_epilogue(tx, torch, M, N, K, steps, warmup, act, out_dtype, s
 
 def bench_fp8_grouped(tx, torch, G, total, N, K, steps, warmup):
     """Grouped fp8 scaled GEMM (mixture-of-experts layer): `total` routed
-    rows split unevenly over G experts (tx.workloads.moe_group_sizes), each
+    rows split unevenly over G experts (workloads.moe_group_sizes), each
     expert's N x K weights; one grouped launch, and the same products as a
     loop of G plain calls for comparison.  Random finite e4m3fn codes."""
     import numpy as np
-    from tx import workloads
+    import workloads
     dev = torch.device("cuda:0")
     sizes = workloads.moe_group_sizes(total, G)
     off_np = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
@@ -195,7 +196,7 @@ def bench_fp8_grouped(tx, torch, G, total, N, K, steps, warmup):
 def bench_mx_gemm(tx, torch, M, N, K, steps, warmup, sets=2, fp4=False):
     """tt.dot_scaled with MX block scales (e8m0 per 32 K), bf16 out; e4m3fn
     operands, or fp4 (e2m1, two per byte) with ``fp4``."""
-    from tx import workloads
+    import workloads
     dev = torch.device("cuda:0")
     if fp4:
         aq, sa, bq, sb = workloads.mx_fp4_gemm_input(M, N, K)
@@ -245,7 +246,7 @@ def bench_quant(tx, torch, kind, xdt, steps, warmup, rows=8192, K=8192):
 
 
 def bench_bf16_gemm(tx, torch, M, N, K, steps, warmup):
-    from tx import workloads
+    import workloads
     import numpy as np
     dev = torch.device("cuda:0")
     A, B = workloads.bf16_gemm_input(M, N, K)
@@ -258,7 +259,7 @@ def bench_bf16_gemm(tx, torch, M, N, K, steps, warmup):
 
 
 def bench_fp8_convert(tx, torch, steps, warmup, n=16_777_216):
-    from tx import workloads
+    import workloads
     dev = torch.device("cuda:0")
     x_np = workloads.fp8_input(n)
     sets = ring_count(5 * n)
@@ -276,7 +277,7 @@ def bench_fp8_convert(tx, torch, steps, warmup, n=16_777_216):
 
 
 def bench_scatter(tx, torch, kind, steps, warmup, n=67_108_864, nbins=65536):
-    from tx import workloads
+    import workloads
     dev = torch.device("cuda:0")
     idx_np, val_np = workloads.scatter_input(n=n, nbins=nbins, kind=kind)
     sets = 2  # 2 x 512 MB of updates > 2 x MALL
@@ -291,7 +292,7 @@ def bench_scatter(tx, torch, kind, steps, warmup, n=67_108_864, nbins=65536):
 
 
 def bench_gemv(tx, torch, M, steps, warmup, N=14336, K=4096, group=128):
-    from tx import workloads
+    import workloads
     import numpy as np
     dev = torch.device("cuda:0")
     x, wq, s = workloads.gemv_input(M, N, K, group)
@@ -317,7 +318,7 @@ def cpu_baseline():
     import numpy as np
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
-    from tx import workloads
+    import workloads
     oracle.build()
     cores = os.cpu_count() or 1
     try:
@@ -523,7 +524,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8e4m3fn",
-        "data": "synthetic (seeded N(0,1), absmax-quantised; see tx/workloads.py)",
+        "data": "synthetic (seeded N(0,1), absmax-quantised; see tests/workloads.py)",
         "config": {"workload": "fp8 e4m3fn scaled GEMM M=N=K=8192, per-row/per-column fp32 "
                                "scales, bf16 output; plus fp32->e4m3fn RNE convert of 16Mi values",
                    "M": 8192, "N": 8192, "K": 8192, "preroll_s": PREROLL_S},

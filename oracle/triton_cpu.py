@@ -249,7 +249,7 @@ def baseline(gemm_rows: int = 64, bf16_rows: int = 64, progress=None) -> dict:
     """
     if IMPORT_ERROR is not None:
         return {"unavailable": IMPORT_ERROR}
-    from tx import workloads
+    import workloads
     step = progress or (lambda name: None)
     out = {"engine": f"triton {triton.__version__} interpreter (TRITON_INTERPRET=1)",
            "host": host_facts()}

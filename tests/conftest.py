@@ -10,7 +10,7 @@ import sys
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for p in (os.path.join(REPO, "triton-ext_amd"), os.path.join(REPO, "oracle"), REPO):
+for p in (os.path.join(REPO, "triton-ext_amd"), os.path.join(REPO, "oracle"), os.path.join(REPO, "tests"), REPO):
     if p not in sys.path:
         sys.path.insert(0, p)
 

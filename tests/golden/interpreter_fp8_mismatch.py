@@ -28,7 +28,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(os.path.dirname(HERE))
-for p in (os.path.join(REPO, "oracle"), os.path.join(REPO, "triton-ext_amd")):
+for p in (os.path.join(REPO, "oracle"), os.path.join(REPO, "triton-ext_amd"), os.path.join(REPO, "tests")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
@@ -84,7 +84,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--n", type=int, default=16_777_216)
     args = ap.parse_args()
-    from tx import workloads
+    import workloads
     x = workloads.fp8_input(args.n)
     print(f"# fp32 -> fp8 RNE: oracle vs Triton interpreter, {x.size:,} convert-workload inputs\n")
     print("| format | " + " | ".join(CLASSES) + " | total mismatches | share |")

@@ -112,6 +112,28 @@ def test_python_mirror_rejects_cpu_tensors(tx):
         tx.get_fp8_format_name(torch.float16)
 
 
+def test_gemv_wrapper_validates_shapes_and_out(tx):
+    """The GEMV mirror checks out, scales and operand shapes before the
+    device, so a short or mistyped out can never reach the kernel."""
+    x = torch.zeros((4, 256), dtype=torch.bfloat16)
+    w = torch.zeros((32, 256), dtype=torch.float8_e5m2)
+    s = torch.ones((32, 2), dtype=torch.float32)
+    with pytest.raises(ValueError, match="out must be"):
+        tx.gemv_fp8_dequant(x, w, s, out=torch.empty((3, 32), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="out must be"):
+        tx.gemv_fp8_dequant(x, w, s, out=torch.empty((4, 32), dtype=torch.float32))
+    with pytest.raises(ValueError, match="out must be"):
+        tx.gemv_fp8_dequant(x, w, s, out=torch.empty((32, 4), dtype=torch.bfloat16).t())
+    with pytest.raises(ValueError, match="incompatible shapes"):
+        tx.gemv_fp8_dequant(x, w, torch.ones((32, 1), dtype=torch.float32))
+    with pytest.raises(ValueError, match="incompatible shapes"):
+        tx.gemv_fp8_dequant(x, w[:, :128], s)
+    with pytest.raises(ValueError, match="2-D"):
+        tx.gemv_fp8_dequant(x.reshape(-1), w, s)
+    with pytest.raises(ValueError, match="GPU tensors only"):
+        tx.gemv_fp8_dequant(x, w, s)
+
+
 _P = ctypes.c_void_p(256)   # a non-NULL, 256-byte aligned stand-in: these calls fail before any access
 
 

@@ -23,7 +23,7 @@ REL = {"f32": 2.0 ** -23, "bf16": 2.0 ** -8, "f16": 2.0 ** -11, "e4m3fn": 2.0 **
 
 
 def _inputs(M, N, K, seed):
-    from tx import workloads
+    import workloads
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=seed)
     bias = np.random.default_rng(seed).standard_normal(N).astype(np.float32) * 3
     return aq, sa, bq, sb, bias

@@ -52,7 +52,7 @@ def test_encode_golden_inputs(tx, oracle, dev, fmt, sat, rounding):
 @pytest.mark.parametrize("sat", [False, True])
 def test_roundtrip_config_full_size(tx, oracle, dev, fmt, sat):
     """16,777,216 values of the fp8 round-trip workload, encode then decode."""
-    from tx import workloads
+    import workloads
     x_np = workloads.fp8_input()
     x = torch.from_numpy(x_np).to(dev)
     q = tx.fp_to_fp(x, FMTS[fmt], saturate=sat)

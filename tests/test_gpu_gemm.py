@@ -58,12 +58,24 @@ def sample_rows(M, k=24, seed=0):
     return sorted(r for r in rows if 0 <= r < M)
 
 
+def block_rows(M, seed=0):
+    """One random row in every 128-row block (so in each half of every
+    256-row tile, i.e. in every wavefront's share of it), plus the first and
+    last rows: a misplaced, duplicated or skipped tile or wave block shows up
+    in at least one of them."""
+    g = np.random.default_rng(seed)
+    rows = {0, M - 1}
+    for b0 in range(0, M, 128):
+        rows.add(int(g.integers(b0, min(b0 + 128, M))))
+    return sorted(rows)
+
+
 # --------------------------------------------------------------------- bf16
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (17, 19, 23), (64, 64, 64), (128, 128, 128),
                                    (255, 257, 130), (300, 64, 1000), (513, 129, 72),
                                    (1024, 1024, 256), (33, 4097, 520)])
 def test_bf16_small_shapes(tx, oracle, dev, M, N, K):
-    from tx import workloads
+    import workloads
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=M * 7 + N)
     C = tx.dot(_t_bf16(A, dev), _t_bf16(B, dev))
     r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
@@ -74,7 +86,7 @@ def test_bf16_small_shapes(tx, oracle, dev, M, N, K):
 def test_bf16_narrow_tile_and_split_k(tx, oracle, dev, M, N, K):
     """Fewer 256x256 tiles than CUs: 256x128 tiles, and K split into fp32
     partial planes (8 and 4 splits here, N not a multiple of 4 in the last)."""
-    from tx import workloads
+    import workloads
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=M + N)
     C = tx.dot(_t_bf16(A, dev), _t_bf16(B, dev))
     r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
@@ -86,7 +98,7 @@ def test_bf16_padded_fast_path(tx, oracle, dev, K):
     """Rows not 16-byte aligned in a product of >= 2^30 multiply-adds: the
     operands are copied into zero-padded rows and take the fast path (row
     lengths of 2006, 2004 and 2008 bytes: source loads of 2, 4 and 8 bytes)."""
-    from tx import workloads
+    import workloads
     M, N = 1100, 1040
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=77)
     C = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
@@ -97,10 +109,10 @@ def test_bf16_padded_fast_path(tx, oracle, dev, K):
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (4095, 4097, 4100)])
 def test_bf16_config_shapes(tx, oracle, dev, M, N, K):
-    from tx import workloads
+    import workloads
     A, B = workloads.bf16_gemm_input(M, N, K)
     C = _np_bits(tx.dot(_t_bf16(A, dev), _t_bf16(B, dev)))
-    rows = sample_rows(M)
+    rows = sorted(set(block_rows(M, seed=M)) | set(sample_rows(M)))
     for r in rows:
         r32, r16 = oracle.gemm_bf16_rows(A, B, r, r + 1)
         check_close(C[r:r + 1], r32, r16, BF16_TOL)
@@ -119,7 +131,7 @@ def test_bf16_output_rounding_exact(tx, oracle, dev, M, N, K):
     tie).  Row 0 of A holds +Inf, row 1 a NaN: Inf * b keeps b's sign, Inf * 0
     and NaN * b are NaN.  Shapes cover the 256x256 and 256x128 tiles, split K
     and the generic kernel."""
-    from tx import workloads
+    import workloads
     g = np.random.default_rng(M + K)
     a = np.zeros((M, K), np.float32)
     a[np.arange(M), np.arange(M) % K] = g.uniform(0.5, 2.0, M) * g.choice([-1.0, 1.0], M)
@@ -148,7 +160,7 @@ def test_scratch_reuse_across_streams(tx, oracle, dev):
     library keeps per stream: shapes that grow and shrink it, interleaved on
     two streams with no synchronisation between the calls, all come out
     right."""
-    from tx import workloads
+    import workloads
     shapes = [(300, 500, 4096), (1100, 1040, 1003), (257, 501, 2048), (600, 1000, 2050),
               (130, 260, 8192), (1024, 1100, 1001)]
     inputs = [workloads.bf16_gemm_input(M, N, K, seed_stream=40 + i) for i, (M, N, K) in enumerate(shapes)]
@@ -169,7 +181,7 @@ def test_scratch_reuse_across_streams(tx, oracle, dev):
 
 
 def test_bf16_strided_and_unaligned(tx, oracle, dev):
-    from tx import workloads
+    import workloads
     M, N, K = 200, 150, 333
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=99)
     # odd row strides force the narrow-load kernel variants
@@ -194,7 +206,7 @@ def test_bf16_degenerate(tx, dev):
 
 
 def test_bf16_matmul_wrapper_and_table(tx, oracle, dev):
-    from tx import workloads
+    import workloads
     M, N, K = 96, 80, 64
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=5)
     b_kn = _t_bf16(B, dev).t()  # column-major K x N view
@@ -217,7 +229,7 @@ def _fp8_run(tx, dev, aq, sa, bq, sb, fa=torch.float8_e4m3fn, fb=torch.float8_e4
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (16, 48, 128), (100, 200, 300), (256, 256, 512),
                                    (16, 1000, 4096), (600, 300, 260)])
 def test_fp8_small_shapes(tx, oracle, dev, M, N, K):
-    from tx import workloads
+    import workloads
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=M + 3 * N)
     C = _fp8_run(tx, dev, aq, sa, bq, sb)
     r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, M)
@@ -249,7 +261,7 @@ def test_fp8_format_mixes(tx, oracle, dev, fa, fb):
 def test_fp8_narrow_tile_and_split_k(tx, oracle, dev, M, N, K, fa, fb):
     """256x128 tiles with K split into fp32 partial planes; the scales are
     applied by the reduction."""
-    from tx import workloads
+    import workloads
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=M * 3 + N)
     td = {1: torch.float8_e4m3fn, 2: torch.float8_e5m2}
     if fa == 2:  # reinterpret the e4m3 codes as e5m2: finite, wider range
@@ -263,7 +275,7 @@ def test_column_tail_strip(tx, oracle, dev):
     """N just past a multiple of 256 where the last tile column would cost a
     whole round: the full columns take 256x256 tiles, the tail a second,
     split-K product."""
-    from tx import workloads
+    import workloads
     M, N, K = 4096, 4112, 1024
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=21)
     C = _fp8_run(tx, dev, aq, sa, bq, sb)
@@ -281,7 +293,7 @@ def test_column_tail_strip(tx, oracle, dev):
 def test_tall_narrow_fast_path(tx, oracle, dev):
     """N below one 256-column block with enough row tiles to fill every CU:
     no column strip is split off (it would leave nothing for the main tiles)."""
-    from tx import workloads
+    import workloads
     # rows are few columns wide: check the sampled rows as one set
     M, N, K = 65536 + 40, 40, 256
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=23)
@@ -302,7 +314,7 @@ def test_tall_narrow_fast_path(tx, oracle, dev):
 def test_fp8_padded_fast_path(tx, oracle, dev):
     """Odd K (rows not 16-byte aligned) in a product of >= 2^30 multiply-adds:
     zero-padded copies of the operands take the fast path."""
-    from tx import workloads
+    import workloads
     M, N, K = 1000, 1100, 1001
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=13)
     C = _fp8_run(tx, dev, aq, sa, bq, sb)
@@ -335,15 +347,25 @@ def test_fp8_skinny_shapes(tx, oracle, dev, M, N, K, fa, fb):
     check_close(C, r32, r16, FP8_TOL)
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (512, 14336, 4096), (16, 4096, 14336),
-                                   (512, 4096, 14336), (8192, 8192, 8192)])
+@pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (512, 14336, 4096), (8192, 14336, 4096),
+                                   (16, 4096, 14336), (512, 4096, 14336), (8192, 4096, 14336),
+                                   (8192, 8192, 8192)])
 def test_fp8_config_shapes(tx, oracle, dev, M, N, K):
-    from tx import workloads
+    """Every fp8 config shape: the oracle checks one row in every 128-row
+    block of C (each half of every 256-row tile) plus random rows, each row
+    over all N columns (every column tile); then full-size scale linearity."""
+    import workloads
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
     C = _fp8_run(tx, dev, aq, sa, bq, sb)
-    for r in sample_rows(M, k=8 if M * N * K > 1e11 else 16):
-        r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r, r + 1)
-        check_close(C[r:r + 1], r32, r16, FP8_TOL)
+    rows = sorted(set(block_rows(M, seed=M + N)) | set(sample_rows(M, k=8)))
+    r32 = np.empty((len(rows), N), np.float32)
+    r16 = np.empty((len(rows), N), np.uint16)
+    for i, r in enumerate(rows):
+        a32, a16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r, r + 1)
+        r32[i], r16[i] = a32[0], a16[0]
+    check_close(C[rows], r32, r16, FP8_TOL)
+    for i, r in enumerate(rows):  # and row by row: no row may hide behind the others
+        check_close(C[r:r + 1], r32[i:i + 1], r16[i:i + 1], FP8_TOL)
     # full-size property: scale linearity, C(2 * sa) == 2 * C bit-exactly
     C2 = _fp8_run(tx, dev, aq, (2 * sa).astype(np.float32), bq, sb)
     assert np.array_equal(bf16_f32(C2), 2 * bf16_f32(C))
@@ -352,7 +374,7 @@ def test_fp8_config_shapes(tx, oracle, dev, M, N, K):
 # --------------------------------------------------------------------- gemv
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_gemv_config_full(tx, oracle, dev, M):
-    from tx import workloads
+    import workloads
     x, wq, s = workloads.gemv_input(M)
     y = tx.gemv_fp8_dequant(_t_bf16(x, dev), torch.from_numpy(wq).to(dev).view(torch.float8_e5m2),
                             torch.from_numpy(s).to(dev))

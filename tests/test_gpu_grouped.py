@@ -209,7 +209,7 @@ def test_grouped_fused_epilogue(tx, oracle, dev, sizes, N, K, act, out, with_bia
     outputs are O(1) and fp32 accumulation error stays far below the bound;
     raw random codes make near-cancelling sums of 1e5-sized terms whose fp32
     error the bound, relative to the saturated output scale, cannot hold."""
-    from tx import workloads
+    import workloads
     g = np.random.default_rng(sum(sizes) + N + EPI_ACT[act])
     M = sum(sizes)
     off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)

@@ -161,7 +161,7 @@ def test_mx_quantised_config(tx, oracle, dev, M, N, K):
     """MX-quantised N(0,1) operands (the reference's quantiser idiom) at full
     size: sampled rows against the oracle, and the full-size scale property
     C(sa + 1) == 2 C bit-exactly."""
-    from tx import workloads
+    import workloads
     aq, sa, bq, sb = workloads.mx_gemm_input(M, N, K)
     got = _run(tx, dev, aq, sa, bq, sb, out="bf16")
     g = np.random.default_rng(1)

@@ -147,7 +147,7 @@ def test_table_entry_point(tx, oracle, dev):
 @pytest.mark.parametrize("kind", ["i32", "f32"])
 def test_zipf_config_full_size(tx, oracle, dev, kind):
     """67,108,864 Zipf(1.1) updates into 65,536 bins."""
-    from tx import workloads
+    import workloads
     idx, val = workloads.scatter_input(kind=kind)
     nbins = 65536
     init = np.zeros(nbins, np.int32 if kind == "i32" else np.float32)

@@ -16,7 +16,7 @@ sys.path.insert(0, os.path.join(HERE, "golden"))
 def test_every_mismatch_has_a_known_cause(oracle, fmt):
     pytest.importorskip("triton")
     import interpreter_fp8_mismatch as M
-    from tx import workloads
+    import workloads
     x = workloads.fp8_input(1 << 20, seed_stream=3)
     counts, n = M.classify(x, fmt)
     assert counts["other"] == 0, counts

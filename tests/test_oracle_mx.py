@@ -194,13 +194,13 @@ def test_fp4_dot_closed_form(oracle, K):
 
 
 def test_fp4_workload_quantiser_matches_triton_mxfp4(oracle):
-    """The benchmark's fp4 quantiser (tx.workloads.quant_mx_fp4): scales by
+    """The benchmark's fp4 quantiser (workloads.quant_mx_fp4): scales by
     the OCP rule floor(log2 absmax) - 2, codes equal to triton's MXFP4Tensor
     rounding of x / scale (packed by its to_packed_tensor), and every
     dequantised value within half an e2m1 step of x (or saturated at 6)."""
     torch = pytest.importorskip("torch")
     mxfp = pytest.importorskip("triton.tools.mxfp")
-    from tx import workloads
+    import workloads
     g = np.random.default_rng(0)
     x = (g.standard_normal((64, 256)) * np.exp2(g.integers(-10, 10, (64, 1)))).astype(np.float32)
     x[0, :32] = 0.0

@@ -96,9 +96,9 @@ def test_bf16_input_is_widened_exactly(oracle):
 
 
 def test_workload_generator_agrees(oracle):
-    """The benchmark's numpy MX quantiser (tx.workloads.quant_mx) gives the
+    """The benchmark's numpy MX quantiser (workloads.quant_mx) gives the
     oracle's bytes."""
-    from tx import workloads
+    import workloads
     g = np.random.default_rng(9)
     x = g.standard_normal((16, 512)).astype(np.float32)
     for name, fmt in (("e4m3fn", 1), ("e5m2", 2)):

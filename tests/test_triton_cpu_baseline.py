@@ -55,7 +55,7 @@ def test_scatter_matches_oracle(tc, oracle, kind):
 
 
 def test_gemm_fp8_matches_oracle(tc, oracle):
-    from tx import workloads
+    import workloads
     M, N, K = 40, 72, 200          # ragged against the 64 x 256 x 128 tile
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K)
     got = _bf16_bits_to_f32(tc.gemm_fp8(aq, bq, sa, sb)).reshape(M, N)
@@ -65,7 +65,7 @@ def test_gemm_fp8_matches_oracle(tc, oracle):
 
 
 def test_gemm_bf16_matches_oracle(tc, oracle):
-    from tx import workloads
+    import workloads
     M, N, K = 33, 65, 130
     a, b = workloads.bf16_gemm_input(M, N, K)
     got = _bf16_bits_to_f32(tc.gemm_bf16(a, b, tile=(32, 64, 64))).reshape(M, N)
@@ -74,7 +74,7 @@ def test_gemm_bf16_matches_oracle(tc, oracle):
 
 
 def test_gemv_matches_oracle(tc, oracle):
-    from tx import workloads
+    import workloads
     x, wq, s = workloads.gemv_input(3, 300, 512, 128)
     got = _bf16_bits_to_f32(tc.gemv(x, wq, s, 128, block_n=128)).reshape(3, 300)
     ref = _bf16_bits_to_f32(oracle.gemv_fp8_dequant(x, wq, s, 128)[1]).reshape(3, 300)

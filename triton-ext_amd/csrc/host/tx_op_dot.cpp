@@ -554,7 +554,7 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
                                       int64_t stride_c, const int32_t *offsets, int64_t groups,
                                       int64_t M, int64_t N, int64_t K, tx_stream_t stream,
                                       const Epilogue &e = Epilogue{}, size_t es = 2,
-                                      int64_t stride_bias = 0) {
+                                      int64_t stride_bias = 0, int32_t *prefix_ws = nullptr) {
   const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
   if (!fa || !fb)
     return fail(TX_INVALID_ARGUMENT, "%s: operand types must be fp8 (got %d, %d)", what, int(a_type),
@@ -615,8 +615,12 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
   ScratchLease pre;  // held until the product is enqueued
   hipFunction_t fn;
   if (grouped) {
-    TX_TRY(pre.acquire(s, 1, size_t(groups + 1) * sizeof(int32_t)));
-    q.tile_prefix = static_cast<int32_t *>(pre.ptr());
+    if (prefix_ws) {  // the caller's workspace (the no-allocation entry point)
+      q.tile_prefix = prefix_ws;
+    } else {
+      TX_TRY(pre.acquire(s, 1, size_t(groups + 1) * sizeof(int32_t)));
+      q.tile_prefix = static_cast<int32_t *>(pre.ptr());
+    }
     TX_TRY(get_kernel(CodeObject::GemmFp8, "tx_gemm_fp8_grouped_prefix", &fn));
     TX_TRY(launch(fn, 1, 1, 256, s, &q, sizeof q, "tx_gemm_fp8_grouped_prefix"));
   }
@@ -628,20 +632,32 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
   return launch(fn, unsigned(mtiles * tiles_n), 1, 64 * kFastWaves, s, &q, sizeof q, kname);
 }
 
-static tx_status dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
-                                        const void *B, tx_dtype b_type, int64_t ldb, int64_t stride_b,
-                                        const float *sb, int64_t stride_sb, const float *bias,
-                                        int64_t stride_bias, int activation, void *C, tx_dtype c_type,
-                                        float c_scale, int64_t ldc, const int32_t *offsets, int64_t groups,
-                                        int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
-  const char *what = "tx_dot_fp8_scaled_grouped";
+// The grouped product with an optional caller workspace for the group tile
+// prefix (groups + 1 int32); NULL: the library's stream scratch.
+tx_status dot_fp8_scaled_grouped_ws(const char *what, const void *A, tx_dtype a_type, int64_t lda,
+                                    const float *sa, const void *B, tx_dtype b_type, int64_t ldb,
+                                    int64_t stride_b, const float *sb, int64_t stride_sb, const float *bias,
+                                    int64_t stride_bias, int activation, void *C, tx_dtype c_type,
+                                    float c_scale, int64_t ldc, const int32_t *offsets, int64_t groups,
+                                    int64_t M, int64_t N, int64_t K, tx_stream_t stream, int32_t *prefix_ws) {
   if (!offsets && groups > 0 && M > 0 && N > 0)
     return fail(TX_INVALID_ARGUMENT, "%s: NULL group offsets", what);
   Epilogue e;
   size_t es;
   TX_TRY(make_epilogue(what, bias, activation, c_type, c_scale, &e, &es));
   return dot_fp8_grouped_impl(what, A, a_type, lda, 0, sa, 0, B, b_type, ldb, stride_b, sb, stride_sb, C,
-                              ldc, 0, offsets, groups, M, N, K, stream, e, es, stride_bias);
+                              ldc, 0, offsets, groups, M, N, K, stream, e, es, stride_bias, prefix_ws);
+}
+
+static tx_status dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64_t lda, const float *sa,
+                                        const void *B, tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                        const float *sb, int64_t stride_sb, const float *bias,
+                                        int64_t stride_bias, int activation, void *C, tx_dtype c_type,
+                                        float c_scale, int64_t ldc, const int32_t *offsets, int64_t groups,
+                                        int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  return dot_fp8_scaled_grouped_ws("tx_dot_fp8_scaled_grouped", A, a_type, lda, sa, B, b_type, ldb,
+                                       stride_b, sb, stride_sb, bias, stride_bias, activation, C, c_type,
+                                       c_scale, ldc, offsets, groups, M, N, K, stream, nullptr);
 }
 
 static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_dtype w_type,

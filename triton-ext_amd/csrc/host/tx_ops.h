@@ -45,6 +45,17 @@ struct Operands {
   }
 };
 
+// The grouped fp8 dot (tx_dot_fp8_scaled_grouped) with an optional caller
+// workspace for its group tile prefix (groups + 1 int32 on the device);
+// NULL uses the library's stream scratch.  `what` names the entry point in
+// error messages.
+tx_status dot_fp8_scaled_grouped_ws(const char *what, const void *A, tx_dtype a_type, int64_t lda,
+                                    const float *sa, const void *B, tx_dtype b_type, int64_t ldb,
+                                    int64_t stride_b, const float *sb, int64_t stride_sb, const float *bias,
+                                    int64_t stride_bias, int activation, void *C, tx_dtype c_type,
+                                    float c_scale, int64_t ldc, const int32_t *offsets, int64_t groups,
+                                    int64_t M, int64_t N, int64_t K, tx_stream_t stream, int32_t *prefix_ws);
+
 #define TX_TRY(expr)                      \
   do {                                    \
     tx_status _s = (expr);                \

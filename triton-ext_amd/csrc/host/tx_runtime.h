@@ -31,7 +31,8 @@ tx_status fail(tx_status status, const char *fmt, ...)
 void clear_error();
 
 // Resolve kernel `name` of code object `co` on the current device, loading
-// that device's code objects on first use.
+// that device's code objects on first use.  Every kernel handle is resolved
+// at load time into a table that is only read afterwards: no lock, no scan.
 tx_status get_kernel(CodeObject co, const char *name, hipFunction_t *out);
 
 // Enqueue `fn` with one by-value argument block of `args_size` bytes.
@@ -49,11 +50,13 @@ int cu_count();
 // the new one in stream order (hipFreeAsync / hipMallocAsync on the stream):
 // work already enqueued keeps its memory.  Larger requests get a buffer of
 // their own, freed in stream order when the lease ends.  A lease holds the
-// device's scratch lock from acquire() until it is destroyed, so the caller
-// enqueues every launch that uses the buffer while holding it; two calls on
-// one stream from different threads therefore never see one buffer change
-// under them.  (A stream handle that is destroyed and handed out again keeps
-// its predecessor's buffer; its work must have finished, as for any reuse of
+// lock of its (stream, slot) buffer from acquire() until it is destroyed,
+// so the caller enqueues every launch that uses the buffer while holding
+// it: two calls on one stream from different threads never see one buffer
+// change under them, and calls on other streams or slots never wait for
+// it.  A thread asking for a slot it already holds gets an error.  (A
+// stream handle that is destroyed and handed out again keeps its
+// predecessor's buffer; its work must have finished, as for any reuse of
 // memory.)  txShutdown frees the kept buffers.
 constexpr size_t kKeptScratch = size_t(512) << 20;
 
@@ -71,7 +74,7 @@ class ScratchLease {
   void *ptr_ = nullptr;
   hipStream_t stream_ = nullptr;
   bool own_ = false;    // a per-call buffer, freed by the destructor
-  void *lock_ = nullptr;  // the device's scratch mutex while held
+  void *lock_ = nullptr;  // the (stream, slot) buffer whose lock this lease holds
 };
 
 // Free every kept scratch buffer of every device (txShutdown).

@@ -205,6 +205,10 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   // (K = 0: empty ranges, so the prologue's loads read nothing at all)
   const __amdgpu_buffer_rsrc_t rsrc[2] = {make_rsrc(a.A, kb_end ? uint32_t(a.M - 1) * lda_b + kb_end : 0u),
                                           make_rsrc(a.B, kb_end ? uint32_t(a.N - 1) * ldb_b + kb_end : 0u)};
+  // Loads of steps past the last one (the pipeline's look-ahead at the end of
+  // the K loop) go through an empty range: every lane is out of range
+  // whatever its offsets, so they read zeros and touch no memory.
+  const __amdgpu_buffer_rsrc_t rnull[2] = {make_rsrc(a.A, 0u), make_rsrc(a.B, 0u)};
 
   // DMA assignment: wave w fills blocks BLKA*w .. of A and BLKB*w .. of B.
   // Lane i of block q covers row 8q + i/8 and logical chunk
@@ -226,30 +230,40 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
     const int gn = n0 + row;
     vo[1][j] = gn < a.N ? uint32_t(gn) * ldb_b + kch[j & 1] : kOob;
   }
-  // Load block j of operand op of (split-local) step ks into slot `slot`.
-  // Steps past the split's end are loaded but never multiplied.  With TAIL
-  // (K * element size not a multiple of the step), a lane whose chunk lies
-  // past the row end reads zeros; otherwise no chunk ever does, and the load
+  // Source of operand op for (split-local) step ks: its buffer range and K
+  // offset.  Steps past the split's end are loaded but never multiplied;
+  // those past the operand's last step read through the empty range (scalar
+  // selects, once per step and operand).
+  struct Src {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t so;
+  };
+  auto src = [&](int ks, int op) {
+    const bool live = kfirst + ks < ksteps_all;
+    return Src{live ? rsrc[op] : rnull[op], live ? kbase + uint32_t(ks) * kStep : 0u};
+  };
+  // Load block j of operand op from `sr` into slot `slot`.  With TAIL (K *
+  // element size not a multiple of the step), a lane whose chunk lies past
+  // the row end reads zeros; otherwise no chunk ever does, and the load
   // takes its per-lane offset as it is (no vector instructions per load).
-  auto load_op = [&](int ks, int slot, auto op_tag, auto j_tag, auto tail_tag) {
+  auto load_op = [&](const Src &sr, int slot, auto op_tag, auto j_tag, auto tail_tag) {
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     constexpr int blk = op == 0 ? BLKA : BLKB;
-    const uint32_t so = kbase + uint32_t(ks) * kStep;
     uint32_t voff = vo[op][j];
     if constexpr (decltype(tail_tag)::value) {
-      if (so + kch[j & 1] >= kb_end) voff = kOob;
+      if (sr.so + kch[j & 1] >= kb_end) voff = kOob;
     }
     uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[op], (lds_void *)dst, 16, voff, so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(sr.rs, (lds_void *)dst, 16, voff, sr.so, 0, 0);
   };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
   // Load d of the second half of step ks: B of step ks+2 into the slot of A
   // of step ks (d < BLKB), then A of step ks+3 into the slot of B of step ks.
-  auto load = [&](int ks, int slot_a, int slot_b, auto d_tag, auto tail_tag) {
+  auto load = [&](const Src &srb, const Src &sra, int slot_a, int slot_b, auto d_tag, auto tail_tag) {
     constexpr int d = decltype(d_tag)::value;
-    if constexpr (d < BLKB) load_op(ks + 2, slot_a, OpB{}, std::integral_constant<int, d>{}, tail_tag);
-    else load_op(ks + 3, slot_b, OpA{}, std::integral_constant<int, d - BLKB>{}, tail_tag);
+    if constexpr (d < BLKB) load_op(srb, slot_a, OpB{}, std::integral_constant<int, d>{}, tail_tag);
+    else load_op(sra, slot_b, OpA{}, std::integral_constant<int, d - BLKB>{}, tail_tag);
   };
 
   // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
@@ -346,11 +360,14 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
     // step 0 landed, half 0 of step 0 in registers.  The MX scales of step 0
     // go first, so the same wait covers them.
     load_scales(0, scn);
-    static_for<BLKA>([&](auto j) { load_op(0, 0, OpA{}, j, tail); });
-    static_for<BLKB>([&](auto j) { load_op(0, 1, OpB{}, j, tail); });
-    static_for<BLKA>([&](auto j) { load_op(1, 2, OpA{}, j, tail); });
-    static_for<BLKB>([&](auto j) { load_op(1, 3, OpB{}, j, tail); });
-    static_for<BLKA>([&](auto j) { load_op(2, 4, OpA{}, j, tail); });
+    {
+      const Src a0 = src(0, 0), b0 = src(0, 1), a1 = src(1, 0), b1 = src(1, 1), a2 = src(2, 0);
+      static_for<BLKA>([&](auto j) { load_op(a0, 0, OpA{}, j, tail); });
+      static_for<BLKB>([&](auto j) { load_op(b0, 1, OpB{}, j, tail); });
+      static_for<BLKA>([&](auto j) { load_op(a1, 2, OpA{}, j, tail); });
+      static_for<BLKB>([&](auto j) { load_op(b1, 3, OpB{}, j, tail); });
+      static_for<BLKA>([&](auto j) { load_op(a2, 4, OpA{}, j, tail); });
+    }
     wait_and_barrier<2 * BLKA + BLKB>();
     static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
 
@@ -377,13 +394,14 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
       wait_and_barrier<BLKA>();
       __builtin_amdgcn_sched_barrier(0);
       load_scales(ks + 1, scn);  // MX: ahead of this half's DMA loads
+      const Src srb = src(ks + 2, 1), sra = src(ks + 3, 0);
       static_for<NM>([&](auto I) {
         constexpr int i = decltype(I)::value;
         mma(H1{}, I);
         __builtin_amdgcn_sched_barrier(0);
         constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
         static_for<d1 - d0>([&](auto D) {
-          load(ks, sa, sb, std::integral_constant<int, d0 + decltype(D)::value>{}, tail);
+          load(srb, sra, sa, sb, std::integral_constant<int, d0 + decltype(D)::value>{}, tail);
         });
         constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
         static_for<r1 - r0>([&](auto R) {

@@ -441,16 +441,27 @@ def quantize_rowwise(x: torch.Tensor, dtype: torch.dtype = torch.float8_e4m3fn):
 
 def gemv_fp8_dequant(x: torch.Tensor, w_q: torch.Tensor, scales: torch.Tensor, group: int = 128,
                      out: torch.Tensor | None = None) -> torch.Tensor:
-    """Weight-only fp8 GEMV: out[M,N] = bf16(x[M,K] @ (w_q[N,K] * scales[N, k//group]).T)."""
-    _on_gpu(x, w_q, scales, out)
+    """Weight-only fp8 GEMV: out[M,N] = bf16(x[M,K] @ (w_q[N,K] * scales[N, k//group]).T).
+
+    x: bf16 M x K, w_q: fp8 N x K, scales: fp32 N x ceil(K / group), all with
+    contiguous rows; out (optional): a row-major bf16 M x N tensor.  Shapes
+    and types are checked before the device (on CPU tensors too)."""
     if x.dtype != torch.bfloat16 or w_q.dtype not in _FP8 or scales.dtype != torch.float32:
         raise ValueError("x bf16, w_q fp8, scales fp32")
+    if x.dim() != 2 or w_q.dim() != 2 or scales.dim() != 2:
+        raise ValueError("x, w_q and scales must be 2-D")
+    if group <= 0:
+        raise ValueError("group must be positive")
     M, K = x.shape
     N = w_q.shape[0]
-    if w_q.shape[1] != K or scales.shape[0] != N:
-        raise ValueError("incompatible shapes")
+    if w_q.shape[1] != K or tuple(scales.shape) != (N, -(-K // group)):
+        raise ValueError(f"incompatible shapes: x {tuple(x.shape)}, w_q {tuple(w_q.shape)}, "
+                         f"scales {tuple(scales.shape)} (want {N} x {-(-K // group)})")
     if x.stride(1) != 1 or w_q.stride(1) != 1 or scales.stride(1) != 1:
         raise ValueError("rows must be contiguous")
+    if out is not None and (out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1):
+        raise ValueError("out must be a row-major bf16 M x N tensor")
+    _on_gpu(x, w_q, scales, out)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     check(lib.tx_gemv_fp8_dequant(_ptr(x), x.stride(0), _ptr(w_q), _TX_DTYPE[w_q.dtype],
