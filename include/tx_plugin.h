@@ -332,6 +332,30 @@ TX_API tx_status tx_dot_fp8_scaled_grouped(const void *A, tx_dtype a_type, int64
                                            tx_stream_t stream);
 
 /*
+ * tx_dot_fp8_scaled_grouped for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, checks and
+ * results as tx_dot_fp8_scaled_grouped; its group tile prefix lives in a
+ * fixed 64 KiB device array, one per GPU, held until the process ends, so
+ * groups is at most 16383 (more: TX_UNSUPPORTED).  It calls no hipMalloc,
+ * hipFree or other allocating routine once txInit() has run on the device
+ * (txInit loads the code objects and looks up the array; without it the
+ * first call on a device does both).  All calls on one GPU share the
+ * array: calls that overlap on one GPU (different streams, or unordered
+ * threads) race.
+ */
+TX_API tx_status tx_dot_fp8_scaled_grouped_noalloc(const void *A, tx_dtype a_type, int64_t lda,
+                                                   const float *scale_a, const void *B,
+                                                   tx_dtype b_type, int64_t ldb, int64_t stride_b,
+                                                   const float *scale_b, int64_t stride_scale_b,
+                                                   const float *bias, int64_t stride_bias,
+                                                   int activation, void *C, tx_dtype c_type,
+                                                   float c_scale, int64_t ldc,
+                                                   const int32_t *group_offsets, int64_t groups,
+                                                   int64_t M, int64_t N, int64_t K,
+                                                   tx_stream_t stream);
+
+/*
  * Batched tx_dot_fp8_scaled: `batch` products of one shape in one launch,
  * product p on A + p * stride_a bytes, scale_a + p * stride_scale_a,
  * B + p * stride_b bytes, scale_b + p * stride_scale_b and C + p * stride_c

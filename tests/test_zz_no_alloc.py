@@ -1,0 +1,79 @@
+"""GPU: tx_dot_fp8_scaled_grouped_noalloc (the grouped fp8 dot whose group
+tile prefix lives in the library's fixed device array instead of allocated
+scratch) against tx_dot_fp8_scaled_grouped, through the C ABI.
+
+Both entry points run the same kernels in the same order, so the outputs
+must be bit-identical.  Two calls in a row, the second smaller (fewer
+groups and rows, and the fused epilogue), so the second reads a prefix
+array that still holds the first call's longer contents.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _codes(g, *shape):
+    c = g.integers(0, 0x7F, size=shape, dtype=np.uint8)   # finite e4m3fn magnitudes
+    return c | (g.integers(0, 2, size=shape, dtype=np.uint8) << 7)
+
+
+def _problem(dev, seed, groups, M, N, K):
+    g = np.random.default_rng(seed)
+    sizes = g.multinomial(M, np.ones(groups) / groups)
+    sizes[groups // 2] = 0                          # an empty group
+    sizes[0] += M - sizes.sum()
+    off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    t = dict(
+        A=torch.from_numpy(_codes(g, M, K)).to(dev).view(torch.float8_e4m3fn),
+        B=torch.from_numpy(_codes(g, groups, N, K)).to(dev).view(torch.float8_e4m3fn),
+        sa=torch.from_numpy(g.uniform(0.5, 2, M).astype(np.float32) * 1e-3).to(dev),
+        sb=torch.from_numpy(g.uniform(0.5, 2, (groups, N)).astype(np.float32) * 1e-3).to(dev),
+        bias=torch.from_numpy(g.standard_normal((groups, N)).astype(np.float32)).to(dev),
+        off=torch.from_numpy(off).to(dev),
+    )
+    return t, groups, M, N, K
+
+
+def _noalloc(tx, t, groups, M, N, K, out, bias, act, c_type, c_scale):
+    L, lib = tx.lib, tx._lib
+    st = L.tx_dot_fp8_scaled_grouped_noalloc(
+        ctypes.c_void_p(t["A"].data_ptr()), lib.FP8E4M3FN, K, ctypes.c_void_p(t["sa"].data_ptr()),
+        ctypes.c_void_p(t["B"].data_ptr()), lib.FP8E4M3FN, K, N * K, ctypes.c_void_p(t["sb"].data_ptr()), N,
+        None if bias is None else ctypes.c_void_p(bias.data_ptr()), 0 if bias is None else N, act,
+        ctypes.c_void_p(out.data_ptr()), c_type, c_scale, N, ctypes.c_void_p(t["off"].data_ptr()),
+        groups, M, N, K, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, (st, lib.last_error())
+
+
+def test_noalloc_grouped_matches_the_allocating_entry(tx, dev):
+    # call 1: 6 groups over 1000 rows, bf16 out
+    t, G, M, N, K = _problem(dev, 1, 6, 1000, 384, 256)
+    ref = tx.dot_scaled_rowcol_grouped(t["A"], t["sa"], t["B"], t["sb"], t["off"])
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    _noalloc(tx, t, G, M, N, K, out, None, tx._lib.ACT_NONE, tx._lib.BF16, 1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    # call 2, right after and smaller: 3 groups over 300 rows, bias + gelu -> e4m3fn
+    t2, G2, M2, N2, K2 = _problem(dev, 2, 3, 300, 384, 256)
+    ref2 = tx.dot_scaled_rowcol_grouped(t2["A"], t2["sa"], t2["B"], t2["sb"], t2["off"], bias=t2["bias"],
+                                        activation="gelu_tanh", out_dtype=torch.float8_e4m3fn, out_scale=0.25)
+    out2 = torch.zeros((M2, N2), dtype=torch.float8_e4m3fn, device=dev)
+    _noalloc(tx, t2, G2, M2, N2, K2, out2, t2["bias"], tx._lib.ACT_GELU_TANH, tx._lib.FP8E4M3FN, 0.25)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.view(torch.uint8), ref2.view(torch.uint8))
+    assert torch.count_nonzero(out2.view(torch.uint8)) > 0
+
+
+def test_noalloc_grouped_rejects_too_many_groups(tx, dev):
+    t, G, M, N, K = _problem(dev, 3, 4, 64, 64, 128)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    st = tx.lib.tx_dot_fp8_scaled_grouped_noalloc(
+        ctypes.c_void_p(t["A"].data_ptr()), tx._lib.FP8E4M3FN, K, ctypes.c_void_p(t["sa"].data_ptr()),
+        ctypes.c_void_p(t["B"].data_ptr()), tx._lib.FP8E4M3FN, K, N * K, ctypes.c_void_p(t["sb"].data_ptr()), N,
+        None, 0, 0, ctypes.c_void_p(out.data_ptr()), tx._lib.BF16, 1.0, N, ctypes.c_void_p(t["off"].data_ptr()),
+        16384, M, N, K, None)
+    assert st == tx._lib.UNSUPPORTED and "16383" in tx._lib.last_error()

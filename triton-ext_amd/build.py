@@ -89,8 +89,17 @@ def write_embed(paths) -> str:
     return asm
 
 
+# Host sources that also define device data (the no-allocation entry point's
+# workspace array): compiled by hipcc for the host and gfx950, registered
+# with the HIP runtime when the library loads.
+HIP_HOST_FLAGS = [
+    f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-fno-exceptions",
+    "-fno-rtti", "-Wall", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
 def build_host(asm: str) -> str:
-    srcs = sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp")) + glob.glob(os.path.join(CSRC, "host", "*.hip")))
     objs = []
     inc = ["-I", os.path.join(REPO, "include"), "-I", CSRC, "-I", os.path.join(CSRC, "host"),
            "-I", os.path.join(ROCM, "include")]
@@ -98,7 +107,10 @@ def build_host(asm: str) -> str:
 
     def compile_one(src):
         obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-        _run([cxx, *HOST_FLAGS, *inc, "-c", src, "-o", obj])
+        if src.endswith(".hip"):
+            _run([_hipcc(), *HIP_HOST_FLAGS, *inc, "-c", src, "-o", obj])
+        else:
+            _run([cxx, *HOST_FLAGS, *inc, "-c", src, "-o", obj])
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=4) as ex:

@@ -401,8 +401,12 @@ TX_API tx_status txInit(void) {
   tx::clear_error();
   hipFunction_t fn;
   // Loading happens inside device_state; resolving one kernel proves the
-  // code objects are usable.
-  return tx::get_kernel(tx::CodeObject::Fp8Codec, "tx_fp8_decode_e4m3fn_vec", &fn);
+  // code objects are usable.  The no-allocation entry point's workspace is
+  // looked up here too, so that entry point allocates nothing later.
+  tx_status s = tx::get_kernel(tx::CodeObject::Fp8Codec, "tx_fp8_decode_e4m3fn_vec", &fn);
+  if (s != TX_SUCCESS) return s;
+  void *ws = nullptr;
+  return tx::noalloc_scratch(&ws);
 }
 
 TX_API void txShutdown(void) {

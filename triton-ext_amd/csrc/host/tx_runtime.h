@@ -40,6 +40,10 @@ tx_status launch(hipFunction_t fn, unsigned grid_x, unsigned grid_y,
                  unsigned block_x, hipStream_t stream, void *args,
                  size_t args_size, const char *what);
 
+// The current device's copy of the no-allocation entry point's workspace
+// (tx_noalloc.hip), its address looked up once per device.
+tx_status noalloc_scratch(void **out);
+
 // Number of compute units of the current device (cached per device).
 int cu_count();
 

@@ -41,7 +41,8 @@ EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
-    "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped", "tx_dot_fp8_scaled_batched",
+    "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped",
+    "tx_dot_fp8_scaled_grouped_noalloc", "tx_dot_fp8_scaled_batched",
     "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
     "tx_gemv_fp8_dequant",
 ]
@@ -128,6 +129,9 @@ def _load():
     L.tx_dot_fp8_scaled_grouped.argtypes = [P, I, I64, P, P, I, I64, I64, P, I64, P, I64, I, P, I, ctypes.c_float,
                                             I64, P, I64, I64, I64, I64, P]
     L.tx_dot_fp8_scaled_grouped.restype = I
+    L.tx_dot_fp8_scaled_grouped_noalloc.argtypes = [P, I, I64, P, P, I, I64, I64, P, I64, P, I64, I, P, I, ctypes.c_float,
+                                            I64, P, I64, I64, I64, I64, P]
+    L.tx_dot_fp8_scaled_grouped_noalloc.restype = I
     L.tx_dot_fp8_scaled_batched.argtypes = [P, I, I64, I64, P, I64, P, I, I64, I64, P, I64, P, I64, I64, I64,
                                             I64, I64, I64, P]
     L.tx_dot_fp8_scaled_batched.restype = I
