@@ -52,8 +52,41 @@ BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
 MALL_BYTES = 256 << 20
 
 
-def progress(step):
+def progress(step, algo_bytes=None):
+    """Report a finished workload; the launch windows timed() recorded since
+    the last call are labelled with it (for --windows)."""
+    for w in _PENDING_WINDOWS:
+        WINDOWS.append(dict(w, workload=step, algo_bytes=algo_bytes))
+    _PENDING_WINDOWS.clear()
     print(f"bench: {step} done ({time.perf_counter() - T_START:.1f} s)", file=sys.stderr, flush=True)
+
+
+# Host-clock intervals around each workload's launches, in the two clocks a
+# profiler may stamp dispatches with, so counter records can be assigned to
+# workloads afterwards (--windows, --pmc-summary).
+WINDOWS = []
+_PENDING_WINDOWS = []
+
+
+def _clocks():
+    return {"boot": time.clock_gettime_ns(time.CLOCK_BOOTTIME), "mono": time.monotonic_ns()}
+
+
+def build_digest():
+    """Digest of everything the device code and the library are built from:
+    the sources under triton-ext_amd/csrc and the build script.  Counter
+    tables carry the digest of the build they were measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    root = os.path.join(REPO, "triton-ext_amd")
+    files = [os.path.join(root, "build.py")]
+    for d, _, names in os.walk(os.path.join(root, "csrc")):
+        files += [os.path.join(d, n) for n in names if n.endswith((".hip", ".h", ".cpp", ".c"))]
+    for f in sorted(files):
+        h.update(os.path.relpath(f, REPO).encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
 
 
 T_START = time.perf_counter()
@@ -69,10 +102,16 @@ def parse():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run only a 256 MiB device copy (known-size kernel for scaling the "
                         "FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV",
-                                                     "CAL_WRITE_CSV"),
-                   help="print the HBM traffic table from rocprofv3 counter_collection.csv files "
-                        "of a --quick run and of a --calibrate-copy run")
+    p.add_argument("--windows", metavar="JSON",
+                   help="write each workload's launch windows (host clocks) and the build digest")
+    p.add_argument("--pmc-summary", nargs=6, metavar=("FETCH_WINDOWS", "FETCH_CSV", "WRITE_WINDOWS",
+                                                     "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
+                   help="print the HBM traffic table from the rocprofv3 counter_collection.csv "
+                        "files of two --windows runs (FETCH_SIZE, WRITE_SIZE) and of two "
+                        "--calibrate-copy runs")
+    p.add_argument("--mfma-summary", nargs=2, metavar=("WINDOWS_JSON", "MFMA_CSV"),
+                   help="print MFMA busy and clock per GEMM workload from a --windows run "
+                        "counted with SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, SQ_BUSY_CYCLES")
     return p.parse_args()
 
 
@@ -83,6 +122,8 @@ def timed(fn, steps, warmup):
     """Average ms per launch of fn(i) over exactly `steps` launches, after the
     clock pre-roll and `warmup` untimed launches."""
     import torch
+    torch.cuda.synchronize()
+    window = {"t0": _clocks()}
     t0 = time.perf_counter()
     i = 0
     while time.perf_counter() - t0 < PREROLL_S:
@@ -101,6 +142,8 @@ def timed(fn, steps, warmup):
     end.record()
     end.synchronize()
     torch.cuda.synchronize()
+    window["t1"] = _clocks()
+    _PENDING_WINDOWS.append(window)
     return start.elapsed_time(end) / steps
 
 
@@ -276,6 +319,61 @@ def bench_fp8_convert(tx, torch, steps, warmup, n=16_777_216):
             "decode_ms": ms_dec, "decode_gbs": dec_gbs}
 
 
+def bench_convert_pair(tx, torch, src, dst, steps, warmup, n=16_777_216):
+    """tt.fp_to_fp between two of bf16 / fp16 / e4m3fn / e5m2 (RNE, not
+    saturating); the source is the fp32 workload cast (RNE) to `src`."""
+    import workloads
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(workloads.fp8_input(n)).to(dev)
+    if src.itemsize == 1:
+        x = tx.fp_to_fp(x, src)
+    else:
+        x = x.to(src)
+    per = src.itemsize + dst.itemsize
+    sets = ring_count(per * n)
+    xs = [x.clone() for _ in range(sets)]
+    ys = [torch.empty(n, dtype=dst, device=dev) for _ in range(sets)]
+    ms = timed(lambda i: tx.fp_to_fp(xs[i % sets], dst, out=ys[i % sets]), steps, warmup)
+    return {"ms": ms, "gbs": per * n / (ms * 1e-3) / 1e9, "bytes": per * n, "sets": sets}
+
+
+def bench_encode_sizes(tx, torch, steps, warmup, sizes=(67_108_864, 268_435_456)):
+    """The headline encode at larger sizes: per-launch fixed cost (wave launch,
+    the first bytes' latency, the drain) weighs less as the size grows."""
+    import workloads
+    dev = torch.device("cuda:0")
+    base = torch.from_numpy(workloads.fp8_input(16_777_216)).to(dev)
+    out = {}
+    for n in sizes:
+        sets = ring_count(5 * n)
+        xs = [base.repeat(n // base.numel()) for _ in range(sets)]
+        qs = [torch.empty(n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(sets)]
+        ms = timed(lambda i: tx.fp_to_fp(xs[i % sets], torch.float8_e4m3fn, out=qs[i % sets]), steps, warmup)
+        out[n] = (ms, 5.0 * n)
+        del xs, qs
+    return out
+
+
+def bench_torch_streams(torch, steps, warmup, n=16_777_216):
+    """torch's own kernels over the convert's 16 Mi fp32 values, for reference:
+    a cast to uint8 (the encode's 4 B -> 1 B traffic shape), a device copy
+    (the runtime's copy kernel) and a sum (read only)."""
+    dev = torch.device("cuda:0")
+    out = {}
+    sets = ring_count(5 * n)
+    xs = [torch.randn(n, device=dev) for _ in range(sets)]
+    ys = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(sets)]
+    ms = timed(lambda i: ys[i % sets].copy_(xs[i % sets]), steps, warmup)
+    out["cast fp32->uint8 (4 B read, 1 B written per value)"] = (ms, 5.0 * n)
+    zs = [torch.empty(n, device=dev) for _ in range(sets)]
+    ms = timed(lambda i: zs[i % sets].copy_(xs[i % sets]), steps, warmup)
+    out["copy fp32 (4 B read, 4 B written per value)"] = (ms, 8.0 * n)
+    acc = torch.empty((), device=dev)
+    ms = timed(lambda i: torch.sum(xs[i % sets], dim=0, out=acc), steps, warmup)
+    out["sum fp32 (4 B read per value)"] = (ms, 4.0 * n)
+    return out
+
+
 def bench_scatter(tx, torch, kind, steps, warmup, n=67_108_864, nbins=65536):
     import workloads
     dev = torch.device("cuda:0")
@@ -362,7 +460,7 @@ def cpu_baseline():
 
 
 COPY_BYTES = 256 << 20
-TRAFFIC_TABLE = os.path.join(REPO, "profiles", "hbm_traffic_fp8_gemm_8192_fp8_convert_16Mi.md")
+TRAFFIC_TABLE = os.path.join(REPO, "profiles", "hbm_traffic_bench_workloads.md")
 
 
 def calibrate_copy():
@@ -376,64 +474,142 @@ def calibrate_copy():
     print(json.dumps({"calibration": "copy", "bytes": COPY_BYTES, "launches": 5}))
 
 
-def _pmc_per_kernel(path, counter):
-    """Average per-dispatch value of `counter` for each kernel in a rocprofv3
-    counter_collection.csv (values of one dispatch are summed first)."""
+def _dispatches(path, counters):
+    """Per-dispatch records of a rocprofv3 counter_collection.csv: kernel,
+    grid, start / end timestamps and each counter in `counters` (the rows of
+    one dispatch and counter are summed)."""
     import csv
-    per_dispatch = {}
+    out = {}
     with open(path) as f:
         for row in csv.DictReader(f):
-            if row["Counter_Name"] != counter:
+            if row["Counter_Name"] not in counters:
                 continue
-            key = (row["Dispatch_Id"], row["Kernel_Name"])
-            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
-    out = {}
-    for (_, name), v in per_dispatch.items():
-        out.setdefault(name, []).append(v)
-    return out
+            d = out.setdefault(row["Dispatch_Id"], {
+                "kernel": row["Kernel_Name"], "grid": int(row["Grid_Size"]),
+                "t0": int(row["Start_Timestamp"]), "t1": int(row["End_Timestamp"]), "c": {}})
+            d["c"][row["Counter_Name"]] = d["c"].get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    return list(out.values())
 
 
-def pmc_summary(fetch_csv, write_csv, cal_fetch_csv, cal_write_csv):
-    fetch = _pmc_per_kernel(fetch_csv, "FETCH_SIZE")
-    write = _pmc_per_kernel(write_csv, "WRITE_SIZE")
+def _assign(windows, disp):
+    """Label dispatches with the workload whose launch window holds their
+    start, in whichever host clock the profiler's timestamps follow."""
+    best = None
+    for clock in ("boot", "mono"):
+        spans = sorted((w["t0"][clock], w["t1"][clock], w) for w in windows)
+        hits = []
+        for d in disp:
+            for lo, hi, w in spans:
+                if lo <= d["t0"] <= hi:
+                    hits.append((d, w))
+                    break
+        if best is None or len(hits) > len(best):
+            best = hits
+    return best
+
+
+def _short(name):
+    return name.split("(")[0][:72] if not name.startswith("void ") else name[5:].split("<")[0][:72]
+
+
+def pmc_summary(fetch_windows, fetch_csv, write_windows, write_csv, cal_fetch_csv, cal_write_csv):
+    with open(fetch_windows) as f:
+        meta = json.load(f)
+    with open(write_windows) as f:
+        meta_w = json.load(f)
+    if meta_w["digest"] != meta["digest"]:
+        sys.exit("the FETCH_SIZE and WRITE_SIZE runs were made on different builds")
     # the copy's dispatches are the ones that move the most data
-    cal_f = sorted(v for vs in _pmc_per_kernel(cal_fetch_csv, "FETCH_SIZE").values() for v in vs)[-5:]
-    cal_w = sorted(v for vs in _pmc_per_kernel(cal_write_csv, "WRITE_SIZE").values() for v in vs)[-5:]
+    cal_f = sorted(d["c"]["FETCH_SIZE"] for d in _dispatches(cal_fetch_csv, {"FETCH_SIZE"}))[-5:]
+    cal_w = sorted(d["c"]["WRITE_SIZE"] for d in _dispatches(cal_write_csv, {"WRITE_SIZE"}))[-5:]
     kib = COPY_BYTES / 1024
     f_scale = kib / (sum(cal_f) / len(cal_f))
     w_scale = kib / (sum(cal_w) / len(cal_w))
+    print(f"build digest: {meta['digest']}")
+    print()
     print(f"copy calibration: {COPY_BYTES} B copied; FETCH_SIZE reads "
           f"{sum(cal_f) / len(cal_f):.0f} KiB, WRITE_SIZE {sum(cal_w) / len(cal_w):.0f} KiB per "
           f"launch; scale factors fetch {f_scale:.4f}, write {w_scale:.4f}")
     print()
-    print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes per launch |")
-    print("|---|---|---|---|---|")
-    for name in sorted(set(fetch) | set(write)):
-        fv, wv = fetch.get(name, [0.0]), write.get(name, [0.0])
+    rows = {}
+    for counter, path, m in (("FETCH_SIZE", fetch_csv, meta), ("WRITE_SIZE", write_csv, meta_w)):
+        for d, w in _assign(m["windows"], _dispatches(path, {counter})):
+            key = (w["workload"], _short(d["kernel"]), d["grid"])
+            r = rows.setdefault(key, {"algo": w.get("algo_bytes"), "FETCH_SIZE": [], "WRITE_SIZE": []})
+            r[counter].append(d["c"][counter])
+    order = {w["workload"]: i for i, w in enumerate(meta["windows"])}
+    print("| workload | kernel | grid | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB "
+          "| traffic bytes per launch | algorithmic bytes per step | traffic / algorithmic |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for key in sorted(rows, key=lambda k: (order.get(k[0], 1 << 30), k[1], k[2])):
+        r = rows[key]
+        fv, wv = r["FETCH_SIZE"] or [0.0], r["WRITE_SIZE"] or [0.0]
         fk, wk = sum(fv) / len(fv), sum(wv) / len(wv)
         traffic = (fk * f_scale + wk * w_scale) * 1024
-        print(f"| {name[:90]} | {len(fv)} | {fk:.0f} | {wk:.0f} | {traffic:.0f} |")
+        algo = r["algo"]
+        ratio = f"{traffic / algo:.3f}" if algo else ""
+        print(f"| {key[0]} | {key[1]} | {key[2]} | {max(len(r['FETCH_SIZE']), len(r['WRITE_SIZE']))} "
+              f"| {fk:.0f} | {wk:.0f} | {traffic:.0f} | {int(algo) if algo else ''} | {ratio} |")
 
 
-def traffic_from_table(kernel_prefix):
-    """HBM bytes per launch of a kernel from the committed counter summary, or None."""
+def mfma_summary(windows_json, mfma_csv):
+    with open(windows_json) as f:
+        meta = json.load(f)
+    names = {"SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES"}
+    rows = {}
+    for d, w in _assign(meta["windows"], _dispatches(mfma_csv, names)):
+        if d["c"].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) <= 0.0:
+            continue
+        key = (w["workload"], _short(d["kernel"]), d["grid"])
+        rows.setdefault(key, []).append(d)
+    order = {w["workload"]: i for i, w in enumerate(meta["windows"])}
+    print(f"build digest: {meta['digest']}")
+    print()
+    print("| workload | kernel | grid | dispatches | SQ_VALU_MFMA_BUSY_CYCLES | GRBM_GUI_ACTIVE per XCD "
+          "| duration us | clock GHz | MFMA busy |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for key in sorted(rows, key=lambda k: (order.get(k[0], 1 << 30), k[1], k[2])):
+        ds = rows[key]
+        busy = sum(d["c"]["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds) / len(ds)
+        gui = sum(d["c"]["GRBM_GUI_ACTIVE"] for d in ds) / len(ds) / XCDS
+        dur = sum(d["t1"] - d["t0"] for d in ds) / len(ds)
+        print(f"| {key[0]} | {key[1]} | {key[2]} | {len(ds)} | {busy:.4g} | {gui:.0f} | {dur / 1e3:.1f} "
+              f"| {gui / dur:.2f} | {busy / (gui * SIMDS):.1%} |")
+
+
+XCDS = 8
+SIMDS = 1024  # 256 CUs x 4 SIMDs
+
+
+def traffic_from_table(workload, kernel_prefix):
+    """HBM bytes per launch of a kernel on a workload, from the committed
+    counter table, and whether the table was made on another build."""
     if not os.path.exists(TRAFFIC_TABLE):
-        return None
+        return None, None
+    digest, value = None, None
     with open(TRAFFIC_TABLE) as f:
         for line in f:
+            if line.startswith("build digest:"):
+                digest = line.split(":", 1)[1].strip()
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cells) == 5 and cells[0].startswith(kernel_prefix):
+            if len(cells) == 9 and cells[0] == workload and cells[1].startswith(kernel_prefix):
                 try:
-                    return int(float(cells[4]))
+                    value = int(float(cells[6]))
                 except ValueError:
-                    return None
-    return None
+                    pass
+    if value is None:
+        return None, None
+    return value, {"table": os.path.relpath(TRAFFIC_TABLE, REPO), "table_build": digest,
+                   "this_build": build_digest(), "stale": digest != build_digest()}
 
 
 def main():
     args = parse()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.mfma_summary:
+        mfma_summary(*args.mfma_summary)
         return
     if args.calibrate_copy:
         calibrate_copy()
@@ -449,9 +625,9 @@ def main():
     K, W = args.steps, args.warmup
 
     gemm = bench_fp8_gemm(tx, torch, 8192, 8192, 8192, K, W)
-    progress("fp8 GEMM 8192^3")
+    progress("fp8 GEMM 8192^3", gemm["bytes"])
     conv = bench_fp8_convert(tx, torch, max(K, 50), W)
-    progress("fp8 convert 16Mi")
+    progress("fp8 convert 16Mi", conv["bytes"])
     secondary = []
     if not args.quick:
         for (m, n, k) in [(16, 14336, 4096), (512, 14336, 4096), (8192, 14336, 4096),
@@ -463,55 +639,78 @@ def main():
                               "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
                               "gbs": r["bytes"] / (r["ms"] * 1e-3) / 1e9})
-            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")), r.get("bytes"))
         for act, odt, oname in (("gelu_tanh", torch.float8_e4m3fn, "e4m3fn"), ("silu", torch.bfloat16, "bf16")):
             r = bench_fp8_gemm_epilogue(tx, torch, 8192, 8192, 8192, K, W, act, odt)
             secondary.append({"op": f"fp8 scaled GEMM + bias + {act} -> {oname} (fused)",
                               "shape": [8192, 8192, 8192], "ms": r["ms"], "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
-            progress(secondary[-1]["op"])
+            progress(secondary[-1]["op"], r.get("bytes"))
         for (m, n, k) in [(8192, 8192, 8192), (512, 14336, 4096)]:
             r = bench_mx_gemm(tx, torch, m, n, k, K, W, sets=ring_count(m * k + n * k) if m <= 512 else 2)
             secondary.append({"op": "MX-scaled fp8 GEMM (e8m0 per 32 K)", "shape": [m, n, k],
                               "ms": r["ms"], "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS})
-            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")), r.get("bytes"))
         for (G, total, n, k) in [(8, 16384, 14336, 4096), (64, 8192, 2048, 4096)]:
             r = bench_fp8_grouped(tx, torch, G, total, n, k, K, W)
             secondary.append({"op": f"grouped fp8 scaled GEMM, {G} experts (one launch)",
                               "shape": [total, n, k], "ms": r["ms"], "tflops": r["tflops"],
                               "frac_mfma": r["tflops"] / FP8_PEAK_TFLOPS,
                               "loop_of_plain_ms": r["ms_loop"], "group_rows": r["sizes"]})
-            progress(secondary[-1]["op"])
+            progress(secondary[-1]["op"], r.get("bytes"))
         r = bench_mx_gemm(tx, torch, 8192, 8192, 8192, K, W, fp4=True)
         secondary.append({"op": "MX-scaled fp4 GEMM (e2m1, e8m0 per 32 K)", "shape": [8192, 8192, 8192],
                           "ms": r["ms"], "tflops": r["tflops"], "frac_mfma": r["tflops"] / FP4_PEAK_TFLOPS})
-        progress(secondary[-1]["op"])
+        progress(secondary[-1]["op"], r.get("bytes"))
         for kind, xdt in (("mx", "f32"), ("mx", "bf16"), ("rowwise", "f32"), ("rowwise", "bf16")):
             r = bench_quant(tx, torch, kind, xdt, max(K, 50), W)
             secondary.append({"op": f"absmax+fp8 quantise ({kind}) {xdt} 8192x8192 -> e4m3fn",
                               "ms": r["ms"], "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS})
-            progress(secondary[-1]["op"])
+            progress(secondary[-1]["op"], r.get("bytes"))
         for (m, n, k) in [(4096, 4096, 4096), (4095, 4097, 4100)]:
             r = bench_bf16_gemm(tx, torch, m, n, k, K, W)
             secondary.append({"op": "bf16 GEMM", "shape": [m, n, k], "ms": r["ms"],
                               "tflops": r["tflops"], "frac_mfma": r["tflops"] / BF16_PEAK_TFLOPS})
-            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")), r.get("bytes"))
         for kind in ("i32", "f32"):
             r = bench_scatter(tx, torch, kind, K, W)
             secondary.append({"op": f"scatter-reduce {kind} 64Mi->65536 Zipf(1.1)", "ms": r["ms"],
                               "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS,
                               "gupdates_per_s": r["updates_per_s"] / 1e9})
-            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")))
+            progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")), r.get("bytes"))
         for m in (1, 4, 16):
             r = bench_gemv(tx, torch, m, max(K, 50), W)
             secondary.append({"op": "fp8 e5m2 dequant GEMV", "shape": [m, 14336, 4096],
                               "ms": r["ms"], "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS})
-            progress(f"fp8 e5m2 dequant GEMV M={m}")
+            progress(f"fp8 e5m2 dequant GEMV M={m}", r["bytes"])
         secondary.append({"op": "fp8 decode e4m3fn->fp32 16Mi", "ms": conv["decode_ms"],
                           "gbs": conv["decode_gbs"], "frac_hbm": conv["decode_gbs"] / HBM_PEAK_GBS})
+        for size in (67_108_864, 268_435_456):
+            for n, (ms, nbytes) in bench_encode_sizes(tx, torch, max(K, 50), W, (size,)).items():
+                secondary.append({"op": f"fp8 encode fp32->e4m3fn (RNE) {n >> 20}Mi", "ms": ms,
+                                  "gbs": nbytes / (ms * 1e-3) / 1e9,
+                                  "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+                progress(secondary[-1]["op"], nbytes)
+        for name, (ms, nbytes) in bench_torch_streams(torch, max(K, 50), W).items():
+            secondary.append({"op": f"reference: torch {name} 16Mi", "ms": ms,
+                              "gbs": nbytes / (ms * 1e-3) / 1e9,
+                              "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+        progress("reference: torch cast, copy, sum 16Mi")
+        for sname, sdt, dname, ddt in (("bf16", torch.bfloat16, "e4m3fn", torch.float8_e4m3fn),
+                                       ("e4m3fn", torch.float8_e4m3fn, "bf16", torch.bfloat16),
+                                       ("fp16", torch.float16, "e5m2", torch.float8_e5m2)):
+            r = bench_convert_pair(tx, torch, sdt, ddt, max(K, 50), W)
+            secondary.append({"op": f"tt.fp_to_fp {sname}->{dname} (RNE) 16Mi", "ms": r["ms"],
+                              "gbs": r["gbs"], "frac_hbm": r["gbs"] / HBM_PEAK_GBS})
+            progress(secondary[-1]["op"], r.get("bytes"))
 
+    if args.windows:
+        with open(args.windows, "w") as f:
+            json.dump({"digest": build_digest(), "windows": WINDOWS}, f)
     cpu = None if args.no_cpu else cpu_baseline()
+    gemm_traffic = traffic_from_table("fp8 GEMM 8192^3", "tx_gemm_fp8_e4m3fn_e4m3fn_fast")
+    conv_traffic = traffic_from_table("fp8 convert 16Mi", "tx_fp8_encode_e4m3fn_rtne_vec")
     line = {
         "metric": METRIC,
         "value": round(gemm["tflops"], 2),
@@ -531,12 +730,12 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm["tflops"], 2),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm["tflops"] / FP8_PEAK_TFLOPS, 4),
-                     "traffic": traffic_from_table("tx_gemm_fp8_e4m3fn_e4m3fn_fast")},
+                     "traffic": gemm_traffic[0], "traffic_source": gemm_traffic[1]},
         "fp8_convert": {"value": round(conv["gbs"], 1), "unit": "GB/s", "ms": round(conv["ms"], 5),
                         "roofline": {"bound": "hbm", "achieved": round(conv["gbs"], 1),
                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                      "frac": round(conv["gbs"] / HBM_PEAK_GBS, 4),
-                                     "traffic": traffic_from_table("tx_fp8_encode_e4m3fn_rtne_vec")},
+                                     "traffic": conv_traffic[0], "traffic_source": conv_traffic[1]},
                         "buffer_sets": conv["sets"]},
         "cpu_baseline": cpu,
         "secondary": secondary,

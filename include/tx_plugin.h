@@ -201,7 +201,17 @@ TX_API const char *txVersion(void);
  *    (bf16) with the input's sign bit.
  *  - TX_FP8E4M3FN / TX_FP8E5M2 -> TX_F32 (exact; NaN codes give 0x7FC00000
  *    with the code's sign).
- * TX_RS needs random bits: use tx_fp_to_fp_with_rbits (TX_UNSUPPORTED here).
+ *  - TX_BF16 / TX_F16 / TX_FP8E4M3FN / TX_FP8E5M2 -> any other of TX_F32,
+ *    TX_BF16, TX_F16, TX_FP8E4M3FN, TX_FP8E5M2 (x.to(tl.float8e4nv) on bf16
+ *    activations, fp8 -> bf16 upcasts, ...): the source value widened to
+ *    fp32 (exactly) and converted as above, so it is rounded once, with the
+ *    same rounding, saturation and NaN rules.  Conversions to a format that
+ *    holds every source value (fp8 -> fp16 / bf16 / fp32, fp16 / bf16 ->
+ *    fp32) are exact under any rounding; saturation there only maps e5m2's
+ *    +-Inf to +-max of an fp16 / bf16 destination (an fp32 destination
+ *    keeps infinities, as the fp8 -> fp32 decode does).
+ * TX_RS needs random bits and an fp32 source: use tx_fp_to_fp_with_rbits
+ * (TX_UNSUPPORTED here).
  */
 TX_API tx_status tx_fp_to_fp(const void *src, tx_dtype src_type, void *dst,
                              tx_dtype dst_type, int64_t n,

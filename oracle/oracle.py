@@ -132,6 +132,35 @@ def encode_fmt(x, fmt: int, rtz: bool = False, sat: bool = False, nthreads: int 
     return out
 
 
+F32 = 0
+
+
+def widen(codes, fmt: int) -> np.ndarray:
+    """Codes of format fmt (F32 values, BF16 / F16 uint16 bits, fp8 uint8) ->
+    their fp32 values, exactly (every bf16, fp16 and fp8 value is an fp32
+    value; NaN stays NaN)."""
+    if fmt == F32:
+        return np.ascontiguousarray(codes, np.float32)
+    if fmt == BF16:
+        return (np.asarray(codes, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    if fmt == F16:
+        return np.asarray(codes, np.uint16).view(np.float16).astype(np.float32)
+    return decode(codes, fmt)
+
+
+def convert(codes, src: int, dst: int, rtz: bool = False, sat: bool = False) -> np.ndarray:
+    """tt.fp_to_fp between any two of fp32, bf16, fp16, e4m3fn, e5m2
+    (semantic.py:807-827 casts through tt.fp_to_fp, default rounding RTNE at
+    :809): the source widened exactly to fp32, then encoded once as an fp32
+    source is (encode_fmt: RNE or RTZ, the saturating clamp idiom of
+    mxfp8_utils.py:36-38).  An fp32 destination is the widened value
+    (saturation does not apply to it, as for the fp8 -> fp32 decode)."""
+    x = widen(codes, src)
+    if dst == F32:
+        return x
+    return encode_fmt(x, dst, rtz=rtz, sat=sat)
+
+
 def round_rs(x, rbits, fmt: int, nthreads: int = 0) -> np.ndarray:
     """fp32 -> codes of format fmt with stochastic rounding (one uint32 of
     random bits per element; definition in tx_oracle.c)."""

@@ -91,4 +91,4 @@ def test_invalid_requests_raise(tx, dev):
     with pytest.raises(tx.TxError, match="UNSUPPORTED"):
         tx.fp_to_fp(x, torch.float8_e4m3fn, rounding="rs")
     with pytest.raises(tx.TxError, match="UNSUPPORTED"):
-        tx.fp_to_fp(x.to(torch.bfloat16), torch.float8_e4m3fn)
+        tx.fp_to_fp(x.to(torch.bfloat16), torch.float8_e4m3fn, rounding="rs")

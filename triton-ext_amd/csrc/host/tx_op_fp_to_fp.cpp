@@ -1,5 +1,6 @@
-// tt.fp_to_fp entry points (fp32 <-> fp8, fp32 -> fp16 / bf16, stochastic
-// rounding with random bits) and their table registration.
+// tt.fp_to_fp entry points (fp32 <-> fp8, fp32 -> fp16 / bf16, bf16 / fp16 /
+// fp8 to any other of these formats, stochastic rounding with random bits)
+// and their table registration.
 //
 // Reference: tt.fp_to_fp is emitted by semantic.cast (semantic.py:807-827,
 // default rounding RTNE at :809), passed through the plugin's conversion
@@ -32,20 +33,22 @@ const char *fmt_name(tx_dtype t) {
 bool is_fp8(tx_dtype t) { return t == TX_FP8E4M3FN || t == TX_FP8E5M2; }
 bool is_16(tx_dtype t) { return t == TX_BF16 || t == TX_F16; }
 
+// The vector kernel covers the largest multiple of `step` elements (its
+// block step) of [0, n); the tail kernel the rest.
 tx_status run(const char *vec_name, const char *tail_name, const void *src,
               void *dst, int64_t n, bool vec_ok, hipStream_t stream,
-              const uint32_t *rbits = nullptr) {
+              const uint32_t *rbits = nullptr, int64_t step = kChunk) {
   tx_fp8_codec_args args{src, dst, 0, n, rbits};
-  int64_t n_vec = vec_ok ? (n / kChunk) * kChunk : 0;
+  int64_t n_vec = vec_ok ? (n / step) * step : 0;
   const int cus = cu_count();
   if (n_vec > 0) {
     hipFunction_t fn;
     TX_TRY(get_kernel(CodeObject::Fp8Codec, vec_name, &fn));
     args.start = 0;
     args.n = n_vec;
-    // One block step per chunk, capped at 32 resident blocks per CU; the
-    // kernels loop over the remaining chunks.
-    int64_t grid = std::min<int64_t>(n_vec / kChunk, int64_t(cus) * 32);
+    // One block per step, capped at 32 resident blocks per CU; the kernels
+    // loop over the remaining steps.
+    int64_t grid = std::min<int64_t>(n_vec / step, int64_t(cus) * 32);
     TX_TRY(launch(fn, unsigned(grid), 1, kBlock, stream, &args, sizeof args, vec_name));
   }
   if (n_vec < n) {
@@ -91,6 +94,35 @@ static tx_status fp_to_fp(const void *src, tx_dtype src_type, void *dst,
     std::snprintf(tail, sizeof tail, "tx_fp8_decode_%s_tail", fmt_name(src_type));
     const bool vec_ok = aligned(src, 4) && aligned(dst, 16);
     return run(vec, tail, src, dst, n, vec_ok, s);
+  }
+  // bf16 / fp16 / fp8 sources: widened to fp32 exactly, then rounded once.
+  // Destinations that hold every source value (fp8 -> bf16 / fp16, bf16 /
+  // fp16 -> fp32) are exact whatever the rounding; saturation there only
+  // maps e5m2's +-Inf to the 16-bit format's +-max (an fp32 destination,
+  // as in the fp8 -> fp32 decode, keeps infinities).
+  if ((src_fp8 || is_16(src_type)) && (dst_fp8 || is_16(dst_type) || dst_type == TX_F32) &&
+      src_type != dst_type) {
+    if (rounding == TX_RS)
+      return fail(TX_UNSUPPORTED, "tx_fp_to_fp: stochastic rounding takes a float32 source (got %d)",
+                  int(src_type));
+    if (rounding != TX_RTNE && rounding != TX_RTZ)
+      return fail(TX_INVALID_ARGUMENT, "tx_fp_to_fp: rounding %d", int(rounding));
+    const bool exact = dst_type == TX_F32 || (src_fp8 && is_16(dst_type));
+    const char *sn = fmt_name(src_type), *dn = dst_type == TX_F32 ? "f32" : fmt_name(dst_type);
+    if (!sn || !dn) return fail(TX_UNSUPPORTED, "tx_fp_to_fp: conversion %d -> %d", int(src_type), int(dst_type));
+    char mode[16];
+    std::snprintf(mode, sizeof mode, "%s", exact ? "exact" : rounding == TX_RTZ ? "rtz" : "rtne");
+    const bool sat_matters = !exact || (src_type == TX_FP8E5M2 && is_16(dst_type));
+    const char *sat = (sat_matters && saturate) ? "_sat" : "";
+    std::snprintf(vec, sizeof vec, "tx_cvt_%s_%s_%s%s_vec", sn, dn, mode, sat);
+    std::snprintf(tail, sizeof tail, "tx_cvt_%s_%s_%s%s_tail", sn, dn, mode, sat);
+    // units of 16 / max(sizes) elements: 16-byte accesses on the wider side
+    const int ss = src_fp8 ? 1 : 2, ds = dst_type == TX_F32 ? 4 : dst_fp8 ? 1 : 2;
+    const int e = 16 / std::max(ss, ds);
+    const bool vec_ok = aligned(src, size_t(e * ss)) && aligned(dst, size_t(e * ds));
+    // two chunks per block step where a value moves 3 bytes or fewer
+    const int64_t step = kChunk * (ss + ds <= 3 ? 2 : 1);
+    return run(vec, tail, src, dst, n, vec_ok, s, nullptr, step);
   }
   return fail(TX_UNSUPPORTED, "tx_fp_to_fp: conversion %d -> %d is not served",
               int(src_type), int(dst_type));

@@ -224,6 +224,137 @@ __device__ __forceinline__ void cvt_tail(const tx_fp8_codec_args &a) {
   }
 }
 
+// ------------------------------------ conversions between any two formats
+// Source codes of fp32 (bits), bf16, fp16, e4m3fn or e5m2 widen to fp32
+// exactly (every bf16, fp16 and fp8 value is an fp32 value), then take the
+// encoders above, so each result is the source value rounded once.
+constexpr int F32 = 0;  // tx_dtype of fp32
+
+template <int T>
+struct Bytes {
+  static constexpr int v = T == F32 ? 4 : (T == BF16 || T == F16) ? 2 : 1;
+};
+
+// code -> fp32 bits, exact.  fp16: normal codes re-biased (exponent + 112),
+// subnormal codes mant * 2^-24 (an exact int -> float conversion times a
+// power of two), Inf / NaN kept (NaN stays NaN).
+template <int SRC>
+__device__ __forceinline__ uint32_t widen(uint32_t c) {
+  if constexpr (SRC == F32) {
+    return c;
+  } else if constexpr (SRC == BF16) {
+    return c << 16;
+  } else if constexpr (SRC == F16) {
+    const uint32_t e = (c >> 10) & 0x1Fu, m = c & 0x3FFu;
+    const uint32_t nrm = ((e + 112u) << 23) | (m << 13);
+    const uint32_t sub = __float_as_uint(float(m) * 0x1p-24f);
+    const uint32_t r = e == 0u ? sub : (e == 31u ? (0x7F800000u | (m << 13)) : nrm);
+    return r | ((c & 0x8000u) << 16);
+  } else {
+    return decode<SRC>(c);
+  }
+}
+
+// fp32 bits -> code of DST (fp32: the bits), MODE 0 rtne, 1 rtz.
+template <int DST, int MODE, bool SAT>
+__device__ __forceinline__ uint32_t narrow(uint32_t u) {
+  if constexpr (DST == F32) return u;
+  else if constexpr (MODE == 1) return encode_rtz<DST, SAT>(u);
+  else return encode_rtne<DST, SAT>(u);
+}
+
+template <int B> struct Unit;  // a B-byte memory access
+template <> struct Unit<4> { using T = uint32_t; };
+template <> struct Unit<8> { using T = txd::u32x2; };
+template <> struct Unit<16> { using T = txd::u32x4; };
+
+template <int B>
+__device__ __forceinline__ void unit_words(const typename Unit<B>::T &v, uint32_t (&w)[4]) {
+  if constexpr (B == 4) { w[0] = v; w[1] = w[2] = w[3] = 0u; }
+  else if constexpr (B == 8) { w[0] = v.x; w[1] = v.y; w[2] = w[3] = 0u; }
+  else { w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w; }
+}
+template <int B>
+__device__ __forceinline__ typename Unit<B>::T words_unit(const uint32_t (&w)[4]) {
+  if constexpr (B == 4) return w[0];
+  else if constexpr (B == 8) return txd::u32x2{w[0], w[1]};
+  else return txd::u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// One unit of E elements: the source unit's words in, the destination
+// unit's words out.
+template <int SRC, int DST, int MODE, bool SAT, int E>
+__device__ __forceinline__ void cvt_unit(const uint32_t (&w)[4], uint32_t (&o)[4]) {
+  constexpr int S = Bytes<SRC>::v, D = Bytes<DST>::v;
+  constexpr uint32_t SM = S == 4 ? 0xFFFFFFFFu : (1u << (8 * S)) - 1u;
+  constexpr uint32_t DM = D == 4 ? 0xFFFFFFFFu : (1u << (8 * D)) - 1u;
+  o[0] = o[1] = o[2] = o[3] = 0u;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const uint32_t c = (w[(i * S) / 4] >> (8 * ((i * S) % 4))) & SM;
+    const uint32_t y = narrow<DST, MODE, SAT>(widen<SRC>(c)) & DM;
+    o[(i * D) / 4] |= y << (8 * ((i * D) % 4));
+  }
+}
+
+// Chunks per block step of the generic vector conversion: two where a value
+// moves 3 bytes or fewer, so every lane keeps at least 64 bytes of loads
+// and stores in flight (the host sizes its vector range to match).
+template <int SRC, int DST>
+struct Steps {
+  static constexpr int v = Bytes<SRC>::v + Bytes<DST>::v <= 3 ? 2 : 1;
+};
+
+// Vector conversion: [start, n) with (n - start) a multiple of R * kChunk.
+// Each thread converts 16 * R elements per block step in units of
+// E = 16 / max(S, D) elements, so the wider side of the conversion moves 16
+// bytes per lane and both sides are wave-contiguous; src aligned to E * S
+// bytes, dst to E * D bytes.  All loads of a step are issued before the
+// first conversion.
+template <int SRC, int DST, int MODE, bool SAT, int R = Steps<SRC, DST>::v>
+__device__ __forceinline__ void cvt2_vec(const tx_fp8_codec_args &a) {
+  constexpr int S = Bytes<SRC>::v, D = Bytes<DST>::v;
+  constexpr int E = 16 / (S > D ? S : D), U = 16 / E;  // elements per unit, units per chunk
+  constexpr int LB = E * S, SB = E * D;
+  static_assert(kBlock * U * E == kChunk, "16 elements per thread and chunk");
+  using LT = typename Unit<LB>::T;
+  using ST = typename Unit<SB>::T;
+  const LT *src = reinterpret_cast<const LT *>(static_cast<const uint8_t *>(a.src) + a.start * S);
+  ST *dst = reinterpret_cast<ST *>(static_cast<uint8_t *>(a.dst) + a.start * D);
+  const int64_t nsteps = (a.n - a.start) / (int64_t(R) * kChunk);
+  for (int64_t c = blockIdx.x; c < nsteps; c += gridDim.x) {
+    const int64_t w0 = c * (kBlock * U * R) + threadIdx.x;
+    LT v[U * R];
+#pragma unroll
+    for (int u = 0; u < U * R; ++u) v[u] = __builtin_nontemporal_load(src + w0 + u * kBlock);
+#pragma unroll
+    for (int u = 0; u < U * R; ++u) {
+      uint32_t w[4], o[4];
+      unit_words<LB>(v[u], w);
+      cvt_unit<SRC, DST, MODE, SAT, E>(w, o);
+      __builtin_nontemporal_store(words_unit<SB>(o), dst + w0 + u * kBlock);
+    }
+  }
+}
+
+template <int SRC, int DST, int MODE, bool SAT>
+__device__ __forceinline__ void cvt2_tail(const tx_fp8_codec_args &a) {
+  constexpr int S = Bytes<SRC>::v, D = Bytes<DST>::v;
+  const uint8_t *src = static_cast<const uint8_t *>(a.src);
+  uint8_t *dst = static_cast<uint8_t *>(a.dst);
+  for (int64_t i = a.start + int64_t(blockIdx.x) * kBlock + threadIdx.x; i < a.n;
+       i += int64_t(gridDim.x) * kBlock) {
+    uint32_t c;
+    if constexpr (S == 4) c = reinterpret_cast<const uint32_t *>(src)[i];
+    else if constexpr (S == 2) c = reinterpret_cast<const uint16_t *>(src)[i];
+    else c = src[i];
+    const uint32_t y = narrow<DST, MODE, SAT>(widen<SRC>(c));
+    if constexpr (D == 4) reinterpret_cast<uint32_t *>(dst)[i] = y;
+    else if constexpr (D == 2) reinterpret_cast<uint16_t *>(dst)[i] = uint16_t(y);
+    else dst[i] = uint8_t(y);
+  }
+}
+
 // ----------------------------------------------------------- quantisers
 // x element i of a row as fp32 (XT 0: fp32, 1: bf16 bits).
 template <int XT>
@@ -522,3 +653,38 @@ TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e5m2_vec(const tx_fp8_cod
 TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e5m2_tail(const tx_fp8_codec_args a) {
   decode_tail<E5M2>(a);
 }
+
+// Conversions with a bf16, fp16 or fp8 source: tx_cvt_<src>_<dst>_<rounding>[_sat].
+// Rounding ones come in rtne / rtz, saturating or not; exact ones (to a
+// format that holds every source value) once, as _exact, plus _exact_sat
+// where the source has infinities and the destination a saturating form.
+#define TX_CVT2(NAME, SRC, DST, MODE, SAT)                                                  \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_cvt_##NAME##_vec(const tx_fp8_codec_args a) {  \
+    cvt2_vec<SRC, DST, MODE, SAT>(a);                                                       \
+  }                                                                                         \
+  TX_KERNEL void __launch_bounds__(kBlock) tx_cvt_##NAME##_tail(const tx_fp8_codec_args a) { \
+    cvt2_tail<SRC, DST, MODE, SAT>(a);                                                      \
+  }
+#define TX_CVT2_ROUNDING(S, D, SRC, DST)            \
+  TX_CVT2(S##_##D##_rtne, SRC, DST, 0, false)       \
+  TX_CVT2(S##_##D##_rtne_sat, SRC, DST, 0, true)    \
+  TX_CVT2(S##_##D##_rtz, SRC, DST, 1, false)        \
+  TX_CVT2(S##_##D##_rtz_sat, SRC, DST, 1, true)
+
+TX_CVT2_ROUNDING(bf16, e4m3fn, BF16, E4M3FN)
+TX_CVT2_ROUNDING(bf16, e5m2, BF16, E5M2)
+TX_CVT2_ROUNDING(bf16, f16, BF16, F16)
+TX_CVT2_ROUNDING(f16, e4m3fn, F16, E4M3FN)
+TX_CVT2_ROUNDING(f16, e5m2, F16, E5M2)
+TX_CVT2_ROUNDING(f16, bf16, F16, BF16)
+TX_CVT2_ROUNDING(e4m3fn, e5m2, E4M3FN, E5M2)
+TX_CVT2_ROUNDING(e5m2, e4m3fn, E5M2, E4M3FN)
+TX_CVT2(bf16_f32_exact, BF16, F32, 0, false)
+TX_CVT2(f16_f32_exact, F16, F32, 0, false)
+TX_CVT2(e4m3fn_bf16_exact, E4M3FN, BF16, 0, false)
+TX_CVT2(e4m3fn_f16_exact, E4M3FN, F16, 0, false)
+TX_CVT2(e5m2_bf16_exact, E5M2, BF16, 0, false)
+TX_CVT2(e5m2_f16_exact, E5M2, F16, 0, false)
+// e5m2 holds +-Inf: saturating makes them +-max of the destination
+TX_CVT2(e5m2_bf16_exact_sat, E5M2, BF16, 0, true)
+TX_CVT2(e5m2_f16_exact_sat, E5M2, F16, 0, true)

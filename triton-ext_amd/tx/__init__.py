@@ -91,8 +91,9 @@ def _on_gpu(*ts):
 # --------------------------------------------------------------------------
 def fp_to_fp(x: torch.Tensor, dtype, rounding="rtne", saturate: bool = False,
              out: torch.Tensor | None = None, rbits: torch.Tensor | None = None) -> torch.Tensor:
-    """tt.fp_to_fp, elementwise: fp32 -> fp8 (e4m3fn / e5m2), fp16 or bf16, or
-    fp8 -> fp32.
+    """tt.fp_to_fp, elementwise: fp32 -> fp8 (e4m3fn / e5m2), fp16 or bf16;
+    fp8 -> fp32; and bf16 / fp16 / fp8 -> any other of those formats (the
+    source widened exactly to fp32, then rounded once as an fp32 source is).
 
     rounding: "rtne" (Triton's default downcast, semantic.py:809), "rtz", or
     "rs" (stochastic, fp32 source only, needs rbits: one int32/uint32 of random
