@@ -49,6 +49,7 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA
 FP4_PEAK_TFLOPS = 10100.0    # dense fp4 MFMA
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
+F16_PEAK_TFLOPS = 2500.0     # dense fp16 MFMA
 MALL_BYTES = 256 << 20
 
 
@@ -299,6 +300,23 @@ def bench_bf16_gemm(tx, torch, M, N, K, steps, warmup):
     ms = timed(lambda i: tx.dot(At, Bt, out=C), steps, warmup)
     flops = 2.0 * M * N * K
     return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+
+
+def bench_matmul16(tx, torch, S, steps, warmup):
+    """The reference's matmul benchmark (test_amd_gemm_pipelined.py:355-399):
+    matmul(a, b) on fp16 S x S operands, b row-major, fp16 output allocated
+    per call, against torch.matmul on the same tensors (its rocBLAS line)."""
+    import workloads
+    import numpy as np
+    dev = torch.device("cuda:0")
+    A, B = workloads.matmul16_input(S, S, S)
+    a = torch.from_numpy(A.view(np.int16)).to(dev).view(torch.float16)
+    b = torch.from_numpy(B.view(np.int16)).to(dev).view(torch.float16)
+    ms = timed(lambda i: tx.matmul(a, b), steps, warmup)
+    ms_torch = timed(lambda i: torch.matmul(a, b), steps, warmup)
+    flops = 2.0 * S ** 3
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "torch_ms": ms_torch,
+            "torch_tflops": flops / (ms_torch * 1e-3) / 1e12, "bytes": 6.0 * S * S}
 
 
 def bench_fp8_convert(tx, torch, steps, warmup, n=16_777_216):
@@ -673,6 +691,13 @@ def main():
             secondary.append({"op": "bf16 GEMM", "shape": [m, n, k], "ms": r["ms"],
                               "tflops": r["tflops"], "frac_mfma": r["tflops"] / BF16_PEAK_TFLOPS})
             progress(secondary[-1]["op"] + " " + str(secondary[-1].get("shape", "")), r.get("bytes"))
+        for S in (256, 512, 1024, 2048, 4096, 8192):
+            r = bench_matmul16(tx, torch, S, K if S >= 4096 else max(K, 50), W)
+            secondary.append({"op": "matmul fp16, b row-major K x N, fp16 out (the reference's "
+                                    "matmul caller)", "shape": [S, S, S], "ms": r["ms"],
+                              "tflops": r["tflops"], "frac_mfma": r["tflops"] / F16_PEAK_TFLOPS,
+                              "torch_matmul_ms": r["torch_ms"], "torch_matmul_tflops": r["torch_tflops"]})
+            progress(f"matmul fp16 {S}^3", r["bytes"])
         for kind in ("i32", "f32"):
             r = bench_scatter(tx, torch, kind, K, W)
             secondary.append({"op": f"scatter-reduce {kind} 64Mi->65536 Zipf(1.1)", "ms": r["ms"],

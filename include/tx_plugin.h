@@ -107,6 +107,13 @@ typedef enum tx_rmw_op {
   TX_RMW_XOR = 8
 } tx_rmw_op;
 
+/* Storage of tt.dot's B operand (K x N) in tx_dot. */
+typedef enum tx_b_layout {
+  TX_B_NK = 0, /* column-major K x N: N rows of K elements, row stride ldb >= K */
+  TX_B_KN = 1  /* row-major K x N: K rows of N elements, row stride ldb >= N
+                  (the layout of the reference's matmul(a, b) caller) */
+} tx_b_layout;
+
 /* Activations of the fp8 GEMM's fused epilogue (tx_dot_fp8_scaled_ex). */
 typedef enum tx_activation {
   TX_ACT_NONE = 0,
@@ -273,6 +280,29 @@ TX_API tx_status tx_atomic_rmw_scatter(void *bins, tx_dtype bins_type,
 TX_API tx_status tx_dot_bf16(const void *A, int64_t lda, const void *B,
                              int64_t ldb, void *C, int64_t ldc, int64_t M,
                              int64_t N, int64_t K, tx_stream_t stream);
+
+/*
+ * tt.dot with 16-bit operands, fp32 accumulation and a 16-bit output:
+ * C[m,n] = out_rne(sum_k A[m,k] * B[k,n]).
+ * Replaces Triton's MFMA lowering of tt.dot for fp16 / bf16 operands
+ * (TritonDotPattern, uTLXConversionPatterns.cpp:227-296) behind the
+ * reference's only AMD GEMM caller: matmul(a, b) with fp16 a (M x K,
+ * row-major) and fp16 b (K x N, row-major), fp16 output
+ * (test_amd_gemm_pipelined.py:303-331; its kernel accumulates in fp32 and
+ * casts, :259-299).
+ * ab_type: TX_BF16 or TX_F16 (both operands).  c_type: TX_BF16 or TX_F16.
+ * A: row-major M x K, row stride lda (elements).
+ * B: b_layout TX_B_NK (N rows of K, ldb >= K) or TX_B_KN (K rows of N,
+ *    ldb >= N).  A TX_B_KN operand is first transposed into the library's
+ *    stream scratch (N rows of K rounded up to 64, zero-filled), which fails
+ *    with TX_GENERIC_FAILURE if that allocation fails.
+ * C: row-major M x N, row stride ldc.
+ * Any M, N, K >= 0 (K = 0 gives zeros).
+ */
+TX_API tx_status tx_dot(const void *A, tx_dtype ab_type, int64_t lda,
+                        const void *B, tx_b_layout b_layout, int64_t ldb,
+                        void *C, tx_dtype c_type, int64_t ldc, int64_t M,
+                        int64_t N, int64_t K, tx_stream_t stream);
 
 /*
  * tt.dot on fp8 operands with a per-row / per-column scale epilogue:

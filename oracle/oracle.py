@@ -61,6 +61,8 @@ def lib():
         L.txo_f32_to_bf16.restype = ctypes.c_uint16
         L.txo_gemm_bf16_rows.argtypes = [P, I64, P, I64, I64, I64, I64, I64,
                                          P, P, I]
+        L.txo_gemm16_rows.argtypes = [P, I64, P, I64, I, I, I64, I64, I64, I64, P, I]
+        L.txo_gemm16_rows.restype = I
         L.txo_gemm_fp8_scaled_rows.argtypes = [P, I64, P, I64, P, P, I64, I64,
                                                I, I, I64, I64, P, P, I]
         L.txo_gemv_fp8_dequant.argtypes = [P, I64, P, I64, P, I64, I64, I64,
@@ -244,6 +246,26 @@ def gemm_bf16_rows(A, B, r0: int, r1: int, nthreads: int = 0):
     o16 = np.empty((r1 - r0, N), np.uint16)
     lib().txo_gemm_bf16_rows(_p(A), K, _p(B), K, N, K, r0, r1, _p(o32),
                              _p(o16), nthreads)
+    return o32, o16
+
+
+def gemm16_rows(A, B, r0: int, r1: int, fmt: int = BF16, b_kn: bool = False,
+                out_fmt: int | None = None, nthreads: int = 0):
+    """Rows [r0, r1) of A @ B for 16-bit operands (fmt BF16 or F16, both).
+
+    A: uint16 M x K; B: uint16 N x K (b_kn False) or K x N (b_kn True, the
+    row-major b of the reference's matmul).  Returns (fp32 of the fp64
+    accumulation, its RNE rounding to out_fmt (default fmt) as uint16)."""
+    A = _c(A, np.uint16)
+    B = _c(B, np.uint16)
+    K = A.shape[1]
+    N = B.shape[1] if b_kn else B.shape[0]
+    o32 = np.empty((r1 - r0, N), np.float32)
+    rc = lib().txo_gemm16_rows(_p(A), K, _p(B), B.shape[1], int(bool(b_kn)), fmt, N, K, r0, r1,
+                               _p(o32), nthreads)
+    if rc:
+        raise ValueError(f"txo_gemm16_rows: {rc}")
+    o16 = encode_fmt(o32, fmt if out_fmt is None else out_fmt).reshape(o32.shape)
     return o32, o16
 
 

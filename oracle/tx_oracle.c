@@ -507,6 +507,17 @@ static uint16_t f32_to_bf16_rne(float x) {
 
 TXO_API uint16_t txo_f32_to_bf16(float x) { return f32_to_bf16_rne(x); }
 
+/* fp16 bits -> fp32, exact: subnormals m * 2^-24, normals (1024 + m) *
+ * 2^(e - 25), e = 31 Inf / NaN. */
+static float f16_to_f32(uint16_t h) {
+  const int e = (h >> 10) & 31, m = h & 1023;
+  float v;
+  if (e == 0) v = ldexpf((float)m, -24);
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = ldexpf((float)(1024 + m), e - 25);
+  return (h & 0x8000) ? -v : v;
+}
+
 /* ------------------------------------------------------------------------ */
 /* tt.dot, bf16 operands, fp32 accumulate, bf16 output.                      */
 /* C[m,n] = sum_k A[m,k] * B[k,n]; the reference kernel accumulates in fp32  */
@@ -540,6 +551,49 @@ TXO_API void txo_gemm_bf16_rows(const uint16_t *A, int64_t lda,
     free(arow);
   }
   (void)nthreads;
+}
+
+/* ------------------------------------------------------------------------ */
+/* tt.dot, 16-bit operands (fmt 3 bf16 or 6 fp16, both operands), any B      */
+/* layout: B given as N rows of K (b_kn = 0, the column-major K x N of the    */
+/* function above) or as K rows of N (b_kn = 1: the row-major b of the        */
+/* reference's matmul(a, b), test_amd_gemm_pipelined.py:303-331).  Rows       */
+/* [r0, r1) of the fp64 sum, returned as float (the caller rounds to the      */
+/* output type).  B is widened once into an fp32 copy of N x K (n-major).     */
+/* ------------------------------------------------------------------------ */
+TXO_API int txo_gemm16_rows(const uint16_t *A, int64_t lda, const uint16_t *B,
+                            int64_t ldb, int b_kn, int fmt, int64_t N, int64_t K,
+                            int64_t r0, int64_t r1, float *out_f32, int nthreads) {
+  if (fmt != 3 && fmt != 6) return -1;
+  float *bw = (float *)malloc(sizeof(float) * (size_t)(N > 0 ? N : 1) * (size_t)(K > 0 ? K : 1));
+  if (!bw) return -2;
+#ifdef _OPENMP
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t k = 0; k < K; ++k) {
+      const uint16_t h = b_kn ? B[k * ldb + n] : B[n * ldb + k];
+      bw[n * K + k] = fmt == 3 ? bf16_to_f32(h) : f16_to_f32(h);
+    }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+  for (int64_t m = r0; m < r1; ++m) {
+    double *arow = (double *)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+    for (int64_t k = 0; k < K; ++k)
+      arow[k] = fmt == 3 ? bf16_to_f32(A[m * lda + k]) : f16_to_f32(A[m * lda + k]);
+    for (int64_t n = 0; n < N; ++n) {
+      const float *bcol = bw + n * K;
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k) acc += arow[k] * (double)bcol[k];
+      out_f32[(m - r0) * N + n] = (float)acc;
+    }
+    free(arow);
+  }
+  free(bw);
+  (void)nthreads;
+  return 0;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -210,12 +210,21 @@ def test_bf16_matmul_wrapper_and_table(tx, oracle, dev):
     M, N, K = 96, 80, 64
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=5)
     b_kn = _t_bf16(B, dev).t()  # column-major K x N view
-    C1 = tx.matmul(_t_bf16(A, dev), b_kn)
+    C1 = tx.dot(_t_bf16(A, dev), _t_bf16(B, dev))
     C2 = torch.empty_like(C1)
     tx.invoke("tt.dot", [C2, _t_bf16(A, dev), _t_bf16(B, dev), M, N, K, K, K, N])
     r32, r16 = oracle.gemm_bf16_rows(A, B, 0, M)
     check_close(_np_bits(C1), r32, r16, BF16_TOL)
     assert torch.equal(C1, C2)
+    # matmul's output is fp16, as the reference's (c = torch.empty(..., float16))
+    C3 = tx.matmul(_t_bf16(A, dev), b_kn)
+    assert C3.dtype == torch.float16
+    C4 = tx.dot(_t_bf16(A, dev), _t_bf16(B, dev), out_dtype=torch.float16)
+    assert torch.equal(C3, C4)
+    ref16 = oracle.encode_fmt(r32, oracle.F16).reshape(r32.shape)
+    got = C3.view(torch.int16).cpu().numpy().view(np.uint16)
+    d = np.abs(got.view(np.float16).astype(np.float64) - ref16.view(np.float16).astype(np.float64))
+    assert d.max() <= BF16_TOL * np.abs(r32).max()
 
 
 # ---------------------------------------------------------------------- fp8

@@ -106,6 +106,18 @@ def bf16_gemm_input(M: int, N: int, K: int, seed_stream: int = 0):
     return to_bf16_bits(a), to_bf16_bits(b)
 
 
+def matmul16_input(M: int, N: int, K: int, fp16: bool = True, seed_stream: int = 0):
+    """The reference matmul test's operands (test_amd_gemm_pipelined.py:338-343:
+    torch.randn a (M x K) and b (K x N), fp16): returns (A bits uint16[M,K],
+    B bits uint16[K,N], row-major), fp16 or bf16 (RNE) codes of N(0,1) values."""
+    g = rng(7, seed_stream)
+    a = g.standard_normal((M, K), dtype=np.float32)
+    b = g.standard_normal((K, N), dtype=np.float32)
+    if fp16:
+        return a.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    return to_bf16_bits(a), to_bf16_bits(b)
+
+
 # -------------------------------------------------------------- fp8 (c=4)
 def _quant_rows(x: np.ndarray, fmax: float, dtype):
     absmax = np.abs(x).max(axis=1).astype(np.float32)

@@ -217,29 +217,92 @@ const char *fp8_name(tx_dtype t) {
 
 }  // namespace
 
-static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
-                          int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
-  TX_TRY(check_gemm("tx_dot_bf16", A, lda, B, ldb, C, ldc, M, N, K));
+// tt.dot with 16-bit operands (bf16 / fp16) and a 16-bit output.  Kernel
+// names: tx_gemm_<operands>_<variant>[_out_<output>]; the split-K reduce
+// is the output type's.
+static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda, const void *B,
+                       tx_b_layout layout, int64_t ldb, void *C, tx_dtype ct, int64_t ldc,
+                       int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  if (ab != TX_BF16 && ab != TX_F16)
+    return fail(TX_INVALID_ARGUMENT, "%s: operand type must be bf16 or fp16 (got %d)", what, int(ab));
+  if (ct != TX_BF16 && ct != TX_F16)
+    return fail(TX_INVALID_ARGUMENT, "%s: output type must be bf16 or fp16 (got %d)", what, int(ct));
+  if (layout != TX_B_NK && layout != TX_B_KN)
+    return fail(TX_INVALID_ARGUMENT, "%s: B layout %d", what, int(layout));
+  const bool kn = layout == TX_B_KN && K > 0;
+  // B's row-length check is the layout's: K (N x K storage) or N (K x N)
+  TX_TRY(check_gemm(what, A, lda, B, kn ? K : ldb, C, ldc, M, N, K));
+  if (kn && ldb < N)
+    return fail(TX_INVALID_ARGUMENT, "%s: stride smaller than row length (ldb=%lld < N=%lld)", what,
+                (long long)ldb, (long long)N);
   if (M == 0 || N == 0) return TX_SUCCESS;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const char *pfx = ab == TX_BF16 ? "bf16" : "f16";
+  const char *sfx = ct == ab ? "" : (ct == TX_F16 ? "_out_f16" : "_out_bf16");
+  const char *reduce = ct == TX_BF16 ? "tx_gemm_bf16_splitk_reduce" : "tx_gemm_f16_splitk_reduce";
+  char base[64];
+  std::snprintf(base, sizeof base, "tx_gemm_%s_fast%s", pfx, sfx);
   tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
                     int32_t(K), 0, 0, 0};
-  if (fast_ok(A, lda * 2, B, ldb * 2, K * 2, M, N))
-    return launch_fast("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce", CodeObject::GemmBf16,
-                       args, K * 2, 2, s);
+  if (kn) {
+    // B^T into stream scratch (slot 0): N rows of kp = K rounded up to a
+    // whole 64-element (128-byte) step, zero-filled; A is copied into
+    // zero-padded rows of kp too when the fast path cannot read it as is.
+    const int64_t kp = (K + 63) / 64 * 64;
+    const bool a_pad = !(aligned(A, 16) && (lda * 2) % 16 == 0 && (K * 2) % 16 == 0);
+    const int64_t lim = int64_t(1) << 31;
+    if (N * kp * 2 >= lim || (a_pad ? M * kp * 2 : (M - 1) * lda * 2 + K * 2) >= lim)
+      return fail(TX_UNSUPPORTED, "%s: an operand exceeds the 2 GiB range of the GEMM's buffer loads",
+                  what);
+    if (kp / 64 > 65535) return fail(TX_UNSUPPORTED, "%s: K = %lld too large for the transpose grid", what,
+                                     (long long)K);
+    const size_t bt_bytes = size_t(N) * size_t(kp) * 2;
+    const size_t a_bytes = a_pad ? size_t(M) * size_t(kp) * 2 : 0;
+    ScratchLease ws;  // held until every launch using it is enqueued
+    TX_TRY(ws.acquire(s, 0, bt_bytes + a_bytes));
+    uint16_t *wb = static_cast<uint16_t *>(ws.ptr());
+    uint16_t *wa = wb + size_t(N) * size_t(kp);
+    const bool tvec = aligned(B, 16) && (ldb * 2) % 16 == 0;
+    const char *tname = tvec ? "tx_gemm_16_transpose_kn_v16" : "tx_gemm_16_transpose_kn_v2";
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::GemmBf16, tname, &fn));
+    tx_pad_args ta{B, wb, ldb, kp, int32_t(K), int32_t(N), int32_t(kp), 0};
+    TX_TRY(launch(fn, unsigned((N + 63) / 64), unsigned(kp / 64), 256, s, &ta, sizeof ta, tname));
+    args.B = wb;
+    args.ldb = kp;
+    if (a_pad) {
+      TX_TRY(get_kernel(CodeObject::GemmBf16, "tx_gemm_bf16_pad_rows", &fn));
+      tx_pad_args pa{A, wa, lda, kp, int32_t(M), int32_t(K), int32_t(kp),
+                     pad_load_bytes(A, lda * 2, K * 2)};
+      const int64_t ga = std::min<int64_t>((M * kp / 8 + 255) / 256, int64_t(cu_count()) * 16);
+      TX_TRY(launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, "tx_gemm_bf16_pad_rows"));
+      args.A = wa;
+      args.lda = kp;
+      args.K = int32_t(kp);
+    }
+    return launch_fast(base, reduce, CodeObject::GemmBf16, args, int64_t(args.K) * 2, 2, s);
+  }
+  if (layout == TX_B_KN) args.ldb = K;  // K = 0: B is never read
+  if (fast_ok(A, lda * 2, B, args.ldb * 2, K * 2, M, N))
+    return launch_fast(base, reduce, CodeObject::GemmBf16, args, K * 2, 2, s);
   {
     tx_gemm_args padded = args;
-    const tx_status st = launch_padded("tx_gemm_bf16_fast", "tx_gemm_bf16_splitk_reduce",
-                                       "tx_gemm_bf16_pad_rows", CodeObject::GemmBf16, padded, 2, s);
+    const tx_status st = launch_padded(base, reduce, "tx_gemm_bf16_pad_rows", CodeObject::GemmBf16,
+                                       padded, 2, s);
     if (st != TX_UNSUPPORTED) return st;
     clear_error();
   }
   static const int widths[] = {16, 8, 2};
-  const int vec = pick_vec(A, lda * 2, B, ldb * 2, K * 2, widths, 3);
+  const int vec = pick_vec(A, lda * 2, B, args.ldb * 2, K * 2, widths, 3);
   const int tile = use_big_tile(M, N) ? 256 : 128;
   char kname[64];
-  std::snprintf(kname, sizeof kname, "tx_gemm_bf16_%dx%d_v%d", tile, tile, vec);
+  std::snprintf(kname, sizeof kname, "tx_gemm_%s_%dx%d_v%d%s", pfx, tile, tile, vec, sfx);
   return launch_gemm(kname, CodeObject::GemmBf16, args, tile, tile, s);
+}
+
+static tx_status dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  return dot16("tx_dot_bf16", A, TX_BF16, lda, B, TX_B_NK, ldb, C, TX_BF16, ldc, M, N, K, stream);
 }
 
 // The fp8 GEMM's optional epilogue (tx_dot_fp8_scaled_ex).
@@ -714,10 +777,12 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
 }
 
 // Table forms.
-// tt.dot: {C (result), A, B, M, N, K, lda, ldb, ldc}
+// tt.dot: {C (result), A, B, M, N, K, lda, ldb, ldc[, ab_type, c_type,
+// b_layout]} -- without the last three, bf16 operands and output and B
+// stored N x K.
 static tx_status dot_op(tx_value *v, size_t count, tx_stream_t stream) {
   Operands o{v, count, "tt.dot"};
-  TX_TRY(o.need(9));
+  if (count != 9) TX_TRY(o.need(12));
   void *C, *A, *B;
   int64_t M, N, K, lda, ldb, ldc;
   TX_TRY(o.ptr(0, &C));
@@ -729,7 +794,14 @@ static tx_status dot_op(tx_value *v, size_t count, tx_stream_t stream) {
   TX_TRY(o.integer(6, &lda));
   TX_TRY(o.integer(7, &ldb));
   TX_TRY(o.integer(8, &ldc));
-  return dot_bf16(A, lda, B, ldb, C, ldc, M, N, K, stream);
+  int64_t ab = TX_BF16, ct = TX_BF16, layout = TX_B_NK;
+  if (count == 12) {
+    TX_TRY(o.integer(9, &ab));
+    TX_TRY(o.integer(10, &ct));
+    TX_TRY(o.integer(11, &layout));
+  }
+  return dot16("tt.dot", A, tx_dtype(ab), lda, B, tx_b_layout(layout), ldb, C, tx_dtype(ct), ldc, M,
+               N, K, stream);
 }
 
 // tt.dot_scaled.rowcol: {C (result), A, B, scale_a, scale_b, M, N, K, lda, ldb,
@@ -912,7 +984,9 @@ static tx_status dot_fp8_ex_op(tx_value *v, size_t count, tx_stream_t stream) {
 }
 
 static const bool reg_dot = register_op(
-    "tt.dot", dot_op, "C:bf16*(result), A:bf16*, B:bf16* (N x K), M, N, K, lda, ldb, ldc");
+    "tt.dot", dot_op,
+    "C:bf16|f16*(result), A:bf16|f16*, B:bf16|f16* (N x K, or K x N with b_layout 1), M, N, K, lda, "
+    "ldb, ldc[, ab_type:i32, c_type:i32, b_layout:i32]");
 static const bool reg_dot_fp8 = register_op(
     "tt.dot_scaled.rowcol", dot_fp8_op,
     "C:bf16*(result), A:fp8*, B:fp8* (N x K), scale_a:f32*, scale_b:f32*, M, N, K, lda, ldb, "
@@ -946,6 +1020,13 @@ static const bool reg_gemv = register_op(
 }  // namespace tx
 
 extern "C" {
+
+TX_API tx_status tx_dot(const void *A, tx_dtype ab_type, int64_t lda, const void *B,
+                        tx_b_layout b_layout, int64_t ldb, void *C, tx_dtype c_type, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot16("tx_dot", A, ab_type, lda, B, b_layout, ldb, C, c_type, ldc, M, N, K, stream);
+}
 
 TX_API tx_status tx_dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                              int64_t ldc, int64_t M, int64_t N, int64_t K, tx_stream_t stream) {

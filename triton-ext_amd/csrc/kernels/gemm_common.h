@@ -256,4 +256,61 @@ __device__ __forceinline__ void pad_rows(const tx_pad_args &a) {
   }
 }
 
+// A row-major K x N operand of 16-bit elements (`rows` = K source rows of
+// `cols` = N elements, pitch src_ld) -> N rows of dst_cols (a multiple of
+// 64, >= K) elements, pitch dst_ld: dst[n][k] = src[k][n], zero for k >= K.
+// One workgroup of 256 threads per 64 (n) x 64 (k) tile, blockIdx.x the n
+// tile, blockIdx.y the k tile.  Thread t loads 8 consecutive n of source
+// rows k and k + 1 (k = 2 (t / 8), n = 8 (t % 8) within the tile; 16-byte
+// loads when VEC) and writes them to LDS as 8 dwords (k, k + 1) in the rows
+// of their n; then each thread writes two 16-byte runs of 8 k of one n.
+// The LDS tile is 64 rows of 36 dwords with the dword column XORed by
+// 8 (row / 8 mod 4): the 64 lanes' dword writes then fall at most two to a
+// bank, and a 16-byte read of dwords 4q .. 4q + 3 stays contiguous.
+template <bool VEC>
+__device__ __forceinline__ void transpose_kn(const tx_pad_args &a) {
+  constexpr int P = 36;  // LDS row pitch in dwords
+  __shared__ __attribute__((aligned(16))) uint32_t t[64 * P];
+  const int tid = threadIdx.x;
+  const int n0 = blockIdx.x * 64, k0 = blockIdx.y * 64;
+  const uint16_t *src = static_cast<const uint16_t *>(a.src);
+  {
+    const int p = tid >> 3, c = tid & 7;
+    const int k = k0 + 2 * p, n = n0 + 8 * c;
+    uint32_t lo[4] = {0u, 0u, 0u, 0u}, hi[4] = {0u, 0u, 0u, 0u};  // n pairs of rows k, k + 1
+    auto load = [&](int kk, uint32_t (&w)[4]) {
+      if (kk >= a.rows) return;
+      const uint16_t *row = src + int64_t(kk) * a.src_ld + n;
+      if (VEC && n + 8 <= a.cols) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(row);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (n + j < a.cols) w[j / 2] |= uint32_t(row[j]) << (16 * (j % 2));
+      }
+    };
+    load(k, lo);
+    load(k + 1, hi);
+    const int col = p ^ (8 * (c & 3));  // row 8c + j has (row / 8) mod 4 = c mod 4
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t e0 = (lo[j / 2] >> (16 * (j % 2))) & 0xFFFFu;
+      const uint32_t e1 = (hi[j / 2] >> (16 * (j % 2))) & 0xFFFFu;
+      t[(8 * c + j) * P + col] = e0 | (e1 << 16);
+    }
+  }
+  __syncthreads();
+  uint16_t *dst = static_cast<uint16_t *>(a.dst);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int u = tid + 256 * i;
+    const int r = u >> 3, q = u & 7;  // tile row n0 + r, k run 8q .. 8q + 7
+    const int d0 = (4 * q) ^ (8 * ((r >> 3) & 3));
+    const u32x4 w = *reinterpret_cast<const u32x4 *>(&t[r * P + d0]);
+    if (n0 + r < a.cols)
+      *reinterpret_cast<u32x4 *>(dst + int64_t(n0 + r) * a.dst_ld + k0 + 8 * q) = w;
+  }
+}
+
 }  // namespace txg

@@ -106,7 +106,14 @@ __host__ __device__ constexpr int spread_hi(int i, int n, int over) {
 // (32 bytes per lane: chunks 2g and 2g+1 of the half, g = lane / 32).
 template <class C>
 __device__ __forceinline__ void mfma32(txd::f32x16 &acc, const i32x8 &mb, const i32x8 &ma) {
-  if constexpr (!C::FP8) {
+  if constexpr (C::F16) {
+    const txd::f16x8 b0 = __builtin_bit_cast(txd::f16x8, __builtin_shufflevector(mb, mb, 0, 1, 2, 3));
+    const txd::f16x8 b1 = __builtin_bit_cast(txd::f16x8, __builtin_shufflevector(mb, mb, 4, 5, 6, 7));
+    const txd::f16x8 a0 = __builtin_bit_cast(txd::f16x8, __builtin_shufflevector(ma, ma, 0, 1, 2, 3));
+    const txd::f16x8 a1 = __builtin_bit_cast(txd::f16x8, __builtin_shufflevector(ma, ma, 4, 5, 6, 7));
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(b0, a0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(b1, a1, acc, 0, 0, 0);
+  } else if constexpr (!C::FP8) {
     const txd::bf16x8 b0 = __builtin_bit_cast(txd::bf16x8, __builtin_shufflevector(mb, mb, 0, 1, 2, 3));
     const txd::bf16x8 b1 = __builtin_bit_cast(txd::bf16x8, __builtin_shufflevector(mb, mb, 4, 5, 6, 7));
     const txd::bf16x8 a0 = __builtin_bit_cast(txd::bf16x8, __builtin_shufflevector(ma, ma, 0, 1, 2, 3));
@@ -153,8 +160,6 @@ __device__ __forceinline__ void wait_and_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-// Output element types of the fast tile.
-enum FastOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
 
 // The tile (tm, tn) of C (256 x BN elements at row 256 tm, column BN tn),
 // split `split` of a.splits along K.  TRANS (bf16 out, no split): the tile
@@ -169,7 +174,8 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   constexpr bool FP4 = C::EL_A_ == EL_E2M1;
   static_assert(!FP4 || (MX && C::EL_B_ == EL_E2M1), "fp4: MX-scaled, both operands");
   constexpr int SD = FP4 ? 2 : 1;  // MX scale dwords per row and K step (4 blocks each)
-  static_assert(OUT == OUT_BF16 || MX, "fp16 / fp32 output: MX variant only");
+  static_assert(OUT == OUT_BF16 || MX || (OUT == OUT_F16 && !C::FP8),
+                "fp16 output: MX or 16-bit operands; fp32 output: MX only");
   static_assert(!EPI || (C::FP8 && !MX && OUT == OUT_BF16), "fused epilogue: row/column-scaled fp8");
   static_assert(!TRANS || (!EPI && OUT == OUT_BF16), "transposed store: plain bf16 output");
   // Wave grid WM x WN.  256x128 tiles with 8 waves take 4 x 2 (64 x 64 per

@@ -7,12 +7,16 @@
 namespace txg {
 
 // Operand element kinds for the MFMA selection.
-enum { EL_BF16 = 0, EL_E4M3 = 1, EL_E5M2 = 2, EL_E2M1 = 4 };  // e2m1: fp4, two per byte along K
+enum { EL_BF16 = 0, EL_E4M3 = 1, EL_E5M2 = 2, EL_E2M1 = 4, EL_F16 = 5 };  // e2m1: fp4, two per byte along K
+
+// Output element types of the tiles (16-bit kinds round to nearest even).
+enum GemmOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
 
 template <int EL_A, int EL_B, int BM_, int BN_, int WM_, int WN_, int VEC_>
 struct GemmCfg {
   static constexpr int EL_A_ = EL_A, EL_B_ = EL_B;
-  static constexpr bool FP8 = EL_A != EL_BF16;
+  static constexpr bool FP8 = EL_A != EL_BF16 && EL_A != EL_F16;  // else 16-bit operands
+  static constexpr bool F16 = EL_A == EL_F16;
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, VEC = VEC_;
   static constexpr int T = 64 * WM * WN;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -29,7 +33,12 @@ template <int EL> struct F8Code { static constexpr int v = EL == EL_E5M2 ? 1 : E
 
 template <class C>
 __device__ __forceinline__ f32x4 mfma_step(f32x4 acc, const u32x4 (&mfa)[2], const u32x4 (&mfb)[2]) {
-  if constexpr (!C::FP8) {
+  if constexpr (C::F16) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(txd::f16x8, mfa[0]),
+                                                 __builtin_bit_cast(txd::f16x8, mfb[0]), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(txd::f16x8, mfa[1]),
+                                                 __builtin_bit_cast(txd::f16x8, mfb[1]), acc, 0, 0, 0);
+  } else if constexpr (!C::FP8) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(txd::bf16x8, mfa[0]),
                                                   __builtin_bit_cast(txd::bf16x8, mfb[0]), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(txd::bf16x8, mfa[1]),
@@ -46,8 +55,9 @@ __device__ __forceinline__ f32x4 mfma_step(f32x4 acc, const u32x4 (&mfa)[2], con
   return acc;
 }
 
-template <class C>
+template <class C, int OUT = OUT_BF16>
 __device__ __forceinline__ void gemm_tile(const tx_gemm_args &a) {
+  static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "generic tile: bf16 out, or fp16 out of 16-bit operands");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE_BYTES];
 
   int tm, tn;
@@ -162,12 +172,16 @@ __device__ __forceinline__ void gemm_tile(const tx_gemm_args &a) {
       } else {
         uint16_t *dst = Cb + int64_t(m) * a.ldc + n;
         if (cvec && n + 3 < a.N) {
-          txd::u32x2 p = {txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
+          txd::u32x2 p = OUT == OUT_F16
+                             ? txd::u32x2{txd::pack_f16x2(v[0], v[1]), txd::pack_f16x2(v[2], v[3])}
+                             : txd::u32x2{txd::pack_bf16x2(v[0], v[1]), txd::pack_bf16x2(v[2], v[3])};
           *reinterpret_cast<txd::u32x2 *>(dst) = p;
         } else {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            if (n + j < a.N) dst[j] = uint16_t(txd::f32_to_bf16_bits(v[j]));
+            if (n + j < a.N)
+              dst[j] = OUT == OUT_F16 ? uint16_t(txd::pack_f16x2(v[j], 0.0f))
+                                      : uint16_t(txd::f32_to_bf16_bits(v[j]));
         }
       }
     }

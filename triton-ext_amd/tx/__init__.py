@@ -162,37 +162,69 @@ def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor
     return old if return_old else bins
 
 
-def dot(a: torch.Tensor, b_nk: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """tt.dot on bf16: out[M,N] = a[M,K] @ b where b is column-major K x N,
-    passed as its N x K (K-contiguous) storage ``b_nk``.  fp32 accumulate,
-    bf16 output."""
-    _on_gpu(a, b_nk, out)
-    if a.dtype != torch.bfloat16 or b_nk.dtype != torch.bfloat16:
-        raise ValueError("dot takes bf16 operands")
-    if a.dim() != 2 or b_nk.dim() != 2 or a.shape[1] != b_nk.shape[1]:
-        raise ValueError(f"incompatible shapes {tuple(a.shape)} and {tuple(b_nk.shape)} (N x K)")
-    if a.stride(1) != 1 or b_nk.stride(1) != 1:
-        raise ValueError("operands must be K-contiguous")
+_DOT16 = (torch.bfloat16, torch.float16)
+
+
+def _dot16(a, b, b_layout, out, out_dtype):
+    _on_gpu(a, b, out)
+    if a.dtype not in _DOT16 or b.dtype != a.dtype:
+        raise ValueError(f"dot takes two bf16 or two fp16 operands (got {a.dtype}, {b.dtype})")
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("dot takes 2-D operands")
     M, K = a.shape
-    N = b_nk.shape[0]
+    if b_layout == _lib.B_NK:
+        N = b.shape[0]
+        if b.shape[1] != K:
+            raise ValueError(f"incompatible shapes {tuple(a.shape)} and {tuple(b.shape)} (N x K)")
+    else:
+        N = b.shape[1]
+        if b.shape[0] != K:
+            raise ValueError(f"incompatible shapes {tuple(a.shape)} and {tuple(b.shape)} (K x N)")
+    if a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("operand rows must be contiguous")
+    out_dtype = a.dtype if out_dtype is None else out_dtype
+    if out_dtype not in _DOT16:
+        raise ValueError("out_dtype must be bf16 or fp16")
     if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
-    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
-        raise ValueError("out must be a row-major bf16 M x N tensor")
-    check(lib.tx_dot_bf16(_ptr(a), a.stride(0), _ptr(b_nk), b_nk.stride(0), _ptr(out),
-                          out.stride(0), M, N, K, _stream(a)))
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"out must be a row-major {out_dtype} M x N tensor")
+    check(lib.tx_dot(_ptr(a), _TX_DTYPE[a.dtype], a.stride(0), _ptr(b), b_layout, b.stride(0),
+                     _ptr(out), _TX_DTYPE[out_dtype], out.stride(0), M, N, K, _stream(a)))
     return out
 
 
+def dot(a: torch.Tensor, b_nk: torch.Tensor, out: torch.Tensor | None = None, *,
+        out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """tt.dot on 16-bit operands: out[M,N] = a[M,K] @ b where b is column-major
+    K x N, passed as its N x K (K-contiguous) storage ``b_nk``.  Both operands
+    bf16 or both fp16; fp32 accumulate; output bf16 or fp16 (default: the
+    operands' type), rounded to nearest even."""
+    return _dot16(a, b_nk, _lib.B_NK, out, out_dtype)
+
+
+def dot_kn(a: torch.Tensor, b_kn: torch.Tensor, out: torch.Tensor | None = None, *,
+           out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """dot with b stored row-major K x N (rows of N contiguous), the layout of
+    the reference's matmul caller; b is transposed into the library's stream
+    scratch first."""
+    return _dot16(a, b_kn, _lib.B_KN, out, out_dtype)
+
+
 def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """Host wrapper in the shape of the reference's matmul(a, b)
-    (test_amd_gemm_pipelined.py:303-331): a is M x K, b is K x N; allocates
-    the output.  b must be column-major (b.stride(0) == 1), i.e. a transposed
-    view of an N x K tensor."""
+    """The reference's matmul(a, b) (test_amd_gemm_pipelined.py:303-331): a
+    (M x K, contiguous) times b (K x N), fp16 output allocated here, as its
+    `c = torch.empty((M, N), dtype=torch.float16)`.  Operands fp16 (the
+    reference's test_op and benchmark) or bf16.  b may be row-major (the
+    reference's case), column-major, or any other strides (copied to
+    row-major first)."""
     assert a.shape[1] == b.shape[0], "Incompatible dimensions"
-    if b.stride(0) != 1:
-        raise ValueError("b must be column-major (K-contiguous); pass w.t() of an N x K tensor")
-    return dot(a, b.t())
+    assert a.is_contiguous(), "Matrix A must be contiguous"
+    if b.dim() == 2 and b.shape[1] > 0 and b.stride(1) == 1:
+        return _dot16(a, b, _lib.B_KN, None, torch.float16)
+    if b.dim() == 2 and b.shape[0] > 0 and b.stride(0) == 1:
+        return _dot16(a, b.t(), _lib.B_NK, None, torch.float16)
+    return _dot16(a, b.contiguous(), _lib.B_KN, None, torch.float16)
 
 
 _ACT = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "relu": _lib.ACT_RELU,

@@ -35,12 +35,14 @@ RMW = {"add": 0, "fadd": 1, "max": 2, "min": 3, "umax": 4, "umin": 5,
        "and": 6, "or": 7, "xor": 8}
 # tx_value_kind
 VALUE_PTR, VALUE_INT = 0, 1
+# tx_b_layout
+B_NK, B_KN = 0, 1
 
 # Every symbol include/tx_plugin.h declares.
 EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
-    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16",
+    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16", "tx_dot",
     "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped",
     "tx_dot_fp8_scaled_grouped_noalloc", "tx_dot_fp8_scaled_batched",
     "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
@@ -121,6 +123,8 @@ def _load():
     L.tx_atomic_rmw_scatter.restype = I
     L.tx_dot_bf16.argtypes = [P, I64, P, I64, P, I64, I64, I64, I64, VP]
     L.tx_dot_bf16.restype = I
+    L.tx_dot.argtypes = [P, I, I64, P, I, I64, P, I, I64, I64, I64, I64, VP]
+    L.tx_dot.restype = I
     L.tx_dot_fp8_scaled.argtypes = [P, I, I64, P, P, I, I64, P, P, I64, I64, I64, I64, VP]
     L.tx_dot_fp8_scaled.restype = I
     L.tx_dot_fp8_scaled_ex.argtypes = [P, I, I64, P, P, I, I64, P, P, I, P, I, ctypes.c_float,
