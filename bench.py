@@ -469,6 +469,9 @@ def cpu_baseline():
     progress("cpu baseline: triton interpreter")
     return {
         "value": gemm_tflops, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+        "what": "the oracle: this repository's C restatement of the path (OpenMP, fp64 "
+                "accumulation), not the reference's own CPU path; that path, plain-Triton kernels "
+                "of each op under Triton's interpreter, is under triton_interpreter",
         "sample": f"oracle fp8 scaled GEMM, {rows} of 8192 rows of M=N=K=8192 "
                   f"({2.0 * rows * N * K / 1e9:.0f} GFLOP in {dt:.1f} s, fp64 accumulate)",
         "fp8_convert": {"value": 5.0 * x.size / dt_conv / 1e9, "unit": "GB/s",

@@ -20,8 +20,11 @@ same operations, written for this timing:
 * ``gemm_bf16_kernel`` tiled ``tl.dot`` of bf16 tiles upcast to fp32 first:
   the interpreter keeps bf16 as raw uint16 (interpreter.py:186-187) and its
   ``create_dot`` (:630-637) does not convert them;
+* ``gemm_f16_kn_kernel`` the reference's matmul operands: fp16 a (M x K) and
+  row-major fp16 b (K x N), upcast to fp32 for tl.dot, fp16 output;
+* ``decode_kernel``   fp8 codes back to fp32 (the round trip's decode leg);
 * ``gemv_kernel``     e5m2 weights dequantised by per-group fp32 scales,
-  multiplied by one bf16 activation row.
+  multiplied by one bf16 activation row per program.
 
 The interpreter's own numerics differ from the fp8/bf16 semantics in places
 (its fp8 rounding and its truncating fp32->bf16 cast); the results here are
@@ -63,6 +66,13 @@ if IMPORT_ERROR is None:
         if SAT:
             x = tl.clamp(x, -MAXV, MAXV)
         tl.store(y_ptr + offs, x.to(DST), mask=m)
+
+    @triton.jit
+    def decode_kernel(x_ptr, y_ptr, n, BLOCK: tl.constexpr):
+        offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+        m = offs < n
+        x = tl.load(x_ptr + offs, mask=m, other=0.0)
+        tl.store(y_ptr + offs, x.to(tl.float32), mask=m)
 
     @triton.jit
     def scatter_kernel(bins_ptr, idx_ptr, v_ptr, n, BLOCK: tl.constexpr):
@@ -112,6 +122,25 @@ if IMPORT_ERROR is None:
                  mask=mm[:, None] & mn[None, :])
 
     @triton.jit
+    def gemm_f16_kn_kernel(a_ptr, b_ptr, c_ptr, M, N, K,
+                           BM: tl.constexpr, BN: tl.constexpr, BK: tl.constexpr):
+        # the reference's matmul operands: a M x K, b K x N row-major, fp16 out
+        rm = tl.program_id(0) * BM + tl.arange(0, BM)
+        rn = tl.program_id(1) * BN + tl.arange(0, BN)
+        rk = tl.arange(0, BK)
+        mm = rm < M
+        mn = rn < N
+        acc = tl.zeros((BM, BN), dtype=tl.float32)
+        for k in range(0, K, BK):
+            kk = k + rk
+            mk = kk < K
+            a = tl.load(a_ptr + rm[:, None] * K + kk[None, :], mask=mm[:, None] & mk[None, :], other=0.0)
+            b = tl.load(b_ptr + kk[:, None] * N + rn[None, :], mask=mk[:, None] & mn[None, :], other=0.0)
+            acc += tl.dot(a.to(tl.float32), b.to(tl.float32))
+        tl.store(c_ptr + rm[:, None] * N + rn[None, :], acc.to(tl.float16),
+                 mask=mm[:, None] & mn[None, :])
+
+    @triton.jit
     def gemv_kernel(x_ptr, w_ptr, s_ptr, y_ptr, N, K,
                     BN: tl.constexpr, G: tl.constexpr):
         rn = tl.program_id(0) * BN + tl.arange(0, BN)
@@ -149,6 +178,15 @@ def convert(x: np.ndarray, fmt: str = "e4m3fn", sat: bool = False, block: int = 
     yv = y.view(torch.float8_e4m3fn if fmt == "e4m3fn" else torch.float8_e5m2)
     convert_kernel[(triton.cdiv(x.size, block),)](xt, yv, x.size, DST=dst, SAT=sat, MAXV=maxv,
                                                  BLOCK=block)
+    return y.numpy()
+
+
+def decode(codes: np.ndarray, fmt: str = "e4m3fn", block: int = 65536) -> np.ndarray:
+    """fp8 codes -> fp32 through the interpreter's cast."""
+    _need()
+    ct = _t(codes.astype(np.uint8, copy=False), torch.float8_e4m3fn if fmt == "e4m3fn" else torch.float8_e5m2)
+    y = torch.empty(codes.size, dtype=torch.float32)
+    decode_kernel[(triton.cdiv(codes.size, block),)](ct, y, codes.size, BLOCK=block)
     return y.numpy()
 
 
@@ -191,14 +229,30 @@ def gemm_bf16(a_bits, b_bits, rows=None, tile=GEMM_TILE) -> np.ndarray:
     return c.view(torch.uint16).numpy()
 
 
-def gemv(x_bits, wq, s, group: int = 128, block_n: int = 256) -> np.ndarray:
-    """y (bf16 bits, M x N) = x (M x K bf16 bits) times dequant(Wq e5m2 N x K, s N x K/group)^T."""
+def gemm_f16_kn(a_bits, b_bits, rows=None, tile=GEMM_TILE) -> np.ndarray:
+    """C[:rows] (fp16 bits) = A B with A M x K and B K x N (row-major) fp16 bits."""
+    _need()
+    M, K = a_bits.shape
+    N = b_bits.shape[1]
+    rows = M if rows is None else rows
+    BM, BN, BK = tile
+    c = torch.empty(rows, N, dtype=torch.float16)
+    gemm_f16_kn_kernel[(triton.cdiv(rows, BM), triton.cdiv(N, BN))](
+        _t(a_bits[:rows], torch.float16), _t(b_bits, torch.float16), c, rows, N, K,
+        BM=BM, BN=BN, BK=BK)
+    return c.view(torch.uint16).numpy()
+
+
+def gemv(x_bits, wq, s, group: int = 128, block_n: int = 256, rows=None) -> np.ndarray:
+    """y (bf16 bits, rows x N) = x (M x K bf16 bits) times dequant(Wq e5m2 N x K,
+    s N x K/group)^T, for the first `rows` rows of x (default all)."""
     _need()
     M, K = x_bits.shape
+    rows = M if rows is None else rows
     N = wq.shape[0]
-    y = torch.empty(M, N, dtype=torch.bfloat16)
-    gemv_kernel[(triton.cdiv(N, block_n), M)](
-        _t(x_bits, torch.bfloat16), _t(wq, torch.float8_e5m2), _t(s), y, N, K,
+    y = torch.empty(rows, N, dtype=torch.bfloat16)
+    gemv_kernel[(triton.cdiv(N, block_n), rows)](
+        _t(x_bits[:rows], torch.bfloat16), _t(wq, torch.float8_e5m2), _t(s), y, N, K,
         BN=block_n, G=group)
     return y.view(torch.uint16).numpy()
 
@@ -255,12 +309,17 @@ def baseline(gemm_rows: int = 64, bf16_rows: int = 64, progress=None) -> dict:
            "host": host_facts()}
 
     x = workloads.fp8_input()
-    for fmt, sat in (("e4m3fn", False), ("e4m3fn", True)):
-        _, dt = _clock(lambda: convert(x, fmt, sat))
+    for fmt, sat in (("e4m3fn", False), ("e4m3fn", True), ("e5m2", False), ("e5m2", True)):
+        codes, dt = _clock(lambda: convert(x, fmt, sat))
         out[f"convert_{fmt}_{'sat' if sat else 'nonsat'}"] = {
             "value": 5.0 * x.size / dt / 1e9, "unit": "GB/s", "seconds": dt,
             "sample": f"full: {x.size:,} fp32 values, BLOCK=65536"}
-    del x
+        if not sat:
+            _, dt = _clock(lambda: decode(codes, fmt))
+            out[f"decode_{fmt}"] = {
+                "value": 5.0 * x.size / dt / 1e9, "unit": "GB/s", "seconds": dt,
+                "sample": f"full: {x.size:,} codes back to fp32 (the round trip's decode leg)"}
+    del x, codes
     step("interpreter convert")
 
     for kind in ("i32", "f32"):
@@ -293,9 +352,26 @@ def baseline(gemm_rows: int = 64, bf16_rows: int = 64, progress=None) -> dict:
                   f"time scaled by {4096 // bf16_rows}"}
     step("interpreter bf16 GEMM sample")
 
-    xg, wq, s = workloads.gemv_input(1)
-    _, dt = _clock(lambda: gemv(xg, wq, s))
-    nb = wq.size + 4 * s.size + 2 * xg.size + 2 * xg.shape[0] * wq.shape[0]
-    out["gemv_e5m2_m1"] = {"value": nb / dt / 1e9, "unit": "GB/s", "seconds": dt,
-                           "sample": "full: M=1, N=14336, K=4096, group 128"}
+    a, b = workloads.matmul16_input(bf16_rows, 4096, 4096)
+    _, dt = _clock(lambda: gemm_f16_kn(a, b))
+    out["matmul_f16_kn_4096"] = {
+        "value": 2.0 * bf16_rows * 4096 * 4096 / dt / 1e12, "unit": "TFLOP/s",
+        "seconds_sample": dt, "seconds_extrapolated": dt * 4096 / bf16_rows,
+        "sample": f"extrapolated: the reference's matmul operands (fp16 a, row-major fp16 b), "
+                  f"programs of the first {bf16_rows} of 4096 rows of C, time scaled by "
+                  f"{4096 // bf16_rows}"}
+    step("interpreter fp16 matmul sample")
+
+    for m in (1, 4, 16):
+        xg, wq, s = workloads.gemv_input(m)
+        rows = 1  # every row's programs stream all of W: time is linear in the rows
+        _, dt = _clock(lambda: gemv(xg, wq, s, rows=rows))
+        dt_all = dt * m / rows
+        nb = wq.size + 4 * s.size + 2 * xg.size + 2 * m * wq.shape[0]
+        out[f"gemv_e5m2_m{m}"] = {
+            "value": nb / dt_all / 1e9, "unit": "GB/s", "seconds": dt_all,
+            "sample": (f"full: M=1, N=14336, K=4096, group 128" if m == 1 else
+                       f"extrapolated: the programs of the first of {m} rows (each row's "
+                       f"stream all of W), time scaled by {m}")}
+    step("interpreter GEMV")
     return out
