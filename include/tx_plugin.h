@@ -104,7 +104,8 @@ typedef enum tx_rmw_op {
   TX_RMW_UMIN = 5, /* unsigned int32 min */
   TX_RMW_AND = 6,
   TX_RMW_OR = 7,
-  TX_RMW_XOR = 8
+  TX_RMW_XOR = 8,
+  TX_RMW_XCHG = 9  /* exchange: the bin takes val (any 32-bit bins) */
 } tx_rmw_op;
 
 /* Storage of tt.dot's B operand (K x N) in tx_dot. */
@@ -259,12 +260,34 @@ TX_API tx_status tx_fp_to_fp_with_rbits(const void *src, tx_dtype src_type, void
  * If old != NULL, every update instead returns the bin's value before it was
  * applied (the tt.atomic_rmw result) in old[i] (0 for dropped updates), and
  * no pre-aggregation is done.
+ * TX_RMW_XCHG takes TX_I32, TX_U32 or TX_F32 bins (the 32-bit pattern is
+ * exchanged) and is one atomic per update: where several updates hit one
+ * bin they apply one at a time in an order the hardware picks, so the bin
+ * ends with one of their values and, with old, their old values are the
+ * bin's initial value and the other updates' values.
  */
 TX_API tx_status tx_atomic_rmw_scatter(void *bins, tx_dtype bins_type,
                                        int64_t nbins, const int32_t *idx,
                                        const void *val, const uint8_t *mask,
                                        int64_t n, tx_rmw_op op, void *old,
                                        tx_stream_t stream);
+
+/*
+ * tt.atomic_cas in scatter form: for every i < n with mask[i] != 0 (mask may
+ * be NULL) and 0 <= idx[i] < nbins, atomically
+ *   old[i] = bins[idx[i]]; if (old[i] == cmp[i]) bins[idx[i]] = val[i];
+ * comparing the 32-bit patterns (bins_type TX_I32, TX_U32 or TX_F32; cmp
+ * and val of the same type).  Replaces Triton's per-lane lowering of
+ * tl.atomic_cas (tt.atomic_cas, passed through at
+ * uTLXConversionPatterns.cpp:610).  old may be NULL; dropped updates return
+ * 0.  Updates of one bin apply one at a time in an order the hardware
+ * picks.
+ */
+TX_API tx_status tx_atomic_cas_scatter(void *bins, tx_dtype bins_type,
+                                       int64_t nbins, const int32_t *idx,
+                                       const void *cmp, const void *val,
+                                       const uint8_t *mask, int64_t n,
+                                       void *old, tx_stream_t stream);
 
 /*
  * tt.dot with bf16 operands, fp32 accumulation and bf16 output:

@@ -233,6 +233,119 @@ def bf16_to_f32(h) -> np.ndarray:
 
 
 # -------------------------------------------------------------------- gemm
+def atomic_xchg_seq(bins, idx, val, mask=None):
+    """tt.atomic_rmw xchg applied one update at a time in element order, one
+    of the orders a device may pick: returns (bins after, old per update; 0
+    for dropped updates).  32-bit patterns.  Where indices repeat, results
+    from another order differ; atomic_xchg_consistent checks those."""
+    b = np.array(bins, copy=True).view(np.uint32)
+    v = np.asarray(val).view(np.uint32)
+    idx = np.asarray(idx, np.int64)
+    old = np.zeros(idx.size, np.uint32)
+    live = (idx >= 0) & (idx < b.size)
+    if mask is not None:
+        live &= np.asarray(mask) != 0
+    for i in np.flatnonzero(live):
+        k = idx[i]
+        old[i] = b[k]
+        b[k] = v[i]
+    return b.view(np.asarray(bins).dtype), old.view(np.asarray(val).dtype)
+
+
+def atomic_cas_seq(bins, idx, cmp, val, mask=None):
+    """tt.atomic_cas applied one update at a time in element order (one of the
+    orders a device may pick): old = bins[k]; if old == cmp (bit for bit):
+    bins[k] = val.  Returns (bins after, old per update; 0 for dropped
+    updates)."""
+    b = np.array(bins, copy=True).view(np.uint32)
+    c = np.asarray(cmp).view(np.uint32)
+    v = np.asarray(val).view(np.uint32)
+    idx = np.asarray(idx, np.int64)
+    old = np.zeros(idx.size, np.uint32)
+    live = (idx >= 0) & (idx < b.size)
+    if mask is not None:
+        live &= np.asarray(mask) != 0
+    for i in np.flatnonzero(live):
+        k = idx[i]
+        old[i] = b[k]
+        if b[k] == c[i]:
+            b[k] = v[i]
+    return b.view(np.asarray(bins).dtype), old.view(np.asarray(val).dtype)
+
+
+def _live(idx, nbins, mask):
+    idx = np.asarray(idx, np.int64)
+    live = (idx >= 0) & (idx < nbins)
+    if mask is not None:
+        live &= np.asarray(mask) != 0
+    return idx, live
+
+
+def atomic_xchg_consistent(init, final, idx, val, old, mask=None) -> bool:
+    """Whether (final, old) is the outcome of the exchanges applied one at a
+    time in SOME order: per bin, the old values of its updates together with
+    its final value are its initial value together with its updates' values
+    (as multisets), untouched bins keep their value and dropped updates
+    return 0.  (In an order, each exchange hands back the value the previous
+    one wrote, so the values written form one chain from the initial value.)"""
+    init = np.asarray(init).view(np.uint32)
+    final = np.asarray(final).view(np.uint32)
+    v = np.asarray(val).view(np.uint32)
+    o = np.asarray(old).view(np.uint32)
+    idx, live = _live(idx, init.size, mask)
+    if np.any(o[~live] != 0):
+        return False
+    touched = np.zeros(init.size, bool)
+    touched[idx[live]] = True
+    if np.any(final[~touched] != init[~touched]):
+        return False
+    bins = np.flatnonzero(touched)
+    lhs = (np.concatenate([idx[live], bins]), np.concatenate([o[live], final[bins]]))
+    rhs = (np.concatenate([idx[live], bins]), np.concatenate([v[live], init[bins]]))
+    lo = np.lexsort((lhs[1], lhs[0]))
+    ro = np.lexsort((rhs[1], rhs[0]))
+    return bool(np.array_equal(lhs[0][lo], rhs[0][ro]) and np.array_equal(lhs[1][lo], rhs[1][ro]))
+
+
+def atomic_cas_first_wins_consistent(init_value, final, idx, val, old, nbins) -> bool:
+    """The first-writer-wins pattern (every bin starts at init_value, every
+    update compares against init_value, values distinct and != init_value):
+    in any order exactly one update per touched bin sees init_value and
+    stores its value, and every other update of that bin sees that value."""
+    final = np.asarray(final).view(np.uint32)
+    v = np.asarray(val).view(np.uint32)
+    o = np.asarray(old).view(np.uint32)
+    idx = np.asarray(idx, np.int64)
+    e = np.uint32(init_value)
+    win = o == e
+    touched = np.bincount(idx, minlength=nbins) > 0
+    wins = np.bincount(idx[win], minlength=nbins)
+    if not np.array_equal(wins, touched.astype(np.int64)):
+        return False
+    if np.any(final[idx[win]] != v[win]) or np.any(o[~win] != final[idx[~win]]):
+        return False
+    return bool(np.all(final[~touched] == e))
+
+
+def atomic_cas_ticket_consistent(final, idx, cmp, old, nbins) -> bool:
+    """The ticket pattern (bins start at 0; the updates of a bin with k
+    updates compare against 0 .. k-1 once each and store cmp + 1): in any
+    order the successful updates (old == cmp) of a bin are exactly those with
+    cmp < final, and every other update saw a value in [0, final] other than
+    its cmp."""
+    final = np.asarray(final, np.int64)
+    c = np.asarray(cmp, np.int64)
+    o = np.asarray(old, np.int64)
+    idx = np.asarray(idx, np.int64)
+    ok = o == c
+    f = final[idx]
+    if not np.array_equal(ok, c < f):
+        return False
+    if not np.array_equal(np.bincount(idx[ok], minlength=nbins), np.asarray(final, np.int64)):
+        return False
+    return bool(np.all((o[~ok] >= 0) & (o[~ok] <= f[~ok])))
+
+
 def gemm_bf16_rows(A, B, r0: int, r1: int, nthreads: int = 0):
     """Rows [r0, r1) of A @ B^T-stored-B (B given as N x K, K contiguous).
 

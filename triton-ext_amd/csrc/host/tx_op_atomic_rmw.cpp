@@ -1,4 +1,5 @@
-// tt.atomic_rmw scatter entry point and its table registration.
+// tt.atomic_rmw and tt.atomic_cas scatter entry points and their table
+// registrations.
 //
 // Reference: tl.atomic_add / tl.atomic_max ... lower to tt.atomic_rmw, which
 // the plugin passes through unchanged (uTLXConversionPatterns.cpp:611); the
@@ -32,8 +33,14 @@ const char *op_name(tx_rmw_op op) {
     case TX_RMW_AND: return "and";
     case TX_RMW_OR: return "or";
     case TX_RMW_XOR: return "xor";
+    case TX_RMW_XCHG: return "xchg";
   }
   return nullptr;
+}
+
+// One thread per update (grid-stride beyond 64 workgroups per CU).
+unsigned direct_grid(int64_t n) {
+  return unsigned(std::min<int64_t>((n + 255) / 256, int64_t(cu_count()) * 64));
 }
 
 }  // namespace
@@ -53,6 +60,9 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
   if (op == TX_RMW_FADD) {
     if (bins_type != TX_F32)
       return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: fadd needs TX_F32 bins");
+  } else if (op == TX_RMW_XCHG) {
+    if (bins_type != TX_I32 && bins_type != TX_U32 && bins_type != TX_F32)
+      return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: xchg needs 32-bit bins");
   } else if (bins_type != TX_I32 && bins_type != TX_U32) {
     return fail(TX_INVALID_ARGUMENT,
                 "tx_atomic_rmw_scatter: integer ops need TX_I32 or TX_U32 bins");
@@ -68,6 +78,11 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
   const int cus = cu_count();
   tx_scatter_args args{bins, idx, val, mask, old, n, int32_t(nbins), 0, 0, 0};
   char kname[64];
+  if (op == TX_RMW_XCHG) {
+    hipFunction_t fn;
+    TX_TRY(get_kernel(CodeObject::Scatter, "tx_scatter_xchg", &fn));
+    return launch(fn, direct_grid(n), 1, 256, s, &args, sizeof args, "tx_scatter_xchg");
+  }
   if (old) {
     std::snprintf(kname, sizeof kname, "tx_scatter_%s_old", name);
     hipFunction_t fn;
@@ -128,10 +143,60 @@ static tx_status atomic_rmw_op(tx_value *v, size_t count, tx_stream_t stream) {
                             static_cast<const uint8_t *>(mask), n, tx_rmw_op(op), old, stream);
 }
 
+static tx_status atomic_cas_scatter(void *bins, tx_dtype bins_type, int64_t nbins,
+                                    const int32_t *idx, const void *cmp, const void *val,
+                                    const uint8_t *mask, int64_t n, void *old,
+                                    tx_stream_t stream) {
+  if (n < 0 || nbins < 0)
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: n = %lld, nbins = %lld",
+                (long long)n, (long long)nbins);
+  if (nbins > INT32_MAX)
+    return fail(TX_UNSUPPORTED, "tx_atomic_cas_scatter: nbins %lld exceeds int32 indexing",
+                (long long)nbins);
+  if (bins_type != TX_I32 && bins_type != TX_U32 && bins_type != TX_F32)
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: bins must be 32-bit (got type %d)",
+                int(bins_type));
+  if (n == 0) return TX_SUCCESS;
+  if (!idx || !cmp || !val || (!bins && nbins > 0))
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: NULL buffer");
+  if (!aligned(idx, 4) || !aligned(cmp, 4) || !aligned(val, 4) || (bins && !aligned(bins, 4)) ||
+      (old && !aligned(old, 4)))
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: buffers must be 4-byte aligned");
+  tx_cas_args args{bins, idx, static_cast<const uint32_t *>(cmp), static_cast<const uint32_t *>(val),
+                   mask, static_cast<uint32_t *>(old), n, int32_t(nbins), 0};
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::Scatter, "tx_scatter_cas", &fn));
+  return launch(fn, direct_grid(n), 1, 256, static_cast<hipStream_t>(stream), &args, sizeof args,
+                "tx_scatter_cas");
+}
+
+// Table form: operands = {bins (result slot), idx, cmp, val, mask, old, nbins,
+// n, bins_type}.  mask and old may be NULL pointers.
+static tx_status atomic_cas_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.atomic_cas"};
+  TX_TRY(o.need(9));
+  void *bins, *idx, *cmp, *val, *mask, *old;
+  int64_t nbins, n, bt;
+  TX_TRY(o.ptr(0, &bins));
+  TX_TRY(o.ptr(1, &idx));
+  TX_TRY(o.ptr(2, &cmp));
+  TX_TRY(o.ptr(3, &val));
+  TX_TRY(o.ptr(4, &mask));
+  TX_TRY(o.ptr(5, &old));
+  TX_TRY(o.integer(6, &nbins));
+  TX_TRY(o.integer(7, &n));
+  TX_TRY(o.integer(8, &bt));
+  return atomic_cas_scatter(bins, tx_dtype(bt), nbins, static_cast<const int32_t *>(idx), cmp, val,
+                            static_cast<const uint8_t *>(mask), n, old, stream);
+}
+
 static const bool registered = register_op(
     "tt.atomic_rmw", atomic_rmw_op,
     "bins(result), idx:i32*, val, mask:u8*|null, old|null, nbins:i64, n:i64, "
     "bins_type:i32, op:i32");
+static const bool registered_cas = register_op(
+    "tt.atomic_cas", atomic_cas_op,
+    "bins(result), idx:i32*, cmp, val, mask:u8*|null, old|null, nbins:i64, n:i64, bins_type:i32");
 
 }  // namespace tx
 
@@ -142,4 +207,12 @@ extern "C" TX_API tx_status tx_atomic_rmw_scatter(void *bins, tx_dtype bins_type
                                                   tx_stream_t stream) {
   tx::clear_error();
   return tx::atomic_rmw_scatter(bins, bins_type, nbins, idx, val, mask, n, op, old, stream);
+}
+
+extern "C" TX_API tx_status tx_atomic_cas_scatter(void *bins, tx_dtype bins_type, int64_t nbins,
+                                                  const int32_t *idx, const void *cmp,
+                                                  const void *val, const uint8_t *mask, int64_t n,
+                                                  void *old, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::atomic_cas_scatter(bins, bins_type, nbins, idx, cmp, val, mask, n, old, stream);
 }

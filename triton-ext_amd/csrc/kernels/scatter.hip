@@ -522,3 +522,31 @@ TX_SCATTER_KERNELS(umin, UMIN)
 TX_SCATTER_KERNELS(and, AND)
 TX_SCATTER_KERNELS(or, OR)
 TX_SCATTER_KERNELS(xor, XOR)
+
+// tt.atomic_rmw xchg and tt.atomic_cas: one global atomic per update on the
+// bin's 32-bit pattern (int32, uint32 and fp32 bins alike; CAS compares bit
+// for bit).  The updates of one bin are applied one at a time in an order
+// the hardware picks, so each update's old value is the bin's value after
+// some set of that bin's earlier-applied updates.  Updates outside
+// [0, nbins) or masked off return 0 and change nothing.
+TX_KERNEL void __launch_bounds__(256) tx_scatter_xchg(const tx_scatter_args a) {
+  uint32_t *bins = static_cast<uint32_t *>(a.bins);
+  const uint32_t *vals = static_cast<const uint32_t *>(a.val);
+  uint32_t *old = static_cast<uint32_t *>(a.old);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) {
+    const int32_t k = a.idx[i];
+    uint32_t r = 0u;
+    if (k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0)) r = atomicExch(bins + k, vals[i]);
+    if (old) old[i] = r;
+  }
+}
+
+TX_KERNEL void __launch_bounds__(256) tx_scatter_cas(const tx_cas_args a) {
+  uint32_t *bins = static_cast<uint32_t *>(a.bins);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) {
+    const int32_t k = a.idx[i];
+    uint32_t r = 0u;
+    if (k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0)) r = atomicCAS(bins + k, a.cmp[i], a.val[i]);
+    if (a.old) a.old[i] = r;
+  }
+}

@@ -50,6 +50,19 @@ typedef struct tx_scatter_args {
   int32_t window;      /* windowed kernels: bins per window */
 } tx_scatter_args;
 
+/* tt.atomic_cas in scatter form: 32-bit bins, compared bit for bit */
+typedef struct tx_cas_args {
+  void *bins;
+  const int32_t *idx;
+  const uint32_t *cmp;
+  const uint32_t *val;
+  const uint8_t *mask; /* may be NULL */
+  uint32_t *old;       /* may be NULL */
+  int64_t n;
+  int32_t nbins;
+  int32_t pad;
+} tx_cas_args;
+
 /* GEMM, both operands K-contiguous ("A row-major, B column-major").
  * Element strides for bf16; byte strides for fp8. */
 typedef struct tx_gemm_args {

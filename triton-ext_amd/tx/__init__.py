@@ -136,7 +136,8 @@ def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor
                mask: torch.Tensor | None = None, return_old: bool = False):
     """tt.atomic_rmw, scatter form: bins[idx[i]] (op)= val[i] for all i, in place.
 
-    op: add | fadd | max | min | umax | umin | and | or | xor (as tl.atomic_*).
+    op: add | fadd | max | min | umax | umin | and | or | xor | xchg (as
+    tl.atomic_*; xchg takes int32, uint32 or fp32 bins).
     Updates with idx outside [0, len(bins)) or mask[i] == 0 are dropped.
     return_old=True returns, per update, the bin's value before it (the
     tt.atomic_rmw result); that form does no pre-aggregation.
@@ -159,6 +160,34 @@ def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor
     check(lib.tx_atomic_rmw_scatter(_ptr(bins), _TX_DTYPE[bins.dtype], bins.numel(), _ptr(idx),
                                     _ptr(val), _ptr(mask), idx.numel(), _lib.RMW[op], _ptr(old),
                                     _stream(bins)))
+    return old if return_old else bins
+
+
+def atomic_cas(bins: torch.Tensor, idx: torch.Tensor, cmp: torch.Tensor, val: torch.Tensor,
+               mask: torch.Tensor | None = None, return_old: bool = True):
+    """tt.atomic_cas, scatter form: for every i (not masked off, idx in range),
+    atomically old[i] = bins[idx[i]]; if old[i] == cmp[i]: bins[idx[i]] = val[i]
+    (32-bit patterns compared bit for bit; int32, uint32 or fp32 bins).
+    Returns old (the tt.atomic_cas result; 0 for dropped updates), or bins
+    when return_old is False."""
+    _on_gpu(bins, idx, cmp, val, mask)
+    if idx.dtype != torch.int32:
+        raise ValueError("idx must be int32")
+    if bins.dtype not in (torch.int32, torch.uint32, torch.float32):
+        raise ValueError("atomic_cas takes int32, uint32 or fp32 bins")
+    if cmp.dtype != bins.dtype or val.dtype != bins.dtype:
+        raise ValueError("cmp, val and bins must have the same dtype")
+    for t in (bins, idx, cmp, val) + ((mask,) if mask is not None else ()):
+        if not t.is_contiguous():
+            raise ValueError("atomic_cas needs contiguous tensors")
+    n = idx.numel()
+    if cmp.numel() != n or val.numel() != n or (mask is not None and mask.numel() != n):
+        raise ValueError("idx, cmp, val (and mask) must have the same number of elements")
+    if mask is not None and mask.dtype not in (torch.uint8, torch.bool):
+        raise ValueError("mask must be uint8 or bool")
+    old = torch.empty_like(val) if return_old else None
+    check(lib.tx_atomic_cas_scatter(_ptr(bins), _TX_DTYPE[bins.dtype], bins.numel(), _ptr(idx),
+                                    _ptr(cmp), _ptr(val), _ptr(mask), n, _ptr(old), _stream(bins)))
     return old if return_old else bins
 
 

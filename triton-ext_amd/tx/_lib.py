@@ -32,7 +32,7 @@ ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 RTNE, RTZ, RS = 0, 1, 2
 # tx_rmw_op
 RMW = {"add": 0, "fadd": 1, "max": 2, "min": 3, "umax": 4, "umin": 5,
-       "and": 6, "or": 7, "xor": 8}
+       "and": 6, "or": 7, "xor": 8, "xchg": 9}
 # tx_value_kind
 VALUE_PTR, VALUE_INT = 0, 1
 # tx_b_layout
@@ -42,7 +42,8 @@ B_NK, B_KN = 0, 1
 EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion",
-    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_dot_bf16", "tx_dot",
+    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_atomic_cas_scatter",
+    "tx_dot_bf16", "tx_dot",
     "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped",
     "tx_dot_fp8_scaled_grouped_noalloc", "tx_dot_fp8_scaled_batched",
     "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
@@ -121,6 +122,8 @@ def _load():
     L.tx_fp_to_fp_with_rbits.restype = I
     L.tx_atomic_rmw_scatter.argtypes = [P, I, I64, P, P, P, I64, I, P, VP]
     L.tx_atomic_rmw_scatter.restype = I
+    L.tx_atomic_cas_scatter.argtypes = [P, I, I64, P, P, P, P, I64, P, VP]
+    L.tx_atomic_cas_scatter.restype = I
     L.tx_dot_bf16.argtypes = [P, I64, P, I64, P, I64, I64, I64, I64, VP]
     L.tx_dot_bf16.restype = I
     L.tx_dot.argtypes = [P, I, I64, P, I, I64, P, I, I64, I64, I64, I64, VP]
