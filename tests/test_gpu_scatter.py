@@ -106,6 +106,48 @@ def test_other_integer_ops(tx, dev, op, ufunc, dtype, nbins):
     assert np.array_equal(got, ref)
 
 
+def _skewed_keys(g, n, nbins, hot_lo, hot_frac):
+    """hot_frac of the keys uniform in one 36,864-bin window starting at
+    hot_lo (so the single-pass path takes it), the rest uniform over all
+    bins, with 1% of the keys out of range (negative or >= nbins)."""
+    hot = g.random(n) < hot_frac
+    idx = np.where(hot, hot_lo + g.integers(0, 36864, n), g.integers(0, nbins, n)).astype(np.int32)
+    bad = g.random(n) < 0.01
+    idx[bad] = np.where(g.random(int(bad.sum())) < 0.5, -1 - g.integers(0, 5, int(bad.sum())),
+                        nbins + g.integers(0, 5, int(bad.sum()))).astype(np.int32)
+    return idx
+
+
+@pytest.mark.parametrize("nbins,hot_lo", [(65536, 0), (65536, 20480), (100_000, 61440), (147_456, 55296),
+                                          (73_728, 36864)])
+@pytest.mark.parametrize("op", ["add", "fadd", "max", "xor"])
+def test_single_window_with_spill(tx, oracle, dev, nbins, hot_lo, op):
+    """More than one window and skewed keys: the one-pass path (the best
+    window in LDS, every other in-range update by a global atomic), with
+    masked and out-of-range updates, on windows that do not start at 0."""
+    g = np.random.default_rng(nbins + hot_lo)
+    n = 3_000_000
+    idx = _skewed_keys(g, n, nbins, hot_lo, 0.9)
+    mask = (g.random(n) < 0.95).astype(np.uint8)
+    if op == "fadd":
+        val = g.standard_normal(n).astype(np.float32)
+        init = g.standard_normal(nbins).astype(np.float32)
+        got = _run(tx, dev, op, init, idx, val, mask)
+        _check_f32(got, init, nbins, idx, val, oracle, mask)
+        return
+    ufunc = {"add": np.add, "max": np.maximum, "xor": np.bitwise_xor}[op]
+    dtype = np.uint32 if op == "xor" else np.int32
+    info = np.iinfo(dtype)
+    val = g.integers(info.min, info.max, size=n, dtype=np.int64, endpoint=True).astype(dtype)
+    init = g.integers(info.min, info.max, size=nbins, dtype=np.int64, endpoint=True).astype(dtype)
+    ref = init.copy()
+    live = (idx >= 0) & (idx < nbins) & (mask != 0)
+    with np.errstate(over="ignore"):
+        ufunc.at(ref, idx[live], val[live])
+    got = _run(tx, dev, op, init, idx, val, mask)
+    assert np.array_equal(got, ref)
+
+
 def test_return_old_counter(tx, dev):
     """tt.atomic_rmw's result: each update sees a distinct prior value, as in
     the reference's counter tests (test_tlx.py:7672-7723)."""

@@ -96,11 +96,9 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
   if (windows <= kMaxWindows) {
     std::snprintf(kname, sizeof kname, "tx_scatter_%s_windowed", name);
     TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
-    // One workgroup per CU at a time (the table fills most of a CU's LDS).
-    // One chunk of updates per CU and `windows` workgroups per chunk: when
-    // the key distribution loads one window more than the others (skewed
-    // keys), the CUs that finish the light windows take over the remaining
-    // workgroups of the heavy one.
+    // One workgroup per CU at a time (the table fills a CU's LDS) and one
+    // chunk of updates per workgroup; the workgroup itself makes one pass
+    // per window, or a single pass when its chunk's keys are skewed.
     int64_t chunks = std::max<int64_t>(8, cus);
     int64_t per = (n + chunks - 1) / chunks;
     per = (per + kWinStep - 1) / kWinStep * kWinStep;
@@ -109,9 +107,7 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
     args.per_block = int32_t(per);
     args.splits = int32_t(windows);
     args.window = int32_t(kDirectSlots);
-    // workgroups come in groups of 8 chunks x `windows` windows
-    const int64_t grid = (chunks + 7) / 8 * 8 * windows;
-    return launch(fn, unsigned(grid), 1, kAggBlock, s, &args, sizeof args, kname);
+    return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
   }
   std::snprintf(kname, sizeof kname, "tx_scatter_%s_hashed", name);
   TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));

@@ -10,8 +10,12 @@
 //      ballot/read-lane loop before they reach a shared atomic (spill path);
 //   3. workgroup: an LDS table owned by the workgroup.  Up to 4 x 36,864
 //      bins the table is direct-mapped (slot = bin - window start), with the
-//      bin range cut into windows that each fit in LDS and one workgroup per
-//      (chunk of updates, window); beyond that it is an open addressing hash
+//      bin range cut into windows that each fit in LDS, one workgroup per
+//      chunk of updates making one pass per window -- or, when a sample of
+//      the chunk finds one window holding most updates (skewed keys), a
+//      single pass that privatises that window and sends the rest to global
+//      atomics through per-wavefront LDS queues; beyond 4 windows it is an
+//      open addressing hash
 //      table (Fibonacci hash, bounded linear probing) keyed by bin, and
 //      updates whose probe sequence is full spill to global atomics after a
 //      wavefront-level combine.  At the end the table is flushed with one
@@ -38,6 +42,12 @@ constexpr int kHot = 8;  // HotKeys::take names each of the kHot sums
 constexpr int kSampleLog2 = 11;
 constexpr int kSampleSlots = 1 << kSampleLog2;
 constexpr uint32_t kHotMinCount = 16;        // of at most 4 x kBlock samples
+// Per-wavefront spill queue of the one-pass window (see spill_push): kQueue
+// keys and kQueue values per wavefront, in the LDS words the fp32 hot-key
+// sample uses before the pass.
+constexpr uint32_t kQueue = 128;
+constexpr int kAuxWords = 2 * kSampleSlots;  // 16 KiB: the sample's keys and counts, or the queues
+static_assert(kBlock / 64 * 2 * kQueue <= kAuxWords, "spill queues fit in the auxiliary LDS");
 
 template <int OP> struct OpTraits;
 template <> struct OpTraits<ADD> { using T = uint32_t; static __device__ T id() { return 0u; } };
@@ -125,39 +135,75 @@ __device__ __forceinline__ void wave_combine_global(T *bins, bool pending, uint3
   }
 }
 
+// Out-of-window updates of the one-pass window.  A global atomic inside the
+// streaming loop would hold up the loads issued after it (vmcnt counts
+// loads, stores and atomics together, in order), so each wavefront appends
+// them to its queue in LDS (keys at q[0 .. kQueue), values at q[kQueue ..
+// 2 kQueue); ballot + mbcnt give the slots) and sends the queue to global
+// memory with whole-wavefront atomics only when it would overflow and at the
+// end of the pass.  qn (the queue's fill) is wavefront-uniform.
+template <int OP, typename T>
+__device__ __forceinline__ void spill_flush(const uint32_t *q, uint32_t qn, T *bins) {
+  for (uint32_t i = threadIdx.x & 63; i < qn; i += 64)
+    atomic_combine<OP, T>(bins + q[i], __builtin_bit_cast(T, q[kQueue + i]));
+}
+
+template <int OP, typename T>
+__device__ __forceinline__ void spill_push(uint32_t *q, uint32_t &qn, T *bins, bool sp, uint32_t key, T v) {
+  const uint64_t m = __ballot(sp);
+  if (m == 0) return;
+  const uint32_t cnt = uint32_t(__popcll(m));
+  if (qn + cnt > kQueue) {
+    spill_flush<OP, T>(q, qn, bins);
+    qn = 0;
+  }
+  if (sp) {
+    const uint32_t pos = qn + __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u));
+    q[pos] = key;
+    q[kQueue + pos] = __builtin_bit_cast(uint32_t, v);
+  }
+  qn += cnt;
+}
+
 // Hot keys of one workgroup's fp32 window.  ds_add_f32 retires about 0.3
 // lanes per clock per CU however its addresses fall, so the compare-and-swap
 // in wave_lds_combine carries fp32 adds; it loses whenever several lanes of
 // an instruction, or several wavefronts at once, hit one bin, and skewed keys
 // (Zipf: the top 8 of 65,536 bins draw a third of the updates) make that
-// common.  Each workgroup therefore samples the first 4 x kBlock updates of
-// its chunk, counts the in-window keys in a small LDS hash table, and takes
-// up to kHot keys seen at least kHotMinCount times.  Their updates never touch
-// LDS: every lane sums them in registers (one accumulator per hot key), and
-// the sums are reduced over the wavefront and added to the table once, at the
-// end of the chunk.  Which keys are chosen only moves work between the two
-// paths; the sums are the same either way (up to fp32 rounding order).
+// common.  (Integer ops do not use them: their native LDS atomics lose less
+// to same-address lanes than the register accumulators cost.)  Each
+// workgroup therefore samples the first 4 x kBlock
+// updates of its chunk, counts the in-window keys in a small LDS hash table,
+// and takes up to kHot keys seen at least kHotMinCount times.  Their updates
+// never touch LDS: every lane combines them in registers (one accumulator
+// per hot key), and the accumulators are reduced over the wavefront and
+// combined into the table once, at the end of the chunk.  Which keys are
+// chosen only moves work between the two paths; integer results are the
+// same either way, fp32 sums up to rounding order.
+template <int OP>
 struct HotKeys {
+  using T = typename OpTraits<OP>::T;
   int n = 0;            // number of hot keys (workgroup-uniform)
   uint32_t r[kHot];     // their window-relative slots (same in every lane); unused: kEmpty
-  float acc[kHot];      // this lane's partial sums
+  T acc[kHot];          // this lane's partial results
 
-  // Route one update: a pending update on a hot slot is added to that slot's
-  // sum and stops pending.  Lanes that are not pending add -0, which changes
-  // no sum; no pending slot equals kEmpty (pending slots are below the window
-  // size).
-  __device__ __forceinline__ void take(bool &pend, uint32_t slot, float v) {
-    const float x = pend ? v : -0.0f;
+  // Route one update: a pending update on a hot slot is combined into that
+  // slot's accumulator and stops pending.  Lanes that are not pending
+  // combine the identity; no pending slot equals kEmpty (pending slots are
+  // below the window size).
+  __device__ __forceinline__ void take(bool &pend, uint32_t slot, T v) {
+    const T x = pend ? v : OpTraits<OP>::id();
     bool hit = false;
 #pragma unroll
     for (int t = 0; t < kHot; ++t) {
       const bool m = slot == r[t];
-      acc[t] += m ? x : -0.0f;
+      acc[t] = combine<OP, T>(acc[t], m ? x : OpTraits<OP>::id());
       hit = hit || m;
     }
-    // The sums are complete here, before any LDS atomic of this update: left
-    // to itself the compiler sinks the adds past the atomics and keeps all
-    // kHot compare masks alive in scalar registers across them.
+    // The accumulators are complete here, before any LDS atomic of this
+    // update: left to itself the compiler sinks the combines past the
+    // atomics and keeps all kHot compare masks alive in scalar registers
+    // across them.
     asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]),
                  "+v"(acc[5]), "+v"(acc[6]), "+v"(acc[7])::"memory");
     pend = pend && !hit;
@@ -218,17 +264,22 @@ struct Scatter {
 
   // Combine 4 updates into the LDS window [lo, lo + nb).  A key outside the
   // window (negative keys included: they wrap to large unsigned values) or
-  // with a zero mask byte is dropped; lo + nb <= nbins <= INT32_MAX.
-  template <bool HOT>
-  static __device__ __forceinline__ void apply(T *table, uint32_t lo, uint32_t nb, HotKeys &hot,
+  // with a zero mask byte is dropped, or with SPILL, when it is in
+  // [0, nbins), goes to the wavefront's spill queue q; lo + nb <= nbins <=
+  // INT32_MAX.
+  template <bool HOT, bool SPILL>
+  static __device__ __forceinline__ void apply(T *table, uint32_t lo, uint32_t nb, T *bins, uint32_t nbins,
+                                               uint32_t *q, uint32_t &qn, HotKeys<OP> &hot,
                                                const txd::i32x4 &k, const txd::u32x4 &v, uint32_t m) {
     const int32_t kk[4] = {k.x, k.y, k.z, k.w};
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t r = uint32_t(kk[j]) - lo;
-      bool pend = r < nb && ((m >> (8 * j)) & 0xFFu) != 0;
+      const bool live = ((m >> (8 * j)) & 0xFFu) != 0;
+      bool pend = r < nb && live;
       const T x = __builtin_bit_cast(T, vv[j]);
+      if constexpr (SPILL) spill_push<OP, T>(q, qn, bins, live && !pend && uint32_t(kk[j]) < nbins, uint32_t(kk[j]), x);
       if constexpr (OP == FADD && HOT) hot.take(pend, r, x);
       wave_lds_combine<OP, T>(table, pend, r, x);
     }
@@ -240,9 +291,11 @@ struct Scatter {
   // run.  Slot d always holds an iteration congruent to d mod kDepth, so the
   // slots are compile-time registers; refills past the last iteration re-read
   // the last one (in range, never applied).
-  template <bool MASK, bool HOT>
+  template <bool MASK, bool HOT, bool SPILL>
   static __device__ __forceinline__ void stream(const tx_scatter_args &a, T *table, uint32_t lo,
-                                                uint32_t nb, HotKeys &hot, int64_t e0, int64_t groups) {
+                                                uint32_t nb, uint32_t *q, uint32_t &qn, HotKeys<OP> &hot,
+                                                int64_t e0, int64_t groups) {
+    T *bins = reinterpret_cast<T *>(a.bins);
     txd::i32x4 k[kDepth];
     txd::u32x4 v[kDepth];
     uint32_t m[kDepth];
@@ -253,20 +306,74 @@ struct Scatter {
       const int64_t eg = e0 + g * kDepth * kIter;
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        apply<HOT>(table, lo, nb, hot, k[d], v[d], m[d]);
+        apply<HOT, SPILL>(table, lo, nb, bins, uint32_t(a.nbins), q, qn, hot, k[d], v[d], m[d]);
         const int64_t en = eg + (d + kDepth) * kIter;
         fetch<MASK>(a, en < last ? en : last, k[d], v[d], m[d]);
       }
     }
   }
 
+  // The best single window for a chunk: counts the first 4 x kBlock updates
+  // of the chunk per block of kWinBlock bins, and returns (workgroup-uniform)
+  // the start of the `window`-bin window, at a multiple of kWinBlock, that
+  // holds the most of them, with that count and the number sampled.  Every
+  // workgroup of a chunk reads the same sample, so they all agree.  The
+  // counts live in `cnt`, the first words of the workgroup's window table
+  // (set up only afterwards).  Needs the whole workgroup; ends with a
+  // barrier.
+  static constexpr int kWinBlock = 2048;
+  static constexpr int kMaxWinBlocks = 4 * kDirectSlots / kWinBlock;
+  static __device__ void pick_window(const tx_scatter_args &a, int64_t begin, int64_t end, bool vec,
+                                     uint32_t window, uint32_t *cnt, uint32_t &base, uint32_t &hits,
+                                     uint32_t &total) {
+    for (int s = threadIdx.x; s < kMaxWinBlocks + 2; s += kBlock) cnt[s] = 0u;
+    __syncthreads();
+    {
+      uint32_t key[4];
+      T val[4];
+      bool ok[4];
+      load4(a, begin + 4 * int64_t(threadIdx.x), end, vec, key, val, ok);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (ok[j]) atomicAdd(&cnt[key[j] / kWinBlock], 1u);  // key < nbins <= 4 x kDirectSlots
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      const int nblk = int((uint32_t(a.nbins) + kWinBlock - 1) / kWinBlock);
+      const int wblk = int(window / kWinBlock);
+      const int ncand = nblk > wblk ? nblk - wblk + 1 : 1;
+      uint32_t sum = 0u, all = 0u;
+      if (lane < ncand)
+        for (int i = lane; i < lane + wblk && i < nblk; ++i) sum += cnt[i];
+      for (int i = lane; i < nblk; i += 64) all += cnt[i];
+      // best candidate: most hits, then the lowest start
+      uint32_t best = lane < ncand ? (sum << 8) | uint32_t(255 - lane) : 0u;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+        all += __shfl_xor(all, off);
+      }
+      if (lane == 0) {
+        cnt[kMaxWinBlocks] = best;
+        cnt[kMaxWinBlocks + 1] = all;
+      }
+    }
+    __syncthreads();
+    const uint32_t best = __builtin_amdgcn_readfirstlane(cnt[kMaxWinBlocks]);
+    total = __builtin_amdgcn_readfirstlane(cnt[kMaxWinBlocks + 1]);
+    hits = best >> 8;
+    base = uint32_t(255 - (best & 0xFFu)) * kWinBlock;
+    __syncthreads();
+  }
+
   // Picks the workgroup's hot keys (HotKeys) from the first 4 x kBlock
   // updates of its chunk; on return every lane holds the same set, with
   // zeroed sums.  Needs the whole workgroup; ends with a barrier.
   static __device__ void sample_hot(const tx_scatter_args &a, uint32_t lo, uint32_t nb, int64_t begin,
-                                    int64_t end, bool vec, HotKeys &hot) {
-    __shared__ uint32_t skey[kSampleSlots];
-    __shared__ uint32_t scnt[kSampleSlots];
+                                    int64_t end, bool vec, uint32_t *aux, HotKeys<OP> &hot) {
+    uint32_t *skey = aux, *scnt = aux + kSampleSlots;
     for (int s = threadIdx.x; s < kSampleSlots; s += kBlock) {
       skey[s] = kEmpty;
       scnt[s] = 0u;
@@ -342,51 +449,52 @@ struct Scatter {
       // kept in vector registers: scalar registers are the scarcer resource
       // in the unrolled update loop
       hot.r[t] = t < hot.n ? skey[t] : kEmpty;
-      hot.acc[t] = -0.0f;
+      hot.acc[t] = OpTraits<OP>::id();
     }
   }
 
-  // Windowed LDS privatisation.  The bin range is cut into `splits` windows
-  // of `window` bins (each fits in LDS); `splits` workgroups read the same
-  // chunk of updates and each privatises one window, so every update lands
-  // in exactly one LDS histogram.  Workgroup b takes window (b / 8) % splits
-  // and chunk (b / (8 splits)) * 8 + b % 8: the workgroups sharing a chunk
-  // sit on the same XCD (workgroups are dispatched round-robin over 8 XCDs),
-  // so the repeated reads of a chunk are served by that XCD's L2 or the
-  // Infinity Cache rather than HBM.  With one window this is plain LDS
-  // privatisation of all bins.
-  static __device__ void windowed(const tx_scatter_args &a) {
-    __shared__ T table[kDirectSlots];
-    const int b = blockIdx.x;
-    const int w = (b / 8) % a.splits;
-    const int64_t chunk = int64_t(b / (8 * a.splits)) * 8 + b % 8;
-    const int64_t begin = chunk * a.per_block;
-    if (begin >= a.n) return;  // uniform: the whole workgroup leaves
-    const int64_t end = begin + a.per_block < a.n ? begin + a.per_block : a.n;
-    const uint32_t lo = uint32_t(w) * uint32_t(a.window);
-    const uint32_t nb = min(uint32_t(a.window), uint32_t(a.nbins) - lo);  // bins in this window
+  // One pass of a workgroup over its chunk with the LDS window [lo, lo + nb):
+  // set the table to the identity, (fp32) pick the hot keys, stream the
+  // chunk, then combine the hot keys' and the table's results into the bins
+  // with one global atomic per touched slot.  With SPILL, in-range updates
+  // outside the window go to the bins through the wavefront spill queues in
+  // aux; without it they are left to the chunk's other passes.
+  static __device__ void pass(const tx_scatter_args &a, T *table, uint32_t *aux, uint32_t lo, uint32_t nb,
+                              bool spill, int64_t begin, int64_t end, bool vec) {
     for (uint32_t s = threadIdx.x; s < nb; s += kBlock) table[s] = OpTraits<OP>::id();
-    const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
-                     (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
-    HotKeys hot;
-    if constexpr (OP == FADD) sample_hot(a, lo, nb, begin, end, vec, hot);
+    HotKeys<OP> hot;
+    if constexpr (OP == FADD) sample_hot(a, lo, nb, begin, end, vec, aux, hot);
     __syncthreads();
+    T *bins = reinterpret_cast<T *>(a.bins);
+    uint32_t *q = aux + (threadIdx.x / 64) * 2 * kQueue;
+    uint32_t qn = 0;
     int64_t e = begin + 4 * int64_t(threadIdx.x);
     if (vec) {
       // Whole groups of kDepth full iterations go through the pipelined loop.
       const int64_t groups = (end - begin) / (kDepth * kIter);
       if (groups > 0) {
-        if (OP == FADD && hot.n > 0) {
-          if (a.mask) stream<true, true>(a, table, lo, nb, hot, e, groups);
-          else stream<false, true>(a, table, lo, nb, hot, e, groups);
+        const bool h = OP == FADD && hot.n > 0;
+        if (spill) {
+          if (h) {
+            if (a.mask) stream<true, true, true>(a, table, lo, nb, q, qn, hot, e, groups);
+            else stream<false, true, true>(a, table, lo, nb, q, qn, hot, e, groups);
+          } else {
+            if (a.mask) stream<true, false, true>(a, table, lo, nb, q, qn, hot, e, groups);
+            else stream<false, false, true>(a, table, lo, nb, q, qn, hot, e, groups);
+          }
         } else {
-          if (a.mask) stream<true, false>(a, table, lo, nb, hot, e, groups);
-          else stream<false, false>(a, table, lo, nb, hot, e, groups);
+          if (h) {
+            if (a.mask) stream<true, true, false>(a, table, lo, nb, q, qn, hot, e, groups);
+            else stream<false, true, false>(a, table, lo, nb, q, qn, hot, e, groups);
+          } else {
+            if (a.mask) stream<true, false, false>(a, table, lo, nb, q, qn, hot, e, groups);
+            else stream<false, false, false>(a, table, lo, nb, q, qn, hot, e, groups);
+          }
         }
         e += groups * kDepth * kIter;
       }
     }
-    // Remaining iterations: a uniform trip count (the combine needs every
+    // Remaining iterations: a uniform trip count (the combines need every
     // lane of the wavefront); lanes past `end` carry no update.
     const int64_t first = e - 4 * int64_t(threadIdx.x);
     for (int64_t eb = first; eb < end; eb += kIter) {
@@ -398,30 +506,61 @@ struct Scatter {
       for (int j = 0; j < 4; ++j) {
         const uint32_t r = key[j] - lo;  // wraps for keys below the window
         bool pend = ok[j] && r < nb;
+        if (spill) spill_push<OP, T>(q, qn, bins, ok[j] && !pend, key[j], val[j]);
         if constexpr (OP == FADD) {
           if (hot.n > 0) hot.take(pend, r, val[j]);
         }
         wave_lds_combine<OP, T>(table, pend, r, val[j]);
       }
     }
-    if constexpr (OP == FADD) {
-      // the hot keys' sums: one LDS add per wavefront and key
+    if (spill) spill_flush<OP, T>(q, qn, bins);
+    // the hot keys' accumulators: one LDS combine per wavefront and key
 #pragma unroll
-      for (int t = 0; t < kHot; ++t) {
-        if (t < hot.n) {
-          float x = hot.acc[t];
+    for (int t = 0; t < kHot; ++t) {
+      if (t < hot.n) {
+        T x = hot.acc[t];
 #pragma unroll
-          for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-          if ((threadIdx.x & 63) == 0) atomicAdd(&table[hot.r[t]], x);
-        }
+        for (int off = 32; off >= 1; off >>= 1) x = combine<OP, T>(x, __shfl_xor(x, off));
+        if ((threadIdx.x & 63) == 0) atomic_combine<OP, T>(&table[hot.r[t]], x);
       }
     }
     __syncthreads();
-    T *bins = reinterpret_cast<T *>(a.bins) + lo;
     for (uint32_t s = threadIdx.x; s < nb; s += kBlock) {
       const T v = table[s];
-      if (!is_identity<OP, T>(v)) atomic_combine<OP, T>(bins + s, v);
+      if (!is_identity<OP, T>(v)) atomic_combine<OP, T>(bins + lo + s, v);
     }
+    __syncthreads();  // the table and aux are reused by the next pass
+  }
+
+  // Windowed LDS privatisation, one workgroup per chunk of updates.  Up to
+  // `window` bins the table holds them all and one pass does the chunk.
+  // Beyond that the bin range is cut into `splits` windows of `window` bins
+  // (each fits in LDS).  The chunk's first 4 x kBlock updates decide how:
+  // when the best single window holds at least 3/4 of them (skewed keys) the
+  // workgroup makes one pass with that window and spills the rest (one read
+  // of the chunk); otherwise it makes one pass per window, each reading the
+  // whole chunk.
+  static __device__ void windowed(const tx_scatter_args &a) {
+    __shared__ T table[kDirectSlots];
+    __shared__ uint32_t aux[kAuxWords];
+    const int64_t begin = int64_t(blockIdx.x) * a.per_block;
+    if (begin >= a.n) return;  // uniform: the whole workgroup leaves
+    const int64_t end = begin + a.per_block < a.n ? begin + a.per_block : a.n;
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.idx) | reinterpret_cast<uintptr_t>(a.val)) & 15) == 0 &&
+                     (!a.mask || (reinterpret_cast<uintptr_t>(a.mask) & 3) == 0);
+    const uint32_t W = uint32_t(a.window), nbins = uint32_t(a.nbins);
+    if (a.splits > 1) {
+      uint32_t base, hits, total;
+      pick_window(a, begin, end, vec, W, reinterpret_cast<uint32_t *>(table), base, hits, total);
+      if (total > 0u && 4u * hits >= 3u * total) {
+        pass(a, table, aux, base, min(W, nbins - base), true, begin, end, vec);
+      } else {
+        for (int w = 0; w < a.splits; ++w)
+          pass(a, table, aux, uint32_t(w) * W, min(W, nbins - uint32_t(w) * W), false, begin, end, vec);
+      }
+      return;
+    }
+    pass(a, table, aux, 0u, min(W, nbins), false, begin, end, vec);
   }
 
   // Hash-table LDS cache with global spill.
