@@ -70,8 +70,10 @@ tx_status launch_gemm(const char *kname, CodeObject co, tx_gemm_args &args, int 
   return launch(fn, unsigned(grid), 1, threads, s, &args, sizeof args, kname);
 }
 
-// Wavefronts per workgroup of the fast path (two per SIMD).
+// Wavefronts per workgroup of the fast path (two per SIMD) and of its
+// persistent variant (one per SIMD).
 constexpr int kFastWaves = 8;
+constexpr int kPersistWaves = 4;
 // Largest M served by the skinny fp8 kernel (4 blocks of 16 rows).
 constexpr int64_t kSkinnyMaxM = 64;
 // Split K only while every split keeps at least this many 128-byte K steps.
@@ -100,11 +102,38 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 // separate, second fast-path product (few tiles, so 256x128 with K split).
 constexpr int64_t kStripMaxN = 64;
 
+// The persistent 4-wavefront kernel (`base`_persist, gemm_persist.h) takes
+// the 256 x 256 products it was built for: no fused epilogue or K split, K a
+// whole number (>= 2) of 128-byte steps, N a multiple of 8, C rows 16-byte
+// aligned and addressable with 32-bit byte offsets.
+bool persist_ok(const tx_gemm_args &args, int64_t k_bytes) {
+  if (args.epi || args.splits > 1 || k_bytes % 128 != 0 || k_bytes < 256 || args.N % 8 != 0) return false;
+  if (!aligned(args.C, 16) || args.ldc % 8 != 0) return false;
+  const int64_t c_bytes = ((int64_t(args.M) - 1) * args.ldc + args.N) * 2;
+  return c_bytes < (int64_t(1) << 31);
+}
+
 tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_gemm_args &args,
-                      int64_t k_bytes, int es, hipStream_t s) {
+                      int64_t k_bytes, int es, hipStream_t s, bool persist = false) {
   const int64_t cus = cu_count();
   const int64_t tiles_m = (args.M + 255) / 256;
   char kname[96];
+  // 256 x 256 tiles: the persistent kernel when it applies, else one
+  // workgroup per tile
+  auto launch_big = [&](tx_gemm_args &ga) -> tx_status {
+    if (persist && persist_ok(ga, k_bytes)) {
+      std::snprintf(kname, sizeof kname, "%s_persist", base);
+      ga.tiles_m = int32_t((ga.M + 255) / 256);
+      ga.tiles_n = int32_t((ga.N + 255) / 256);
+      ga.group_m = std::min<int32_t>(kGroupM, ga.tiles_m);
+      hipFunction_t fn;
+      TX_TRY(get_kernel(co, kname, &fn));
+      const int64_t grid = std::min<int64_t>(int64_t(ga.tiles_m) * ga.tiles_n, cus);
+      return launch(fn, unsigned(grid), 1, 64 * kPersistWaves, s, &ga, sizeof ga, kname);
+    }
+    std::snprintf(kname, sizeof kname, "%s", base);
+    return launch_gemm(kname, co, ga, 256, 256, s, 64 * kFastWaves);
+  };
   if (tiles_m * ((args.N + 255) / 256) >= cus) {
     std::snprintf(kname, sizeof kname, "%s", base);
     const int64_t full = args.N / 256, tail = args.N % 256;
@@ -120,10 +149,10 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
       if (args.bias) strip_args.bias = args.bias + n0;
       strip_args.N = int32_t(tail);
       args.N = int32_t(n0);
-      TX_TRY(launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves));
-      return launch_fast(base, reduce, co, strip_args, k_bytes, es, s);
+      TX_TRY(launch_big(args));
+      return launch_fast(base, reduce, co, strip_args, k_bytes, es, s, persist);
     }
-    return launch_gemm(kname, co, args, 256, 256, s, 64 * kFastWaves);
+    return launch_big(args);
   }
   std::snprintf(kname, sizeof kname, "%s_n128", base);
   const int64_t tiles = tiles_m * ((args.N + 127) / 128);
@@ -206,7 +235,7 @@ tx_status launch_padded(const char *base, const char *reduce, const char *pad, C
     args.B = wb;
     args.ldb = kp;
     args.K = int32_t(kp);
-    st = launch_fast(base, reduce, co, args, kp * es, es, s);
+    st = launch_fast(base, reduce, co, args, kp * es, es, s, true);
   }
   return st;
 }
@@ -280,11 +309,11 @@ static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda
       args.lda = kp;
       args.K = int32_t(kp);
     }
-    return launch_fast(base, reduce, CodeObject::GemmBf16, args, int64_t(args.K) * 2, 2, s);
+    return launch_fast(base, reduce, CodeObject::GemmBf16, args, int64_t(args.K) * 2, 2, s, true);
   }
   if (layout == TX_B_KN) args.ldb = K;  // K = 0: B is never read
   if (fast_ok(A, lda * 2, B, args.ldb * 2, K * 2, M, N))
-    return launch_fast(base, reduce, CodeObject::GemmBf16, args, K * 2, 2, s);
+    return launch_fast(base, reduce, CodeObject::GemmBf16, args, K * 2, 2, s, true);
   {
     tx_gemm_args padded = args;
     const tx_status st = launch_padded(base, reduce, "tx_gemm_bf16_pad_rows", CodeObject::GemmBf16,
@@ -374,7 +403,7 @@ static tx_status dot_fp8_impl(const char *what, const void *A, tx_dtype a_type, 
   }
   std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_fast%s", fa, fb, with_epi ? "_epi" : "");
   if (fast_ok(A, lda, B, ldb, K, M, N))
-    return launch_fast(kname, "tx_gemm_fp8_splitk_reduce", CodeObject::GemmFp8, args, K, 1, s);
+    return launch_fast(kname, "tx_gemm_fp8_splitk_reduce", CodeObject::GemmFp8, args, K, 1, s, true);
   {
     tx_gemm_args padded = args;
     const tx_status st = launch_padded(kname, "tx_gemm_fp8_splitk_reduce", "tx_gemm_fp8_pad_rows",

@@ -44,6 +44,21 @@ TX_GEMM16_FAST(bf16, EL_BF16, _out_f16, OUT_F16)
 TX_GEMM16_FAST(f16, EL_F16, , OUT_F16)
 TX_GEMM16_FAST(f16, EL_F16, _out_bf16, OUT_BF16)
 
+// The persistent 4-wavefront tile (one workgroup per CU; see gemm_persist.h)
+// for products of at least one 256 x 256 tile per CU whose K is a whole
+// number (>= 2) of 64-element steps, N a multiple of 8 and C 16-byte aligned.
+#include "gemm_persist.h"
+
+#define TX_GEMM16_PERSIST(PFX, EL, SFX, OUT)                                                           \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_##PFX##_fast##SFX##_persist(const tx_gemm_args a) { \
+    gemm_persist<GemmCfg<EL, EL, 256, 256, 2, 2, 16>, OUT>(a);                                          \
+  }
+
+TX_GEMM16_PERSIST(bf16, EL_BF16, , OUT_BF16)
+TX_GEMM16_PERSIST(bf16, EL_BF16, _out_f16, OUT_F16)
+TX_GEMM16_PERSIST(f16, EL_F16, , OUT_F16)
+TX_GEMM16_PERSIST(f16, EL_F16, _out_bf16, OUT_BF16)
+
 // Split-K reductions, by output type.
 TX_KERNEL void __launch_bounds__(256) tx_gemm_bf16_splitk_reduce(const tx_gemm_args a) {
   splitk_reduce<false>(a);

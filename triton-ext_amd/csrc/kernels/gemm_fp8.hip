@@ -44,6 +44,21 @@ TX_GEMM_FP8_FAST(e5m2, e5m2, EL_E5M2, EL_E5M2)
 TX_GEMM_FP8_FAST(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
 TX_GEMM_FP8_FAST(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 
+// The persistent 4-wavefront tile (one workgroup per CU; see gemm_persist.h)
+// for products of at least one 256 x 256 tile per CU whose K is a whole
+// number (>= 2) of 128-byte steps, N a multiple of 8 and C 16-byte aligned.
+#include "gemm_persist.h"
+
+#define TX_GEMM_FP8_PERSIST(FA, FB, ELA, ELB)                                                            \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_##FA##_##FB##_fast_persist(const tx_gemm_args a) { \
+    gemm_persist<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>>(a);                                               \
+  }
+
+TX_GEMM_FP8_PERSIST(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)
+TX_GEMM_FP8_PERSIST(e5m2, e5m2, EL_E5M2, EL_E5M2)
+TX_GEMM_FP8_PERSIST(e4m3fn, e5m2, EL_E4M3, EL_E5M2)
+TX_GEMM_FP8_PERSIST(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
+
 // The same tiles with the fused epilogue (bias, activation, output type).
 #define TX_GEMM_FP8_FAST_EPI(FA, FB, ELA, ELB)                                                        \
   TX_KERNEL void __launch_bounds__(512) tx_gemm_fp8_##FA##_##FB##_fast_epi(const tx_gemm_args a) {      \

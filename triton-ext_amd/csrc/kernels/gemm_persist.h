@@ -1,0 +1,337 @@
+// Persistent 4-wavefront GEMM for aligned operands whose K is a whole number
+// of 128-byte steps: one workgroup per CU walks its share of the 256 x 256
+// tiles, and the LDS-DMA pipeline of gemm_fast.h runs as one continuous
+// stream of (tile, K step) pairs, so the first steps of the next tile are
+// loaded while the current one finishes and no tile pays a pipeline fill.
+//
+// Layout per workgroup: 4 wavefronts (one per SIMD) in a 2 x 2 grid, each
+// owning a 128 x 128 block of the tile; the 16 accumulator blocks of 32 x 32
+// (256 registers) live in AGPRs.  Against the 8-wavefront tile this reads a
+// third less from LDS per MFMA (1 KiB instead of 1.5), which the power-
+// limited clock turns into speed.
+//
+// The K loop is that of gemm_fast_tile_at (ring of 5 LDS slots of 32 KiB,
+// B of step s+2 and A of step s+3 loaded during the second half of step s,
+// fragments one 64-byte half ahead in registers, one barrier per step), with
+// s counting steps over all tiles of the workgroup.  Each operand's loads go
+// through a buffer resource for the tile they belong to: base at the tile's
+// first row, range ending after its last valid row, so rows past M / N read
+// as zero; steps past the workgroup's last tile use an empty range.
+//
+// Epilogue (between tiles, no LDS: the ring already holds the next tile's
+// first steps): the row scales are loaded when the tile starts and the
+// column scales of the first 32-column block during its last K step; per
+// 32 x 32 block the accumulators are scaled, rounded to bf16 / fp16 (RNE),
+// and lanes l and l + 32, which hold columns 8j .. 8j + 3 and 8j + 4 .. 8j + 7
+// of one row, exchange halves (v_permlane32_swap) so that each lane stores
+// 8 consecutive columns with one 16-byte store.  The first K step of each
+// tile starts its MFMAs from a zero accumulator operand, so the accumulators
+// are never cleared explicitly.
+#pragma once
+
+#include "gemm_fast.h"
+
+namespace txg {
+
+namespace persist {
+constexpr int kWaves = 4;
+
+// Buffer resource for rows r0 .. r0 + 255 of an operand with `rows` rows of
+// `ld_b` bytes, K step bytes kb_end: rows past the operand's end are outside
+// the range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, int r0, int rows, uint32_t ld_b,
+                                                            uint32_t kb_end) {
+  const int valid = min(256, rows - r0);
+  return make_rsrc(static_cast<const uint8_t *>(base) + int64_t(r0) * ld_b, uint32_t(valid - 1) * ld_b + kb_end);
+}
+}  // namespace persist
+
+template <class C, int OUT = OUT_BF16>
+__device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
+  using namespace fast;
+  static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "bf16 output, or fp16 out of 16-bit operands");
+  constexpr int NW = persist::kWaves;
+  constexpr int TM = 128, TN = 128, FM = 4, FN = 4;
+  constexpr int NM = FM * FN, NF = FM + FN, NR = 2 * NF;
+  constexpr int BLKA = 32 / NW, BLKB = 32 / NW, ND = BLKA + BLKB;
+  constexpr int RW = NM / 2;
+  constexpr bool ROWCOL = C::FP8;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
+
+  const int total = a.tiles_m * a.tiles_n;
+  const int G = int(gridDim.x);
+  const int w = int(blockIdx.x);
+  const int T = w < total ? (total - w + G - 1) / G : 0;  // tiles of this workgroup
+  if (T == 0) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % 2, wn = wave / 2;
+  constexpr int ES = C::FP8 ? 1 : 2;
+  const uint32_t kb_end = uint32_t(a.K) * ES;
+  const int KS = int(kb_end / kStep);  // K steps per tile (>= 1)
+  const int S = T * KS;                // steps of the workgroup
+  const uint32_t lda_b = uint32_t(a.lda) * ES, ldb_b = uint32_t(a.ldb) * ES;
+
+  // Per-lane DMA offsets within a tile: row * ld + chunk for the wave's
+  // first two blocks (the chunk swizzle depends on the block's parity only);
+  // block j adds 8 j rows, and the K step, in the scalar offset.
+  const uint32_t kch[2] = {16u * uint32_t((lane & 7) ^ ((lane >> 4) & 7)),
+                           16u * uint32_t((lane & 7) ^ ((4 + (lane >> 4)) & 7))};
+  uint32_t vo[2][2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    vo[0][e] = uint32_t(8 * (BLKA * wave + e) + (lane >> 3)) * lda_b + kch[e];
+    vo[1][e] = uint32_t(8 * (BLKB * wave + e) + (lane >> 3)) * ldb_b + kch[e];
+  }
+  const uint32_t ld8[2] = {8u * lda_b, 8u * ldb_b};
+  using OpA = std::integral_constant<int, 0>;
+  using OpB = std::integral_constant<int, 1>;
+  auto coords = [&](int t, int *tm, int *tn) { tile_coords(w + t * G, a.tiles_m, a.tiles_n, a.group_m, tm, tn); };
+
+  // Load cursor of one operand: the step it is at and the buffer resource of
+  // that step's tile (an empty range past the last tile).  Steps advance
+  // one at a time.
+  struct Cursor {
+    int t, k;
+    __amdgpu_buffer_rsrc_t rs;
+  };
+  auto set_tile = [&](Cursor &c, auto op_tag) {
+    constexpr int op = decltype(op_tag)::value;
+    if (c.t < T) {
+      int tm, tn;
+      coords(c.t, &tm, &tn);
+      c.rs = op == 0 ? persist::tile_rsrc(a.A, tm * 256, a.M, lda_b, kb_end)
+                     : persist::tile_rsrc(a.B, tn * 256, a.N, ldb_b, kb_end);
+    } else {
+      c.rs = make_rsrc(op == 0 ? a.A : a.B, 0u);
+    }
+  };
+  auto advance = [&](Cursor &c, auto op_tag) {
+    if (++c.k == KS) {
+      c.k = 0;
+      ++c.t;
+      set_tile(c, op_tag);
+    }
+  };
+  auto load_op = [&](const Cursor &c, int slot, auto op_tag, auto j_tag) {
+    constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
+    constexpr int blk = op == 0 ? BLKA : BLKB;
+    uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *)dst, 16, vo[op][j & 1],
+                                             uint32_t(c.k) * kStep + uint32_t(j & ~1) * ld8[op], 0, 0);
+  };
+
+  const int frow = lane & 31, fg = lane >> 5;
+  int ro[2][2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int chunk = 4 * h + (C::FP8 ? fg + 2 * e : 2 * fg + e);
+      ro[0][h][e] = off(wm * TM + frow, chunk);
+      ro[1][h][e] = off(wn * TN + frow, chunk);
+    }
+  txd::i32x4 fr[2][NF][2];
+  auto read = [&](int slot_a, int slot_b, auto h_tag, auto r_tag) {
+    constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
+    constexpr int f = o == 0 ? 0 : o == 1 ? FM : o <= FM ? o - 1 : o;
+    const uint8_t *Sp = lds + (f < FM ? slot_a : slot_b) * kSlotBytes;
+    const int byte = f < FM ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - FM);
+    fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(Sp + byte);
+  };
+  txd::f32x16 acc[FN][FM];
+  // MFMA i of a K half: B block i / FM against A block i % FM; FIRST: the
+  // tile's first step, from a zero accumulator.
+  auto mma = [&](auto h_tag, auto i_tag, auto first_tag) {
+    constexpr int h = decltype(h_tag)::value, i = decltype(i_tag)::value, fn = i / FM, fm = i % FM;
+    const i32x8 va = __builtin_shufflevector(fr[h][fm][0], fr[h][fm][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const i32x8 vb = __builtin_shufflevector(fr[h][FM + fn][0], fr[h][FM + fn][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    if constexpr (decltype(first_tag)::value && h == 0) acc[fn][fm] = txd::f32x16{};
+    mfma32<C>(acc[fn][fm], vb, va);
+  };
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
+
+  // Prologue: steps 0, 0, 1, 1, 2 (A0 B0 A1 B1 A2) of the first tile.
+  Cursor ca, cb;
+  ca.t = ca.k = cb.t = cb.k = 0;
+  set_tile(ca, OpA{});
+  set_tile(cb, OpB{});
+  static_for<BLKA>([&](auto j) { load_op(ca, 0, OpA{}, j); });
+  static_for<BLKB>([&](auto j) { load_op(cb, 1, OpB{}, j); });
+  advance(ca, OpA{});
+  advance(cb, OpB{});
+  static_for<BLKA>([&](auto j) { load_op(ca, 2, OpA{}, j); });
+  static_for<BLKB>([&](auto j) { load_op(cb, 3, OpB{}, j); });
+  advance(ca, OpA{});
+  advance(cb, OpB{});  // next B load: step 2
+  static_for<BLKA>([&](auto j) { load_op(ca, 4, OpA{}, j); });
+  advance(ca, OpA{});  // next A load: step 3
+  wait_and_barrier<2 * BLKA + BLKB>();
+  static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
+
+  // One K step: half 0 (reads of half 1), barrier, half 1 (loads of B s+2
+  // and A s+3, reads of half 0 of step s+1).  FIRST: the tile's first step
+  // (MFMAs from a zero accumulator); VM: loads and stores allowed in flight
+  // at the barrier (the next step's operands are older than the last VM);
+  // LAST: the tile's last step, whose A s+3 loads wait until after the
+  // epilogue (their slot stages the output tile), as do the reads of the
+  // next step's first half (their registers hold the column scales).
+  int sa = 0, sb = 1;
+  auto step = [&](auto first_tag, auto vm_tag, auto last_tag) {
+    constexpr int VM = decltype(vm_tag)::value;
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;
+    static_for<NM>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      mma(H0{}, I, first_tag);
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+      static_for<r1 - r0>([&](auto R) { read(sa, sb, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{}); });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    wait_and_barrier<VM>();
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<NM>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      mma(H1{}, I, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
+      static_for<d1 - d0>([&](auto D) {
+        constexpr int d = d0 + decltype(D)::value;
+        if constexpr (d < BLKB) load_op(cb, sa, OpB{}, std::integral_constant<int, d>{});
+        else if constexpr (!LAST) load_op(ca, sb, OpA{}, std::integral_constant<int, d - BLKB>{});
+      });
+      constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+      if constexpr (!LAST)
+        static_for<r1 - r0>([&](auto R) { read(na, nb, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{}); });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    advance(cb, OpB{});
+    if constexpr (!LAST) advance(ca, OpA{});
+    sa = na;
+    sb = nb;
+  };
+  using VmStep = std::integral_constant<int, BLKA>;
+  // The epilogue issues exactly kEpiStores stores per wave, then the last
+  // step's deferred BLKA loads of A; the next tile's first barrier may
+  // leave all of them in flight.
+  constexpr int kEpiStores = FM * 8;
+  using VmAfterEpi = std::integral_constant<int, BLKB + kEpiStores>;
+  static_assert(BLKB + kEpiStores < 64, "vmcnt range");
+  // Scale loads issued before the last step (row scales, 16 column-scale
+  // vectors) that its barrier leaves in flight with the step's own A loads.
+  constexpr int kScaleLoads = ROWCOL ? FM + 16 : 0;
+  using VmLast = std::integral_constant<int, BLKA + kScaleLoads>;
+  static_assert(BLKA + kScaleLoads < 64, "vmcnt range");
+
+  // C as a buffer: a store whose row or column block lies past M / N gets an
+  // offset past the range and is dropped (N is a multiple of 8 and rows of
+  // C are 16-byte aligned, so a 16-byte column block is wholly in or out).
+  const __amdgpu_buffer_rsrc_t crs =
+      make_rsrc(a.C, uint32_t((int64_t(a.M - 1) * a.ldc + a.N) * 2));
+  // Staging: wave w owns bytes 8 KiB w .. +8 KiB of the slot its last step's
+  // A s+3 loads would have filled (the same bytes those loads fill once the
+  // epilogue is done, so no other wave ever touches them): 32 rows x 256
+  // bytes, 16-byte chunk c of row r at c ^ (r % 16).
+  for (int t = 0; t < T; ++t) {
+    int tm, tn;
+    coords(t, &tm, &tn);
+    const int m0 = tm * 256, n0 = tn * 256;
+    if (t == 0) step(std::true_type{}, VmStep{}, std::false_type{});
+    else step(std::true_type{}, VmAfterEpi{}, std::false_type{});
+    for (int k = 1; k < KS - 1; ++k) step(std::false_type{}, VmStep{}, std::false_type{});
+    // Scales load just before the last step and are waited for after it
+    // with vmcnt(BLKB), leaving its B loads in flight.  Loads and waits are
+    // written out: the compiler does not count the LDS-DMA loads when it
+    // places waits, so its own wait here would be vmcnt(0), a full drain of
+    // the next tile's operand loads (vector-memory operations complete in
+    // order, so vmcnt(n) with n = the operations issued since guarantees a
+    // load).  Rows past M read row M - 1 and columns past N the last four;
+    // their stores are dropped.
+    float sav[FM];
+    txd::f32x4 sb4[FN][4];  // columns 32 fn + 8 jj + 4 g .. + 3 of the wave's
+    if constexpr (ROWCOL) {
+      const int nl = n0 + wn * TN + 4 * fg;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const float *ps = a.scale_a + min(m0 + wm * TM + fm * 32 + frow, a.M - 1);
+        asm volatile("global_load_dword %0, %1, off" : "=v"(sav[fm]) : "v"(ps) : "memory");
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float *ps = a.scale_b + min(nl + 32 * fn + 8 * jj, a.N - 4);
+          asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(sb4[fn][jj]) : "v"(ps) : "memory");
+        }
+    }
+    const int stage_slot = sb;  // the last step's B slot: its A s+3 loads go there
+    step(std::false_type{}, VmLast{}, std::true_type{});  // the last step (KS >= 2)
+    if constexpr (ROWCOL) {
+      asm volatile("s_waitcnt vmcnt(%4)" : "+v"(sav[0]), "+v"(sav[1]), "+v"(sav[2]), "+v"(sav[3]) : "n"(BLKB));
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+        asm volatile("" : "+v"(sb4[fn][0]), "+v"(sb4[fn][1]), "+v"(sb4[fn][2]), "+v"(sb4[fn][3]));
+    }
+    // Epilogue, per 32-row block fm: scale, round, and exchange halves so
+    // that lane l < 32 holds columns 16 p .. 16 p + 7 and lane l + 32
+    // columns 16 p + 8 .. + 15 of row l % 32 (p = 2 fn + pr); stage the
+    // wave's 32 x 128 block, then store 4 rows of 256 bytes per instruction.
+    uint8_t *stg = lds + stage_slot * kSlotBytes + wave * 8192;
+    const int srow = lane >> 4, schunk = lane & 15;  // read-back: row 4 i + srow, chunk schunk
+    const int n_st = n0 + wn * TN + 8 * schunk;
+    const uint32_t coloff = n_st < a.N ? uint32_t(n_st) * 2u : kOob;
+    static_for<FM>([&](auto fm_tag) {
+      constexpr int fm = decltype(fm_tag)::value;
+      static_for<FN>([&](auto fn_tag) {
+        constexpr int fn = decltype(fn_tag)::value;
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          uint32_t pk[2][2];
+#pragma unroll
+          for (int jl = 0; jl < 2; ++jl) {
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              // read the accumulator where it is used (the compiler would
+              // otherwise copy whole tiles out of the AGPRs at once)
+              asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[q]) : "a"(acc[fn][fm][4 * (2 * pr + jl) + q]));
+              if constexpr (ROWCOL) v[q] = v[q] * sav[fm] * sb4[fn][2 * pr + jl][q];
+            }
+            pk[jl][0] = OUT == OUT_F16 ? txd::pack_f16x2(v[0], v[1]) : txd::pack_bf16x2(v[0], v[1]);
+            pk[jl][1] = OUT == OUT_F16 ? txd::pack_f16x2(v[2], v[3]) : txd::pack_bf16x2(v[2], v[3]);
+          }
+          uint32_t o[4];
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(pk[0][d], pk[1][d], false, false);
+            o[d] = sw[0];
+            o[2 + d] = sw[1];
+          }
+          const int chunk = 2 * (2 * fn + pr) + fg;
+          *reinterpret_cast<txd::u32x4 *>(stg + frow * 256 + ((chunk ^ (frow & 15)) << 4)) =
+              txd::u32x4{o[0], o[1], o[2], o[3]};
+        }
+      });
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 4 * i + srow;
+        const txd::u32x4 w = *reinterpret_cast<const txd::u32x4 *>(stg + r * 256 + ((schunk ^ (r & 15)) << 4));
+        const int m = m0 + wm * TM + fm * 32 + r;
+        const uint32_t voff = (m >= a.M || coloff == kOob) ? kOob : uint32_t(m) * uint32_t(a.ldc) * 2u + coloff;
+        __builtin_amdgcn_raw_buffer_store_b128(w, crs, voff, 0, 0);
+      }
+    });
+    // the deferred A s+3 loads (after this wave's last staging reads) and
+    // the next step's first-half fragments
+    __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));
+    static_for<BLKA>([&](auto j) { load_op(ca, stage_slot, OpA{}, j); });
+    advance(ca, OpA{});
+    static_for<NR>([&](auto r) { read(sa, sb, H0{}, r); });
+  }
+  // Drain the trailing (empty-range) loads before the workgroup's LDS is released.
+  wait_and_barrier<0>();
+}
+
+}  // namespace txg
