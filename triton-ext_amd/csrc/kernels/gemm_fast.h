@@ -248,28 +248,29 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
     const bool live = kfirst + ks < ksteps_all;
     return Src{live ? rsrc[op] : rnull[op], live ? kbase + uint32_t(ks) * kStep : 0u};
   };
-  // Load block j of operand op from `sr` into slot `slot`.  With TAIL (K *
-  // element size not a multiple of the step), a lane whose chunk lies past
-  // the row end reads zeros; otherwise no chunk ever does, and the load
-  // takes its per-lane offset as it is (no vector instructions per load).
-  auto load_op = [&](const Src &sr, int slot, auto op_tag, auto j_tag, auto tail_tag) {
+  // Load block j of operand op from `sr` into the LDS operand buffer at byte
+  // `base`.  With TAIL (K * element size not a multiple of the step), a lane
+  // whose chunk lies past the row end reads zeros; otherwise no chunk ever
+  // does, and the load takes its per-lane offset as it is (no vector
+  // instructions per load).
+  auto load_op = [&](const Src &sr, int base, auto op_tag, auto j_tag, auto tail_tag) {
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     constexpr int blk = op == 0 ? BLKA : BLKB;
     uint32_t voff = vo[op][j];
     if constexpr (decltype(tail_tag)::value) {
       if (sr.so + kch[j & 1] >= kb_end) voff = kOob;
     }
-    uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
+    uint8_t *dst = lds + base + (blk * wave + j) * 1024;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(sr.rs, (lds_void *)dst, 16, voff, sr.so, 0, 0);
   };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
-  // Load d of the second half of step ks: B of step ks+2 into the slot of A
-  // of step ks (d < BLKB), then A of step ks+3 into the slot of B of step ks.
-  auto load = [&](const Src &srb, const Src &sra, int slot_a, int slot_b, auto d_tag, auto tail_tag) {
+  // Load d of the second half of a step: B (d < BLKB) from srb into the
+  // buffer at byte dst_b, then A from sra into dst_a.
+  auto load = [&](const Src &srb, const Src &sra, int dst_b, int dst_a, auto d_tag, auto tail_tag) {
     constexpr int d = decltype(d_tag)::value;
-    if constexpr (d < BLKB) load_op(srb, slot_a, OpB{}, std::integral_constant<int, d>{}, tail_tag);
-    else load_op(sra, slot_b, OpA{}, std::integral_constant<int, d - BLKB>{}, tail_tag);
+    if constexpr (d < BLKB) load_op(srb, dst_b, OpB{}, std::integral_constant<int, d>{}, tail_tag);
+    else load_op(sra, dst_a, OpA{}, std::integral_constant<int, d - BLKB>{}, tail_tag);
   };
 
   // Fragment reads: lane l holds row l % 32 of a 32-row block and, for K half
@@ -325,10 +326,11 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   txd::i32x4 fr[2][NF][2];  // [K half][fragment][16-byte piece]
   // Read r of a K half: fragments in the order the MFMAs consume them
   // (A0, B0, A1 .. A(FM-1), B1 .., two 16-byte pieces each.
-  auto read = [&](int slot_a, int slot_b, auto h_tag, auto r_tag) {
+  // (base_a, base_b: the step's A and B buffers in LDS, in bytes)
+  auto read = [&](int base_a, int base_b, auto h_tag, auto r_tag) {
     constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
     constexpr int f = o == 0 ? 0 : o == 1 ? FM : o <= FM ? o - 1 : o;
-    const uint8_t *S = lds + (f < FM ? slot_a : slot_b) * kSlotBytes;
+    const uint8_t *S = lds + (f < FM ? base_a : base_b);
     const int byte = f < FM ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - FM);
     fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(S + byte);
   };
@@ -361,21 +363,80 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   constexpr int RW = NM / 2;  // reads follow the first RW MFMAs of a half
 
   // The prologue and the K loop, with or without the K-tail zero fill.
+  // Ring of LDS operand buffers.  Standard: 5 slots of one operand of one
+  // step (32 KiB), A of step k in slot 2k mod 5 and B in 2k + 1 mod 5; during
+  // the second half of step k, B of step k+2 and A of step k+3 go into the
+  // two slots step k frees, so B has one step to arrive and A two.  HS (256 x
+  // 128 tiles without MX scales): 3 stages of one whole step (A 32 KiB, then
+  // B 16 KiB), step k in stage k mod 3, and the second half of step k loads
+  // both operands of step k+3 into its stage: two steps for each, which the
+  // tiles that stream B from HBM (products with few rows) need.
+  constexpr bool HS = BN == 128 && !MX;
+  constexpr int kStage = (256 + BN) * kStep;  // HS stage: A, then B
+  static_assert(!HS || 3 * kStage <= kSlots * kSlotBytes, "HS stages fit in LDS");
   auto pipeline = [&](auto tail) {
+    if constexpr (HS) {
+      // Prologue: steps 0, 1 and 2 in flight, step 0 landed, half 0 of step
+      // 0 in registers.
+      static_for<3>([&](auto s_tag) {
+        constexpr int st = decltype(s_tag)::value;
+        const Src as = src(st, 0), bs = src(st, 1);
+        static_for<BLKA>([&](auto j) { load_op(as, st * kStage, OpA{}, j, tail); });
+        static_for<BLKB>([&](auto j) { load_op(bs, st * kStage + 256 * kStep, OpB{}, j, tail); });
+      });
+      wait_and_barrier<2 * ND>();
+      static_for<NR>([&](auto r) { read(0, 256 * kStep, H0{}, r); });
+      int st = 0;  // stage of step ks (uniform)
+      for (int ks = 0; ks < ksteps; ++ks) {
+        const int nt = st == 2 ? 0 : st + 1;
+        const int ca = st * kStage, cb = ca + 256 * kStep, xa = nt * kStage, xb = xa + 256 * kStep;
+        static_for<NM>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          mma(H0{}, I);
+          __builtin_amdgcn_sched_barrier(0);
+          constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+          static_for<r1 - r0>([&](auto R) {
+            read(ca, cb, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+          });
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        // step ks+1 landed for every wave (step ks+2 may still be in flight);
+        // the stage of step ks is free
+        wait_and_barrier<ND>();
+        __builtin_amdgcn_sched_barrier(0);
+        const Src srb = src(ks + 3, 1), sra = src(ks + 3, 0);
+        static_for<NM>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          mma(H1{}, I);
+          __builtin_amdgcn_sched_barrier(0);
+          constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
+          static_for<d1 - d0>([&](auto D) {
+            load(srb, sra, cb, ca, std::integral_constant<int, d0 + decltype(D)::value>{}, tail);
+          });
+          constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
+          static_for<r1 - r0>([&](auto R) {
+            read(xa, xb, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+          });
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        st = nt;
+      }
+      return;
+    }
     // Prologue: A0 B0 A1 B1 A2 in flight (steps past the end read as zeros),
     // step 0 landed, half 0 of step 0 in registers.  The MX scales of step 0
     // go first, so the same wait covers them.
     load_scales(0, scn);
     {
       const Src a0 = src(0, 0), b0 = src(0, 1), a1 = src(1, 0), b1 = src(1, 1), a2 = src(2, 0);
-      static_for<BLKA>([&](auto j) { load_op(a0, 0, OpA{}, j, tail); });
-      static_for<BLKB>([&](auto j) { load_op(b0, 1, OpB{}, j, tail); });
-      static_for<BLKA>([&](auto j) { load_op(a1, 2, OpA{}, j, tail); });
-      static_for<BLKB>([&](auto j) { load_op(b1, 3, OpB{}, j, tail); });
-      static_for<BLKA>([&](auto j) { load_op(a2, 4, OpA{}, j, tail); });
+      static_for<BLKA>([&](auto j) { load_op(a0, 0 * kSlotBytes, OpA{}, j, tail); });
+      static_for<BLKB>([&](auto j) { load_op(b0, 1 * kSlotBytes, OpB{}, j, tail); });
+      static_for<BLKA>([&](auto j) { load_op(a1, 2 * kSlotBytes, OpA{}, j, tail); });
+      static_for<BLKB>([&](auto j) { load_op(b1, 3 * kSlotBytes, OpB{}, j, tail); });
+      static_for<BLKA>([&](auto j) { load_op(a2, 4 * kSlotBytes, OpA{}, j, tail); });
     }
     wait_and_barrier<2 * BLKA + BLKB>();
-    static_for<NR>([&](auto r) { read(0, 1, H0{}, r); });
+    static_for<NR>([&](auto r) { read(0, kSlotBytes, H0{}, r); });
 
     int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
     for (int ks = 0; ks < ksteps; ++ks) {
@@ -391,7 +452,7 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
         __builtin_amdgcn_sched_barrier(0);
         constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
         static_for<r1 - r0>([&](auto R) {
-          read(sa, sb, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+          read(sa * kSlotBytes, sb * kSlotBytes, H1{}, std::integral_constant<int, r0 + decltype(R)::value>{});
         });
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -407,11 +468,12 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
         __builtin_amdgcn_sched_barrier(0);
         constexpr int d0 = spread_lo(i, ND, NM), d1 = spread_hi(i, ND, NM);
         static_for<d1 - d0>([&](auto D) {
-          load(srb, sra, sa, sb, std::integral_constant<int, d0 + decltype(D)::value>{}, tail);
+          load(srb, sra, sa * kSlotBytes, sb * kSlotBytes, std::integral_constant<int, d0 + decltype(D)::value>{},
+               tail);
         });
         constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
         static_for<r1 - r0>([&](auto R) {
-          read(na, nb, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
+          read(na * kSlotBytes, nb * kSlotBytes, H0{}, std::integral_constant<int, r0 + decltype(R)::value>{});
         });
         __builtin_amdgcn_sched_barrier(0);
       });
