@@ -21,6 +21,11 @@ constexpr int64_t kAggStep = 4 * kAggBlock;
 constexpr int64_t kWinStep = 3 * kAggStep;  // windowed kernel: its pipelined loop takes 3 steps at a time
 constexpr int64_t kDirectSlots = 36864;  // bins per LDS window
 constexpr int64_t kMaxWindows = 4;       // beyond this the hash-table kernel is used
+// Spill buffer of the windowed kernel's one-pass path: records per
+// wavefront region (16 wavefronts per workgroup), and the chunk of records
+// per workgroup of the second launch that folds them into the bins.
+constexpr int64_t kSpillWave = 512;
+constexpr int64_t kSpillChunk = 3 * kWinStep;
 
 const char *op_name(tx_rmw_op op) {
   switch (op) {
@@ -107,7 +112,29 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
     args.per_block = int32_t(per);
     args.splits = int32_t(windows);
     args.window = int32_t(kDirectSlots);
-    return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
+    if (windows == 1) return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
+    // Several windows: a workgroup whose keys are skewed makes one pass with
+    // its best window and writes the in-range updates outside it to its
+    // wavefronts' regions of a spill buffer in stream scratch (slot 0); a
+    // second launch of the same kernel folds those records (unused ones are
+    // marked out of range) into the bins, with direct global atomics for
+    // whatever spills again.  Without the buffer the first launch sends its
+    // spills to global atomics itself.
+    const int64_t records = chunks * (kAggBlock / 64) * kSpillWave;
+    ScratchLease sp;  // held until both launches are enqueued
+    if (sp.acquire(s, 0, size_t(records) * 8) != TX_SUCCESS) {
+      clear_error();
+      return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
+    }
+    args.spill_keys = static_cast<uint32_t *>(sp.ptr());
+    args.spill_vals = args.spill_keys + records;
+    args.spill_wave = int32_t(kSpillWave);
+    TX_TRY(launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname));
+    tx_scatter_args fold{bins, reinterpret_cast<const int32_t *>(args.spill_keys), args.spill_vals, nullptr,
+                         nullptr, records, int32_t(nbins), int32_t(kSpillChunk), int32_t(windows),
+                         int32_t(kDirectSlots)};
+    const int64_t fold_chunks = (records + kSpillChunk - 1) / kSpillChunk;
+    return launch(fn, unsigned(fold_chunks), 1, kAggBlock, s, &fold, sizeof fold, kname);
   }
   std::snprintf(kname, sizeof kname, "tx_scatter_%s_hashed", name);
   TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));

@@ -148,13 +148,49 @@ __device__ __forceinline__ void spill_flush(const uint32_t *q, uint32_t qn, T *b
     atomic_combine<OP, T>(bins + q[i], __builtin_bit_cast(T, q[kQueue + i]));
 }
 
+// The wavefront's region of the spill buffer (see tx_scatter_args): `fill`
+// records written of `cap` (both wavefront-uniform); keys == NULL: none.
+struct SpillRegion {
+  uint32_t *keys = nullptr, *vals = nullptr;
+  uint32_t fill = 0, cap = 0;
+  __device__ __forceinline__ void init(const tx_scatter_args &a) {
+    if (!a.spill_keys) return;
+    const int64_t r = (int64_t(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64) * a.spill_wave;
+    keys = a.spill_keys + r;
+    vals = a.spill_vals + r;
+    cap = uint32_t(a.spill_wave);
+  }
+  // mark the unused records (every lane of the wavefront takes part)
+  __device__ __forceinline__ void close() {
+    if (!keys) return;
+    for (uint32_t i = fill + (threadIdx.x & 63); i < cap; i += 64) keys[i] = 0xFFFFFFFFu;
+  }
+};
+
+// Send the queue's qn records to the region when they fit (whole-wavefront
+// stores, read again by a second launch of the windowed kernel), else to the
+// bins with global atomics.
 template <int OP, typename T>
-__device__ __forceinline__ void spill_push(uint32_t *q, uint32_t &qn, T *bins, bool sp, uint32_t key, T v) {
+__device__ __forceinline__ void spill_out(const uint32_t *q, uint32_t qn, T *bins, SpillRegion &sr) {
+  if (sr.keys && sr.fill + qn <= sr.cap) {
+    for (uint32_t i = threadIdx.x & 63; i < qn; i += 64) {
+      sr.keys[sr.fill + i] = q[i];
+      sr.vals[sr.fill + i] = q[kQueue + i];
+    }
+    sr.fill += qn;
+  } else {
+    spill_flush<OP, T>(q, qn, bins);
+  }
+}
+
+template <int OP, typename T>
+__device__ __forceinline__ void spill_push(uint32_t *q, uint32_t &qn, T *bins, SpillRegion &sr, bool sp,
+                                           uint32_t key, T v) {
   const uint64_t m = __ballot(sp);
   if (m == 0) return;
   const uint32_t cnt = uint32_t(__popcll(m));
   if (qn + cnt > kQueue) {
-    spill_flush<OP, T>(q, qn, bins);
+    spill_out<OP, T>(q, qn, bins, sr);
     qn = 0;
   }
   if (sp) {
@@ -269,7 +305,7 @@ struct Scatter {
   // INT32_MAX.
   template <bool HOT, bool SPILL>
   static __device__ __forceinline__ void apply(T *table, uint32_t lo, uint32_t nb, T *bins, uint32_t nbins,
-                                               uint32_t *q, uint32_t &qn, HotKeys<OP> &hot,
+                                               uint32_t *q, uint32_t &qn, SpillRegion &sr, HotKeys<OP> &hot,
                                                const txd::i32x4 &k, const txd::u32x4 &v, uint32_t m) {
     const int32_t kk[4] = {k.x, k.y, k.z, k.w};
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
@@ -279,7 +315,8 @@ struct Scatter {
       const bool live = ((m >> (8 * j)) & 0xFFu) != 0;
       bool pend = r < nb && live;
       const T x = __builtin_bit_cast(T, vv[j]);
-      if constexpr (SPILL) spill_push<OP, T>(q, qn, bins, live && !pend && uint32_t(kk[j]) < nbins, uint32_t(kk[j]), x);
+      if constexpr (SPILL)
+        spill_push<OP, T>(q, qn, bins, sr, live && !pend && uint32_t(kk[j]) < nbins, uint32_t(kk[j]), x);
       if constexpr (OP == FADD && HOT) hot.take(pend, r, x);
       wave_lds_combine<OP, T>(table, pend, r, x);
     }
@@ -293,8 +330,8 @@ struct Scatter {
   // the last one (in range, never applied).
   template <bool MASK, bool HOT, bool SPILL>
   static __device__ __forceinline__ void stream(const tx_scatter_args &a, T *table, uint32_t lo,
-                                                uint32_t nb, uint32_t *q, uint32_t &qn, HotKeys<OP> &hot,
-                                                int64_t e0, int64_t groups) {
+                                                uint32_t nb, uint32_t *q, uint32_t &qn, SpillRegion &sr,
+                                                HotKeys<OP> &hot, int64_t e0, int64_t groups) {
     T *bins = reinterpret_cast<T *>(a.bins);
     txd::i32x4 k[kDepth];
     txd::u32x4 v[kDepth];
@@ -306,7 +343,7 @@ struct Scatter {
       const int64_t eg = e0 + g * kDepth * kIter;
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        apply<HOT, SPILL>(table, lo, nb, bins, uint32_t(a.nbins), q, qn, hot, k[d], v[d], m[d]);
+        apply<HOT, SPILL>(table, lo, nb, bins, uint32_t(a.nbins), q, qn, sr, hot, k[d], v[d], m[d]);
         const int64_t en = eg + (d + kDepth) * kIter;
         fetch<MASK>(a, en < last ? en : last, k[d], v[d], m[d]);
       }
@@ -323,7 +360,7 @@ struct Scatter {
   // barrier.
   static constexpr int kWinBlock = 2048;
   static constexpr int kMaxWinBlocks = 4 * kDirectSlots / kWinBlock;
-  static __device__ void pick_window(const tx_scatter_args &a, int64_t begin, int64_t end, bool vec,
+  static __device__ __forceinline__ void pick_window(const tx_scatter_args &a, int64_t begin, int64_t end, bool vec,
                                      uint32_t window, uint32_t *cnt, uint32_t &base, uint32_t &hits,
                                      uint32_t &total) {
     for (int s = threadIdx.x; s < kMaxWinBlocks + 2; s += kBlock) cnt[s] = 0u;
@@ -371,7 +408,7 @@ struct Scatter {
   // Picks the workgroup's hot keys (HotKeys) from the first 4 x kBlock
   // updates of its chunk; on return every lane holds the same set, with
   // zeroed sums.  Needs the whole workgroup; ends with a barrier.
-  static __device__ void sample_hot(const tx_scatter_args &a, uint32_t lo, uint32_t nb, int64_t begin,
+  static __device__ __forceinline__ void sample_hot(const tx_scatter_args &a, uint32_t lo, uint32_t nb, int64_t begin,
                                     int64_t end, bool vec, uint32_t *aux, HotKeys<OP> &hot) {
     uint32_t *skey = aux, *scnt = aux + kSampleSlots;
     for (int s = threadIdx.x; s < kSampleSlots; s += kBlock) {
@@ -459,7 +496,7 @@ struct Scatter {
   // with one global atomic per touched slot.  With SPILL, in-range updates
   // outside the window go to the bins through the wavefront spill queues in
   // aux; without it they are left to the chunk's other passes.
-  static __device__ void pass(const tx_scatter_args &a, T *table, uint32_t *aux, uint32_t lo, uint32_t nb,
+  static __device__ __forceinline__ void pass(const tx_scatter_args &a, T *table, uint32_t *aux, uint32_t lo, uint32_t nb,
                               bool spill, int64_t begin, int64_t end, bool vec) {
     for (uint32_t s = threadIdx.x; s < nb; s += kBlock) table[s] = OpTraits<OP>::id();
     HotKeys<OP> hot;
@@ -468,6 +505,8 @@ struct Scatter {
     T *bins = reinterpret_cast<T *>(a.bins);
     uint32_t *q = aux + (threadIdx.x / 64) * 2 * kQueue;
     uint32_t qn = 0;
+    SpillRegion sr;
+    if (spill) sr.init(a);
     int64_t e = begin + 4 * int64_t(threadIdx.x);
     if (vec) {
       // Whole groups of kDepth full iterations go through the pipelined loop.
@@ -476,19 +515,19 @@ struct Scatter {
         const bool h = OP == FADD && hot.n > 0;
         if (spill) {
           if (h) {
-            if (a.mask) stream<true, true, true>(a, table, lo, nb, q, qn, hot, e, groups);
-            else stream<false, true, true>(a, table, lo, nb, q, qn, hot, e, groups);
+            if (a.mask) stream<true, true, true>(a, table, lo, nb, q, qn, sr, hot, e, groups);
+            else stream<false, true, true>(a, table, lo, nb, q, qn, sr, hot, e, groups);
           } else {
-            if (a.mask) stream<true, false, true>(a, table, lo, nb, q, qn, hot, e, groups);
-            else stream<false, false, true>(a, table, lo, nb, q, qn, hot, e, groups);
+            if (a.mask) stream<true, false, true>(a, table, lo, nb, q, qn, sr, hot, e, groups);
+            else stream<false, false, true>(a, table, lo, nb, q, qn, sr, hot, e, groups);
           }
         } else {
           if (h) {
-            if (a.mask) stream<true, true, false>(a, table, lo, nb, q, qn, hot, e, groups);
-            else stream<false, true, false>(a, table, lo, nb, q, qn, hot, e, groups);
+            if (a.mask) stream<true, true, false>(a, table, lo, nb, q, qn, sr, hot, e, groups);
+            else stream<false, true, false>(a, table, lo, nb, q, qn, sr, hot, e, groups);
           } else {
-            if (a.mask) stream<true, false, false>(a, table, lo, nb, q, qn, hot, e, groups);
-            else stream<false, false, false>(a, table, lo, nb, q, qn, hot, e, groups);
+            if (a.mask) stream<true, false, false>(a, table, lo, nb, q, qn, sr, hot, e, groups);
+            else stream<false, false, false>(a, table, lo, nb, q, qn, sr, hot, e, groups);
           }
         }
         e += groups * kDepth * kIter;
@@ -506,14 +545,17 @@ struct Scatter {
       for (int j = 0; j < 4; ++j) {
         const uint32_t r = key[j] - lo;  // wraps for keys below the window
         bool pend = ok[j] && r < nb;
-        if (spill) spill_push<OP, T>(q, qn, bins, ok[j] && !pend, key[j], val[j]);
+        if (spill) spill_push<OP, T>(q, qn, bins, sr, ok[j] && !pend, key[j], val[j]);
         if constexpr (OP == FADD) {
           if (hot.n > 0) hot.take(pend, r, val[j]);
         }
         wave_lds_combine<OP, T>(table, pend, r, val[j]);
       }
     }
-    if (spill) spill_flush<OP, T>(q, qn, bins);
+    if (spill) {
+      spill_out<OP, T>(q, qn, bins, sr);
+      sr.close();
+    }
     // the hot keys' accumulators: one LDS combine per wavefront and key
 #pragma unroll
     for (int t = 0; t < kHot; ++t) {
@@ -540,7 +582,7 @@ struct Scatter {
   // workgroup makes one pass with that window and spills the rest (one read
   // of the chunk); otherwise it makes one pass per window, each reading the
   // whole chunk.
-  static __device__ void windowed(const tx_scatter_args &a) {
+  static __device__ __forceinline__ void windowed(const tx_scatter_args &a) {
     __shared__ T table[kDirectSlots];
     __shared__ uint32_t aux[kAuxWords];
     const int64_t begin = int64_t(blockIdx.x) * a.per_block;
@@ -557,6 +599,9 @@ struct Scatter {
       } else {
         for (int w = 0; w < a.splits; ++w)
           pass(a, table, aux, uint32_t(w) * W, min(W, nbins - uint32_t(w) * W), false, begin, end, vec);
+        SpillRegion sr;  // nothing spilled: every record of the regions unused
+        sr.init(a);
+        sr.close();
       }
       return;
     }

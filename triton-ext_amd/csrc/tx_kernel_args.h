@@ -48,6 +48,15 @@ typedef struct tx_scatter_args {
   int32_t per_block;   /* updates per chunk (multiple of 4 * blockDim) */
   int32_t splits;      /* windowed kernels: bin windows (workgroups per chunk) */
   int32_t window;      /* windowed kernels: bins per window */
+  /* windowed kernels, one-pass path: in-range updates outside the window go
+   * to the spill buffer (keys at spill_keys, values at spill_vals), region
+   * (chunk * 16 + wavefront) of spill_wave records each, unused records
+   * marked with key -1; a full region sends the rest to global atomics.
+   * NULL: all of them go to global atomics. */
+  uint32_t *spill_keys;
+  uint32_t *spill_vals;
+  int32_t spill_wave;
+  int32_t reserved;
 } tx_scatter_args;
 
 /* tt.atomic_cas in scatter form: 32-bit bins, compared bit for bit */
