@@ -110,6 +110,8 @@ def parse():
                    help="print the HBM traffic table from the rocprofv3 counter_collection.csv "
                         "files of two --windows runs (FETCH_SIZE, WRITE_SIZE) and of two "
                         "--calibrate-copy runs")
+    p.add_argument("--trace-summary", nargs=2, metavar=("WINDOWS_JSON", "TRACE_CSV"),
+                   help="print the per-workload kernel duration table of a kernel-trace run")
     p.add_argument("--mfma-summary", nargs=2, metavar=("WINDOWS_JSON", "MFMA_CSV"),
                    help="print MFMA busy and clock per GEMM workload from a --windows run "
                         "counted with SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, SQ_BUSY_CYCLES")
@@ -602,6 +604,37 @@ XCDS = 8
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 
 
+def trace_summary(windows_json, trace_csv):
+    """Per-workload kernel durations of a `rocprofv3 --kernel-trace` run of the
+    bench (made with --windows): every dispatch labelled with the workload
+    whose launch window holds its start; the last 20 of a group are the timed
+    launches of the GEMM and scatter lines."""
+    import csv
+    with open(windows_json) as f:
+        meta = json.load(f)
+    disp = []
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            disp.append({"kernel": row["Kernel_Name"], "t0": int(row["Start_Timestamp"]),
+                         "t1": int(row["End_Timestamp"]),
+                         "grid": f"{int(row['Grid_Size_X']) // max(1, int(row['Workgroup_Size_X']))} x "
+                                 f"{row['Workgroup_Size_X']}"})
+    rows = {}
+    for d, w in _assign(meta["windows"], disp):
+        key = (w["workload"], _short(d["kernel"]), d["grid"])
+        rows.setdefault(key, []).append(d["t1"] - d["t0"])
+    order = {w["workload"]: i for i, w in enumerate(meta["windows"])}
+    print(f"build digest: {meta['digest']}")
+    print()
+    print("| workload | kernel | grid (workgroups x threads) | dispatches | avg us (all) | avg us (last 20) |")
+    print("|---|---|---|---|---|---|")
+    for key in sorted(rows, key=lambda k: (order.get(k[0], 1 << 30), k[1], k[2])):
+        ds = rows[key]
+        last = ds[-20:]
+        print(f"| {key[0]} | `{key[1]}` | {key[2]} | {len(ds)} | {sum(ds) / len(ds) / 1e3:.2f} "
+              f"| {sum(last) / len(last) / 1e3:.2f} |")
+
+
 def traffic_from_table(workload, kernel_prefix):
     """HBM bytes per launch of a kernel on a workload, from the committed
     counter table, and whether the table was made on another build."""
@@ -631,6 +664,9 @@ def main():
         return
     if args.mfma_summary:
         mfma_summary(*args.mfma_summary)
+        return
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
         return
     if args.calibrate_copy:
         calibrate_copy()
