@@ -711,6 +711,51 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
 
 template <bool ROWCOL, int OUT = OUT_BF16>
 __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
+  // 16-bit output, no fused epilogue, N and ldc multiples of 8, C (and the
+  // column scales) 16-byte aligned, at most 8 splits: eight consecutive n
+  // per thread (the partial planes are 32-byte aligned then), every
+  // split's 32 bytes loaded before the adds (same order of additions as the
+  // general loop below), scales as vectors, one 16-byte store.
+  if constexpr (OUT != OUT_F32) {
+    if (!a.epi && (a.N & 7) == 0 && (a.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(a.C) & 15) == 0 &&
+        a.splits <= 8 && (!ROWCOL || (reinterpret_cast<uintptr_t>(a.scale_b) & 15) == 0)) {
+      const int64_t octs_per_row = a.N / 8;
+      const int64_t total = int64_t(a.M) * octs_per_row;
+      const int64_t plane = int64_t(a.M) * a.N;
+      for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+           t += int64_t(gridDim.x) * blockDim.x) {
+        const int m = int(t / octs_per_row);
+        const int n = int(t % octs_per_row) * 8;
+        const float *p = a.part + int64_t(m) * a.N + n;
+        txd::f32x4 x[8][2];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          if (s < a.splits) {
+            x[s][0] = *reinterpret_cast<const txd::f32x4 *>(p + s * plane);
+            x[s][1] = *reinterpret_cast<const txd::f32x4 *>(p + s * plane + 4);
+          }
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          if (s < a.splits)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] += x[s][i / 4][i % 4];
+        if constexpr (ROWCOL) {
+          const float sa = a.scale_a[m];
+          const txd::f32x4 sb0 = *reinterpret_cast<const txd::f32x4 *>(a.scale_b + n);
+          const txd::f32x4 sb1 = *reinterpret_cast<const txd::f32x4 *>(a.scale_b + n + 4);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = v[i] * sa * (i < 4 ? sb0[i] : sb1[i - 4]);
+        }
+        txd::u32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = OUT == OUT_F16 ? txd::pack_f16x2(v[2 * i], v[2 * i + 1]) : txd::pack_bf16x2(v[2 * i], v[2 * i + 1]);
+        *reinterpret_cast<txd::u32x4 *>(reinterpret_cast<uint16_t *>(a.C) + int64_t(m) * a.ldc + n) = o;
+      }
+      return;
+    }
+  }
   const int64_t quads_per_row = (a.N + 3) / 4;
   const int64_t total = int64_t(a.M) * quads_per_row;
   const int64_t plane = int64_t(a.M) * a.N;
