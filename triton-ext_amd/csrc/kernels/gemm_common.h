@@ -194,17 +194,9 @@ __device__ __forceinline__ u32x4 load_chunk(const uint8_t *row_ptr, int kb, int 
   return v;
 }
 
-// Map a linear workgroup id to a (tile_m, tile_n) pair: first regroup the ids
-// so that each of the 8 XCDs (workgroups are dispatched round-robin over
-// XCDs) gets a contiguous range of tile ids, then rasterise tile ids in
-// groups of group_m tile rows so neighbouring tiles share A and B panels in
-// the XCD's L2.
-__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int group_m,
-                                            int *tm, int *tn) {
-  const int total = tiles_m * tiles_n;
-  const int per = total / 8, rem = total % 8;
-  const int x = wg % 8, i = wg / 8;
-  const int pid = x * per + (x < rem ? x : rem) + i;
+// Tile id -> (tile_m, tile_n) in groups of group_m tile rows, so that
+// neighbouring tiles share A and B panels.
+__device__ __forceinline__ void raster_coords(int pid, int tiles_m, int tiles_n, int group_m, int *tm, int *tn) {
   const int in_group = group_m * tiles_n;
   const int gid = pid / in_group;
   const int first_m = gid * group_m;
@@ -212,6 +204,34 @@ __device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, in
   const int r = pid % in_group;
   *tm = first_m + r % gsz;
   *tn = r / gsz;
+}
+
+// Regroup linear workgroup ids so that each of the 8 XCDs (workgroups are
+// dispatched round-robin over XCDs) gets a contiguous range of `total` ids.
+__device__ __forceinline__ int xcd_contiguous(int wg, int total) {
+  const int per = total / 8, rem = total % 8;
+  const int x = wg % 8, i = wg / 8;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
+// Map a linear workgroup id to a (tile_m, tile_n) pair: XCD-contiguous tile
+// ids, rasterised in groups of group_m tile rows so that neighbouring tiles
+// share A and B panels in the XCD's L2.
+__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int group_m,
+                                            int *tm, int *tn) {
+  raster_coords(xcd_contiguous(wg, tiles_m * tiles_n), tiles_m, tiles_n, group_m, tm, tn);
+}
+
+// Split-K grids (tiles x splits workgroups): XCD-contiguous ids taken
+// split-major, so the workgroups of one XCD run one split (one K range of A,
+// which its L2 then holds) over neighbouring tiles, and the tiles that share
+// a B column panel in that K range run on the same XCD at the same time.
+__device__ __forceinline__ void split_coords(int wg, int tiles_m, int tiles_n, int splits, int group_m,
+                                             int *tm, int *tn, int *split) {
+  const int tiles = tiles_m * tiles_n;
+  const int pid = xcd_contiguous(wg, tiles * splits);
+  *split = pid / tiles;
+  raster_coords(pid % tiles, tiles_m, tiles_n, group_m, tm, tn);
 }
 
 // Copy rows into a zero-padded buffer (see tx_pad_args): one 16-byte chunk of

@@ -699,14 +699,14 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
 // Split-K reduction: C[m, n] = out(scale_a[m] * scale_b[n] * sum_s P[s][m][n])
 // (ROWCOL: the fp8 row / column scales; out: bf16 or fp16 round to nearest
 // even, or fp32), four consecutive n per thread.
-// One workgroup per tile of a single product: with K split, workgroup b
-// computes split b % splits of tile b / splits.
+// One workgroup per tile of a single product, or per (tile, split) pair
+// with K split (split_coords).
 template <class C, int BN, int NW = fast::kWaves, bool MX = false, int OUT = OUT_BF16, bool EPI = false>
 __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
-  const int splits = a.splits > 1 ? a.splits : 1;
-  int tm, tn;
-  tile_coords(int(blockIdx.x) / splits, a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
-  gemm_fast_tile_at<C, BN, NW, MX, OUT, EPI>(a, tm, tn, int(blockIdx.x) % splits);
+  int tm, tn, split = 0;
+  if (a.splits > 1) split_coords(int(blockIdx.x), a.tiles_m, a.tiles_n, a.splits, a.group_m, &tm, &tn, &split);
+  else tile_coords(int(blockIdx.x), a.tiles_m, a.tiles_n, a.group_m, &tm, &tn);
+  gemm_fast_tile_at<C, BN, NW, MX, OUT, EPI>(a, tm, tn, split);
 }
 
 template <bool ROWCOL, int OUT = OUT_BF16>
