@@ -32,7 +32,10 @@
  *    steady-state calls allocate nothing; requests above 512 MiB get a
  *    buffer per call.  If the allocation fails, tx_dot_bf16 and
  *    tx_dot_fp8_scaled run without it and tx_dot_scaled_mx returns the
- *    error.  No other entry point
+ *    error.  tx_atomic_rmw_scatter (aggregating form, more bins than one
+ *    36,864-bin LDS window) takes the same scratch for its spill buffer
+ *    (8 bytes x 8,192 records per CU: 16 MiB on 256 CUs) and without it
+ *    sends those updates to global atomics.  No other entry point
  *    allocates device memory.  txShutdown frees the kept scratch.  The
  *    library owns its code-object handles, loaded once per device on first
  *    use (or by txInit) and unloaded by txShutdown.
