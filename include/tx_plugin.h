@@ -22,7 +22,7 @@
  *  - The caller owns every input and output buffer.  tx_dot_bf16,
  *    tx_dot_fp8_scaled[_ex] and tx_dot_scaled_mx may use device scratch that
  *    the library keeps per (device, stream): fp32 split-K partial planes
- *    (at most 8 x M x N x 4 bytes) when the output tiles leave CUs idle,
+ *    (at most 16 x M x N x 4 bytes) when the output tiles leave CUs idle,
  *    zero-padded copies of A and B when rows are not 16-byte aligned in a
  *    product of at least 2^30 multiply-adds (tx_dot_scaled_mx: in any
  *    product), the e4m3fn expansion of an fp4 operand that meets an fp8

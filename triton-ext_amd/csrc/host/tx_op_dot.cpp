@@ -77,8 +77,8 @@ constexpr int kPersistWaves = 4;
 // Largest M served by the skinny fp8 kernel (4 blocks of 16 rows).
 constexpr int64_t kSkinnyMaxM = 64;
 // Split K only while every split keeps at least this many 128-byte K steps.
-constexpr int64_t kMinStepsPerSplit = 8;
-constexpr int64_t kMaxSplits = 8;
+constexpr int64_t kMinStepsPerSplit = 4;
+constexpr int64_t kMaxSplits = 16;
 
 // The LDS-DMA fast path needs 16-byte aligned rows and a row length that is a
 // multiple of 16 bytes, and operands small enough that a 32-bit buffer offset
@@ -93,7 +93,7 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 // Launch the fast path (kernel `base`, or `base`_n128): 256x256 tiles while
 // they give at least one tile per CU (see kStripMaxN for a narrow column
 // tail); otherwise 256x128 tiles, and when those
-// still leave CUs idle, K is split (at most 8 ways, at least 8 K steps per
+// still leave CUs idle, K is split (at most 16 ways, at least 4 K steps per
 // split) into fp32 partial planes in the library's stream scratch
 // (ScratchLease, slot 1) that the `reduce` kernel sums, scales and rounds
 // into C.

@@ -709,6 +709,8 @@ __device__ __forceinline__ void gemm_fast_tile(const tx_gemm_args &a) {
   gemm_fast_tile_at<C, BN, NW, MX, OUT, EPI>(a, tm, tn, split);
 }
 
+constexpr int kReduceBatch = 16;  // splits whose loads are in flight together
+
 template <bool ROWCOL, int OUT = OUT_BF16>
 __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
   // 16-bit output, no fused epilogue, N and ldc multiples of 8, C (and the
@@ -766,16 +768,27 @@ __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
     const int n = int(t % quads_per_row) * 4;
     const float *p = a.part + int64_t(m) * a.N + n;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if ((a.N & 3) == 0) {
-      for (int s = 0; s < a.splits; ++s) {
-        const txd::f32x4 x = *reinterpret_cast<const txd::f32x4 *>(p + s * plane);
-        v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
-      }
-    } else {
-      for (int s = 0; s < a.splits; ++s)
+    // Splits in batches of kReduceBatch, each batch's loads issued before
+    // its adds (in split order, so the sum is the same as one at a time).
+    for (int s0 = 0; s0 < a.splits; s0 += kReduceBatch) {
+      txd::f32x4 x[kReduceBatch];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (n + i < a.N) v[i] += p[s * plane + i];
+      for (int j = 0; j < kReduceBatch; ++j) {
+        const int s = s0 + j;
+        if (s < a.splits) {
+          if ((a.N & 3) == 0) {
+            x[j] = *reinterpret_cast<const txd::f32x4 *>(p + s * plane);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[j][i] = n + i < a.N ? p[s * plane + i] : 0.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kReduceBatch; ++j)
+        if (s0 + j < a.splits) {
+          v[0] += x[j].x; v[1] += x[j].y; v[2] += x[j].z; v[3] += x[j].w;
+        }
     }
     float sa = 1.0f;
     if constexpr (ROWCOL) sa = a.scale_a[m];
