@@ -784,11 +784,12 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
   char kname[48];
   hipFunction_t fn;
   if (M == 1 && K * 2 <= 32768) {  // x fits the kernel's LDS stage
-    // streaming VALU kernel: two W rows per wavefront, 8 wavefronts
+    // streaming VALU kernel: two W rows per wavefront, 4 wavefronts, x in
+    // K * 2 bytes of dynamic LDS
     std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s_lin_m1", fw);
     TX_TRY(get_kernel(CodeObject::Gemv, kname, &fn));
-    return launch(fn, unsigned((N + 15) / 16), 1, 512, static_cast<hipStream_t>(stream), &args, sizeof args,
-                  kname);
+    return launch(fn, unsigned((N + 7) / 8), 1, 256, static_cast<hipStream_t>(stream), &args, sizeof args,
+                  kname, unsigned(K * 2));
   }
   // 16 or 32 W rows per workgroup, K split over its wavefronts.  Many column
   // blocks: 4 wavefronts, each with two 16-row W blocks sharing its x reads

@@ -378,12 +378,12 @@ int cu_count() {
 
 tx_status launch(hipFunction_t fn, unsigned grid_x, unsigned grid_y,
                  unsigned block_x, hipStream_t stream, void *args,
-                 size_t args_size, const char *what) {
+                 size_t args_size, const char *what, unsigned shared_bytes) {
   if (grid_x == 0 || grid_y == 0) return TX_SUCCESS;
   void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args,
                     HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_size,
                     HIP_LAUNCH_PARAM_END};
-  hipError_t e = hipModuleLaunchKernel(fn, grid_x, grid_y, 1, block_x, 1, 1, 0,
+  hipError_t e = hipModuleLaunchKernel(fn, grid_x, grid_y, 1, block_x, 1, 1, shared_bytes,
                                        stream, nullptr, config);
   if (e != hipSuccess)
     return fail(TX_LAUNCH_ERROR, "launch of %s failed: %s", what,

@@ -38,7 +38,7 @@ tx_status get_kernel(CodeObject co, const char *name, hipFunction_t *out);
 // Enqueue `fn` with one by-value argument block of `args_size` bytes.
 tx_status launch(hipFunction_t fn, unsigned grid_x, unsigned grid_y,
                  unsigned block_x, hipStream_t stream, void *args,
-                 size_t args_size, const char *what);
+                 size_t args_size, const char *what, unsigned shared_bytes = 0);
 
 // The current device's copy of the no-allocation entry point's workspace
 // (tx_noalloc.hip), its address looked up once per device.

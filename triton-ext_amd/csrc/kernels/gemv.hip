@@ -264,32 +264,37 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
 }
 
 // One row of x (M = 1, batch-1 decode): a plain streaming dot on the VALU.  Wave w of
-// workgroup b owns W rows 2 (8 b + w) and 2 (8 b + w) + 1 and walks them in
+// workgroup b owns W rows 2 (4 b + w) and 2 (4 b + w) + 1 and walks them in
 // 1 KiB slices (lane l: bytes 16 l .. 16 l + 15 of the slice, so one load
-// instruction reads 1 KiB of one row, contiguous, non-temporal), four
+// instruction reads 1 KiB of one row, contiguous, non-temporal), two
 // slices of both rows in flight at a time.  x (M x K bf16, at most
-// kLinMaxX bytes) is staged in LDS once per workgroup, which keeps the
-// registers to the W stream and the occupancy at 8 waves per SIMD.  The
-// codes become fp32 through gfx950's packed conversions (exact for every
-// finite code), each lane's 16 products are summed in fp32 and scaled by
-// their group's scale (16 consecutive K never cross a group: group % 128
-// == 0), and the lanes' sums meet in a butterfly reduction.
+// kLinMaxX bytes) is staged in LDS once per workgroup, in dynamic LDS of
+// exactly its size, which keeps the registers to the W stream (54) and the
+// occupancy at 8 waves per SIMD.  Small workgroups of 4 wavefronts (8 W
+// rows) spread the rows evenly over the CUs (14336 rows: 7 workgroups per
+// CU; 8 wavefronts and 16 rows per workgroup left 3 or 4 per CU and ran
+// 14.4 against 11.9 us).  The codes become fp32 through gfx950's packed
+// conversions (exact for every finite code), each lane's 16 products are
+// summed in fp32 and scaled by their group's scale (16 consecutive K never
+// cross a group: group % 128 == 0), and the lanes' sums meet in a butterfly
+// reduction.
 constexpr int kLinMaxX = 32768;
+constexpr int kLinWaves = 4;
 
 template <int FMT, int MB>
 __device__ __forceinline__ void gemv_lin(const tx_gemv_args &a) {
-  constexpr int RPW = 2, CB = 4;  // rows per wave, 1 KiB slices per batch
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kLinMaxX / 2];
+  constexpr int RPW = 2, CB = 2;  // rows per wave, 1 KiB slices per batch
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // MB x K, K * MB * 2 <= kLinMaxX
   // the wave index is uniform: row bases stay scalar, loads take a 32-bit lane offset
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // x rows into LDS (row pitch K), 16 bytes per thread and step
-  for (int e = 8 * int(threadIdx.x); e < MB * a.K; e += 8 * 512) {
+  for (int e = 8 * int(threadIdx.x); e < MB * a.K; e += 8 * 64 * kLinWaves) {
     const int m = e / a.K, k = e - m * a.K;
     *reinterpret_cast<txd::u32x4 *>(xs + e) =
         m < a.M ? *reinterpret_cast<const txd::u32x4 *>(a.x + int64_t(m) * a.ldx + k) : txd::u32x4{0, 0, 0, 0};
   }
   __syncthreads();
-  const int row0 = (int(blockIdx.x) * 8 + wave) * RPW;
+  const int row0 = (int(blockIdx.x) * kLinWaves + wave) * RPW;
   if (row0 >= a.N) return;  // whole wave, after the only barrier
   const int nslices = (a.K + 1023) / 1024;
   float acc[RPW][MB];
@@ -366,8 +371,8 @@ __device__ __forceinline__ void gemv_lin(const tx_gemv_args &a) {
 
 // Streaming VALU kernels for M = 1: tx_gemv_fp8_<w format>_lin_m1 (at M = 2 the
 // MFMA kernel is faster: 17.4 against ~16 us at 14336 x 4096).
-#define TX_GEMV_LIN(NAME, FMT, MB)                                                               \
-  TX_KERNEL void __launch_bounds__(512) tx_gemv_fp8_##NAME##_lin_m##MB(const tx_gemv_args a) {   \
+#define TX_GEMV_LIN(NAME, FMT, MB)                                                                      \
+  TX_KERNEL void __launch_bounds__(64 * kLinWaves, 8) tx_gemv_fp8_##NAME##_lin_m##MB(const tx_gemv_args a) { \
     gemv_lin<FMT, MB>(a);                                                                        \
   }
 TX_GEMV_LIN(e5m2, 2, 1)
