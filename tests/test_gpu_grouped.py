@@ -122,6 +122,27 @@ def test_grouped_large_big_tiles(tx, oracle, dev):
             check_close(got[r:r + 1], r32, r16, FP8_TOL)
 
 
+@pytest.mark.parametrize("fa,fb", [(1, 1), (2, 1)])
+def test_grouped_persistent_uneven(tx, oracle, dev, fa, fb):
+    """Groups of uneven, empty and non-multiple-of-256 sizes with enough
+    256 x 256 tiles for the persistent kernel (each workgroup walks the real
+    tiles of every group): every row of every group against the oracle, the
+    rows before and after the groups untouched."""
+    g = np.random.default_rng(30 + fa)
+    sizes = [300, 0, 17, 1500, 255, 900]
+    M, off, aq, bq, sa, sb = _grouped_case(g, sizes, 8192, 512, fa, fb, lead=40, tail=70)
+    C = torch.full((M, 8192), 7.0, dtype=torch.bfloat16, device=dev)
+    _run_grouped(tx, dev, aq, bq, sa, sb, off, fa, fb, out=C)
+    got = _bits(C)
+    seven = np.uint16(0x40E0)
+    assert np.all(got[:40] == seven) and np.all(got[M - 70:] == seven)
+    for p in range(len(sizes)):
+        r0, r1 = int(off[p]), int(off[p + 1])
+        if r1 > r0:
+            r32, r16 = oracle.gemm_fp8_scaled_rows(aq[r0:r1], bq[p], sa[r0:r1], sb[p], 0, r1 - r0, fa, fb)
+            check_close(got[r0:r1], r32, r16, FP8_TOL)
+
+
 def test_single_group_equals_plain_product(tx, dev):
     """One group over all rows runs the plain product's 256 x 256 tile with
     the same K order: bit-identical output."""

@@ -717,6 +717,17 @@ static tx_status dot_fp8_grouped_impl(const char *what, const void *A, tx_dtype 
     TX_TRY(launch(fn, 1, 1, 256, s, &q, sizeof q, "tx_gemm_fp8_grouped_prefix"));
   }
   char kname[80];
+  // 256 x 256 tiles of a grouped product without an epilogue: the
+  // persistent kernel (one workgroup per CU walking the real tiles, whose
+  // count it reads from the prefix) when K is a whole number (>= 2) of
+  // 128-byte steps and C rows are 16-byte aligned.
+  if (grouped && big && !e.on() && K % 128 == 0 && K >= 256 && N % 8 == 0 && aligned(C, 16) && ldc % 8 == 0 &&
+      ((M - 1) * ldc + N) * 2 < (int64_t(1) << 31)) {
+    std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped_persist", fa, fb);
+    TX_TRY(get_kernel(CodeObject::GemmFp8, kname, &fn));
+    return launch(fn, unsigned(std::min<int64_t>(mtiles * tiles_n, cus)), 1, 64 * kPersistWaves, s, &q, sizeof q,
+                  kname);
+  }
   if (trans) std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped_t", fa, fb);
   else std::snprintf(kname, sizeof kname, "tx_gemm_fp8_%s_%s_grouped%s%s", fa, fb, e.on() ? "_epi" : "",
                      big ? "" : "_n128");

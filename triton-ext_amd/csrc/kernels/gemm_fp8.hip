@@ -49,9 +49,12 @@ TX_GEMM_FP8_FAST(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 // number (>= 2) of 128-byte steps, N a multiple of 8 and C 16-byte aligned.
 #include "gemm_persist.h"
 
-#define TX_GEMM_FP8_PERSIST(FA, FB, ELA, ELB)                                                            \
-  TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_##FA##_##FB##_fast_persist(const tx_gemm_args a) { \
-    gemm_persist<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>>(a);                                               \
+#define TX_GEMM_FP8_PERSIST(FA, FB, ELA, ELB)                                                               \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_##FA##_##FB##_fast_persist(const tx_gemm_args a) {    \
+    gemm_persist<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>>(a);                                                  \
+  }                                                                                                         \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_fp8_##FA##_##FB##_grouped_persist(const tx_grouped_args q) { \
+    gemm_persist<GemmCfg<ELA, ELB, 256, 256, 2, 2, 16>, OUT_BF16, true>(q.g, &q);                            \
   }
 
 TX_GEMM_FP8_PERSIST(e4m3fn, e4m3fn, EL_E4M3, EL_E4M3)

@@ -54,8 +54,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, in
 }
 }  // namespace persist
 
-template <class C, int OUT = OUT_BF16>
-__device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
+// GROUPED: the tiles of a grouped product (tx_grouped_args with offsets;
+// the m-tile prefix already written by tx_gemm_fp8_grouped_prefix), a the
+// shared fields q->g: tile t of the workgroup is (problem p, m tile, n tile)
+// of expert p's rows offsets[p] .. offsets[p + 1] of A, C and scale_a against
+// B + p stride_b and scale_b + p stride_sb.
+template <class C, int OUT = OUT_BF16, bool GROUPED = false>
+__device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_grouped_args *q = nullptr) {
   using namespace fast;
   static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "bf16 output, or fp16 out of 16-bit operands");
   constexpr int NW = persist::kWaves;
@@ -66,7 +71,9 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
   constexpr bool ROWCOL = C::FP8;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
-  const int total = a.tiles_m * a.tiles_n;
+  // m tiles: the grouped product's real count is only on the device
+  const int tiles_m = GROUPED ? q->tile_prefix[q->groups] : a.tiles_m;
+  const int total = tiles_m * a.tiles_n;
   const int G = int(gridDim.x);
   const int w = int(blockIdx.x);
   const int T = w < total ? (total - w + G - 1) / G : 0;  // tiles of this workgroup
@@ -94,8 +101,44 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
   const uint32_t ld8[2] = {8u * lda_b, 8u * ldb_b};
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
-  auto coords = [&](int t, int *tm, int *tn) {
-    tile_coords(w + t * G, a.tiles_n, a.tiles_m, min(8, a.tiles_n), tn, tm);  // transposed grid
+  // Tile t of the workgroup: its operands and output (for a grouped product,
+  // those of its problem) and its m / n tile.
+  struct TileDesc {
+    const uint8_t *A, *B;
+    uint8_t *out;  // C
+    const float *sa, *sb;
+    int rows, tm, tn;
+  };
+  auto desc = [&](int t) {
+    TileDesc d;
+    int vm;
+    tile_coords(w + t * G, a.tiles_n, tiles_m, min(8, a.tiles_n), &d.tn, &vm);  // transposed grid
+    d.A = static_cast<const uint8_t *>(a.A);
+    d.B = static_cast<const uint8_t *>(a.B);
+    d.out = static_cast<uint8_t *>(a.C);
+    d.sa = a.scale_a;
+    d.sb = a.scale_b;
+    d.rows = a.M;
+    d.tm = vm;
+    if constexpr (GROUPED) {
+      const int32_t *Tp = q->tile_prefix;
+      int lo = 0, hi = q->groups - 1;  // the last problem p with Tp[p] <= vm
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (Tp[mid] <= vm) lo = mid;
+        else hi = mid - 1;
+      }
+      const int r1 = min(max(q->offsets[lo + 1], 0), a.M);
+      const int r0 = min(max(q->offsets[lo], 0), r1);
+      d.A += int64_t(r0) * a.lda;
+      d.B += int64_t(lo) * q->stride_b;
+      d.out += int64_t(r0) * a.ldc * 2;
+      d.sa += r0;
+      d.sb += int64_t(lo) * q->stride_sb;
+      d.rows = r1 - r0;
+      d.tm = vm - Tp[lo];
+    }
+    return d;
   };
 
   // Load cursor of one operand: the step it is at and the buffer resource of
@@ -108,10 +151,9 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
   auto set_tile = [&](Cursor &c, auto op_tag) {
     constexpr int op = decltype(op_tag)::value;
     if (c.t < T) {
-      int tm, tn;
-      coords(c.t, &tm, &tn);
-      c.rs = op == 0 ? persist::tile_rsrc(a.A, tm * 256, a.M, lda_b, kb_end)
-                     : persist::tile_rsrc(a.B, tn * 256, a.N, ldb_b, kb_end);
+      const TileDesc d = desc(c.t);
+      c.rs = op == 0 ? persist::tile_rsrc(d.A, d.tm * 256, d.rows, lda_b, kb_end)
+                     : persist::tile_rsrc(d.B, d.tn * 256, a.N, ldb_b, kb_end);
     } else {
       c.rs = make_rsrc(op == 0 ? a.A : a.B, 0u);
     }
@@ -235,19 +277,18 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
   using VmLast = std::integral_constant<int, BLKA + kScaleLoads>;
   static_assert(BLKA + kScaleLoads < 64, "vmcnt range");
 
-  // C as a buffer: a store whose row or column block lies past M / N gets an
-  // offset past the range and is dropped (N is a multiple of 8 and rows of
-  // C are 16-byte aligned, so a 16-byte column block is wholly in or out).
-  const __amdgpu_buffer_rsrc_t crs =
-      make_rsrc(a.C, uint32_t((int64_t(a.M - 1) * a.ldc + a.N) * 2));
   // Staging: wave w owns bytes 8 KiB w .. +8 KiB of the slot its last step's
   // A s+3 loads would have filled (the same bytes those loads fill once the
   // epilogue is done, so no other wave ever touches them): 32 rows x 256
   // bytes, 16-byte chunk c of row r at c ^ (r % 16).
   for (int t = 0; t < T; ++t) {
-    int tm, tn;
-    coords(t, &tm, &tn);
-    const int m0 = tm * 256, n0 = tn * 256;
+    const TileDesc d = desc(t);
+    const int m0 = d.tm * 256, n0 = d.tn * 256;
+    // C as a buffer: a store whose row or column block lies past M / N gets
+    // an offset past the range and is dropped (N is a multiple of 8 and rows
+    // of C are 16-byte aligned, so a 16-byte column block is wholly in or
+    // out).
+    const __amdgpu_buffer_rsrc_t crs = make_rsrc(d.out, uint32_t((int64_t(d.rows - 1) * a.ldc + a.N) * 2));
     if (t == 0) step(std::true_type{}, VmStep{}, std::false_type{});
     else step(std::true_type{}, VmAfterEpi{}, std::false_type{});
     for (int k = 1; k < KS - 1; ++k) step(std::false_type{}, VmStep{}, std::false_type{});
@@ -265,14 +306,14 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
       const int nl = n0 + wn * TN + 4 * fg;
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        const float *ps = a.scale_a + min(m0 + wm * TM + fm * 32 + frow, a.M - 1);
+        const float *ps = d.sa + min(m0 + wm * TM + fm * 32 + frow, d.rows - 1);
         asm volatile("global_load_dword %0, %1, off" : "=v"(sav[fm]) : "v"(ps) : "memory");
       }
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const float *ps = a.scale_b + min(nl + 32 * fn + 8 * jj, a.N - 4);
+          const float *ps = d.sb + min(nl + 32 * fn + 8 * jj, a.N - 4);
           asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(sb4[fn][jj]) : "v"(ps) : "memory");
         }
     }
@@ -329,7 +370,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a) {
         const int r = 4 * i + srow;
         const txd::u32x4 w = *reinterpret_cast<const txd::u32x4 *>(stg + r * 256 + ((schunk ^ (r & 15)) << 4));
         const int m = m0 + wm * TM + fm * 32 + r;
-        const uint32_t voff = (m >= a.M || coloff == kOob) ? kOob : uint32_t(m) * uint32_t(a.ldc) * 2u + coloff;
+        const uint32_t voff = (m >= d.rows || coloff == kOob) ? kOob : uint32_t(m) * uint32_t(a.ldc) * 2u + coloff;
         __builtin_amdgcn_raw_buffer_store_b128(w, crs, voff, 0, 0);
       }
     });
