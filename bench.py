@@ -115,6 +115,8 @@ def parse():
     p.add_argument("--mfma-summary", nargs=2, metavar=("WINDOWS_JSON", "MFMA_CSV"),
                    help="print MFMA busy and clock per GEMM workload from a --windows run "
                         "counted with SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, SQ_BUSY_CYCLES")
+    p.add_argument("--lds-summary", nargs=2, metavar=("WINDOWS_JSON", "LDS_CSV"),
+                   help="print the LDS counter table of a --pmc run of the bench made with --windows")
     return p.parse_args()
 
 
@@ -602,6 +604,38 @@ def mfma_summary(windows_json, mfma_csv):
 
 XCDS = 8
 SIMDS = 1024  # 256 CUs x 4 SIMDs
+LDS_COUNTERS = ("SQ_INSTS_LDS", "SQ_LDS_IDX_ACTIVE", "SQ_LDS_ADDR_CONFLICT", "SQ_LDS_BANK_CONFLICT",
+                "GRBM_GUI_ACTIVE")
+
+
+def lds_summary(windows_json, lds_csv):
+    """LDS counters per workload and kernel: how much of the cycles the LDS
+    spends on indexed operations goes to same-address conflicts (atomics
+    from many lanes on one bin) and to bank conflicts."""
+    with open(windows_json) as f:
+        meta = json.load(f)
+    rows = {}
+    for d, w in _assign(meta["windows"], _dispatches(lds_csv, set(LDS_COUNTERS))):
+        if d["c"].get("SQ_INSTS_LDS", 0.0) <= 0.0:
+            continue
+        rows.setdefault((w["workload"], _short(d["kernel"]), d["grid"]), []).append(d)
+    order = {w["workload"]: i for i, w in enumerate(meta["windows"])}
+    print(f"build digest: {meta['digest']}")
+    print()
+    print("| workload | kernel | grid | dispatches | duration us | SQ_INSTS_LDS | SQ_LDS_IDX_ACTIVE "
+          "| SQ_LDS_ADDR_CONFLICT | SQ_LDS_BANK_CONFLICT | address conflict / LDS active "
+          "| bank conflict / LDS active | LDS active / (GRBM_GUI_ACTIVE per XCD x 256 CUs) |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|")
+    for key in sorted(rows, key=lambda k: (order.get(k[0], 1 << 30), k[1], k[2])):
+        ds = rows[key]
+        m = {c: sum(d["c"].get(c, 0.0) for d in ds) / len(ds) for c in LDS_COUNTERS}
+        dur = sum(d["t1"] - d["t0"] for d in ds) / len(ds)
+        act = m["SQ_LDS_IDX_ACTIVE"]
+        cyc = m["GRBM_GUI_ACTIVE"] / XCDS * 256
+        print(f"| {key[0]} | {key[1]} | {key[2]} | {len(ds)} | {dur / 1e3:.1f} | {m['SQ_INSTS_LDS']:.4g} "
+              f"| {act:.4g} | {m['SQ_LDS_ADDR_CONFLICT']:.4g} | {m['SQ_LDS_BANK_CONFLICT']:.4g} "
+              f"| {m['SQ_LDS_ADDR_CONFLICT'] / act if act else 0:.1%} "
+              f"| {m['SQ_LDS_BANK_CONFLICT'] / act if act else 0:.1%} | {act / cyc if cyc else 0:.1%} |")
 
 
 def trace_summary(windows_json, trace_csv):
@@ -664,6 +698,9 @@ def main():
         return
     if args.mfma_summary:
         mfma_summary(*args.mfma_summary)
+        return
+    if args.lds_summary:
+        lds_summary(*args.lds_summary)
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary)
