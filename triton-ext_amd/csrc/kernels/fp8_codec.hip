@@ -281,10 +281,62 @@ __device__ __forceinline__ typename Unit<B>::T words_unit(const uint32_t (&w)[4]
   else return txd::u32x4{w[0], w[1], w[2], w[3]};
 }
 
+// fp8 -> bf16 / fp16 for the four codes of one word: every fp8 value is a
+// bf16 and an fp16 value, so no rounding mode matters.  Finite codes go
+// through gfx950's packed fp8 -> fp32 conversion (exact) and keep the top
+// half of the fp32 bits (bf16) or convert to fp16 (exact, so truncation
+// is as good as rounding); e5m2 -> fp16 is byte placement (e5m2 is the top
+// byte of fp16).  Inf and NaN codes are then set to the encoders' results:
+// NaN to the format's NaN code with the sign, e5m2 Inf to Inf, or to the
+// largest finite value when saturating.  Out: o[0] = values 0, 1, o[1] =
+// values 2, 3.
+template <int SRC, int DST, bool SAT>
+__device__ __forceinline__ void fp8x4_to_16(uint32_t w, uint32_t (&o)[2]) {
+  using FD = Fp8Format<DST>;
+  if constexpr (SRC == E5M2 && DST == F16) {
+    o[0] = __builtin_amdgcn_perm(0u, w, 0x010c000cu);  // b1 << 24 | b0 << 8
+    o[1] = __builtin_amdgcn_perm(0u, w, 0x030c020cu);  // b3 << 24 | b2 << 8
+  } else {
+    const auto lo = SRC == E4M3FN ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false)
+                                  : __builtin_amdgcn_cvt_pk_f32_bf8(int(w), false);
+    const auto hi = SRC == E4M3FN ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true)
+                                  : __builtin_amdgcn_cvt_pk_f32_bf8(int(w), true);
+    if constexpr (DST == BF16) {
+      o[0] = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u);
+      o[1] = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u);
+    } else {
+      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo[0], lo[1]));
+      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(hi[0], hi[1]));
+    }
+  }
+  constexpr uint32_t SPEC = SRC == E4M3FN ? 0x7Fu : 0x7Cu;  // magnitude bits set in Inf / NaN codes
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t c = (w >> (8 * j)) & 0xFFu;
+    const uint32_t mag = c & 0x7Fu;
+    const uint32_t inf = SAT ? FD::MAXC : FD::OVF;
+    const uint32_t sv = ((SRC == E5M2 && mag == 0x7Cu) ? inf : FD::NANC) | ((c & 0x80u) << 8);
+    const int sh = 16 * (j & 1);
+    uint32_t &r = o[j >> 1];
+    r = (mag & SPEC) == SPEC ? (r & ~(0xFFFFu << sh)) | (sv << sh) : r;
+  }
+}
+
 // One unit of E elements: the source unit's words in, the destination
 // unit's words out.
 template <int SRC, int DST, int MODE, bool SAT, int E>
 __device__ __forceinline__ void cvt_unit(const uint32_t (&w)[4], uint32_t (&o)[4]) {
+  if constexpr ((SRC == E4M3FN || SRC == E5M2) && (DST == BF16 || DST == F16)) {
+    static_assert(E == 8, "8 codes in, 16 bytes out");
+    uint32_t h[2];
+    fp8x4_to_16<SRC, DST, SAT>(w[0], h);
+    o[0] = h[0];
+    o[1] = h[1];
+    fp8x4_to_16<SRC, DST, SAT>(w[1], h);
+    o[2] = h[0];
+    o[3] = h[1];
+    return;
+  }
   constexpr int S = Bytes<SRC>::v, D = Bytes<DST>::v;
   constexpr uint32_t SM = S == 4 ? 0xFFFFFFFFu : (1u << (8 * S)) - 1u;
   constexpr uint32_t DM = D == 4 ? 0xFFFFFFFFu : (1u << (8 * D)) - 1u;
