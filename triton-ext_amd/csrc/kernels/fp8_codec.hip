@@ -2,9 +2,13 @@
 //
 // Streaming kernels: every load is a 128-bit, wave-contiguous global load and
 // every store is wave-contiguous, so each wave instruction moves whole cache
-// lines.  The conversion itself is integer bit manipulation on the fp32
-// encoding (no hardware fp8 convert instruction is used), so the rounding,
-// saturation and NaN rules are exactly the ones written here:
+// lines.  The conversion from or to fp32 is integer bit manipulation on the
+// fp32 encoding, so the rounding, saturation and NaN rules are exactly the
+// ones written here.  Between bf16 / fp16 and fp8 (round to nearest even,
+// and every fp8 -> 16-bit decode) the finite values take gfx950's packed
+// fp8 conversions, which give the same codes as these encoders for every
+// 16-bit source value, and the special values are set explicitly to what
+// the encoders give (fp8x4_to_16, f16x4_to_fp8_rtne):
 //
 //  encode (fp32 -> fp8), round to nearest even:
 //   * normal range (|x| >= 2^(1-bias)): re-bias the fp32 exponent field to
@@ -322,10 +326,69 @@ __device__ __forceinline__ void fp8x4_to_16(uint32_t w, uint32_t (&o)[2]) {
   }
 }
 
+// bf16 / fp16 -> fp8, round to nearest even, for the four values of two
+// words: the values widen to fp32 exactly and, clamped to the format's
+// largest finite value, take gfx950's packed conversion, which returns
+// encode_rtne's codes for every clamped bf16 / fp16 value (the conversion
+// tests run every 16-bit source code).  What clamping changes is set explicitly, as
+// encode_rtne has it: NaN to the NaN code with the sign; without
+// saturation, magnitudes that round past the largest finite value (above
+// 464 for e4m3fn: the tie at 464 goes to the even 448; from 61440 up for
+// e5m2: the tie between 57344 and 65536 goes to the even 65536, which
+// overflows) to the overflow code (NaN / Inf) with the sign.
+template <int SRC, int DST, bool SAT>
+__device__ __forceinline__ uint32_t f16x4_to_fp8_rtne(uint32_t w0, uint32_t w1) {
+  using F = Fp8Format<DST>;
+  float x[4];
+  if constexpr (SRC == BF16) {
+    x[0] = __uint_as_float(w0 << 16);
+    x[1] = __uint_as_float(w0 & 0xFFFF0000u);
+    x[2] = __uint_as_float(w1 << 16);
+    x[3] = __uint_as_float(w1 & 0xFFFF0000u);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a = __builtin_bit_cast(h2, w0), b = __builtin_bit_cast(h2, w1);
+    x[0] = float(a[0]);
+    x[1] = float(a[1]);
+    x[2] = float(b[0]);
+    x[3] = float(b[1]);
+  }
+  constexpr float FMAX = DST == E4M3FN ? 448.0f : 57344.0f;
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(x[i], -FMAX), FMAX);
+  int p;
+  if constexpr (DST == E4M3FN) {
+    p = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+    p = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], p, true);
+  } else {
+    p = __builtin_amdgcn_cvt_pk_bf8_f32(c[0], c[1], 0, false);
+    p = __builtin_amdgcn_cvt_pk_bf8_f32(c[2], c[3], p, true);
+  }
+  uint32_t code = uint32_t(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t s = (__float_as_uint(x[i]) >> 24) & 0x80u;
+    const float m = fabsf(x[i]);
+    const bool ovf = !SAT && (DST == E4M3FN ? m > 464.0f : m >= 61440.0f);
+    const bool nan = x[i] != x[i];
+    const uint32_t v = (nan ? F::NANC : F::OVF) | s;
+    code = (nan || ovf) ? (code & ~(0xFFu << (8 * i))) | (v << (8 * i)) : code;
+  }
+  return code;
+}
+
 // One unit of E elements: the source unit's words in, the destination
 // unit's words out.
 template <int SRC, int DST, int MODE, bool SAT, int E>
 __device__ __forceinline__ void cvt_unit(const uint32_t (&w)[4], uint32_t (&o)[4]) {
+  if constexpr ((SRC == BF16 || SRC == F16) && (DST == E4M3FN || DST == E5M2) && MODE == 0) {
+    static_assert(E == 8, "16 bytes in, 8 codes out");
+    o[0] = f16x4_to_fp8_rtne<SRC, DST, SAT>(w[0], w[1]);
+    o[1] = f16x4_to_fp8_rtne<SRC, DST, SAT>(w[2], w[3]);
+    o[2] = o[3] = 0u;
+    return;
+  }
   if constexpr ((SRC == E4M3FN || SRC == E5M2) && (DST == BF16 || DST == F16)) {
     static_assert(E == 8, "8 codes in, 16 bytes out");
     uint32_t h[2];
