@@ -93,11 +93,13 @@ def test_bf16_narrow_tile_and_split_k(tx, oracle, dev, M, N, K):
     check_close(_np_bits(C), r32, r16, BF16_TOL)
 
 
-@pytest.mark.parametrize("K", [1003, 1002, 1004])
+@pytest.mark.parametrize("K", [1003, 1001, 1002, 1004])
 def test_bf16_padded_fast_path(tx, oracle, dev, K):
-    """Rows not 16-byte aligned in a product of >= 2^30 multiply-adds: the
-    operands are copied into zero-padded rows and take the fast path (row
-    lengths of 2006, 2004 and 2008 bytes: source loads of 2, 4 and 8 bytes)."""
+    """Rows not 16-byte aligned in a product of >= 2^30 multiply-adds.  Row
+    lengths of 2006 and 2002 bytes (2-byte aligned rows): the operands are
+    copied into zero-padded rows and take the fast path (source loads of 2
+    bytes); 2004 and 2008 bytes (4-byte aligned): the fast path reads them
+    in place, the last chunk of each row fetched as its last 16 bytes."""
     import workloads
     M, N = 1100, 1040
     A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=77)

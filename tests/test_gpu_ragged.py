@@ -1,0 +1,108 @@
+"""GPU parity of 16-bit dots whose operands the fast path reads in place
+although their rows are not whole 16-byte chunks apart or long (rows 4-byte
+aligned, any K of at least two 64-element steps): the persistent tile
+(tx_gemm_*_persist_kt) for products of at least one 256 x 256 tile per CU,
+the 256 x 128 tile with K split otherwise.
+
+The last chunk of each row is fetched as the row's last 16 bytes and its
+repeated bytes are cleared in registers, so the cases put that chunk at
+every kind of place in the last K step: its first chunk (the lane offsets
+then need the shifted scalar offset to stay non-negative), a middle one,
+the last one, and none (whole chunks past the row end only).  Integer-valued
+operands make every fp32 sum exact, so the outputs must equal the oracle's
+rounding bit for bit: a repeated or dropped K position changes a sum.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_gemm import BF16_TOL, _np_bits, check_close
+
+pytestmark = pytest.mark.gpu
+
+BF16, F16 = 3, 6
+_TD = {BF16: torch.bfloat16, F16: torch.float16}
+
+
+def _int_codes(g, shape, fmt):
+    """Integers in [-3, 3] as bf16 / fp16 bits (exact in both formats)."""
+    x = g.integers(-3, 4, size=shape).astype(np.float32)
+    if fmt == F16:
+        return x.astype(np.float16).view(np.uint16)
+    return (x.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def _dev(bits, fmt, dev, pad=0):
+    """bits (rows x K) on the device, rows `pad` elements longer than K."""
+    rows, k = bits.shape
+    buf = np.zeros((rows, k + pad), np.uint16)
+    buf[:, :k] = bits
+    t = torch.from_numpy(buf.view(np.int16)).to(dev).view(_TD[fmt])
+    return t[:, :k]
+
+
+def _exact(tx, oracle, dev, M, N, K, fmt=BF16, out_fmt=BF16, pad_a=0, pad_b=0, seed=0):
+    g = np.random.default_rng(seed)
+    A = _int_codes(g, (M, K), fmt)
+    B = _int_codes(g, (N, K), fmt)
+    C = _np_bits(tx.dot(_dev(A, fmt, dev, pad_a), _dev(B, fmt, dev, pad_b), out_dtype=_TD[out_fmt]))
+    _, r16 = oracle.gemm16_rows(A, B, 0, M, fmt, out_fmt=out_fmt)
+    bad = np.argwhere(C != r16)
+    assert bad.size == 0, (len(bad), bad[:5].tolist())
+
+
+# K bytes 260 (partial chunk = chunk 0 of the last step), 500 (chunk 7),
+# 400 (chunks past the row end, none partial), 2060 (chunk 0), 2200 (chunk 1)
+@pytest.mark.parametrize("K", [130, 250, 200, 1030, 1100])
+def test_ragged_persistent_exact(tx, oracle, dev, K):
+    # 272 tiles: 16 workgroups walk two (the operand stream crosses tiles)
+    _exact(tx, oracle, dev, 4352, 4096, K, seed=K)
+
+
+@pytest.mark.parametrize("fmt,out_fmt", [(F16, F16), (F16, BF16), (BF16, F16)])
+def test_ragged_persistent_formats(tx, oracle, dev, fmt, out_fmt):
+    _exact(tx, oracle, dev, 4196, 4168, 266, fmt, out_fmt, seed=fmt + out_fmt)
+
+
+def test_ragged_rows_whole_chunks(tx, oracle, dev):
+    """K a whole number of steps but rows 4-byte aligned (pitch K + 2): the
+    persistent tile and the 256 x 128 one read them in place."""
+    _exact(tx, oracle, dev, 4352, 4096, 512, pad_a=2, pad_b=6, seed=5)
+    _exact(tx, oracle, dev, 600, 1000, 512, pad_a=2, pad_b=2, seed=6)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 500, 4100),   # 13 K splits, the last one ragged
+                                   (600, 1000, 1030),
+                                   (257, 501, 2050),
+                                   (255, 257, 130)])   # two K steps
+def test_ragged_narrow_tile_split_k(tx, oracle, dev, M, N, K):
+    _exact(tx, oracle, dev, M, N, K, seed=M + K)
+
+
+def test_ragged_strided_unaligned_out(tx, oracle, dev):
+    """C a view 3 elements into a buffer with row pitch N + 1 (rows 2-byte
+    aligned): every output lands in its row and the rest keeps its contents."""
+    M, N, K = 4352, 4096, 1100
+    g = np.random.default_rng(9)
+    A = _int_codes(g, (M, K), BF16)
+    B = _int_codes(g, (N, K), BF16)
+    flat = torch.full((M * (N + 1) + 8,), 0x7777, dtype=torch.int16, device=dev)
+    out = flat[3:3 + M * (N + 1)].view(M, N + 1)[:, :N].view(torch.bfloat16)
+    tx.dot(_dev(A, BF16, dev), _dev(B, BF16, dev), out=out)
+    allb = flat.cpu().numpy().view(np.uint16)
+    grid = allb[3:3 + M * (N + 1)].reshape(M, N + 1)
+    assert np.all(allb[:3] == 0x7777) and np.all(allb[3 + M * (N + 1):] == 0x7777)
+    assert np.all(grid[:, N] == 0x7777)
+    _, r16 = oracle.gemm16_rows(A, B, 0, M, BF16)
+    assert np.array_equal(grid[:, :N], r16)
+
+
+def test_ragged_normal_values(tx, oracle, dev):
+    """Normal-distributed operands at the ragged config shape's K, full
+    output against the oracle's fp64 sums (the tolerances of the GEMM tests)."""
+    import workloads
+    M, N, K = 4352, 4104, 4100
+    A, B = workloads.bf16_gemm_input(M, N, K, seed_stream=12)
+    C = _np_bits(tx.dot(_dev(A, BF16, dev), _dev(B, BF16, dev)))
+    r32, r16 = oracle.gemm16_rows(A, B, 0, M, BF16)
+    check_close(C, r32, r16, BF16_TOL)

@@ -90,6 +90,17 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
   return (M - 1) * lda_b + k_b < lim && (N - 1) * ldb_b + k_b < lim;
 }
 
+// 16-bit operands the fast path also reads in place (fast::KTail in
+// gemm_fast.h, the persistent and the 256 x 128 tiles): rows 4-byte
+// aligned, and a row length that is not a whole number of 16-byte chunks
+// only with at least two K steps.
+bool fast16_ragged_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t k_b, int64_t M,
+                      int64_t N) {
+  if (!aligned(A, 16) || !aligned(B, 16) || lda_b % 4 || ldb_b % 4 || (k_b % 16 && k_b <= 128)) return false;
+  const int64_t lim = int64_t(1) << 31;
+  return (M - 1) * lda_b + k_b + 16 < lim && (N - 1) * ldb_b + k_b + 16 < lim;
+}
+
 // Launch the fast path (kernel `base`, or `base`_n128): 256x256 tiles while
 // they give at least one tile per CU (see kStripMaxN for a narrow column
 // tail); otherwise 256x128 tiles, and when those
@@ -102,15 +113,18 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 // separate, second fast-path product (few tiles, so 256x128 with K split).
 constexpr int64_t kStripMaxN = 64;
 
-// The persistent 4-wavefront kernel (`base`_persist, gemm_persist.h) takes
-// the 256 x 256 products it was built for: no fused epilogue or K split, K a
-// whole number (>= 2) of 128-byte steps, N a multiple of 8, C rows 16-byte
-// aligned and addressable with 32-bit byte offsets.
-bool persist_ok(const tx_gemm_args &args, int64_t k_bytes) {
-  if (args.epi || args.splits > 1 || k_bytes % 128 != 0 || k_bytes < 256 || args.N % 8 != 0) return false;
-  if (!aligned(args.C, 16) || args.ldc % 8 != 0) return false;
+// The persistent 4-wavefront kernel (gemm_persist.h) takes the 256 x 256
+// products it was built for: no fused epilogue or K split, at least two
+// 128-byte K steps, N a multiple of 8, C addressable with 32-bit byte
+// offsets.  `base`_persist: K a whole number of steps, C rows 16-byte
+// aligned; `base`_persist_kt (16-bit operands, es == 2): any K and any C
+// alignment.  Returns the kernel suffix, or nullptr.
+const char *persist_variant(const tx_gemm_args &args, int64_t k_bytes, int es) {
+  if (args.epi || args.splits > 1 || k_bytes < 256 || args.N % 8 != 0) return nullptr;
   const int64_t c_bytes = ((int64_t(args.M) - 1) * args.ldc + args.N) * 2;
-  return c_bytes < (int64_t(1) << 31);
+  if (c_bytes + 16 >= (int64_t(1) << 31)) return nullptr;
+  if (k_bytes % 128 == 0 && aligned(args.C, 16) && args.ldc % 8 == 0) return "_persist";
+  return es == 2 && aligned(args.C, 2) ? "_persist_kt" : nullptr;
 }
 
 tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_gemm_args &args,
@@ -121,8 +135,9 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
   // 256 x 256 tiles: the persistent kernel when it applies, else one
   // workgroup per tile
   auto launch_big = [&](tx_gemm_args &ga) -> tx_status {
-    if (persist && persist_ok(ga, k_bytes)) {
-      std::snprintf(kname, sizeof kname, "%s_persist", base);
+    const char *pv = persist ? persist_variant(ga, k_bytes, es) : nullptr;
+    if (pv) {
+      std::snprintf(kname, sizeof kname, "%s%s", base, pv);
       ga.tiles_m = int32_t((ga.M + 255) / 256);
       ga.tiles_n = int32_t((ga.N + 255) / 256);
       ga.group_m = std::min<int32_t>(kGroupM, ga.tiles_m);
@@ -131,6 +146,8 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
       const int64_t grid = std::min<int64_t>(int64_t(ga.tiles_m) * ga.tiles_n, cus);
       return launch(fn, unsigned(grid), 1, 64 * kPersistWaves, s, &ga, sizeof ga, kname);
     }
+    // a ragged K (16-bit operands): the persistent and the 256 x 128 tiles only
+    if (k_bytes % 16 != 0) return TX_UNSUPPORTED;
     std::snprintf(kname, sizeof kname, "%s", base);
     return launch_gemm(kname, co, ga, 256, 256, s, 64 * kFastWaves);
   };
@@ -314,6 +331,13 @@ static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda
   if (layout == TX_B_KN) args.ldb = K;  // K = 0: B is never read
   if (fast_ok(A, lda * 2, B, args.ldb * 2, K * 2, M, N))
     return launch_fast(base, reduce, CodeObject::GemmBf16, args, K * 2, 2, s, true);
+  if (fast16_ragged_ok(A, lda * 2, B, args.ldb * 2, K * 2, M, N)) {
+    // TX_UNSUPPORTED (nothing launched): a shape only the 256 x 256 tile takes
+    tx_gemm_args direct = args;
+    const tx_status st = launch_fast(base, reduce, CodeObject::GemmBf16, direct, K * 2, 2, s, true);
+    if (st != TX_UNSUPPORTED) return st;
+    clear_error();
+  }
   {
     tx_gemm_args padded = args;
     const tx_status st = launch_padded(base, reduce, "tx_gemm_bf16_pad_rows", CodeObject::GemmBf16,

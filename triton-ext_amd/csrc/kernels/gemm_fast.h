@@ -1,5 +1,7 @@
-// Fast-path GEMM body for aligned operands (both K-contiguous, 16-byte
-// aligned rows, K * element size a multiple of 16 bytes): 256 x 256 tile,
+// Fast-path GEMM body for K-contiguous operands (16-byte aligned rows and
+// K * element size a multiple of 16 bytes; 16-bit operands in 256 x 128
+// tiles also with 4-byte aligned rows and any K of at least two steps, see
+// fast::KTail): 256 x 256 tile,
 // 8 wavefronts (two per SIMD), each owning a 128 x 64 block of C (64 x 64 in
 // the 256 x 128 variant).
 //
@@ -99,6 +101,48 @@ __host__ __device__ constexpr int spread_lo(int i, int n, int over) {
 }
 __host__ __device__ constexpr int spread_hi(int i, int n, int over) {
   return i >= over ? n : ((i + 1) * n) / over;
+}
+
+// Ragged K of 16-bit operands (rows 4-byte aligned, K bytes kb_end not a
+// whole number of 16-byte chunks, r = kb_end mod 16 > 0, at least two K
+// steps): the last chunk of each row, logical chunk cp of the last K step,
+// is fetched as the row's last 16 bytes [kb_end - 16, kb_end), so nothing
+// past the row is read; its first 16 - r bytes repeat the chunk before and
+// are cleared in both operands' fragments before that step's MFMAs (the
+// duplicated K positions then add 0 x 0, whatever the values).  The loads of
+// the last step take scalar offset - 16 and lane offset + 16 (+ r for the
+// partial chunk), which keeps every lane offset non-negative; chunks past
+// the row use an out-of-range offset and read as zero.
+struct KTail {
+  uint32_t keep[4];  // bytes of the partial chunk kept, per dword
+  int cp;            // the partial chunk of the last step; 8: none
+};
+__device__ __forceinline__ KTail make_ktail(uint32_t kb_end) {
+  KTail t;
+  const int clear = (kb_end & 15u) ? 16 - int(kb_end & 15u) : 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int nz = min(max(clear - 4 * d, 0), 4);
+    t.keep[d] = nz >= 4 ? 0u : (0xFFFFFFFFu << (8 * nz));
+  }
+  t.cp = (kb_end & 15u) ? int((kb_end & 127u) >> 4) : 8;
+  return t;
+}
+// Clear the repeated bytes in the fragments of K half h (16-bit operands:
+// lane l holds chunks 4h + 2g and 4h + 2g + 1 of the step, g = l / 32).
+template <int NF>
+__device__ __forceinline__ void ktail_clear(txd::i32x4 (&fr)[NF][2], int h, int g, const KTail &t) {
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const bool hit = 4 * h + 2 * g + e == t.cp;
+    int m[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) m[d] = hit ? int(t.keep[d]) : -1;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) fr[f][e][d] &= m[d];
+  }
 }
 }  // namespace fast
 
@@ -253,15 +297,37 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
   // whose chunk lies past the row end reads zeros; otherwise no chunk ever
   // does, and the load takes its per-lane offset as it is (no vector
   // instructions per load).
+  // A ragged K (fast::KTail) is served by the 256 x 128 tile with 16-bit
+  // operands (the 256 x 256 one has no registers to spare for it):
+  // the last step's offsets (klast = 0 with a single step, which the host
+  // never sends with a ragged K).
+  constexpr bool RAGGED = !C::FP8 && BN == 128;
+  const KTail kt = make_ktail(kb_end);
+  const uint32_t kb16 = kb_end & ~15u, kr = kb_end & 15u;
+  const uint32_t kbz = kr ? kb16 + 16u : kb_end;  // chunks from here on read as zero
+  const uint32_t klast = uint32_t(ksteps_all - 1) * kStep;
   auto load_op = [&](const Src &sr, int base, auto op_tag, auto j_tag, auto tail_tag) {
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     constexpr int blk = op == 0 ? BLKA : BLKB;
-    uint32_t voff = vo[op][j];
+    uint32_t voff = vo[op][j], so = sr.so;
     if constexpr (decltype(tail_tag)::value) {
-      if (sr.so + kch[j & 1] >= kb_end) voff = kOob;
+      const uint32_t cs = sr.so + kch[j & 1];  // the lane's chunk, in bytes from the row start
+      if constexpr (RAGGED) {
+        if (klast != 0u && sr.so == klast) {
+          // (the empty asm keeps the compiler from holding adjusted copies
+          // of every lane offset in registers across the K loop)
+          asm volatile("" : "+v"(voff));
+          so -= 16u;
+          voff = cs >= kbz ? kOob : voff + (cs == kb16 ? kr : 16u);
+        } else if (cs >= kb_end) {
+          voff = kOob;
+        }
+      } else {
+        if (cs >= kb_end) voff = kOob;
+      }
     }
     uint8_t *dst = lds + base + (blk * wave + j) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(sr.rs, (lds_void *)dst, 16, voff, sr.so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(sr.rs, (lds_void *)dst, 16, voff, so, 0, 0);
   };
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
@@ -390,6 +456,8 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
       for (int ks = 0; ks < ksteps; ++ks) {
         const int nt = st == 2 ? 0 : st + 1;
         const int ca = st * kStage, cb = ca + 256 * kStep, xa = nt * kStage, xb = xa + 256 * kStep;
+        const bool clear = RAGGED && decltype(tail)::value && kt.cp < 8 && kfirst + ks == ksteps_all - 1;
+        if (clear) ktail_clear<NF>(fr[0], 0, fg, kt);
         static_for<NM>([&](auto I) {
           constexpr int i = decltype(I)::value;
           mma(H0{}, I);
@@ -404,6 +472,7 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
         // the stage of step ks is free
         wait_and_barrier<ND>();
         __builtin_amdgcn_sched_barrier(0);
+        if (clear) ktail_clear<NF>(fr[1], 1, fg, kt);
         const Src srb = src(ks + 3, 1), sra = src(ks + 3, 0);
         static_for<NM>([&](auto I) {
           constexpr int i = decltype(I)::value;
@@ -441,6 +510,8 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
     int sa = 0, sb = 1;  // slots of A and B of step ks (uniform)
     for (int ks = 0; ks < ksteps; ++ks) {
       const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;  // step ks+1
+      const bool clear = RAGGED && decltype(tail)::value && kt.cp < 8 && kfirst + ks == ksteps_all - 1;
+      if (clear) ktail_clear<NF>(fr[0], 0, fg, kt);
       if constexpr (MX) {
         // this step's scales (loaded during the previous half) into place
 #pragma unroll
@@ -460,6 +531,7 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
       // ks+2, issued last, may still be in flight); the slots of step ks are free.
       wait_and_barrier<BLKA>();
       __builtin_amdgcn_sched_barrier(0);
+      if (clear) ktail_clear<NF>(fr[1], 1, fg, kt);
       load_scales(ks + 1, scn);  // MX: ahead of this half's DMA loads
       const Src srb = src(ks + 2, 1), sra = src(ks + 3, 0);
       static_for<NM>([&](auto I) {

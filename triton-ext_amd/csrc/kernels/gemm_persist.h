@@ -1,5 +1,7 @@
 // Persistent 4-wavefront GEMM for aligned operands whose K is a whole number
-// of 128-byte steps: one workgroup per CU walks its share of the 256 x 256
+// of 128-byte steps (KTAIL, 16-bit operands: rows 4-byte aligned, any K of
+// at least two steps, read as fast::KTail describes, and C rows of any
+// alignment): one workgroup per CU walks its share of the 256 x 256
 // tiles, and the LDS-DMA pipeline of gemm_fast.h runs as one continuous
 // stream of (tile, K step) pairs, so the first steps of the next tile are
 // loaded while the current one finishes and no tile pays a pipeline fill.
@@ -59,10 +61,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, in
 // shared fields q->g: tile t of the workgroup is (problem p, m tile, n tile)
 // of expert p's rows offsets[p] .. offsets[p + 1] of A, C and scale_a against
 // B + p stride_b and scale_b + p stride_sb.
-template <class C, int OUT = OUT_BF16, bool GROUPED = false>
+template <class C, int OUT = OUT_BF16, bool GROUPED = false, bool KTAIL = false>
 __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_grouped_args *q = nullptr) {
   using namespace fast;
   static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "bf16 output, or fp16 out of 16-bit operands");
+  static_assert(!KTAIL || (!C::FP8 && !GROUPED), "ragged K: 16-bit operands, one product");
   constexpr int NW = persist::kWaves;
   constexpr int TM = 128, TN = 128, FM = 4, FN = 4;
   constexpr int NM = FM * FN, NF = FM + FN, NR = 2 * NF;
@@ -83,7 +86,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
   const int wm = wave % 2, wn = wave / 2;
   constexpr int ES = C::FP8 ? 1 : 2;
   const uint32_t kb_end = uint32_t(a.K) * ES;
-  const int KS = int(kb_end / kStep);  // K steps per tile (>= 1)
+  const int KS = int(KTAIL ? (kb_end + kStep - 1) / kStep : kb_end / kStep);  // K steps per tile (>= 2)
   const int S = T * KS;                // steps of the workgroup
   const uint32_t lda_b = uint32_t(a.lda) * ES, ldb_b = uint32_t(a.ldb) * ES;
 
@@ -99,6 +102,18 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     vo[1][e] = uint32_t(8 * (BLKB * wave + e) + (lane >> 3)) * ldb_b + kch[e];
   }
   const uint32_t ld8[2] = {8u * lda_b, 8u * ldb_b};
+  // KTAIL: the lane offsets of the last K step (scalar offset - 16 there)
+  const KTail kt = make_ktail(kb_end);
+  uint32_t vl[2][2];
+  if constexpr (KTAIL) {
+    const uint32_t kb16 = kb_end & ~15u, kr = kb_end & 15u, kbz = kr ? kb16 + 16u : kb_end;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t cs = uint32_t(KS - 1) * kStep + kch[e];  // the lane's chunk, from the row start
+#pragma unroll
+      for (int op = 0; op < 2; ++op) vl[op][e] = cs >= kbz ? kOob : vo[op][e] + (cs == kb16 ? kr : 16u);
+    }
+  }
   using OpA = std::integral_constant<int, 0>;
   using OpB = std::integral_constant<int, 1>;
   // Tile t of the workgroup: its operands and output (for a grouped product,
@@ -169,8 +184,10 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     constexpr int blk = op == 0 ? BLKA : BLKB;
     uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *)dst, 16, vo[op][j & 1],
-                                             uint32_t(c.k) * kStep + uint32_t(j & ~1) * ld8[op], 0, 0);
+    const bool lk = KTAIL && c.k == KS - 1;  // (c.k >= 1 there)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *)dst, 16, lk ? vl[op][j & 1] : vo[op][j & 1],
+                                             uint32_t(c.k) * kStep + uint32_t(j & ~1) * ld8[op] - (lk ? 16u : 0u),
+                                             0, 0);
   };
 
   const int frow = lane & 31, fg = lane >> 5;
@@ -234,6 +251,8 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     constexpr int VM = decltype(vm_tag)::value;
     constexpr bool LAST = decltype(last_tag)::value;
     const int na = sa >= 3 ? sa - 3 : sa + 2, nb = sb >= 3 ? sb - 3 : sb + 2;
+    const bool clear = KTAIL && LAST && kt.cp < 8;
+    if (clear) ktail_clear<NF>(fr[0], 0, fg, kt);
     static_for<NM>([&](auto I) {
       constexpr int i = decltype(I)::value;
       mma(H0{}, I, first_tag);
@@ -244,6 +263,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     });
     wait_and_barrier<VM>();
     __builtin_amdgcn_sched_barrier(0);
+    if (clear) ktail_clear<NF>(fr[1], 1, fg, kt);
     static_for<NM>([&](auto I) {
       constexpr int i = decltype(I)::value;
       mma(H1{}, I, std::false_type{});
@@ -285,10 +305,12 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     const TileDesc d = desc(t);
     const int m0 = d.tm * 256, n0 = d.tn * 256;
     // C as a buffer: a store whose row or column block lies past M / N gets
-    // an offset past the range and is dropped (N is a multiple of 8 and rows
-    // of C are 16-byte aligned, so a 16-byte column block is wholly in or
-    // out).
-    const __amdgpu_buffer_rsrc_t crs = make_rsrc(d.out, uint32_t((int64_t(d.rows - 1) * a.ldc + a.N) * 2));
+    // an offset past the range and is dropped (N is a multiple of 8, so a
+    // 16-byte column block is wholly in or out).  KTAIL: rows of C may have
+    // any alignment; the buffer starts at the 16-byte boundary below C.
+    const uint32_t cmis = KTAIL ? uint32_t(reinterpret_cast<uintptr_t>(d.out) & 15u) : 0u;
+    const __amdgpu_buffer_rsrc_t crs =
+        make_rsrc(d.out - cmis, uint32_t((int64_t(d.rows - 1) * a.ldc + a.N) * 2) + cmis);
     if (t == 0) step(std::true_type{}, VmStep{}, std::false_type{});
     else step(std::true_type{}, VmAfterEpi{}, std::false_type{});
     for (int k = 1; k < KS - 1; ++k) step(std::false_type{}, VmStep{}, std::false_type{});
@@ -332,7 +354,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     uint8_t *stg = lds + stage_slot * kSlotBytes + wave * 8192;
     const int srow = lane >> 4, schunk = lane & 15;  // read-back: row 4 i + srow, chunk schunk
     const int n_st = n0 + wn * TN + 8 * schunk;
-    const uint32_t coloff = n_st < a.N ? uint32_t(n_st) * 2u : kOob;
+    const uint32_t coloff = n_st < a.N ? uint32_t(n_st) * 2u + cmis : kOob;
     static_for<FM>([&](auto fm_tag) {
       constexpr int fm = decltype(fm_tag)::value;
       static_for<FN>([&](auto fn_tag) {
