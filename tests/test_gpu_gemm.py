@@ -284,8 +284,9 @@ def test_fp8_narrow_tile_and_split_k(tx, oracle, dev, M, N, K, fa, fb):
 
 def test_column_tail_strip(tx, oracle, dev):
     """N just past a multiple of 256 where the last tile column would cost a
-    whole round: the full columns take 256x256 tiles, the tail a second,
-    split-K product."""
+    whole round: the full columns take 256x256 tiles, the tail a second
+    product (fp8: split-K 256x128 tiles; 16-bit, at most 8 columns: the VALU
+    strip kernel)."""
     import workloads
     M, N, K = 4096, 4112, 1024
     aq, sa, bq, sb = workloads.fp8_gemm_input(M, N, K, seed_stream=21)

@@ -2,7 +2,8 @@
 although their rows are not whole 16-byte chunks apart or long (rows 4-byte
 aligned, any K of at least two 64-element steps): the persistent tile
 (tx_gemm_*_persist_kt) for products of at least one 256 x 256 tile per CU,
-the 256 x 128 tile with K split otherwise.
+the 256 x 128 tile with K split otherwise, and the few columns past the last
+256-column block of a wide product by the VALU strip kernel.
 
 The last chunk of each row is fetched as the row's last 16 bytes and its
 repeated bytes are cleared in registers, so the cases put that chunk at
@@ -79,10 +80,23 @@ def test_ragged_narrow_tile_split_k(tx, oracle, dev, M, N, K):
     _exact(tx, oracle, dev, M, N, K, seed=M + K)
 
 
-def test_ragged_strided_unaligned_out(tx, oracle, dev):
+@pytest.mark.parametrize("M,N,K,fmt,out_fmt", [(4095, 4097, 4100, BF16, BF16),
+                                               (4096, 4099, 1030, F16, F16),
+                                               (4096, 4104, 520, BF16, F16),
+                                               (4096, 4102, 263, F16, BF16)])  # 2-byte rows: padded copies
+def test_column_strip_exact(tx, oracle, dev, M, N, K, fmt, out_fmt):
+    """N 1 to 8 columns past a multiple of 256 (a 17th tile column would cost
+    a second round): the columns past the last 256-column block take the
+    16-bit strip kernel."""
+    _exact(tx, oracle, dev, M, N, K, fmt, out_fmt, seed=N)
+
+
+@pytest.mark.parametrize("N", [4096, 4099])
+def test_ragged_strided_unaligned_out(tx, oracle, dev, N):
     """C a view 3 elements into a buffer with row pitch N + 1 (rows 2-byte
-    aligned): every output lands in its row and the rest keeps its contents."""
-    M, N, K = 4352, 4096, 1100
+    aligned): every output lands in its row and the rest keeps its contents
+    (N = 4099: the last 3 columns from the strip kernel)."""
+    M, K = 4096 if N % 256 else 4352, 1100
     g = np.random.default_rng(9)
     A = _int_codes(g, (M, K), BF16)
     B = _int_codes(g, (N, K), BF16)

@@ -112,6 +112,9 @@ bool fast16_ragged_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b
 // kStripMaxN) that would cost a whole extra round of 256x256 tiles is a
 // separate, second fast-path product (few tiles, so 256x128 with K split).
 constexpr int64_t kStripMaxN = 64;
+// The 16-bit strip kernel (gemm_bf16.hip): up to 8 columns, a row per
+// wavefront, 4 per workgroup of 256 threads.
+constexpr int64_t kStripKernelCols = 8, kStripKernelRows = 4;
 
 // The persistent 4-wavefront kernel (gemm_persist.h) takes the 256 x 256
 // products it was built for: no fused epilogue or K split, at least two
@@ -167,6 +170,18 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
       strip_args.N = int32_t(tail);
       args.N = int32_t(n0);
       TX_TRY(launch_big(args));
+      const char *fast = std::strstr(base, "_fast");
+      if (es == 2 && tail <= kStripKernelCols && k_bytes >= 16 && fast && (args.lda * 2) % 4 == 0 &&
+          (args.ldb * 2) % 4 == 0 && aligned(args.A, 4) && aligned(strip_args.B, 4)) {
+        // 16-bit operands, at most 8 columns: the VALU strip kernel for
+        // W >= tail columns (tx_gemm_<operands>_strip<W>[_out_<output>])
+        const int w = tail <= 1 ? 1 : tail <= 2 ? 2 : tail <= 4 ? 4 : 8;
+        std::snprintf(kname, sizeof kname, "%.*s_strip%d%s", int(fast - base), base, w, fast + 5);
+        hipFunction_t fn;
+        TX_TRY(get_kernel(co, kname, &fn));
+        const int64_t grid = (int64_t(args.M) + kStripKernelRows - 1) / kStripKernelRows;
+        return launch(fn, unsigned(grid), 1, 256, s, &strip_args, sizeof strip_args, kname);
+      }
       return launch_fast(base, reduce, co, strip_args, k_bytes, es, s, persist);
     }
     return launch_big(args);

@@ -64,6 +64,115 @@ TX_GEMM16_PERSIST(bf16, EL_BF16, _out_f16, OUT_F16)
 TX_GEMM16_PERSIST(f16, EL_F16, , OUT_F16)
 TX_GEMM16_PERSIST(f16, EL_F16, _out_bf16, OUT_BF16)
 
+// Column strip of a 16-bit product: C[:, 0 .. N) with N <= W (1, 2, 4 or
+// 8), the few columns past the last 256-column block of a larger product
+// (whose 256-row tiles would spend a whole tile of MFMAs on each).  VALU dot
+// products: a wavefront per row, lane l the 16-byte chunks l, l + 64, .. of
+// K, kStripUnroll of them loaded before any is used, read through buffer
+// resources (rows 4-byte aligned); the ragged end of K (K mod 8 elements,
+// K >= 8) as the row's last 16 bytes with the elements before it skipped;
+// fp32 sums reduced across the wave and rounded to nearest even.
+constexpr int kStripWaves = 4, kStripUnroll = 4;
+
+template <int EL>
+__device__ __forceinline__ void widen8(const txd::u32x4 &w, float (&x)[8]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if constexpr (EL == EL_BF16) {
+      x[2 * d] = __uint_as_float(w[d] << 16);
+      x[2 * d + 1] = __uint_as_float(w[d] & 0xFFFF0000u);
+    } else {
+      x[2 * d] = float(__builtin_bit_cast(_Float16, uint16_t(w[d] & 0xFFFFu)));
+      x[2 * d + 1] = float(__builtin_bit_cast(_Float16, uint16_t(w[d] >> 16)));
+    }
+  }
+}
+
+template <int EL, int OUT, int W>
+__device__ __forceinline__ void gemm16_strip(const tx_gemm_args &a) {
+  constexpr int U = kStripUnroll;
+  const int lane = threadIdx.x & 63;
+  const int row = int(blockIdx.x) * kStripWaves + int(threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const uint32_t lda_b = uint32_t(a.lda) * 2u, ldb_b = uint32_t(a.ldb) * 2u, kb = uint32_t(a.K) * 2u;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, uint32_t(a.M - 1) * lda_b + kb);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.B, uint32_t(a.N - 1) * ldb_b + kb);
+  const uint32_t arow = uint32_t(row) * lda_b;
+  uint32_t bcol[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) bcol[j] = uint32_t(min(j, a.N - 1)) * ldb_b;  // columns past N: discarded
+  float acc[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) acc[j] = 0.0f;
+  auto fma8 = [&](const txd::u32x4 &av, const txd::u32x4 (&bv)[W], int first) {
+    float x[8];
+    widen8<EL>(av, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < first) x[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      float b[8];
+      widen8<EL>(bv[j], b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j] = fmaf(x[e], b[e], acc[j]);
+    }
+  };
+  auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_bit_cast(txd::u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+  };
+  const int whole = a.K / 8, rest = a.K % 8;
+  for (int c0 = lane; c0 < whole; c0 += 64 * U) {
+    txd::u32x4 av[U], bv[U][W];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 64 * u;
+      // chunks past the row end read out of the buffers' range (zeros) and are not used
+      const uint32_t ko = c < whole ? uint32_t(c) * 16u : 0x80000000u;
+      av[u] = ld(ra, arow + ko);
+#pragma unroll
+      for (int j = 0; j < W; ++j) bv[u][j] = ld(rb, bcol[j] + ko);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c0 + 64 * u < whole) fma8(av[u], bv[u], 0);
+  }
+  if (rest && lane == (whole & 63)) {
+    txd::u32x4 bv[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) bv[j] = ld(rb, bcol[j] + kb - 16u);
+    fma8(ld(ra, arow + kb - 16u), bv, 8 - rest);
+  }
+  // wave sums; lane j then stores column j
+  float out = 0.0f;
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    float v = acc[j];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (lane == j) out = v;
+  }
+  if (lane < W && lane < a.N) {
+    const uint32_t bits = OUT == OUT_F16 ? txd::pack_f16x2(out, 0.0f) & 0xFFFFu : txd::f32_to_bf16_bits(out);
+    static_cast<uint16_t *>(a.C)[int64_t(row) * a.ldc + lane] = uint16_t(bits);
+  }
+}
+
+#define TX_GEMM16_STRIP_W(PFX, EL, SFX, OUT, W)                                                                  \
+  TX_KERNEL void __launch_bounds__(64 * kStripWaves) tx_gemm_##PFX##_strip##W##SFX(const tx_gemm_args a) { \
+    gemm16_strip<EL, OUT, W>(a);                                                                             \
+  }
+#define TX_GEMM16_STRIP(PFX, EL, SFX, OUT)   \
+  TX_GEMM16_STRIP_W(PFX, EL, SFX, OUT, 1)    \
+  TX_GEMM16_STRIP_W(PFX, EL, SFX, OUT, 2)    \
+  TX_GEMM16_STRIP_W(PFX, EL, SFX, OUT, 4)    \
+  TX_GEMM16_STRIP_W(PFX, EL, SFX, OUT, 8)
+
+TX_GEMM16_STRIP(bf16, EL_BF16, , OUT_BF16)
+TX_GEMM16_STRIP(bf16, EL_BF16, _out_f16, OUT_F16)
+TX_GEMM16_STRIP(f16, EL_F16, , OUT_F16)
+TX_GEMM16_STRIP(f16, EL_F16, _out_bf16, OUT_BF16)
+
 // Split-K reductions, by output type.
 TX_KERNEL void __launch_bounds__(256) tx_gemm_bf16_splitk_reduce(const tx_gemm_args a) {
   splitk_reduce<false>(a);
