@@ -61,6 +61,10 @@ CASES = [
     (512, 2048, 4096, "relu", "e5m2", False, "256x128 split K"),
     (300, 500, 256, "silu", "f32", True, "256x128"),
     (8192, 2088, 256, "relu", "e4m3fn", True, "column strip"),
+    (4352, 4096, 512, "silu", "bf16", True, "256x256, more tiles than CUs"),
+    (4352, 4096, 512, "gelu_tanh", "bf16", False, "256x256, more tiles than CUs"),
+    (4196, 4168, 384, "relu", "bf16", True, "256x256, partial tiles"),
+    (8192, 2088, 256, "none", "bf16", True, "column strip, bf16 out"),
     (16, 1000, 512, "gelu_tanh", "bf16", True, "skinny"),
     (40, 3000, 640, "none", "e4m3fn", True, "skinny"),
     (1000, 1100, 1001, "silu", "bf16", True, "padded"),
@@ -81,6 +85,25 @@ def test_epilogue(tx, oracle, dev, M, N, K, act, out, with_bias, path):
         acc, _ = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, r.start, r.stop)
         ref = oracle.gemm_fp8_epilogue(acc, bias, ACTS[act])
         _check(got[r], ref, out, out_scale)
+
+
+@pytest.mark.parametrize("act,with_bias", [("silu", True), ("gelu_tanh", False), ("relu", True)])
+def test_bf16_output_equals_rounded_f32(tx, oracle, dev, act, with_bias):
+    """Every bf16 output of the fused epilogue is the round-to-nearest-even
+    of the fp32 output of the same product (the same tiles and sums, only
+    the output cast differs): the whole output checked bit for bit."""
+    M, N, K = 4352, 4096, 768
+    aq, sa, bq, sb, bias = _inputs(M, N, K, 7 + ACTS[act])
+    bias = bias if with_bias else None
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    args = (t(aq).view(torch.float8_e4m3fn), t(sa), t(bq).view(torch.float8_e4m3fn), t(sb))
+    kw = dict(bias=None if bias is None else t(bias), activation=act)
+    y16 = tx.dot_scaled_rowcol(*args, out_dtype=torch.bfloat16, **kw)
+    y32 = tx.dot_scaled_rowcol(*args, out_dtype=torch.float32, **kw)
+    a = y16.view(torch.int16).cpu().numpy()
+    b = y32.to(torch.bfloat16).view(torch.int16).cpu().numpy()
+    bad = np.argwhere(a != b)
+    assert bad.size == 0, (len(bad), bad[:5].tolist())
 
 
 def test_fp8_output_saturates(tx, oracle, dev):
