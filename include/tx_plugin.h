@@ -23,9 +23,11 @@
  *    tx_dot_fp8_scaled[_ex] and tx_dot_scaled_mx may use device scratch that
  *    the library keeps per (device, stream): fp32 split-K partial planes
  *    (at most 16 x M x N x 4 bytes) when the output tiles leave CUs idle,
- *    zero-padded copies of A and B when rows are not 16-byte aligned in a
- *    product of at least 2^30 multiply-adds (tx_dot_scaled_mx: in any
- *    product), the e4m3fn expansion of an fp4 operand that meets an fp8
+ *    zero-padded copies of A and B when the kernels cannot read their rows
+ *    in place (fp8: rows not 16-byte aligned or K not a multiple of 16;
+ *    bf16 / fp16: rows not 4-byte aligned, and ragged K in the few shapes
+ *    only the 8-wavefront 256 x 256 tile takes) in a product of at least
+ *    2^30 multiply-adds (tx_dot_scaled_mx: in any product), the e4m3fn expansion of an fp4 operand that meets an fp8
  *    one (tx_dot_scaled_mx), and repacked MX scale rows.  The scratch is allocated
  *    stream-ordered (hipMallocAsync on `stream`) the first time a stream
  *    needs it, grown the same way, and reused by later calls, so
