@@ -401,12 +401,14 @@ def test_gemv_config_full(tx, oracle, dev, M):
                                              (1, 8200, 384, 128, 2), (2, 8208, 256, 256, 1),
                                              (1, 100, 1152, 384, 1), (2, 77, 3072, 128, 2),
                                              (1, 1, 128, 128, 2), (2, 3, 5120, 640, 1), (1, 3, 5120, 640, 1),
-                                             (1, 14336, 4096, 128, 1)])
+                                             (1, 14336, 4096, 128, 1),
+                                             (3, 8200, 1152, 384, 2), (4, 100, 5120, 640, 1)])
 def test_gemv_shapes(tx, oracle, dev, M, N, K, group, fmt):
     """Small and ragged shapes; N >= 8192 takes the wide variants (two W
     blocks per wave when M > 4, with an odd number of 16-row blocks); M = 1
     the streaming kernel (1 KiB slices: K not a multiple of 1024, odd N,
-    groups of 384), M = 2 beside it on the MFMA kernel."""
+    groups of 384), M = 2, 3 and 4 beside it on the MFMA kernel (a streaming
+    kernel for M = 4 ran 22.5 against 16.5 us at 14336 x 4096)."""
     g = np.random.default_rng(M * N)
     x = oracle.f32_to_bf16(g.standard_normal((M, K)).astype(np.float32))
     wq = g.integers(0, 256, size=(N, K), dtype=np.uint8)
