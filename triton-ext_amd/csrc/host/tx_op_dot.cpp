@@ -207,8 +207,9 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
   TX_TRY(launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves, int(args.splits)));
   hipFunction_t fn;
   TX_TRY(get_kernel(co, reduce, &fn));
-  const int64_t quads = args.M * ((args.N + 3) / 4);
-  const int64_t grid = std::min<int64_t>((quads + 255) / 256, cus * 16);
+  // a thread per 4 columns, or per 8 where the reduce's vector path takes N
+  const int64_t units = args.M * (args.N % 8 == 0 ? args.N / 8 : (args.N + 3) / 4);
+  const int64_t grid = std::min<int64_t>((units + 255) / 256, cus * 16);
   return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, reduce);
 }
 
