@@ -194,6 +194,13 @@ TX_API void txShutdown(void);
 /* Library version string. */
 TX_API const char *txVersion(void);
 
+/* Diagnostic with no counterpart in the reference: the number of device
+ * allocations the library has made for its stream scratch since the process
+ * started (split-K partials, padded operand copies, transposes, group tile
+ * prefixes; each first use or growth of a (stream, use) buffer counts one).
+ * Lets a caller that must not allocate check that a call did not. */
+TX_API uint64_t txScratchAllocations(void);
+
 /* ----------------------------------------------------------------------- */
 /* Typed entry points                                                       */
 /* ----------------------------------------------------------------------- */
@@ -340,6 +347,12 @@ TX_API tx_status tx_dot(const void *A, tx_dtype ab_type, int64_t lda,
  * e8m0 block scales.  a_type/b_type are TX_FP8E4M3FN or TX_FP8E5M2.
  * A: row-major M x K bytes (lda); B: column-major, N rows of K bytes (ldb);
  * C: row-major bf16 (ldc).  scale_a has M floats, scale_b has N floats.
+ * Non-finite codes keep their decoded meaning (tt.fp_to_fp's fp8 -> fp32,
+ * uTLXConversionPatterns.cpp:577): e4m3fn 0x7F / 0xFF are NaN, e5m2 0x7C /
+ * 0xFC are +-Inf and its other all-ones-exponent codes NaN, so an output
+ * is NaN where its sum reads a NaN or meets Inf * 0 or Inf - Inf, and
+ * +-Inf where it reads Inf otherwise, on every kernel this entry point (and
+ * the _ex / grouped / batched / MX forms below) may pick.
  */
 TX_API tx_status tx_dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda,
                                    const float *scale_a, const void *B,
@@ -514,7 +527,10 @@ TX_API tx_status tx_quantize_rowwise(const void *x, tx_dtype x_type, int64_t ldx
  * N x K bytes (ldw); scales: fp32 row-major N x ceil(K/group) (ld_scales);
  * y: bf16 row-major M x N (ldy).  K and group are multiples of 128 (the last
  * group may be partial), M <= 64, x and W rows 16-byte aligned, scales 4-byte
- * aligned (TX_UNSUPPORTED otherwise).
+ * aligned (TX_UNSUPPORTED otherwise).  NaN / Inf weight codes (e4m3fn 0x7F /
+ * 0xFF; e5m2 0x7C / 0xFC Inf, the rest of its all-ones exponent NaN) and
+ * NaN / Inf in x propagate as in fp32 arithmetic on the decoded values
+ * (NaN, Inf * 0 and Inf - Inf give NaN), the same for every M.
  */
 TX_API tx_status tx_gemv_fp8_dequant(const void *x, int64_t ldx, const void *W,
                                      tx_dtype w_type, int64_t ldw,

@@ -11,15 +11,12 @@
 // reads) so that lane (r, g) holds 32 codes of row r per 128-element slice.
 // The per-wave partial sums are reduced across the workgroup in LDS.
 //
-// Dequantisation is bit placement, not arithmetic: an fp8 code's magnitude
-// bits shifted so its mantissa lands at the top of the bf16 mantissa, with
-// its sign at bit 15, form a bf16 whose value
-// is exactly W * 2^-(127 - fp8 bias) for every finite code (normal codes keep
-// their exponent field; subnormal codes become bf16 subnormals of the same
-// scaled value).  The factor 2^(127 - bias) is applied once per group partial
-// sum in fp32, before the group scale, so no per-element multiply is needed.
-// Weights are expected finite (saturating quantisation): Inf/NaN codes are
-// not propagated as such.  The products run on the bf16 MFMA
+// Dequantisation is gfx950's scaled fp8 -> bf16 pair conversion
+// (v_cvt_scalef32_pk_bf16_bf8 / _fp8, scale 1): two instructions per four
+// codes, exact for every code (bf16 holds every e4m3fn and e5m2 value,
+// subnormals included), with NaN codes giving NaN and e5m2 Inf giving Inf,
+// so the products propagate them as fp32 arithmetic on the decoded values
+// would.  The products run on the bf16 MFMA
 // v_mfma_f32_16x16x32_bf16 with fp32 accumulation; each 128-wide (group)
 // partial sum is scaled in fp32 before it joins the running sum.
 #include <type_traits>
@@ -30,37 +27,21 @@ namespace {
 
 constexpr int kSlice = 128;     // K elements per slice (one group-scale unit)
 
-// Four fp8 codes (one 32-bit word) -> four bf16 (two words) holding
-// W * 2^-(127 - bias), by bit placement only:
-//  1. v_perm puts code b0 in the high byte of the low 16-bit half and b1 in
-//     the high byte of the high half (low bytes zero): sign at bit 15,
-//     magnitude at bits 14..8;
-//  2. a packed 16-bit arithmetic shift right by (8 - e), e = exponent bits,
-//     moves the exponent field into the low e bits of bf16's exponent field
-//     (bits 6+e .. 7) and the mantissa to the top of bf16's mantissa, and
-//     smears the sign over the bits above;
-//  3. one AND keeps the sign bit, clears the smeared copies and the low bits.
+// Four fp8 codes (one 32-bit word) -> four bf16 (two words): codes 0, 1 into
+// lo (code 0 in the low half), codes 2, 3 into hi.
 template <int FMT>
-__device__ __forceinline__ void fp8x4_to_bf16x4_scaled(uint32_t w, uint32_t &lo, uint32_t &hi) {
-  constexpr int SH = (FMT == 2) ? 3 : 4;                             // 8 - exponent bits
-  constexpr uint32_t KEEP = (FMT == 2) ? 0x8FE08FE0u : 0x87F087F0u;  // sign | magnitude
-  typedef short s16x2 __attribute__((ext_vector_type(2)));
-  const uint32_t p0 = __builtin_amdgcn_perm(0u, w, 0x010c000cu);   // b1<<24 | b0<<8
-  const uint32_t p1 = __builtin_amdgcn_perm(0u, w, 0x030c020cu);   // b3<<24 | b2<<8
-  const s16x2 sh = {SH, SH};
-  const s16x2 q0 = __builtin_bit_cast(s16x2, p0) >> sh;
-  const s16x2 q1 = __builtin_bit_cast(s16x2, p1) >> sh;
-  lo = __builtin_bit_cast(uint32_t, q0) & KEEP;
-  hi = __builtin_bit_cast(uint32_t, q1) & KEEP;
+__device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t &lo, uint32_t &hi) {
+  if constexpr (FMT == 2) {
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false));
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true));
+  } else {
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+  }
 }
 
 template <int FMT, int kWaves, int MB, int NB>
 __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
-  // The bit-placed weights are W * 2^-(127 - bias); the factor is split in
-  // two halves: one folded into every group scale (safe for any scale below
-  // 2^64), the other applied once to the final sum.
-  constexpr float kHalf = (FMT == 2) ? 7.205759403792794e+16f   /* 2^56 */
-                                     : 1.152921504606847e+18f;  /* 2^60 */
   constexpr int kRound = 2;          // slices per round: 256 bytes per W row
   constexpr int kDepth = 2;          // rounds in flight
   constexpr int kTile = 16 * 256;    // one wave's transpose tile
@@ -182,7 +163,7 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
           const uint32_t words[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
           uint32_t wb[16];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) fp8x4_to_bf16x4_scaled<FMT>(words[t], wb[2 * t], wb[2 * t + 1]);
+          for (int t = 0; t < 8; ++t) fp8x4_to_bf16x4<FMT>(words[t], wb[2 * t], wb[2 * t + 1]);
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -199,7 +180,7 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
           const int grp = su / slices_per_group;
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
-            const float sc = scale_of(b, grp) * kHalf;
+            const float sc = scale_of(b, grp);
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
           }
@@ -229,7 +210,7 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
     const int grp = (s_end - 1) / slices_per_group;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float sc = scale_of(b, grp) * kHalf;
+      const float sc = scale_of(b, grp);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
     }
@@ -249,7 +230,6 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
       txd::f32x4 t = red[mb * 64 + lane];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) t += red[(w * MB + mb) * 64 + lane];
-      t *= kHalf;
       const int ncol = n0 + 16 * b + r;
       if (ncol < a.N) {
         const float v[4] = {t.x, t.y, t.z, t.w};
