@@ -52,11 +52,22 @@ def test_find_and_invoke_unknown_op(tx):
 def test_table_operand_validation(tx):
     vals = (tx._lib.TxValue * 3)()
     st = tx.lib.txInvokeOp(b"tt.fp_to_fp", vals, 3, None)
-    assert st == tx._lib.INVALID_ARGUMENT and "expected 7 operands" in tx._lib.last_error()
+    assert st == tx._lib.INVALID_ARGUMENT and "expected 7 or 8 operands" in tx._lib.last_error()
     ops = [tx._lib.TxValue.int(0)] + [tx._lib.TxValue.ptr(None)] * 6
     arr = (tx._lib.TxValue * 7)(*ops)
     st = tx.lib.txInvokeOp(b"tt.fp_to_fp", arr, 7, None)
     assert st == tx._lib.INVALID_ARGUMENT and "must be a pointer" in tx._lib.last_error()
+
+
+def test_null_operand_array_is_rejected(tx):
+    """A NULL operand array with a nonzero count is an argument error for
+    every op of the table, at every count (including each op's own, e.g. 9
+    and 12 for tt.dot, 7 and 8 for tt.fp_to_fp), never a dereference."""
+    for name, _sig in tx.plugin_info()[3]:
+        for count in range(1, 26):
+            st = tx.lib.txInvokeOp(name.encode(), None, count, None)
+            assert st == tx._lib.INVALID_ARGUMENT, (name, count, st)
+            assert "operand array is NULL" in tx._lib.last_error()
 
 
 @pytest.mark.parametrize("call", [

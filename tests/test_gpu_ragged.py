@@ -120,3 +120,31 @@ def test_ragged_normal_values(tx, oracle, dev):
     C = _np_bits(tx.dot(_dev(A, BF16, dev), _dev(B, BF16, dev)))
     r32, r16 = oracle.gemm16_rows(A, B, 0, M, BF16)
     check_close(C, r32, r16, BF16_TOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(4352, 4096, 1031),   # >= 2^30 multiply-adds: padded copies
+                                   (600, 1000, 1031),    # below: the generic kernel
+                                   (4096, 4100, 1031),   # with a column tail of 4
+                                   (4096, 4132, 263)])   # a 36-column tail
+def test_odd_k_even_pitch_exact(tx, oracle, dev, M, N, K):
+    """An odd K read through [:, :K] views of rows K + 1 long: the row
+    pitches are 4-byte multiples but the rows are not whole 4-byte words, so
+    the fast path's in-place read (the last chunk fetched as the row's last
+    16 bytes) does not apply; the products take the zero-padded copies or
+    the generic kernel, bit-exact."""
+    _exact(tx, oracle, dev, M, N, K, pad_a=1, pad_b=1, seed=K + N)
+
+
+def test_tall_column_tail_ragged_k(tx, oracle, dev):
+    """M = 65536 rows (a 256 x 256 tile per CU with one column block), N a
+    20-column tail past 256 (N % 8 != 0) and a ragged K: the main 256 columns
+    on the persistent tile, the tail on the 256 x 128 tile (decided before
+    the main part is launched).  Sampled rows, bit-exact."""
+    M, N, K = 65536, 276, 1030
+    g = np.random.default_rng(65)
+    A = _int_codes(g, (M, K), BF16)
+    B = _int_codes(g, (N, K), BF16)
+    C = _np_bits(tx.dot(_dev(A, BF16, dev), _dev(B, BF16, dev)))
+    for r in sorted({0, 1, M - 1} | set(g.integers(0, M, 40).tolist())):
+        _, r16 = oracle.gemm16_rows(A, B, r, r + 1, BF16)
+        assert np.array_equal(C[r:r + 1], r16), r

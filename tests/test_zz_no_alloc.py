@@ -3,9 +3,14 @@ tile prefix lives in the library's fixed device array instead of allocated
 scratch) against tx_dot_fp8_scaled_grouped, through the C ABI.
 
 Both entry points run the same kernels in the same order, so the outputs
-must be bit-identical.  Two calls in a row, the second smaller (fewer
-groups and rows, and the fused epilogue), so the second reads a prefix
-array that still holds the first call's longer contents.
+must be bit-identical.  Three calls in a row on a stream the library has not
+seen: the second smaller than the first (fewer groups and rows, and the
+fused epilogue), so it reads a prefix array that still holds the first
+call's longer contents; the third large enough for the persistent grouped
+kernel (256 x 256 tiles on every CU, K a whole number of 128-byte steps).
+Across the three, the library's scratch allocation counter and torch's
+reserved memory must not move (the allocating entry point, run afterwards
+on another new stream, does move the counter).
 """
 import ctypes
 
@@ -50,22 +55,36 @@ def _noalloc(tx, t, groups, M, N, K, out, bias, act, c_type, c_scale):
 
 
 def test_noalloc_grouped_matches_the_allocating_entry(tx, dev):
-    # call 1: 6 groups over 1000 rows, bf16 out
-    t, G, M, N, K = _problem(dev, 1, 6, 1000, 384, 256)
-    ref = tx.dot_scaled_rowcol_grouped(t["A"], t["sa"], t["B"], t["sb"], t["off"])
-    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
-    _noalloc(tx, t, G, M, N, K, out, None, tx._lib.ACT_NONE, tx._lib.BF16, 1.0)
+    tx.init()
+    calls = [  # (problem, bias, activation, output dtype, c_scale)
+        (_problem(dev, 1, 6, 1000, 384, 256), False, "none", torch.bfloat16, 1.0),
+        (_problem(dev, 2, 3, 300, 384, 256), True, "gelu_tanh", torch.float8_e4m3fn, 0.25),
+        (_problem(dev, 4, 8, 4096, 4096, 256), False, "none", torch.bfloat16, 1.0),
+    ]
+    acts = {"none": tx._lib.ACT_NONE, "gelu_tanh": tx._lib.ACT_GELU_TANH}
+    ctypes_out = {torch.bfloat16: tx._lib.BF16, torch.float8_e4m3fn: tx._lib.FP8E4M3FN}
+    outs = [torch.zeros((M, N), dtype=odt, device=dev) for (_t, _G, M, N, _K), _b, _a, odt, _c in calls]
     torch.cuda.synchronize()
-    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
-    # call 2, right after and smaller: 3 groups over 300 rows, bias + gelu -> e4m3fn
-    t2, G2, M2, N2, K2 = _problem(dev, 2, 3, 300, 384, 256)
-    ref2 = tx.dot_scaled_rowcol_grouped(t2["A"], t2["sa"], t2["B"], t2["sb"], t2["off"], bias=t2["bias"],
-                                        activation="gelu_tanh", out_dtype=torch.float8_e4m3fn, out_scale=0.25)
-    out2 = torch.zeros((M2, N2), dtype=torch.float8_e4m3fn, device=dev)
-    _noalloc(tx, t2, G2, M2, N2, K2, out2, t2["bias"], tx._lib.ACT_GELU_TANH, tx._lib.FP8E4M3FN, 0.25)
+    allocs0, reserved0 = tx.lib.txScratchAllocations(), torch.cuda.memory_reserved(dev)
+    s_na = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s_na):
+        for ((t, G, M, N, K), use_bias, act, odt, cs), out in zip(calls, outs):
+            _noalloc(tx, t, G, M, N, K, out, t["bias"] if use_bias else None, acts[act], ctypes_out[odt], cs)
     torch.cuda.synchronize()
-    assert torch.equal(out2.view(torch.uint8), ref2.view(torch.uint8))
-    assert torch.count_nonzero(out2.view(torch.uint8)) > 0
+    assert tx.lib.txScratchAllocations() == allocs0
+    assert torch.cuda.memory_reserved(dev) == reserved0
+    s_ref = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s_ref):
+        refs = [tx.dot_scaled_rowcol_grouped(t["A"], t["sa"], t["B"], t["sb"], t["off"],
+                                             bias=t["bias"] if use_bias else None,
+                                             activation=None if act == "none" else act, out_dtype=odt,
+                                             out_scale=cs)
+                for (t, G, M, N, K), use_bias, act, odt, cs in calls]
+    torch.cuda.synchronize()
+    assert tx.lib.txScratchAllocations() > allocs0  # the allocating entry's prefix lease on a new stream
+    for out, ref in zip(outs, refs):
+        assert torch.equal(out.view(torch.uint8), ref.view(torch.uint8))
+        assert torch.count_nonzero(out.view(torch.uint8)) > 0
 
 
 def test_noalloc_grouped_rejects_too_many_groups(tx, dev):

@@ -92,11 +92,14 @@ bool fast_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t
 
 // 16-bit operands the fast path also reads in place (fast::KTail in
 // gemm_fast.h, the persistent and the 256 x 128 tiles): rows 4-byte
-// aligned, and a row length that is not a whole number of 16-byte chunks
-// only with at least two K steps.
+// aligned, a row length of whole 4-byte words (the last chunk of a row is
+// fetched as the row's last 16 bytes, which must stay 4-byte aligned for the
+// buffer loads), and one that is not a whole number of 16-byte chunks only
+// with at least two K steps.  An odd K takes the padded copies.
 bool fast16_ragged_ok(const void *A, int64_t lda_b, const void *B, int64_t ldb_b, int64_t k_b, int64_t M,
                       int64_t N) {
-  if (!aligned(A, 16) || !aligned(B, 16) || lda_b % 4 || ldb_b % 4 || (k_b % 16 && k_b <= 128)) return false;
+  if (!aligned(A, 16) || !aligned(B, 16) || lda_b % 4 || ldb_b % 4 || k_b % 4 || (k_b % 16 && k_b <= 128))
+    return false;
   const int64_t lim = int64_t(1) << 31;
   return (M - 1) * lda_b + k_b + 16 < lim && (N - 1) * ldb_b + k_b + 16 < lim;
 }
@@ -130,8 +133,11 @@ const char *persist_variant(const tx_gemm_args &args, int64_t k_bytes, int es) {
   return es == 2 && aligned(args.C, 2) ? "_persist_kt" : nullptr;
 }
 
+// `narrow` sends the whole product to the 256 x 128 tile (the column tail
+// of a wide product: at most kStripMaxN columns, and any K the 256 x 128
+// tile takes, decided before the main part is launched).
 tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_gemm_args &args,
-                      int64_t k_bytes, int es, hipStream_t s, bool persist = false) {
+                      int64_t k_bytes, int es, hipStream_t s, bool persist = false, bool narrow = false) {
   const int64_t cus = cu_count();
   const int64_t tiles_m = (args.M + 255) / 256;
   char kname[96];
@@ -154,7 +160,7 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
     std::snprintf(kname, sizeof kname, "%s", base);
     return launch_gemm(kname, co, ga, 256, 256, s, 64 * kFastWaves);
   };
-  if (tiles_m * ((args.N + 255) / 256) >= cus) {
+  if (!narrow && tiles_m * ((args.N + 255) / 256) >= cus) {
     std::snprintf(kname, sizeof kname, "%s", base);
     const int64_t full = args.N / 256, tail = args.N % 256;
     const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
@@ -171,7 +177,8 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
       args.N = int32_t(n0);
       TX_TRY(launch_big(args));
       const char *fast = std::strstr(base, "_fast");
-      if (es == 2 && tail <= kStripKernelCols && k_bytes >= 16 && fast && (args.lda * 2) % 4 == 0 &&
+      if (es == 2 && tail <= kStripKernelCols && k_bytes >= 16 && k_bytes % 4 == 0 && fast &&
+          (args.lda * 2) % 4 == 0 &&
           (args.ldb * 2) % 4 == 0 && aligned(args.A, 4) && aligned(strip_args.B, 4)) {
         // 16-bit operands, at most 8 columns: the VALU strip kernel for
         // W >= tail columns (tx_gemm_<operands>_strip<W>[_out_<output>])
@@ -182,7 +189,7 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
         const int64_t grid = (int64_t(args.M) + kStripKernelRows - 1) / kStripKernelRows;
         return launch(fn, unsigned(grid), 1, 256, s, &strip_args, sizeof strip_args, kname);
       }
-      return launch_fast(base, reduce, co, strip_args, k_bytes, es, s, persist);
+      return launch_fast(base, reduce, co, strip_args, k_bytes, es, s, persist, true);
     }
     return launch_big(args);
   }
@@ -863,7 +870,7 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
 // stored N x K.
 static tx_status dot_op(tx_value *v, size_t count, tx_stream_t stream) {
   Operands o{v, count, "tt.dot"};
-  if (count != 9) TX_TRY(o.need(12));
+  TX_TRY(o.need_either(9, 12));
   void *C, *A, *B;
   int64_t M, N, K, lda, ldb, ldc;
   TX_TRY(o.ptr(0, &C));

@@ -162,7 +162,7 @@ static tx_status fp_to_fp_rbits(const void *src, tx_dtype src_type, void *dst,
 // optional operand (ops/NewOps.cpp:253-257).
 static tx_status fp_to_fp_op(tx_value *v, size_t count, tx_stream_t stream) {
   Operands o{v, count, "tt.fp_to_fp"};
-  if (count != 8) TX_TRY(o.need(7));
+  TX_TRY(o.need_either(7, 8));
   void *dst, *src, *rbits = nullptr;
   int64_t n, st, dt, rnd, sat;
   TX_TRY(o.ptr(0, &dst));

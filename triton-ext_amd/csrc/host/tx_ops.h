@@ -30,6 +30,13 @@ struct Operands {
                   count, n);
     return TX_SUCCESS;
   }
+  // Either of two operand counts (an op with optional trailing operands).
+  tx_status need_either(size_t a, size_t b) const {
+    if (!v && n) return fail(TX_INVALID_ARGUMENT, "%s: operand array is NULL", op);
+    if (n != a && n != b)
+      return fail(TX_INVALID_ARGUMENT, "%s: expected %zu or %zu operands, got %zu", op, a, b, n);
+    return TX_SUCCESS;
+  }
   tx_status ptr(size_t i, void **out) const {
     if (v[i].kind != TX_VALUE_PTR)
       return fail(TX_INVALID_ARGUMENT, "%s: operand %zu must be a pointer", op, i);

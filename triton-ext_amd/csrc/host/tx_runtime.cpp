@@ -35,6 +35,8 @@ namespace tx {
 namespace {
 
 thread_local std::string g_last_error;
+// device allocations made for stream scratch (txScratchAllocations)
+std::atomic<uint64_t> g_scratch_allocs{0};
 
 struct CodeObjectImage {
   const char *name;
@@ -309,6 +311,7 @@ tx_status ScratchLease::acquire(hipStream_t stream, int slot, size_t bytes) {
       ptr_ = nullptr;
       return fail(TX_GENERIC_FAILURE, "scratch of %zu bytes: %s", bytes, hipGetErrorString(e));
     }
+    g_scratch_allocs.fetch_add(1, std::memory_order_relaxed);
     own_ = true;
     return TX_SUCCESS;
   }
@@ -337,6 +340,7 @@ tx_status ScratchLease::acquire(hipStream_t stream, int slot, size_t bytes) {
       k->ptr = nullptr;
       return fail(TX_GENERIC_FAILURE, "scratch of %zu bytes: %s", want, hipGetErrorString(e));
     }
+    g_scratch_allocs.fetch_add(1, std::memory_order_relaxed);
     k->bytes = want;
   }
   ptr_ = k->ptr;
@@ -396,6 +400,8 @@ tx_status launch(hipFunction_t fn, unsigned grid_x, unsigned grid_y,
 extern "C" {
 
 TX_API const char *txGetLastError(void) { return tx::g_last_error.c_str(); }
+
+TX_API uint64_t txScratchAllocations(void) { return tx::g_scratch_allocs.load(std::memory_order_relaxed); }
 
 TX_API tx_status txInit(void) {
   tx::clear_error();
