@@ -355,8 +355,30 @@ def bench_fp8_convert(tx, torch, steps, warmup, n=16_777_216):
     ms_dec = timed(lambda i: tx.fp_to_fp(qs[i % sets], torch.float32, out=fs[i % sets]),
                    steps, warmup)
     dec_gbs = 5.0 * n / (ms_dec * 1e-3) / 1e9
+    # the memory system's ceiling for the encode's launch shape and bytes:
+    # the same kernel shape with the conversion taken out (4:1 byte copy)
+    # and a read-only stream of the same fp32 input
+    import ctypes
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def ceiling(kind):
+        def go(i):
+            st = tx.lib.txStreamCeiling(kind, ctypes.c_void_p(xs[i % sets].data_ptr()),
+                                        ctypes.c_void_p(qs[i % sets].data_ptr()), n, cur())
+            if st != 0:
+                raise RuntimeError(tx._lib.last_error())
+        return timed(go, steps, warmup)
+
+    ms_copy, ms_read = ceiling(0), ceiling(1)
     return {"ms": ms, "gbs": enc_gbs, "bytes": 5.0 * n, "sets": sets,
-            "decode_ms": ms_dec, "decode_gbs": dec_gbs}
+            "decode_ms": ms_dec, "decode_gbs": dec_gbs,
+            "ceiling": {"copy_4to1_ms": round(ms_copy, 5),
+                        "copy_4to1_gbs": round(5.0 * n / (ms_copy * 1e-3) / 1e9, 1),
+                        "read_ms": round(ms_read, 5),
+                        "read_gbs": round(4.0 * n / (ms_read * 1e-3) / 1e9, 1),
+                        "encode_over_copy": round(ms_copy / ms, 4),
+                        "what": "the encode's launch shape with the conversion taken out (4 B read, "
+                                "1 B written per value) and reading only (4 B per value), same buffers"}}
 
 
 def bench_convert_pair(tx, torch, src, dst, steps, warmup, n=16_777_216):
@@ -876,7 +898,7 @@ def main():
                                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                      "frac": round(conv["gbs"] / HBM_PEAK_GBS, 4),
                                      "traffic": conv_traffic[0], "traffic_source": conv_traffic[1]},
-                        "buffer_sets": conv["sets"]},
+                        "buffer_sets": conv["sets"], "ceiling": conv["ceiling"]},
     }
     print(json.dumps(line))
 

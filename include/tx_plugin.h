@@ -201,6 +201,16 @@ TX_API const char *txVersion(void);
  * Lets a caller that must not allocate check that a call did not. */
 TX_API uint64_t txScratchAllocations(void);
 
+/* Diagnostic with no counterpart in the reference: HBM ceiling kernels with
+ * exactly the launch shape of the fp32 -> fp8 encode of tx_fp_to_fp, for
+ * measuring how close the encode comes to what the memory system gives that
+ * shape.  kind 0: dst[i] = low byte of the 32-bit word src[i] (4 bytes read,
+ * 1 written per element, no conversion work); kind 1: reads src[0 .. n) and
+ * writes dst only where the XOR of a thread's 16 words equals n (so the
+ * loads stay).  src: n 32-bit words, 16-byte aligned; dst: n bytes, 4-byte
+ * aligned; n a multiple of 4096. */
+TX_API tx_status txStreamCeiling(int kind, const void *src, void *dst, int64_t n, tx_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* Typed entry points                                                       */
 /* ----------------------------------------------------------------------- */

@@ -200,3 +200,17 @@ extern "C" TX_API tx_status tx_fp_to_fp(const void *src, tx_dtype src_type,
   tx::clear_error();
   return tx::fp_to_fp(src, src_type, dst, dst_type, n, rounding, saturate, stream);
 }
+
+extern "C" TX_API tx_status txStreamCeiling(int kind, const void *src, void *dst, int64_t n,
+                                            tx_stream_t stream) {
+  tx::clear_error();
+  if (kind != 0 && kind != 1) return tx::fail(TX_INVALID_ARGUMENT, "txStreamCeiling: kind %d", kind);
+  if (n < 0 || n % tx::kChunk != 0)
+    return tx::fail(TX_INVALID_ARGUMENT, "txStreamCeiling: n = %lld is not a multiple of %lld", (long long)n,
+                    (long long)tx::kChunk);
+  if (n == 0) return TX_SUCCESS;
+  if (!src || !dst || !tx::aligned(src, 16) || !tx::aligned(dst, 4))
+    return tx::fail(TX_INVALID_ARGUMENT, "txStreamCeiling: src must be 16-byte and dst 4-byte aligned");
+  const char *name = kind == 0 ? "tx_stream_copy41_vec" : "tx_stream_read_vec";
+  return tx::run(name, name, src, dst, n, true, static_cast<hipStream_t>(stream));
+}

@@ -756,6 +756,49 @@ TX_ENCODE_KERNELS(e5m2_rtne_sat, E5M2, true, false)
 TX_ENCODE_KERNELS(e5m2_rtz, E5M2, false, true)
 TX_ENCODE_KERNELS(e5m2_rtz_sat, E5M2, true, true)
 
+// HBM ceiling kernels with the vector encoder's exact shape (block, chunk,
+// loads per thread, non-temporal hints, grid), for measurement only
+// (txStreamCeiling): the same bytes as the fp32 -> fp8 encode with no
+// conversion work.  copy41 stores each value's low byte (4 B read, 1 B
+// written per value); read loads every value and stores one word per
+// thread only if the XOR of its 16 words is the improbable a.n (so the
+// loads cannot be dropped).
+__device__ __forceinline__ void stream_copy41(const tx_fp8_codec_args &a) {
+  const txd::u32x4 *src = reinterpret_cast<const txd::u32x4 *>(a.src) + a.start / 4;
+  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst) + a.start / 4;
+  const int64_t nchunks = (a.n - a.start) / kChunk;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t w0 = c * (kChunk / 4) + threadIdx.x;
+    txd::u32x4 v[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) v[j] = __builtin_nontemporal_load(src + w0 + j * kBlock);
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j)
+      __builtin_nontemporal_store(__builtin_amdgcn_perm(v[j].y, v[j].x, 0x0c0c0400u) |
+                                      __builtin_amdgcn_perm(v[j].w, v[j].z, 0x04000c0cu),
+                                  dst + w0 + j * kBlock);
+  }
+}
+
+__device__ __forceinline__ void stream_read(const tx_fp8_codec_args &a) {
+  const txd::u32x4 *src = reinterpret_cast<const txd::u32x4 *>(a.src) + a.start / 4;
+  uint32_t *dst = reinterpret_cast<uint32_t *>(a.dst) + a.start / 4;
+  const int64_t nchunks = (a.n - a.start) / kChunk;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t w0 = c * (kChunk / 4) + threadIdx.x;
+    txd::u32x4 v[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) v[j] = __builtin_nontemporal_load(src + w0 + j * kBlock);
+    uint32_t x = 0;
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    if (x == uint32_t(a.n)) dst[w0] = x;
+  }
+}
+
+TX_KERNEL void __launch_bounds__(kBlock) tx_stream_copy41_vec(const tx_fp8_codec_args a) { stream_copy41(a); }
+TX_KERNEL void __launch_bounds__(kBlock) tx_stream_read_vec(const tx_fp8_codec_args a) { stream_read(a); }
+
 TX_KERNEL void __launch_bounds__(kBlock) tx_fp8_decode_e4m3fn_vec(const tx_fp8_codec_args a) {
   decode_vec<E4M3FN>(a);
 }

@@ -41,7 +41,7 @@ B_NK, B_KN = 0, 1
 # Every symbol include/tx_plugin.h declares.
 EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
-    "txGetLastError", "txInit", "txShutdown", "txVersion", "txScratchAllocations",
+    "txGetLastError", "txInit", "txShutdown", "txVersion", "txScratchAllocations", "txStreamCeiling",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_atomic_cas_scatter",
     "tx_dot_bf16", "tx_dot",
     "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped",
@@ -118,6 +118,8 @@ def _load():
     L.txVersion.argtypes = []
     L.txScratchAllocations.restype = ctypes.c_uint64
     L.txScratchAllocations.argtypes = []
+    L.txStreamCeiling.restype = I
+    L.txStreamCeiling.argtypes = [I, P, P, I64, VP]
     L.tx_fp_to_fp.argtypes = [P, I, P, I, I64, I, I, VP]
     L.tx_fp_to_fp.restype = I
     L.tx_fp_to_fp_with_rbits.argtypes = [P, I, P, I, P, I64, I, I, VP]
