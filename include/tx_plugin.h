@@ -350,6 +350,29 @@ TX_API tx_status tx_dot(const void *A, tx_dtype ab_type, int64_t lda,
                         int64_t N, int64_t K, tx_stream_t stream);
 
 /*
+ * tt.dot with its accumulator operand.  TritonDotPattern keeps c as a real
+ * operand of tt.dot (uTLXConversionPatterns.cpp:273, 290-291) and the
+ * reference's AMD kernel chains it through its K loop (accumulator =
+ * tl.dot(a, b, accumulator), test_amd_gemm_pipelined.py:274, 292):
+ *   D[m,n] = round_d( s[m,n] * sum_k f32(A[m,k]) * f32(B[k,n]) + C[m,n] )
+ * in fp32, with s = scale_a[m] * scale_b[n] for fp8 operands and 1 for
+ * 16-bit ones, rounded once to d_type (TX_F32, TX_BF16 or TX_F16, nearest
+ * even).  Operands: bf16 or fp16 (a_type == b_type; scale_a, scale_b NULL;
+ * B stored N x K or row-major K x N as tx_dot), or fp8 (TX_FP8E4M3FN /
+ * TX_FP8E5M2 in any pairing, B stored N x K, fp32 scale_a[M], scale_b[N]).
+ * C: fp32 row-major M x N (ldc elements), or NULL for D = round_d(s * A.B);
+ * C may be D itself when d_type is TX_F32 and ldc == ldd (accumulating in
+ * place, as the reference's K loop does).  Non-finite values propagate as in
+ * fp32 arithmetic.  Uses stream scratch (fp32 partial sums of M x N per K
+ * split; operand copies when rows are misaligned or B is K x N).
+ */
+TX_API tx_status tx_dot_acc(const void *A, tx_dtype a_type, int64_t lda, const float *scale_a,
+                            const void *B, tx_dtype b_type, tx_b_layout b_layout, int64_t ldb,
+                            const float *scale_b, const float *C, int64_t ldc, void *D,
+                            tx_dtype d_type, int64_t ldd, int64_t M, int64_t N, int64_t K,
+                            tx_stream_t stream);
+
+/*
  * tt.dot on fp8 operands with a per-row / per-column scale epilogue:
  * C[m,n] = bf16_rne(scale_a[m] * scale_b[n] * sum_k f32(A[m,k]) * f32(B[k,n])).
  * No reference kernel exists; the closed form follows the scaled-dot check

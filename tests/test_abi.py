@@ -183,6 +183,21 @@ _P = ctypes.c_void_p(256)   # a non-NULL, 256-byte aligned stand-in: these calls
     (lambda L: L.tx_dot_fp8_scaled_batched(_P, 6, 128, 128 * 64, _P, 64, _P, 1, 128, 128 * 64, _P, 64, _P, 64,
                                           64 * 64, 2, 64, 64, 128, None),
      "INVALID_ARGUMENT", "fp8"),
+    # tt.dot with its accumulator operand
+    (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 1, 0, 64, None, None, 0, _P, 0, 64, 64, 64, 64, None),
+     "INVALID_ARGUMENT", "operands must be"),
+    (lambda L: L.tx_dot_acc(_P, 1, 64, _P, _P, 1, 1, 64, _P, None, 0, _P, 0, 64, 64, 64, 64, None),
+     "UNSUPPORTED", "N x K"),
+    (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 3, 0, 64, None, None, 0, _P, 1, 64, 64, 64, 64, None),
+     "INVALID_ARGUMENT", "output type"),
+    (lambda L: L.tx_dot_acc(_P, 1, 64, None, _P, 2, 0, 64, None, None, 0, _P, 0, 64, 64, 64, 64, None),
+     "INVALID_ARGUMENT", "scale vectors"),
+    (lambda L: L.tx_dot_acc(_P, 6, 64, _P, _P, 6, 0, 64, _P, None, 0, _P, 0, 64, 64, 64, 64, None),
+     "INVALID_ARGUMENT", "scale vectors are for fp8"),
+    (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 3, 0, 64, None, _P, 64, _P, 3, 64, 64, 64, 64, None),
+     "INVALID_ARGUMENT", "only for an fp32 D"),
+    (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 3, 0, 64, None, _P, 32, _P, 0, 64, 64, 64, 64, None),
+     "INVALID_ARGUMENT", "ldc >= N"),
     # quantisers: K a multiple of the 32-element block; input and code types
     (lambda L: L.tx_quantize_mx(_P, 0, 100, _P, 1, 100, _P, 4, 4, 100, None), "INVALID_ARGUMENT", "multiple"),
     (lambda L: L.tx_quantize_mx(_P, 6, 128, _P, 1, 128, _P, 4, 4, 128, None), "INVALID_ARGUMENT", "fp32 or bf16"),

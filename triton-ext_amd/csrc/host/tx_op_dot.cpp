@@ -239,45 +239,80 @@ int pad_load_bytes(const void *src, int64_t ld_bytes, int64_t row_bytes) {
   return 1;
 }
 
-tx_status launch_padded(const char *base, const char *reduce, const char *pad, CodeObject co,
-                        tx_gemm_args &args, int es, hipStream_t s) {
+// Copy A and B into zero-padded rows of kp (K rounded up to a whole
+// 128-byte step) in `ws` (stream scratch slot 0) and point args at them.
+// TX_UNSUPPORTED (nothing launched) when an operand would exceed the GEMM's
+// 31-bit buffer offsets or the scratch cannot be had.
+tx_status pad_operands(const char *pad, CodeObject co, tx_gemm_args &args, int es, hipStream_t s,
+                       ScratchLease &ws) {
   const int64_t per = 16 / es, step = 128 / es;
   const int64_t kp = (int64_t(args.K) + step - 1) / step * step;
-  if (int64_t(args.M) * args.N * args.K < kPadMinWork ||
-      (int64_t(std::max(args.M, args.N)) * kp) * es >= (int64_t(1) << 31))
-    return TX_UNSUPPORTED;
+  if ((int64_t(std::max(args.M, args.N)) * kp) * es >= (int64_t(1) << 31)) return TX_UNSUPPORTED;
   const size_t a_bytes = size_t(args.M) * size_t(kp) * es;
   const size_t b_bytes = size_t(args.N) * size_t(kp) * es;
-  ScratchLease ws;  // held until every launch using it is enqueued
   if (ws.acquire(s, 0, a_bytes + b_bytes) != TX_SUCCESS) {
     clear_error();
     return TX_UNSUPPORTED;
   }
   hipFunction_t fn;
-  tx_status st = get_kernel(co, pad, &fn);
+  TX_TRY(get_kernel(co, pad, &fn));
   const int64_t cus = cu_count();
   uint8_t *wa = static_cast<uint8_t *>(ws.ptr()), *wb = wa + a_bytes;
-  if (st == TX_SUCCESS) {
-    tx_pad_args pa{args.A, wa, args.lda, kp, args.M, args.K, int32_t(kp),
-                   pad_load_bytes(args.A, args.lda * es, int64_t(args.K) * es)};
-    const int64_t ga = std::min<int64_t>((int64_t(args.M) * kp / per + 255) / 256, cus * 16);
-    st = launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, pad);
+  tx_pad_args pa{args.A, wa, args.lda, kp, args.M, args.K, int32_t(kp),
+                 pad_load_bytes(args.A, args.lda * es, int64_t(args.K) * es)};
+  const int64_t ga = std::min<int64_t>((int64_t(args.M) * kp / per + 255) / 256, cus * 16);
+  TX_TRY(launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, pad));
+  tx_pad_args pb{args.B, wb, args.ldb, kp, args.N, args.K, int32_t(kp),
+                 pad_load_bytes(args.B, args.ldb * es, int64_t(args.K) * es)};
+  const int64_t gb = std::min<int64_t>((int64_t(args.N) * kp / per + 255) / 256, cus * 16);
+  TX_TRY(launch(fn, unsigned(gb), 1, 256, s, &pb, sizeof pb, pad));
+  args.A = wa;
+  args.lda = kp;
+  args.B = wb;
+  args.ldb = kp;
+  args.K = int32_t(kp);
+  return TX_SUCCESS;
+}
+
+tx_status launch_padded(const char *base, const char *reduce, const char *pad, CodeObject co,
+                        tx_gemm_args &args, int es, hipStream_t s) {
+  if (int64_t(args.M) * args.N * args.K < kPadMinWork) return TX_UNSUPPORTED;
+  ScratchLease ws;  // held until every launch using it is enqueued
+  TX_TRY(pad_operands(pad, co, args, es, s, ws));
+  return launch_fast(base, reduce, co, args, int64_t(args.K) * es, es, s, true);
+}
+
+// tt.dot with its accumulator operand: the 256 x 128 tile writes the fp32
+// sums to partial planes in stream scratch (slot 1; K split while the tiles
+// leave CUs idle, at least one plane), and the split-K reduce sums them,
+// applies the fp8 scales, adds the accumulator and rounds to the output type
+// (its epilogue path, args.epi / out_kind / acc).  K = 0: the reduce alone.
+tx_status launch_acc(const char *base, const char *reduce, CodeObject co, tx_gemm_args &args, int64_t k_bytes,
+                     hipStream_t s) {
+  const int64_t cus = cu_count();
+  ScratchLease part;  // held until the reduce is enqueued
+  if (k_bytes > 0) {
+    const int64_t tiles = ((int64_t(args.M) + 255) / 256) * ((int64_t(args.N) + 127) / 128);
+    const int64_t ksteps = (k_bytes + 127) / 128;
+    int64_t splits = std::max<int64_t>(1, std::min({kMaxSplits, cus / tiles, ksteps / kMinStepsPerSplit}));
+    const int64_t per = (ksteps + splits - 1) / splits;
+    splits = (ksteps + per - 1) / per;  // no empty split
+    TX_TRY(part.acquire(s, 1, size_t(splits) * size_t(args.M) * size_t(args.N) * sizeof(float)));
+    args.splits = int32_t(splits);
+    args.ksteps_split = int32_t(per);
+    args.part = static_cast<float *>(part.ptr());
+    char kname[96];
+    std::snprintf(kname, sizeof kname, "%s_n128", base);
+    TX_TRY(launch_gemm(kname, co, args, 256, 128, s, 64 * kFastWaves, int(splits)));
+  } else {
+    args.splits = 0;  // no plane: D = round(C)
+    args.part = nullptr;
   }
-  if (st == TX_SUCCESS) {
-    tx_pad_args pb{args.B, wb, args.ldb, kp, args.N, args.K, int32_t(kp),
-                   pad_load_bytes(args.B, args.ldb * es, int64_t(args.K) * es)};
-    const int64_t gb = std::min<int64_t>((int64_t(args.N) * kp / per + 255) / 256, cus * 16);
-    st = launch(fn, unsigned(gb), 1, 256, s, &pb, sizeof pb, pad);
-  }
-  if (st == TX_SUCCESS) {
-    args.A = wa;
-    args.lda = kp;
-    args.B = wb;
-    args.ldb = kp;
-    args.K = int32_t(kp);
-    st = launch_fast(base, reduce, co, args, kp * es, es, s, true);
-  }
-  return st;
+  hipFunction_t fn;
+  TX_TRY(get_kernel(co, reduce, &fn));
+  const int64_t units = int64_t(args.M) * ((int64_t(args.N) + 3) / 4);
+  const int64_t grid = std::min<int64_t>((units + 255) / 256, cus * 16);
+  return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, reduce);
 }
 
 const char *fp8_name(tx_dtype t) {
@@ -285,6 +320,47 @@ const char *fp8_name(tx_dtype t) {
 }
 
 }  // namespace
+
+// A row-major K x N B (the reference's matmul operand) for the 16-bit dot:
+// B^T into stream scratch `ws` (slot 0): N rows of kp = K rounded up to a
+// whole 64-element (128-byte) step, zero-filled; A is copied into
+// zero-padded rows of kp too when the fast path cannot read it as is.
+// args.B / ldb (and A / lda / K) then describe the copies.
+static tx_status transpose_kn(const char *what, tx_gemm_args &args, hipStream_t s, ScratchLease &ws) {
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const void *A = args.A, *B = args.B;
+  const int64_t lda = args.lda, ldb = args.ldb;
+  const int64_t kp = (K + 63) / 64 * 64;
+  const bool a_pad = !(aligned(A, 16) && (lda * 2) % 16 == 0 && (K * 2) % 16 == 0);
+  const int64_t lim = int64_t(1) << 31;
+  if (N * kp * 2 >= lim || (a_pad ? M * kp * 2 : (M - 1) * lda * 2 + K * 2) >= lim)
+    return fail(TX_UNSUPPORTED, "%s: an operand exceeds the 2 GiB range of the GEMM's buffer loads", what);
+  if (kp / 64 > 65535)
+    return fail(TX_UNSUPPORTED, "%s: K = %lld too large for the transpose grid", what, (long long)K);
+  const size_t bt_bytes = size_t(N) * size_t(kp) * 2;
+  const size_t a_bytes = a_pad ? size_t(M) * size_t(kp) * 2 : 0;
+  TX_TRY(ws.acquire(s, 0, bt_bytes + a_bytes));
+  uint16_t *wb = static_cast<uint16_t *>(ws.ptr());
+  uint16_t *wa = wb + size_t(N) * size_t(kp);
+  const bool tvec = aligned(B, 16) && (ldb * 2) % 16 == 0;
+  const char *tname = tvec ? "tx_gemm_16_transpose_kn_v16" : "tx_gemm_16_transpose_kn_v2";
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::GemmBf16, tname, &fn));
+  tx_pad_args ta{B, wb, ldb, kp, int32_t(K), int32_t(N), int32_t(kp), 0};
+  TX_TRY(launch(fn, unsigned((N + 63) / 64), unsigned(kp / 64), 256, s, &ta, sizeof ta, tname));
+  args.B = wb;
+  args.ldb = kp;
+  if (a_pad) {
+    TX_TRY(get_kernel(CodeObject::GemmBf16, "tx_gemm_bf16_pad_rows", &fn));
+    tx_pad_args pa{A, wa, lda, kp, int32_t(M), int32_t(K), int32_t(kp), pad_load_bytes(A, lda * 2, K * 2)};
+    const int64_t ga = std::min<int64_t>((M * kp / 8 + 255) / 256, int64_t(cu_count()) * 16);
+    TX_TRY(launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, "tx_gemm_bf16_pad_rows"));
+    args.A = wa;
+    args.lda = kp;
+    args.K = int32_t(kp);
+  }
+  return TX_SUCCESS;
+}
 
 // tt.dot with 16-bit operands (bf16 / fp16) and a 16-bit output.  Kernel
 // names: tx_gemm_<operands>_<variant>[_out_<output>]; the split-K reduce
@@ -314,41 +390,8 @@ static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda
   tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
                     int32_t(K), 0, 0, 0};
   if (kn) {
-    // B^T into stream scratch (slot 0): N rows of kp = K rounded up to a
-    // whole 64-element (128-byte) step, zero-filled; A is copied into
-    // zero-padded rows of kp too when the fast path cannot read it as is.
-    const int64_t kp = (K + 63) / 64 * 64;
-    const bool a_pad = !(aligned(A, 16) && (lda * 2) % 16 == 0 && (K * 2) % 16 == 0);
-    const int64_t lim = int64_t(1) << 31;
-    if (N * kp * 2 >= lim || (a_pad ? M * kp * 2 : (M - 1) * lda * 2 + K * 2) >= lim)
-      return fail(TX_UNSUPPORTED, "%s: an operand exceeds the 2 GiB range of the GEMM's buffer loads",
-                  what);
-    if (kp / 64 > 65535) return fail(TX_UNSUPPORTED, "%s: K = %lld too large for the transpose grid", what,
-                                     (long long)K);
-    const size_t bt_bytes = size_t(N) * size_t(kp) * 2;
-    const size_t a_bytes = a_pad ? size_t(M) * size_t(kp) * 2 : 0;
     ScratchLease ws;  // held until every launch using it is enqueued
-    TX_TRY(ws.acquire(s, 0, bt_bytes + a_bytes));
-    uint16_t *wb = static_cast<uint16_t *>(ws.ptr());
-    uint16_t *wa = wb + size_t(N) * size_t(kp);
-    const bool tvec = aligned(B, 16) && (ldb * 2) % 16 == 0;
-    const char *tname = tvec ? "tx_gemm_16_transpose_kn_v16" : "tx_gemm_16_transpose_kn_v2";
-    hipFunction_t fn;
-    TX_TRY(get_kernel(CodeObject::GemmBf16, tname, &fn));
-    tx_pad_args ta{B, wb, ldb, kp, int32_t(K), int32_t(N), int32_t(kp), 0};
-    TX_TRY(launch(fn, unsigned((N + 63) / 64), unsigned(kp / 64), 256, s, &ta, sizeof ta, tname));
-    args.B = wb;
-    args.ldb = kp;
-    if (a_pad) {
-      TX_TRY(get_kernel(CodeObject::GemmBf16, "tx_gemm_bf16_pad_rows", &fn));
-      tx_pad_args pa{A, wa, lda, kp, int32_t(M), int32_t(K), int32_t(kp),
-                     pad_load_bytes(A, lda * 2, K * 2)};
-      const int64_t ga = std::min<int64_t>((M * kp / 8 + 255) / 256, int64_t(cu_count()) * 16);
-      TX_TRY(launch(fn, unsigned(ga), 1, 256, s, &pa, sizeof pa, "tx_gemm_bf16_pad_rows"));
-      args.A = wa;
-      args.lda = kp;
-      args.K = int32_t(kp);
-    }
+    TX_TRY(transpose_kn(what, args, s, ws));
     return launch_fast(base, reduce, CodeObject::GemmBf16, args, int64_t(args.K) * 2, 2, s, true);
   }
   if (layout == TX_B_KN) args.ldb = K;  // K = 0: B is never read
@@ -473,6 +516,74 @@ static tx_status dot_fp8_scaled(const void *A, tx_dtype a_type, int64_t lda, con
                                 tx_stream_t stream) {
   return dot_fp8_impl("tx_dot_fp8_scaled", A, a_type, lda, sa, B, b_type, ldb, sb, C, ldc, M, N, K,
                       Epilogue{}, stream);
+}
+
+// tt.dot with its accumulator operand c: TritonDotPattern keeps it as an
+// operand (uTLXConversionPatterns.cpp:273, 290-291) and the reference's AMD
+// kernel chains it through its K loop (accumulator = tl.dot(a, b,
+// accumulator), test_amd_gemm_pipelined.py:274, 292):
+//   D = A.B (times scale_a[m] scale_b[n] for fp8 operands) + C
+// in fp32, rounded once to D's type (fp32, bf16 or fp16, nearest even).
+static tx_status dot_acc(const void *A, tx_dtype a_type, int64_t lda, const float *sa, const void *B,
+                         tx_dtype b_type, tx_b_layout layout, int64_t ldb, const float *sb, const float *Cacc,
+                         int64_t ld_acc, void *D, tx_dtype d_type, int64_t ldd, int64_t M, int64_t N, int64_t K,
+                         tx_stream_t stream) {
+  const char *what = "tx_dot_acc";
+  const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
+  const bool fp8 = fa && fb;
+  const bool b16 = (a_type == TX_BF16 || a_type == TX_F16) && b_type == a_type;
+  if (!fp8 && !b16)
+    return fail(TX_INVALID_ARGUMENT, "%s: operands must be bf16 or fp16 (both the same) or fp8 (got %d, %d)",
+                what, int(a_type), int(b_type));
+  if (layout != TX_B_NK && layout != TX_B_KN)
+    return fail(TX_INVALID_ARGUMENT, "%s: B layout %d", what, int(layout));
+  if (fp8 && layout != TX_B_NK) return fail(TX_UNSUPPORTED, "%s: fp8 operands take B stored N x K", what);
+  if (d_type != TX_F32 && d_type != TX_BF16 && d_type != TX_F16)
+    return fail(TX_INVALID_ARGUMENT, "%s: output type must be fp32, bf16 or fp16 (got %d)", what, int(d_type));
+  const size_t de = d_type == TX_F32 ? 4 : 2;
+  const bool kn = layout == TX_B_KN && K > 0;
+  TX_TRY(check_gemm(what, A, lda, B, kn ? K : ldb, D, ldd, M, N, K, de));
+  if (kn && ldb < N)
+    return fail(TX_INVALID_ARGUMENT, "%s: stride smaller than row length (ldb=%lld < N=%lld)", what,
+                (long long)ldb, (long long)N);
+  if (M == 0 || N == 0) return TX_SUCCESS;
+  if (fp8 && (!sa || !sb)) return fail(TX_INVALID_ARGUMENT, "%s: fp8 operands need both scale vectors", what);
+  if (!fp8 && (sa || sb)) return fail(TX_INVALID_ARGUMENT, "%s: scale vectors are for fp8 operands", what);
+  if (!aligned(sa, 4) || !aligned(sb, 4))
+    return fail(TX_INVALID_ARGUMENT, "%s: scales must be 4-byte aligned", what);
+  if (Cacc) {
+    if (ld_acc < N || !aligned(Cacc, 4))
+      return fail(TX_INVALID_ARGUMENT, "%s: C needs ldc >= N and 4-byte alignment", what);
+    if (static_cast<const void *>(Cacc) == D && !(d_type == TX_F32 && ld_acc == ldd))
+      return fail(TX_INVALID_ARGUMENT, "%s: C may be D itself only for an fp32 D with the same stride", what);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tx_gemm_args args{A, B, D, sa, sb, lda, ldb, ldd, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+  args.epi = 1;
+  args.act = EPI_ACT_NONE;
+  args.out_mul = 1.0f;
+  args.out_kind = d_type == TX_F32 ? EPI_OUT_F32 : d_type == TX_F16 ? EPI_OUT_F16 : EPI_OUT_BF16;
+  args.acc = Cacc;
+  args.ld_acc = ld_acc;
+  const int es = fp8 ? 1 : 2;
+  const CodeObject co = fp8 ? CodeObject::GemmFp8 : CodeObject::GemmBf16;
+  char base[64];
+  if (fp8) std::snprintf(base, sizeof base, "tx_gemm_fp8_%s_%s_fast", fa, fb);
+  else std::snprintf(base, sizeof base, "tx_gemm_%s_fast", a_type == TX_BF16 ? "bf16" : "f16");
+  const char *reduce = fp8 ? "tx_gemm_fp8_splitk_reduce" : "tx_gemm_bf16_splitk_reduce";
+  if (K == 0) return launch_acc(base, reduce, co, args, 0, s);
+  ScratchLease ws;  // operand copies (slot 0), held until the product is enqueued
+  if (kn) {
+    TX_TRY(transpose_kn(what, args, s, ws));
+  } else if (!fast_ok(A, lda * es, B, ldb * es, K * es, M, N) &&
+             !(b16 && fast16_ragged_ok(A, lda * es, B, ldb * es, K * es, M, N))) {
+    const tx_status st =
+        pad_operands(fp8 ? "tx_gemm_fp8_pad_rows" : "tx_gemm_bf16_pad_rows", co, args, es, s, ws);
+    if (st == TX_UNSUPPORTED)
+      return fail(TX_UNSUPPORTED, "%s: operands too large for the zero-padded copies", what);
+    TX_TRY(st);
+  }
+  return launch_acc(base, reduce, co, args, int64_t(args.K) * es, s);
 }
 
 // The fused epilogue's options (bias, tx_activation, output type and, for
@@ -866,11 +977,15 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
 
 // Table forms.
 // tt.dot: {C (result), A, B, M, N, K, lda, ldb, ldc[, ab_type, c_type,
-// b_layout]} -- without the last three, bf16 operands and output and B
-// stored N x K.
+// b_layout[, acc, ld_acc, scale_a, scale_b, b_type]]} -- without the last
+// eight, bf16 operands and output and B stored N x K; with the last five,
+// tt.dot's accumulator operand (acc fp32 M x N or NULL; c_type fp32, bf16 or
+// fp16; fp8 operands with scale_a / scale_b, 16-bit ones with NULL scales;
+// tx_dot_acc).
 static tx_status dot_op(tx_value *v, size_t count, tx_stream_t stream) {
   Operands o{v, count, "tt.dot"};
-  TX_TRY(o.need_either(9, 12));
+  if (count != 17) TX_TRY(o.need_either(9, 12));
+  else TX_TRY(o.need(17));
   void *C, *A, *B;
   int64_t M, N, K, lda, ldb, ldc;
   TX_TRY(o.ptr(0, &C));
@@ -883,10 +998,22 @@ static tx_status dot_op(tx_value *v, size_t count, tx_stream_t stream) {
   TX_TRY(o.integer(7, &ldb));
   TX_TRY(o.integer(8, &ldc));
   int64_t ab = TX_BF16, ct = TX_BF16, layout = TX_B_NK;
-  if (count == 12) {
+  if (count >= 12) {
     TX_TRY(o.integer(9, &ab));
     TX_TRY(o.integer(10, &ct));
     TX_TRY(o.integer(11, &layout));
+  }
+  if (count == 17) {
+    void *acc, *sa, *sb;
+    int64_t ld_acc, bt;
+    TX_TRY(o.ptr(12, &acc));
+    TX_TRY(o.integer(13, &ld_acc));
+    TX_TRY(o.ptr(14, &sa));
+    TX_TRY(o.ptr(15, &sb));
+    TX_TRY(o.integer(16, &bt));
+    return dot_acc(A, tx_dtype(ab), lda, static_cast<const float *>(sa), B, tx_dtype(bt), tx_b_layout(layout),
+                   ldb, static_cast<const float *>(sb), static_cast<const float *>(acc), ld_acc, C, tx_dtype(ct),
+                   ldc, M, N, K, stream);
   }
   return dot16("tt.dot", A, tx_dtype(ab), lda, B, tx_b_layout(layout), ldb, C, tx_dtype(ct), ldc, M,
                N, K, stream);
@@ -1073,8 +1200,9 @@ static tx_status dot_fp8_ex_op(tx_value *v, size_t count, tx_stream_t stream) {
 
 static const bool reg_dot = register_op(
     "tt.dot", dot_op,
-    "C:bf16|f16*(result), A:bf16|f16*, B:bf16|f16* (N x K, or K x N with b_layout 1), M, N, K, lda, "
-    "ldb, ldc[, ab_type:i32, c_type:i32, b_layout:i32]");
+    "C:bf16|f16|f32*(result), A:bf16|f16|fp8*, B:bf16|f16|fp8* (N x K, or K x N with b_layout 1), M, "
+    "N, K, lda, ldb, ldc[, ab_type:i32, c_type:i32, b_layout:i32[, acc:f32*|NULL, ld_acc, "
+    "scale_a:f32*|NULL, scale_b:f32*|NULL, b_type:i32]]");
 static const bool reg_dot_fp8 = register_op(
     "tt.dot_scaled.rowcol", dot_fp8_op,
     "C:bf16*(result), A:fp8*, B:fp8* (N x K), scale_a:f32*, scale_b:f32*, M, N, K, lda, ldb, "
@@ -1114,6 +1242,15 @@ TX_API tx_status tx_dot(const void *A, tx_dtype ab_type, int64_t lda, const void
                         int64_t M, int64_t N, int64_t K, tx_stream_t stream) {
   tx::clear_error();
   return tx::dot16("tx_dot", A, ab_type, lda, B, b_layout, ldb, C, c_type, ldc, M, N, K, stream);
+}
+
+TX_API tx_status tx_dot_acc(const void *A, tx_dtype a_type, int64_t lda, const float *scale_a, const void *B,
+                            tx_dtype b_type, tx_b_layout b_layout, int64_t ldb, const float *scale_b,
+                            const float *C, int64_t ldc, void *D, tx_dtype d_type, int64_t ldd, int64_t M,
+                            int64_t N, int64_t K, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::dot_acc(A, a_type, lda, scale_a, B, b_type, b_layout, ldb, scale_b, C, ldc, D, d_type, ldd, M, N, K,
+                     stream);
 }
 
 TX_API tx_status tx_dot_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,

@@ -560,14 +560,16 @@ __device__ __forceinline__ void gemm_fast_tile_at(const tx_gemm_args &a, int tm,
 
   // Epilogue: lane owns, per (fm, fn, jj), C[m][n .. n+3] with
   // m = m0 + wm*TM + fm*32 + l%32, n = n0 + wn*TN + fn*32 + 8*jj + 4*(l/32).
-  // With K split, the unscaled fp32 sums go to the split's partial plane
+  // With partial planes (K split, or one plane for a reduce that adds tt.dot's
+  // accumulator operand), the unscaled fp32 sums go to the split's plane
   // (row-major M x N); a reduction kernel combines the planes.  An fp32
   // output (MX variant) is stored the same way, straight into C.
-  if (!TRANS && (splits > 1 || OUT == OUT_F32)) {
-    float *P = splits > 1 ? a.part + int64_t(split) * a.M * a.N : static_cast<float *>(a.C);
-    const int64_t ldp = splits > 1 ? a.N : a.ldc;
-    const bool pvec = splits > 1 ? (a.N & 3) == 0
-                                 : ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0 && (a.ldc & 3) == 0);
+  const bool to_part = a.part != nullptr;
+  if (!TRANS && (to_part || OUT == OUT_F32)) {
+    float *P = to_part ? a.part + int64_t(split) * a.M * a.N : static_cast<float *>(a.C);
+    const int64_t ldp = to_part ? a.N : a.ldc;
+    const bool pvec = to_part ? (a.N & 3) == 0
+                              : ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0 && (a.ldc & 3) == 0);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int m = m0 + wm * TM + fm * 32 + frow;
@@ -869,7 +871,8 @@ __device__ __forceinline__ void splitk_reduce(const tx_gemm_args &a) {
       if (n + i >= a.N) break;
       float r = v[i];
       if constexpr (ROWCOL) r = r * sa * a.scale_b[n + i];
-      if (a.epi) {  // fused epilogue of the fp8 GEMM (uniform branch)
+      if (a.epi) {  // fused epilogue (uniform branch), after tt.dot's accumulator operand
+        if (a.acc) r += a.acc[int64_t(m) * a.ld_acc + n + i];
         epi_store1(a, m, n + i, epi_value(a, r, n + i));
         continue;
       }

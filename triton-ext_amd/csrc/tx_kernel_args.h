@@ -109,6 +109,10 @@ typedef struct tx_gemm_args {
   int32_t out_kind;    /* EPI_OUT_* */
   float out_mul;
   int32_t epi;
+  /* tt.dot's accumulator operand (split-K reduce with epi only): fp32 M x N
+   * (ld_acc elements) added to the scaled sum before the bias; NULL: none. */
+  const float *acc;
+  int64_t ld_acc;
 } tx_gemm_args;
 
 /* Grouped / batched fp8 GEMM (row/column scales, bf16 out) over the fast

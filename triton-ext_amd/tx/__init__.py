@@ -256,6 +256,55 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return _dot16(a, b.contiguous(), _lib.B_KN, None, torch.float16)
 
 
+def dot_acc(a: torch.Tensor, b: torch.Tensor, acc: torch.Tensor | None = None, *,
+            b_layout: str = "nk", scale_a: torch.Tensor | None = None,
+            scale_b: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """tt.dot with its accumulator operand: out = round(a @ b + acc) in fp32
+    (the reference's ``accumulator = tl.dot(a, b, accumulator)``,
+    test_amd_gemm_pipelined.py:274).  a: M x K; b: N x K storage of the
+    column-major operand (``b_layout="nk"``) or row-major K x N (``"kn"``,
+    16-bit operands only).  Operands both bf16 or both fp16, or fp8 (any
+    pairing) with fp32 ``scale_a[M]`` and ``scale_b[N]`` multiplying the
+    product.  acc: fp32 M x N or None; out: fp32 (default), bf16 or fp16, and
+    may be acc itself when fp32 (accumulate in place)."""
+    _on_gpu(a, b, acc, scale_a, scale_b, out)
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("dot_acc takes 2-D operands")
+    if b_layout not in ("nk", "kn"):
+        raise ValueError(f"b_layout must be 'nk' or 'kn' (got {b_layout!r})")
+    fp8 = a.dtype in _FP8 and b.dtype in _FP8
+    if not fp8 and not (a.dtype in _DOT16 and b.dtype == a.dtype):
+        raise ValueError(f"dot_acc takes two bf16, two fp16 or two fp8 operands (got {a.dtype}, {b.dtype})")
+    if fp8 and b_layout != "nk":
+        raise ValueError("fp8 operands take b as its N x K storage")
+    if fp8 != (scale_a is not None and scale_b is not None) or (not fp8 and (scale_a is not None or
+                                                                             scale_b is not None)):
+        raise ValueError("scale_a and scale_b go with fp8 operands, and only with them")
+    M, K = a.shape
+    N = b.shape[0] if b_layout == "nk" else b.shape[1]
+    if (b.shape[1] if b_layout == "nk" else b.shape[0]) != K:
+        raise ValueError(f"incompatible shapes {tuple(a.shape)} and {tuple(b.shape)} ({b_layout})")
+    if a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("operand rows must be contiguous")
+    if fp8 and (scale_a.dtype != torch.float32 or scale_b.dtype != torch.float32 or scale_a.numel() != M
+                or scale_b.numel() != N or not scale_a.is_contiguous() or not scale_b.is_contiguous()):
+        raise ValueError("scales must be contiguous fp32 vectors of length M and N")
+    if acc is not None and (acc.dtype != torch.float32 or tuple(acc.shape) != (M, N) or acc.stride(1) != 1):
+        raise ValueError("acc must be a row-major fp32 M x N tensor")
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError("out_dtype must be fp32, bf16 or fp16")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"out must be a row-major {out_dtype} M x N tensor")
+    layout = _lib.B_NK if b_layout == "nk" else _lib.B_KN
+    check(lib.tx_dot_acc(_ptr(a), _TX_DTYPE[a.dtype], a.stride(0), _ptr(scale_a), _ptr(b), _TX_DTYPE[b.dtype],
+                         layout, b.stride(0), _ptr(scale_b), _ptr(acc), 0 if acc is None else acc.stride(0),
+                         _ptr(out), _TX_DTYPE[out_dtype], out.stride(0), M, N, K, _stream(a)))
+    return out
+
+
 _ACT = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "relu": _lib.ACT_RELU,
         "gelu_tanh": _lib.ACT_GELU_TANH, "silu": _lib.ACT_SILU}
 

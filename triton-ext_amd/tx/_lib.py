@@ -43,7 +43,7 @@ EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion", "txScratchAllocations", "txStreamCeiling",
     "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_atomic_cas_scatter",
-    "tx_dot_bf16", "tx_dot",
+    "tx_dot_bf16", "tx_dot", "tx_dot_acc",
     "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped",
     "tx_dot_fp8_scaled_grouped_noalloc", "tx_dot_fp8_scaled_batched",
     "tx_dot_scaled_mx", "tx_quantize_mx", "tx_quantize_rowwise",
@@ -132,6 +132,8 @@ def _load():
     L.tx_dot_bf16.restype = I
     L.tx_dot.argtypes = [P, I, I64, P, I, I64, P, I, I64, I64, I64, I64, VP]
     L.tx_dot.restype = I
+    L.tx_dot_acc.argtypes = [P, I, I64, P, P, I, I, I64, P, P, I64, P, I, I64, I64, I64, I64, VP]
+    L.tx_dot_acc.restype = I
     L.tx_dot_fp8_scaled.argtypes = [P, I, I64, P, P, I, I64, P, P, I64, I64, I64, I64, VP]
     L.tx_dot_fp8_scaled.restype = I
     L.tx_dot_fp8_scaled_ex.argtypes = [P, I, I64, P, P, I, I64, P, P, I, P, I, ctypes.c_float,
