@@ -91,8 +91,11 @@ typedef enum tx_dtype {
   TX_I32 = 4,
   TX_U32 = 5,
   TX_F16 = 6,
-  TX_FP4E2M1 = 7 /* OCP MX fp4: 1 sign, 2 exponent (bias 1), 1 mantissa bit; two per byte,
+  TX_FP4E2M1 = 7, /* OCP MX fp4: 1 sign, 2 exponent (bias 1), 1 mantissa bit; two per byte,
                     the lower K index in the low nibble (tx_dot_scaled_mx operands) */
+  TX_I64 = 8,     /* tl.int64 (tx_atomic_rmw_scatter bins) */
+  TX_U64 = 9,     /* tl.uint64 */
+  TX_F64 = 10     /* tl.float64 */
 } tx_dtype;
 
 /* Rounding modes, numbered as the rounding operand of
@@ -101,16 +104,16 @@ typedef enum tx_rounding { TX_RTNE = 0, TX_RTZ = 1, TX_RS = 2 } tx_rounding;
 
 /* Read-modify-write kinds of tt.atomic_rmw (Triton's RMWOp). */
 typedef enum tx_rmw_op {
-  TX_RMW_ADD = 0,  /* integer add, wraps modulo 2^32 */
-  TX_RMW_FADD = 1, /* fp32 add */
-  TX_RMW_MAX = 2,  /* signed int32 max */
-  TX_RMW_MIN = 3,  /* signed int32 min */
-  TX_RMW_UMAX = 4, /* unsigned int32 max */
-  TX_RMW_UMIN = 5, /* unsigned int32 min */
+  TX_RMW_ADD = 0,  /* integer add, wraps modulo 2^32 (2^64 for 64-bit bins) */
+  TX_RMW_FADD = 1, /* floating-point add: fp32, fp64, fp16 or bf16 bins */
+  TX_RMW_MAX = 2,  /* signed integer max */
+  TX_RMW_MIN = 3,  /* signed integer min */
+  TX_RMW_UMAX = 4, /* unsigned integer max */
+  TX_RMW_UMIN = 5, /* unsigned integer min */
   TX_RMW_AND = 6,
   TX_RMW_OR = 7,
   TX_RMW_XOR = 8,
-  TX_RMW_XCHG = 9  /* exchange: the bin takes val (any 32-bit bins) */
+  TX_RMW_XCHG = 9  /* exchange: the bin takes val (any 32- or 64-bit bins) */
 } tx_rmw_op;
 
 /* Storage of tt.dot's B operand (K x N) in tx_dot. */
@@ -274,16 +277,21 @@ TX_API tx_status tx_fp_to_fp_with_rbits(const void *src, tx_dtype src_type, void
  * be NULL) and 0 <= idx[i] < nbins, atomically bins[idx[i]] = bins[idx[i]]
  * (op) val[i].  Replaces Triton's per-lane lowering of tl.atomic_add and
  * friends (tt.atomic_rmw, passed through at uTLXConversionPatterns.cpp:611;
- * used at test_tlx.py:7627-7629 and 7687).  bins_type is TX_I32 or TX_U32 for
- * the integer ops and TX_F32 for TX_RMW_FADD.  Updates are pre-aggregated
- * (in registers, within a wavefront, and in an LDS table per workgroup)
- * before they reach global memory, so fp32 sums are order-dependent within
- * rounding.
+ * used at test_tlx.py:7627-7629 and 7687).  bins_type is TX_I32, TX_U32,
+ * TX_I64 or TX_U64 for the integer ops and TX_F32, TX_F64, TX_F16 or TX_BF16
+ * for TX_RMW_FADD; val has the bins' type.  Updates are pre-aggregated (in
+ * registers, within a wavefront, and in an LDS table per workgroup) before
+ * they reach global memory, so floating-point sums are order-dependent
+ * within rounding.  fp16 / bf16 bins: a workgroup's updates of one bin are
+ * summed in fp32 and the bin is rounded to nearest even once per such
+ * partial (once per update when the bins exceed one LDS table of 36864, or
+ * with old).  64-bit bins are pre-aggregated up to 18432 bins.
  * If old != NULL, every update instead returns the bin's value before it was
  * applied (the tt.atomic_rmw result) in old[i] (0 for dropped updates), and
  * no pre-aggregation is done.
- * TX_RMW_XCHG takes TX_I32, TX_U32 or TX_F32 bins (the 32-bit pattern is
- * exchanged) and is one atomic per update: where several updates hit one
+ * TX_RMW_XCHG takes TX_I32, TX_U32, TX_F32, TX_I64, TX_U64 or TX_F64 bins
+ * (the bit pattern is exchanged) and is one atomic per update: where several
+ * updates hit one
  * bin they apply one at a time in an order the hardware picks, so the bin
  * ends with one of their values and, with old, their old values are the
  * bin's initial value and the other updates' values.

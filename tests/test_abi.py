@@ -183,6 +183,15 @@ _P = ctypes.c_void_p(256)   # a non-NULL, 256-byte aligned stand-in: these calls
     (lambda L: L.tx_dot_fp8_scaled_batched(_P, 6, 128, 128 * 64, _P, 64, _P, 1, 128, 128 * 64, _P, 64, _P, 64,
                                           64 * 64, 2, 64, 64, 128, None),
      "INVALID_ARGUMENT", "fp8"),
+    # tt.atomic_rmw on 64-bit and 16-bit bins
+    (lambda L: L.tx_atomic_rmw_scatter(_P, 6, 10, _P, _P, None, 5, 0, None, None),
+     "INVALID_ARGUMENT", "fadd only"),
+    (lambda L: L.tx_atomic_rmw_scatter(_P, 8, 10, _P, _P, None, 5, 1, None, None),
+     "INVALID_ARGUMENT", "floating-point bins"),
+    (lambda L: L.tx_atomic_rmw_scatter(_P, 10, 10, _P, _P, None, 5, 2, None, None),
+     "INVALID_ARGUMENT", "fadd or xchg"),
+    (lambda L: L.tx_atomic_rmw_scatter(_P, 8, 10, _P, ctypes.c_void_p(260), None, 5, 0, None, None),
+     "INVALID_ARGUMENT", "8-byte aligned"),
     # tt.dot with its accumulator operand
     (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 1, 0, 64, None, None, 0, _P, 0, 64, 64, 64, 64, None),
      "INVALID_ARGUMENT", "operands must be"),

@@ -50,6 +50,53 @@ unsigned direct_grid(int64_t n) {
 
 }  // namespace
 
+// 64-bit and 16-bit float bins (tx_scatter_<type>_<op>_{table,direct,old},
+// tx_scatter_i64_xchg in scatter.hip): an LDS table per workgroup when the
+// bins fit one (and the updates are at least twice the bins), one global
+// atomic per update otherwise and for the returning-old and xchg forms.
+constexpr int64_t kWideSlots64 = 18432, kWideSlots16 = 36864;
+constexpr unsigned kWideBlock = 1024;
+
+static tx_status atomic_rmw_wide(void *bins, tx_dtype bins_type, int64_t nbins, const int32_t *idx,
+                                 const void *val, const uint8_t *mask, int64_t n, tx_rmw_op op, void *old,
+                                 hipStream_t s) {
+  const char *what = "tx_atomic_rmw_scatter";
+  const bool i64 = bins_type == TX_I64 || bins_type == TX_U64;
+  const bool half = bins_type == TX_F16 || bins_type == TX_BF16;
+  if (half && op != TX_RMW_FADD)
+    return fail(TX_INVALID_ARGUMENT, "%s: fp16 / bf16 bins take fadd only", what);
+  if (bins_type == TX_F64 && op != TX_RMW_FADD && op != TX_RMW_XCHG)
+    return fail(TX_INVALID_ARGUMENT, "%s: fp64 bins take fadd or xchg", what);
+  if (i64 && op == TX_RMW_FADD) return fail(TX_INVALID_ARGUMENT, "%s: fadd needs floating-point bins", what);
+  if (n == 0) return TX_SUCCESS;
+  if (!idx || !val || (!bins && nbins > 0)) return fail(TX_INVALID_ARGUMENT, "%s: NULL buffer", what);
+  const size_t es = half ? 2 : 8;
+  if (!aligned(idx, 4) || !aligned(val, es) || (bins && !aligned(bins, es)) || (old && !aligned(old, es)))
+    return fail(TX_INVALID_ARGUMENT, "%s: idx must be 4-byte and bins / val / old %zu-byte aligned", what, es);
+  tx_scatter_args args{bins, idx, val, mask, old, n, int32_t(nbins), 0, 0, 0};
+  const char *tn = i64 ? "i64" : bins_type == TX_F64 ? "f64" : bins_type == TX_F16 ? "f16" : "bf16";
+  char kname[64];
+  hipFunction_t fn;
+  if (op == TX_RMW_XCHG) {
+    TX_TRY(get_kernel(CodeObject::Scatter, "tx_scatter_i64_xchg", &fn));
+    return launch(fn, direct_grid(n), 1, 256, s, &args, sizeof args, "tx_scatter_i64_xchg");
+  }
+  const int64_t slots = half ? kWideSlots16 : kWideSlots64;
+  if (!old && nbins == 0) return TX_SUCCESS;  // every update is out of range
+  if (!old && nbins <= slots && n >= 2 * nbins) {
+    std::snprintf(kname, sizeof kname, "tx_scatter_%s_%s_table", tn, op_name(op));
+    TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+    const int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(cu_count(), n / (4 * kWideBlock)));
+    int64_t per = (n + chunks - 1) / chunks;
+    if (per > INT32_MAX) per = INT32_MAX;
+    args.per_block = int32_t(per);
+    return launch(fn, unsigned((n + per - 1) / per), 1, kWideBlock, s, &args, sizeof args, kname);
+  }
+  std::snprintf(kname, sizeof kname, "tx_scatter_%s_%s_%s", tn, op_name(op), old ? "old" : "direct");
+  TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+  return launch(fn, direct_grid(n), 1, 256, s, &args, sizeof args, kname);
+}
+
 static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbins,
                                     const int32_t *idx, const void *val,
                                     const uint8_t *mask, int64_t n, tx_rmw_op op,
@@ -62,15 +109,18 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
   if (nbins > INT32_MAX)
     return fail(TX_UNSUPPORTED, "tx_atomic_rmw_scatter: nbins %lld exceeds int32 indexing",
                 (long long)nbins);
+  if (bins_type == TX_I64 || bins_type == TX_U64 || bins_type == TX_F64 || bins_type == TX_F16 ||
+      bins_type == TX_BF16)
+    return atomic_rmw_wide(bins, bins_type, nbins, idx, val, mask, n, op, old, static_cast<hipStream_t>(stream));
   if (op == TX_RMW_FADD) {
     if (bins_type != TX_F32)
-      return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: fadd needs TX_F32 bins");
+      return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: fadd needs TX_F32, TX_F64, TX_F16 or TX_BF16 bins");
   } else if (op == TX_RMW_XCHG) {
     if (bins_type != TX_I32 && bins_type != TX_U32 && bins_type != TX_F32)
-      return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: xchg needs 32-bit bins");
+      return fail(TX_INVALID_ARGUMENT, "tx_atomic_rmw_scatter: xchg needs 32- or 64-bit bins");
   } else if (bins_type != TX_I32 && bins_type != TX_U32) {
     return fail(TX_INVALID_ARGUMENT,
-                "tx_atomic_rmw_scatter: integer ops need TX_I32 or TX_U32 bins");
+                "tx_atomic_rmw_scatter: integer ops need TX_I32, TX_U32, TX_I64 or TX_U64 bins");
   }
   if (n == 0) return TX_SUCCESS;
   if (!idx || !val || (!bins && nbins > 0))

@@ -734,3 +734,225 @@ TX_KERNEL void __launch_bounds__(256) tx_scatter_cas(const tx_cas_args a) {
     if (a.old) a.old[i] = r;
   }
 }
+
+// ---------------------------------------------------------------------------
+// tt.atomic_rmw on 64-bit bins (int64 / uint64: add, max, min, umax, umin,
+// and, or, xor, xchg; fp64: fadd, xchg) and 16-bit float bins (fp16 / bf16:
+// fadd), the element types Triton's atomic_rmw accepts beside the 32-bit
+// ones (the plugin passes every atomic_rmw through,
+// uTLXConversionPatterns.cpp:611).
+//
+// When the bins fit one LDS table (64-bit: 18432 slots of 8 bytes; 16-bit
+// fadd: 36864 fp32 slots), each workgroup combines its chunk of updates in
+// the table with LDS atomics and then adds each touched slot to its bin
+// with one global atomic (wide_table); otherwise every update is one global
+// atomic (wide_direct), which also serves the returning-old and xchg forms.
+// 16-bit fadd sums a workgroup's updates of one bin in fp32 and adds that
+// partial to the bin with a compare-and-swap loop on the aligned 32-bit word
+// that holds it (the other half is written back unchanged), rounding the
+// bin to nearest even once per partial; wide_direct rounds once per update,
+// as a per-element 16-bit atomic does.
+namespace {
+
+enum WideKind { W64I = 0, W64F = 1, WF16 = 2, WBF16 = 3 };
+constexpr int kWideBlock = 1024;
+constexpr int kWideSlots64 = 18432;   // 144 KiB of 8-byte slots
+constexpr int kWideSlots16 = 36864;   // 144 KiB of fp32 partials
+
+template <int KIND>
+struct Wide;
+template <>
+struct Wide<W64I> {
+  using Bin = unsigned long long;
+  using Acc = unsigned long long;
+  static constexpr int kSlots = kWideSlots64;
+};
+template <>
+struct Wide<W64F> {
+  using Bin = double;
+  using Acc = double;
+  static constexpr int kSlots = kWideSlots64;
+};
+template <>
+struct Wide<WF16> {
+  using Bin = uint16_t;
+  using Acc = float;
+  static constexpr int kSlots = kWideSlots16;
+};
+template <>
+struct Wide<WBF16> {
+  using Bin = uint16_t;
+  using Acc = float;
+  static constexpr int kSlots = kWideSlots16;
+};
+
+template <int KIND>
+__device__ __forceinline__ float half_to_f32(uint32_t h) {
+  if constexpr (KIND == WBF16) return txd::bf16_bits_to_f32(h);
+  else return float(__builtin_bit_cast(_Float16, uint16_t(h)));
+}
+
+template <int KIND>
+__device__ __forceinline__ uint32_t f32_to_half(float f) {
+  if constexpr (KIND == WBF16) return txd::f32_to_bf16_bits(f);
+  else return txd::pack_f16x2(f, 0.0f) & 0xFFFFu;
+}
+
+// The identity of each combine (fp adds start from -0, exact for IEEE add).
+template <int KIND, int OP>
+__device__ __forceinline__ typename Wide<KIND>::Acc wide_id() {
+  if constexpr (KIND == W64I) {
+    if constexpr (OP == MAX) return 0x8000000000000000ull;
+    else if constexpr (OP == MIN) return 0x7FFFFFFFFFFFFFFFull;
+    else if constexpr (OP == UMIN || OP == AND) return ~0ull;
+    else return 0ull;
+  } else {
+    return typename Wide<KIND>::Acc(-0.0);
+  }
+}
+
+template <int KIND, int OP>
+__device__ __forceinline__ bool wide_is_id(typename Wide<KIND>::Acc v) {
+  if constexpr (KIND == W64I) return v == wide_id<KIND, OP>();
+  else if constexpr (KIND == W64F) return __builtin_bit_cast(uint64_t, v) == 0x8000000000000000ull;
+  else return __builtin_bit_cast(uint32_t, v) == 0x80000000u;
+}
+
+// Combine v into *p (LDS or global, by the pointer's address space).
+template <int KIND, int OP, typename P, typename V>
+__device__ __forceinline__ void wide_atomic(P *p, V v) {
+  if constexpr (KIND == W64I) {
+    if constexpr (OP == ADD) atomicAdd(p, v);
+    else if constexpr (OP == MAX) atomicMax(reinterpret_cast<long long *>(p), (long long)v);
+    else if constexpr (OP == MIN) atomicMin(reinterpret_cast<long long *>(p), (long long)v);
+    else if constexpr (OP == UMAX) atomicMax(p, v);
+    else if constexpr (OP == UMIN) atomicMin(p, v);
+    else if constexpr (OP == AND) atomicAnd(p, v);
+    else if constexpr (OP == OR) atomicOr(p, v);
+    else atomicXor(p, v);
+  } else {
+    atomicAdd(p, v);
+  }
+}
+
+// bins16[s] = round(bins16[s] + x) through the aligned 32-bit word holding
+// it; returns the bin's prior 16 bits.
+template <int KIND>
+__device__ __forceinline__ uint32_t half_add(uint16_t *bins16, int64_t s, float x) {
+  uint16_t *h = bins16 + s;
+  uint32_t *w = reinterpret_cast<uint32_t *>(reinterpret_cast<uintptr_t>(h) & ~uintptr_t(3));
+  const int sh = (reinterpret_cast<uintptr_t>(h) & 2) ? 16 : 0;
+  uint32_t old = __atomic_load_n(w, __ATOMIC_RELAXED), assumed;
+  do {
+    assumed = old;
+    const uint32_t cur = (assumed >> sh) & 0xFFFFu;
+    const uint32_t nh = f32_to_half<KIND>(half_to_f32<KIND>(cur) + x);
+    old = atomicCAS(w, assumed, (assumed & ~(0xFFFFu << sh)) | (nh << sh));
+  } while (old != assumed);
+  return (assumed >> sh) & 0xFFFFu;
+}
+
+template <int KIND>
+__device__ __forceinline__ typename Wide<KIND>::Acc wide_val(const void *val, int64_t i) {
+  if constexpr (KIND == W64I) return static_cast<const unsigned long long *>(val)[i];
+  else if constexpr (KIND == W64F) return static_cast<const double *>(val)[i];
+  else return half_to_f32<KIND>(static_cast<const uint16_t *>(val)[i]);
+}
+
+__device__ __forceinline__ bool wide_live(const tx_scatter_args &a, int64_t i, int32_t k) {
+  return k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0);
+}
+
+// Chunk per workgroup, the bins in one LDS table.
+template <int KIND, int OP>
+__device__ __forceinline__ void wide_table(const tx_scatter_args &a) {
+  using W = Wide<KIND>;
+  using Acc = typename W::Acc;
+  __shared__ Acc table[W::kSlots];
+  const int64_t begin = int64_t(blockIdx.x) * a.per_block;
+  if (begin >= a.n) return;  // uniform
+  const int64_t end = min(begin + int64_t(a.per_block), a.n);
+  for (int s = threadIdx.x; s < a.nbins; s += kWideBlock) table[s] = wide_id<KIND, OP>();
+  __syncthreads();
+  for (int64_t i = begin + threadIdx.x; i < end; i += kWideBlock) {
+    const int32_t k = a.idx[i];
+    if (wide_live(a, i, k)) {
+      if constexpr (KIND == WF16 || KIND == WBF16) {
+        wave_lds_combine<FADD, float>(table, true, uint32_t(k), wide_val<KIND>(a.val, i));
+      } else {
+        wide_atomic<KIND, OP>(&table[k], wide_val<KIND>(a.val, i));
+      }
+    }
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < a.nbins; s += kWideBlock) {
+    const Acc v = table[s];
+    if (wide_is_id<KIND, OP>(v)) continue;
+    if constexpr (KIND == WF16 || KIND == WBF16) half_add<KIND>(static_cast<uint16_t *>(a.bins), s, v);
+    else wide_atomic<KIND, OP>(static_cast<typename W::Bin *>(a.bins) + s, v);
+  }
+}
+
+// One global atomic per update; OLD: each update's prior bin value to a.old
+// (0 for updates out of range or masked off).  XCHG: the bin takes val.
+template <int KIND, int OP, bool OLD, bool XCHG>
+__device__ __forceinline__ void wide_direct(const tx_scatter_args &a) {
+  using Bin = typename Wide<KIND>::Bin;
+  Bin *bins = static_cast<Bin *>(a.bins);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) {
+    const int32_t k = a.idx[i];
+    Bin r = Bin(0);
+    if (wide_live(a, i, k)) {
+      if constexpr (KIND == WF16 || KIND == WBF16) {
+        r = Bin(half_add<KIND>(reinterpret_cast<uint16_t *>(bins), k, wide_val<KIND>(a.val, i)));
+      } else if constexpr (XCHG) {
+        const unsigned long long v = static_cast<const unsigned long long *>(a.val)[i];
+        r = __builtin_bit_cast(Bin, atomicExch(reinterpret_cast<unsigned long long *>(bins + k), v));
+      } else if constexpr (KIND == W64F) {
+        r = atomicAdd(bins + k, wide_val<KIND>(a.val, i));
+      } else {
+        const unsigned long long v = wide_val<KIND>(a.val, i);
+        unsigned long long *p = bins + k;
+        if constexpr (OP == ADD) r = atomicAdd(p, v);
+        else if constexpr (OP == MAX) r = (unsigned long long)atomicMax(reinterpret_cast<long long *>(p), (long long)v);
+        else if constexpr (OP == MIN) r = (unsigned long long)atomicMin(reinterpret_cast<long long *>(p), (long long)v);
+        else if constexpr (OP == UMAX) r = atomicMax(p, v);
+        else if constexpr (OP == UMIN) r = atomicMin(p, v);
+        else if constexpr (OP == AND) r = atomicAnd(p, v);
+        else if constexpr (OP == OR) r = atomicOr(p, v);
+        else r = atomicXor(p, v);
+      }
+    }
+    if constexpr (OLD) static_cast<Bin *>(a.old)[i] = r;
+  }
+}
+
+}  // namespace
+
+// tx_scatter_<i64|f64|f16|bf16>_<op>_{table,direct,old}; xchg: _xchg (old optional).
+#define TX_WIDE_KERNELS(TN, KIND, ON, OP)                                                                   \
+  TX_KERNEL void __launch_bounds__(kWideBlock) tx_scatter_##TN##_##ON##_table(const tx_scatter_args a) {  \
+    wide_table<KIND, OP>(a);                                                                                \
+  }                                                                                                         \
+  TX_KERNEL void __launch_bounds__(256) tx_scatter_##TN##_##ON##_direct(const tx_scatter_args a) {         \
+    wide_direct<KIND, OP, false, false>(a);                                                                 \
+  }                                                                                                         \
+  TX_KERNEL void __launch_bounds__(256) tx_scatter_##TN##_##ON##_old(const tx_scatter_args a) {            \
+    wide_direct<KIND, OP, true, false>(a);                                                                  \
+  }
+TX_WIDE_KERNELS(i64, W64I, add, ADD)
+TX_WIDE_KERNELS(i64, W64I, max, MAX)
+TX_WIDE_KERNELS(i64, W64I, min, MIN)
+TX_WIDE_KERNELS(i64, W64I, umax, UMAX)
+TX_WIDE_KERNELS(i64, W64I, umin, UMIN)
+TX_WIDE_KERNELS(i64, W64I, and, AND)
+TX_WIDE_KERNELS(i64, W64I, or, OR)
+TX_WIDE_KERNELS(i64, W64I, xor, XOR)
+TX_WIDE_KERNELS(f64, W64F, fadd, FADD)
+TX_WIDE_KERNELS(f16, WF16, fadd, FADD)
+TX_WIDE_KERNELS(bf16, WBF16, fadd, FADD)
+
+TX_KERNEL void __launch_bounds__(256) tx_scatter_i64_xchg(const tx_scatter_args a) {
+  if (a.old) wide_direct<W64I, ADD, true, true>(a);
+  else wide_direct<W64I, ADD, false, true>(a);
+}

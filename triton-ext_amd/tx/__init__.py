@@ -43,6 +43,9 @@ _TX_DTYPE = {
     torch.float16: _lib.F16,
     torch.int32: _lib.I32,
     torch.uint32: _lib.U32,
+    torch.int64: _lib.I64,
+    torch.uint64: _lib.U64,
+    torch.float64: _lib.F64,
 }
 _FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
 
@@ -137,7 +140,10 @@ def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor
     """tt.atomic_rmw, scatter form: bins[idx[i]] (op)= val[i] for all i, in place.
 
     op: add | fadd | max | min | umax | umin | and | or | xor | xchg (as
-    tl.atomic_*; xchg takes int32, uint32 or fp32 bins).
+    tl.atomic_*).  Integer ops take int32, uint32, int64 or uint64 bins;
+    fadd takes fp32, fp64, fp16 or bf16 bins (fp16 / bf16 bins are rounded
+    once per workgroup partial, summed in fp32); xchg takes any 32- or
+    64-bit bins.
     Updates with idx outside [0, len(bins)) or mask[i] == 0 are dropped.
     return_old=True returns, per update, the bin's value before it (the
     tt.atomic_rmw result); that form does no pre-aggregation.
