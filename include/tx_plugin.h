@@ -303,6 +303,17 @@ TX_API tx_status tx_atomic_rmw_scatter(void *bins, tx_dtype bins_type,
                                        tx_stream_t stream);
 
 /*
+ * tt.histogram (passed through beside the atomics at
+ * uTLXConversionPatterns.cpp:605; Triton's tl.histogram(x, num_bins, mask)):
+ * counts[b] = the number of i < n with mask[i] != 0 (mask may be NULL) and
+ * x[i] == b, for 0 <= b < num_bins; values outside [0, num_bins) are not
+ * counted.  counts (int32[num_bins]) is overwritten.  Served by the
+ * aggregating scatter of tx_atomic_rmw_scatter with one added per update.
+ */
+TX_API tx_status tx_histogram(const int32_t *x, const uint8_t *mask, int64_t n, int32_t *counts,
+                              int64_t num_bins, tx_stream_t stream);
+
+/*
  * tt.atomic_cas in scatter form: for every i < n with mask[i] != 0 (mask may
  * be NULL) and 0 <= idx[i] < nbins, atomically
  *   old[i] = bins[idx[i]]; if (old[i] == cmp[i]) bins[idx[i]] = val[i];

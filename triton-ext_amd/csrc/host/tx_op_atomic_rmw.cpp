@@ -50,6 +50,62 @@ unsigned direct_grid(int64_t n) {
 
 }  // namespace
 
+// The aggregating forms (no old values, 32-bit bins): LDS windows or the
+// hash table; args.val == NULL adds 1 per update (tt.histogram).
+static tx_status aggregate(tx_scatter_args args, const char *name, hipStream_t s) {
+  const int64_t n = args.n, nbins = args.nbins;
+  const int cus = cu_count();
+  char kname[64];
+  const int64_t windows = (nbins + kDirectSlots - 1) / kDirectSlots;
+  hipFunction_t fn;
+  if (windows <= kMaxWindows) {
+    std::snprintf(kname, sizeof kname, "tx_scatter_%s_windowed", name);
+    TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+    // One workgroup per CU at a time (the table fills a CU's LDS) and one
+    // chunk of updates per workgroup; the workgroup itself makes one pass
+    // per window, or a single pass when its chunk's keys are skewed.
+    int64_t chunks = std::max<int64_t>(8, cus);
+    int64_t per = (n + chunks - 1) / chunks;
+    per = (per + kWinStep - 1) / kWinStep * kWinStep;
+    if (per > INT32_MAX) per = INT32_MAX / kWinStep * kWinStep;
+    chunks = (n + per - 1) / per;
+    args.per_block = int32_t(per);
+    args.splits = int32_t(windows);
+    args.window = int32_t(kDirectSlots);
+    if (windows == 1) return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
+    // Several windows: a workgroup whose keys are skewed makes one pass with
+    // its best window and writes the in-range updates outside it to its
+    // wavefronts' regions of a spill buffer in stream scratch (slot 0); a
+    // second launch of the same kernel folds those records (unused ones are
+    // marked out of range) into the bins, with direct global atomics for
+    // whatever spills again.  Without the buffer the first launch sends its
+    // spills to global atomics itself.
+    const int64_t records = chunks * (kAggBlock / 64) * kSpillWave;
+    ScratchLease sp;  // held until both launches are enqueued
+    if (sp.acquire(s, 0, size_t(records) * 8) != TX_SUCCESS) {
+      clear_error();
+      return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
+    }
+    args.spill_keys = static_cast<uint32_t *>(sp.ptr());
+    args.spill_vals = args.spill_keys + records;
+    args.spill_wave = int32_t(kSpillWave);
+    TX_TRY(launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname));
+    tx_scatter_args fold{args.bins, reinterpret_cast<const int32_t *>(args.spill_keys), args.spill_vals, nullptr,
+                         nullptr, records, int32_t(nbins), int32_t(kSpillChunk), int32_t(windows),
+                         int32_t(kDirectSlots)};
+    const int64_t fold_chunks = (records + kSpillChunk - 1) / kSpillChunk;
+    return launch(fn, unsigned(fold_chunks), 1, kAggBlock, s, &fold, sizeof fold, kname);
+  }
+  std::snprintf(kname, sizeof kname, "tx_scatter_%s_hashed", name);
+  TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+  int64_t per = (n + cus - 1) / cus;
+  per = (per + kAggStep - 1) / kAggStep * kAggStep;
+  if (per > INT32_MAX) per = INT32_MAX / kAggStep * kAggStep;
+  args.per_block = int32_t(per);
+  const int64_t grid = (n + per - 1) / per;
+  return launch(fn, unsigned(grid), 1, kAggBlock, s, &args, sizeof args, kname);
+}
+
 // 64-bit and 16-bit float bins (tx_scatter_<type>_<op>_{table,direct,old},
 // tx_scatter_i64_xchg in scatter.hip): an LDS table per workgroup when the
 // bins fit one (and the updates are at least twice the bins), one global
@@ -146,54 +202,7 @@ static tx_status atomic_rmw_scatter(void *bins, tx_dtype bins_type, int64_t nbin
     return launch(fn, unsigned(grid), 1, 256, s, &args, sizeof args, kname);
   }
   if (nbins == 0) return TX_SUCCESS;  // every update is out of range
-  const int64_t windows = (nbins + kDirectSlots - 1) / kDirectSlots;
-  hipFunction_t fn;
-  if (windows <= kMaxWindows) {
-    std::snprintf(kname, sizeof kname, "tx_scatter_%s_windowed", name);
-    TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
-    // One workgroup per CU at a time (the table fills a CU's LDS) and one
-    // chunk of updates per workgroup; the workgroup itself makes one pass
-    // per window, or a single pass when its chunk's keys are skewed.
-    int64_t chunks = std::max<int64_t>(8, cus);
-    int64_t per = (n + chunks - 1) / chunks;
-    per = (per + kWinStep - 1) / kWinStep * kWinStep;
-    if (per > INT32_MAX) per = INT32_MAX / kWinStep * kWinStep;
-    chunks = (n + per - 1) / per;
-    args.per_block = int32_t(per);
-    args.splits = int32_t(windows);
-    args.window = int32_t(kDirectSlots);
-    if (windows == 1) return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
-    // Several windows: a workgroup whose keys are skewed makes one pass with
-    // its best window and writes the in-range updates outside it to its
-    // wavefronts' regions of a spill buffer in stream scratch (slot 0); a
-    // second launch of the same kernel folds those records (unused ones are
-    // marked out of range) into the bins, with direct global atomics for
-    // whatever spills again.  Without the buffer the first launch sends its
-    // spills to global atomics itself.
-    const int64_t records = chunks * (kAggBlock / 64) * kSpillWave;
-    ScratchLease sp;  // held until both launches are enqueued
-    if (sp.acquire(s, 0, size_t(records) * 8) != TX_SUCCESS) {
-      clear_error();
-      return launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname);
-    }
-    args.spill_keys = static_cast<uint32_t *>(sp.ptr());
-    args.spill_vals = args.spill_keys + records;
-    args.spill_wave = int32_t(kSpillWave);
-    TX_TRY(launch(fn, unsigned(chunks), 1, kAggBlock, s, &args, sizeof args, kname));
-    tx_scatter_args fold{bins, reinterpret_cast<const int32_t *>(args.spill_keys), args.spill_vals, nullptr,
-                         nullptr, records, int32_t(nbins), int32_t(kSpillChunk), int32_t(windows),
-                         int32_t(kDirectSlots)};
-    const int64_t fold_chunks = (records + kSpillChunk - 1) / kSpillChunk;
-    return launch(fn, unsigned(fold_chunks), 1, kAggBlock, s, &fold, sizeof fold, kname);
-  }
-  std::snprintf(kname, sizeof kname, "tx_scatter_%s_hashed", name);
-  TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
-  int64_t per = (n + cus - 1) / cus;
-  per = (per + kAggStep - 1) / kAggStep * kAggStep;
-  if (per > INT32_MAX) per = INT32_MAX / kAggStep * kAggStep;
-  args.per_block = int32_t(per);
-  const int64_t grid = (n + per - 1) / per;
-  return launch(fn, unsigned(grid), 1, kAggBlock, s, &args, sizeof args, kname);
+  return aggregate(args, name, s);
 }
 
 // Table form: operands = {bins (result slot), idx, val, mask, old, nbins, n,
@@ -263,6 +272,50 @@ static tx_status atomic_cas_op(tx_value *v, size_t count, tx_stream_t stream) {
                             static_cast<const uint8_t *>(mask), n, old, stream);
 }
 
+// tt.histogram (passed through beside the atomics,
+// uTLXConversionPatterns.cpp:605; Triton's tl.histogram(x, num_bins) with
+// its optional mask): counts[b] = #{i < n : mask[i] != 0, x[i] == b} for
+// 0 <= b < num_bins, values outside the range not counted.  counts is
+// overwritten: a zero-fill launch, then the aggregating integer-add scatter
+// with one per update (no value array is read).
+static tx_status histogram(const int32_t *x, const uint8_t *mask, int64_t n, int32_t *counts, int64_t num_bins,
+                           tx_stream_t stream) {
+  const char *what = "tx_histogram";
+  if (n < 0 || num_bins < 0)
+    return fail(TX_INVALID_ARGUMENT, "%s: n = %lld, num_bins = %lld", what, (long long)n, (long long)num_bins);
+  if (num_bins > INT32_MAX) return fail(TX_UNSUPPORTED, "%s: num_bins exceeds int32 indexing", what);
+  if (num_bins == 0) return TX_SUCCESS;
+  if (!counts || (n > 0 && !x)) return fail(TX_INVALID_ARGUMENT, "%s: NULL buffer", what);
+  if (!aligned(counts, 4) || !aligned(x, 4))
+    return fail(TX_INVALID_ARGUMENT, "%s: x and counts must be 4-byte aligned", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  tx_scatter_args zero{counts, nullptr, nullptr, nullptr, nullptr, num_bins, 0, 0, 0, 0};
+  hipFunction_t fn;
+  TX_TRY(get_kernel(CodeObject::Scatter, "tx_scatter_zero_bins", &fn));
+  TX_TRY(launch(fn, direct_grid(num_bins), 1, 256, s, &zero, sizeof zero, "tx_scatter_zero_bins"));
+  if (n == 0) return TX_SUCCESS;
+  tx_scatter_args args{counts, x, nullptr, mask, nullptr, n, int32_t(num_bins), 0, 0, 0};
+  return aggregate(args, "add", s);
+}
+
+// Table form: operands = {counts (result slot, int32[num_bins]), x:i32*,
+// mask:u8*|NULL, n, num_bins}.
+static tx_status histogram_op(tx_value *v, size_t count, tx_stream_t stream) {
+  Operands o{v, count, "tt.histogram"};
+  TX_TRY(o.need(5));
+  void *counts, *x, *mask;
+  int64_t n, nb;
+  TX_TRY(o.ptr(0, &counts));
+  TX_TRY(o.ptr(1, &x));
+  TX_TRY(o.ptr(2, &mask));
+  TX_TRY(o.integer(3, &n));
+  TX_TRY(o.integer(4, &nb));
+  return histogram(static_cast<const int32_t *>(x), static_cast<const uint8_t *>(mask), n,
+                   static_cast<int32_t *>(counts), nb, stream);
+}
+
+static const bool registered_histogram = register_op(
+    "tt.histogram", histogram_op, "counts:i32*(result, num_bins), x:i32*, mask:u8*|null, n:i64, num_bins:i64");
 static const bool registered = register_op(
     "tt.atomic_rmw", atomic_rmw_op,
     "bins(result), idx:i32*, val, mask:u8*|null, old|null, nbins:i64, n:i64, "
@@ -288,4 +341,10 @@ extern "C" TX_API tx_status tx_atomic_cas_scatter(void *bins, tx_dtype bins_type
                                                   void *old, tx_stream_t stream) {
   tx::clear_error();
   return tx::atomic_cas_scatter(bins, bins_type, nbins, idx, cmp, val, mask, n, old, stream);
+}
+
+extern "C" TX_API tx_status tx_histogram(const int32_t *x, const uint8_t *mask, int64_t n, int32_t *counts,
+                                         int64_t num_bins, tx_stream_t stream) {
+  tx::clear_error();
+  return tx::histogram(x, mask, n, counts, num_bins, stream);
 }

@@ -259,7 +259,8 @@ struct Scatter {
     const T *vals = reinterpret_cast<const T *>(a.val);
     if (vec && e + 4 <= end) {
       const txd::i32x4 k4 = __builtin_nontemporal_load(reinterpret_cast<const txd::i32x4 *>(idx + e));
-      const txd::u32x4 v4 = __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(vals + e));
+      const txd::u32x4 v4 = vals ? __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(vals + e))
+                                 : txd::u32x4{1u, 1u, 1u, 1u};
       uint32_t mbits = 0xFFFFFFFFu;
       if (a.mask) mbits = *reinterpret_cast<const uint32_t *>(a.mask + e);
       const int32_t kk[4] = {k4.x, k4.y, k4.z, k4.w};
@@ -280,7 +281,7 @@ struct Scatter {
         if (ok[j]) {
           const int32_t k = idx[i];
           key[j] = uint32_t(k);
-          val[j] = vals[i];
+          val[j] = vals ? vals[i] : __builtin_bit_cast(T, 1u);
           ok[j] = k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0);
         }
       }
@@ -293,7 +294,9 @@ struct Scatter {
   static __device__ __forceinline__ void fetch(const tx_scatter_args &a, int64_t e, txd::i32x4 &k,
                                                txd::u32x4 &v, uint32_t &m) {
     k = __builtin_nontemporal_load(reinterpret_cast<const txd::i32x4 *>(a.idx + e));
-    v = __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(a.val) + e / 4);
+    // no values: every update adds 1 (tt.histogram through the integer add)
+    v = a.val ? __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(a.val) + e / 4)
+              : txd::u32x4{1u, 1u, 1u, 1u};
     if constexpr (MASK) m = *reinterpret_cast<const uint32_t *>(a.mask + e);
     else m = 0xFFFFFFFFu;
   }
@@ -955,4 +958,11 @@ TX_WIDE_KERNELS(bf16, WBF16, fadd, FADD)
 TX_KERNEL void __launch_bounds__(256) tx_scatter_i64_xchg(const tx_scatter_args a) {
   if (a.old) wide_direct<W64I, ADD, true, true>(a);
   else wide_direct<W64I, ADD, false, true>(a);
+}
+
+// counts[0 .. n) = 0 before a histogram's scatter (a kernel rather than a
+// memset, so that a captured graph holds no memset node).
+TX_KERNEL void __launch_bounds__(256) tx_scatter_zero_bins(const tx_scatter_args a) {
+  uint32_t *b = static_cast<uint32_t *>(a.bins);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) b[i] = 0u;
 }

@@ -169,6 +169,21 @@ def atomic_rmw(op: str, bins: torch.Tensor, idx: torch.Tensor, val: torch.Tensor
     return old if return_old else bins
 
 
+def histogram(x: torch.Tensor, num_bins: int, mask: torch.Tensor | None = None) -> torch.Tensor:
+    """tt.histogram (tl.histogram(x, num_bins, mask)): int32 counts of the
+    values 0 .. num_bins - 1 among x (int32) where mask (if given) is nonzero;
+    values outside the range are not counted."""
+    _on_gpu(x, mask)
+    if x.dtype != torch.int32 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous int32 tensor")
+    if mask is not None and (mask.numel() != x.numel() or mask.dtype not in (torch.uint8, torch.bool)
+                             or not mask.is_contiguous()):
+        raise ValueError("mask must be a contiguous uint8 / bool tensor of x's size")
+    counts = torch.empty(int(num_bins), dtype=torch.int32, device=x.device)
+    check(lib.tx_histogram(_ptr(x), _ptr(mask), x.numel(), _ptr(counts), int(num_bins), _stream(x)))
+    return counts
+
+
 def atomic_cas(bins: torch.Tensor, idx: torch.Tensor, cmp: torch.Tensor, val: torch.Tensor,
                mask: torch.Tensor | None = None, return_old: bool = True):
     """tt.atomic_cas, scatter form: for every i (not masked off, idx in range),

@@ -42,7 +42,7 @@ B_NK, B_KN = 0, 1
 EXPORTED = [
     "txGetPluginInfo", "txReleasePluginInfo", "txFindOp", "txInvokeOp",
     "txGetLastError", "txInit", "txShutdown", "txVersion", "txScratchAllocations", "txStreamCeiling",
-    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_atomic_cas_scatter",
+    "tx_fp_to_fp", "tx_fp_to_fp_with_rbits", "tx_atomic_rmw_scatter", "tx_atomic_cas_scatter", "tx_histogram",
     "tx_dot_bf16", "tx_dot", "tx_dot_acc",
     "tx_dot_fp8_scaled", "tx_dot_fp8_scaled_ex", "tx_dot_fp8_scaled_grouped",
     "tx_dot_fp8_scaled_grouped_noalloc", "tx_dot_fp8_scaled_batched",
@@ -126,6 +126,8 @@ def _load():
     L.tx_fp_to_fp_with_rbits.restype = I
     L.tx_atomic_rmw_scatter.argtypes = [P, I, I64, P, P, P, I64, I, P, VP]
     L.tx_atomic_rmw_scatter.restype = I
+    L.tx_histogram.argtypes = [P, P, I64, P, I64, VP]
+    L.tx_histogram.restype = I
     L.tx_atomic_cas_scatter.argtypes = [P, I, I64, P, P, P, P, I64, P, VP]
     L.tx_atomic_cas_scatter.restype = I
     L.tx_dot_bf16.argtypes = [P, I64, P, I64, P, I64, I64, I64, I64, VP]
