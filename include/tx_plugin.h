@@ -95,7 +95,8 @@ typedef enum tx_dtype {
                     the lower K index in the low nibble (tx_dot_scaled_mx operands) */
   TX_I64 = 8,     /* tl.int64 (tx_atomic_rmw_scatter bins) */
   TX_U64 = 9,     /* tl.uint64 */
-  TX_F64 = 10     /* tl.float64 */
+  TX_F64 = 10,    /* tl.float64 */
+  TX_I8 = 11      /* tl.int8 (tx_dot_acc operands) */
 } tx_dtype;
 
 /* Rounding modes, numbered as the rounding operand of
@@ -378,7 +379,11 @@ TX_API tx_status tx_dot(const void *A, tx_dtype ab_type, int64_t lda,
  * 16-bit ones, rounded once to d_type (TX_F32, TX_BF16 or TX_F16, nearest
  * even).  Operands: bf16 or fp16 (a_type == b_type; scale_a, scale_b NULL;
  * B stored N x K or row-major K x N as tx_dot), or fp8 (TX_FP8E4M3FN /
- * TX_FP8E5M2 in any pairing, B stored N x K, fp32 scale_a[M], scale_b[N]).
+ * TX_FP8E5M2 in any pairing, B stored N x K, fp32 scale_a[M], scale_b[N]),
+ * or fp32 (both; fp32 products and sums, input precision "ieee", d_type
+ * TX_F32), or int8 (both TX_I8; exact int32 sums wrapping modulo 2^32,
+ * d_type TX_I32, C then holds int32), these two with B stored N x K and
+ * NULL scales.
  * C: fp32 row-major M x N (ldc elements), or NULL for D = round_d(s * A.B);
  * C may be D itself when d_type is TX_F32 and ldc == ldd (accumulating in
  * place, as the reference's K loop does).  Non-finite values propagate as in

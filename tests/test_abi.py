@@ -204,7 +204,7 @@ _P = ctypes.c_void_p(256)   # a non-NULL, 256-byte aligned stand-in: these calls
     (lambda L: L.tx_dot_acc(_P, 6, 64, _P, _P, 6, 0, 64, _P, None, 0, _P, 0, 64, 64, 64, 64, None),
      "INVALID_ARGUMENT", "scale vectors are for fp8"),
     (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 3, 0, 64, None, _P, 64, _P, 3, 64, 64, 64, 64, None),
-     "INVALID_ARGUMENT", "only for an fp32 D"),
+     "INVALID_ARGUMENT", "only for an fp32 / int32 D"),
     (lambda L: L.tx_dot_acc(_P, 3, 64, None, _P, 3, 0, 64, None, _P, 32, _P, 0, 64, 64, 64, 64, None),
      "INVALID_ARGUMENT", "ldc >= N"),
     # quantisers: K a multiple of the 32-element block; input and code types

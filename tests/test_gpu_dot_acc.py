@@ -189,7 +189,7 @@ def test_dot_acc_table_op_and_errors(tx, oracle, dev):
     st = L.tx_dot_acc(ctypes.c_void_p(at.data_ptr()), lib.BF16, K, None, ctypes.c_void_p(bt.data_ptr()),
                       lib.BF16, lib.B_NK, K, None, ctypes.c_void_p(c.data_ptr()), N,
                       ctypes.c_void_p(c.data_ptr()), lib.BF16, N, M, N, K, None)
-    assert st == lib.INVALID_ARGUMENT and "only for an fp32 D" in lib.last_error()
+    assert st == lib.INVALID_ARGUMENT and "only for an fp32 / int32 D" in lib.last_error()
     q = torch.zeros((M, K), dtype=torch.uint8, device=dev)
     s1 = torch.ones(M, dtype=torch.float32, device=dev)
     st = L.tx_dot_acc(ctypes.c_void_p(q.data_ptr()), lib.FP8E4M3FN, K, ctypes.c_void_p(s1.data_ptr()),
@@ -200,3 +200,56 @@ def test_dot_acc_table_op_and_errors(tx, oracle, dev):
                       lib.FP8E4M3FN, lib.B_NK, K, None, None, 0, ctypes.c_void_p(D1.data_ptr()), lib.BF16, N,
                       M, N, K, None)
     assert st == lib.INVALID_ARGUMENT and "scale" in lib.last_error()
+
+
+@pytest.mark.parametrize("M,N,K,pad", [(1, 1, 1, 0), (17, 19, 23, 0), (128, 128, 128, 0), (300, 500, 4100, 0),
+                                       (1024, 1100, 256, 0), (255, 257, 1031, 1), (600, 700, 999, 3)])
+def test_dot_int8_exact(tx, dev, M, N, K, pad):
+    """tt.dot on int8 operands: exact int32 sums (v_mfma_i32_16x16x64_i8),
+    plus an int32 accumulator; rows padded by `pad` bytes take the narrower
+    loads (1 byte: any alignment)."""
+    g = np.random.default_rng(M + N + K + pad)
+    a = g.integers(-128, 128, (M, K), dtype=np.int64)
+    b = g.integers(-128, 128, (N, K), dtype=np.int64)
+    c = g.integers(-2**20, 2**20, (M, N)).astype(np.int32)
+
+    def put(x):
+        w = np.zeros((x.shape[0], x.shape[1] + pad), np.int8)
+        w[:, :x.shape[1]] = x
+        return torch.from_numpy(w).to(dev)[:, :x.shape[1]]
+
+    D = tx.dot_acc(put(a), put(b), torch.from_numpy(c).to(dev))
+    assert D.dtype == torch.int32
+    want = (a @ b.T + c).astype(np.int64)
+    assert np.array_equal(D.cpu().numpy().astype(np.int64), want)
+
+
+def test_dot_int8_wraps_modulo_2_32(tx, dev):
+    """int32 accumulation wraps: an accumulator near 2^31 plus positive sums."""
+    M, N, K = 64, 64, 1024
+    a = np.full((M, K), 127, np.int8)
+    b = np.full((N, K), 127, np.int8)
+    c = np.full((M, N), 2**31 - 1000, np.int32)
+    D = tx.dot_acc(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), torch.from_numpy(c).to(dev))
+    want = ((127 * 127 * K + (2**31 - 1000)) & 0xFFFFFFFF)
+    want = want - 2**32 if want >= 2**31 else want
+    assert np.all(D.cpu().numpy() == want)
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 19, 23), (300, 500, 1000), (1024, 1024, 1024), (513, 129, 77)])
+def test_dot_fp32(tx, dev, M, N, K):
+    """tt.dot on fp32 operands (input precision ieee): integer values give
+    exact sums, bit for bit; N(0,1) values stay within K * 2^-23 of the
+    float64 product relative to the sum of |products|."""
+    g = np.random.default_rng(M + K)
+    ai = g.integers(-8, 9, (M, K)).astype(np.float32)
+    bi = g.integers(-8, 9, (N, K)).astype(np.float32)
+    c = g.integers(-100, 101, (M, N)).astype(np.float32)
+    D = tx.dot_acc(torch.from_numpy(ai).to(dev), torch.from_numpy(bi).to(dev), torch.from_numpy(c).to(dev))
+    assert np.array_equal(D.cpu().numpy(), (ai.astype(np.float64) @ bi.astype(np.float64).T + c).astype(np.float32))
+    an = g.standard_normal((M, K)).astype(np.float32)
+    bn = g.standard_normal((N, K)).astype(np.float32)
+    E = tx.dot_acc(torch.from_numpy(an).to(dev), torch.from_numpy(bn).to(dev)).cpu().numpy().astype(np.float64)
+    ref = an.astype(np.float64) @ bn.astype(np.float64).T
+    mag = np.abs(an.astype(np.float64)) @ np.abs(bn.astype(np.float64)).T
+    assert np.all(np.abs(E - ref) <= K * 2.0 ** -23 * mag)

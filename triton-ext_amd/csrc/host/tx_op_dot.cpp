@@ -532,15 +532,23 @@ static tx_status dot_acc(const void *A, tx_dtype a_type, int64_t lda, const floa
   const char *fa = fp8_name(a_type), *fb = fp8_name(b_type);
   const bool fp8 = fa && fb;
   const bool b16 = (a_type == TX_BF16 || a_type == TX_F16) && b_type == a_type;
-  if (!fp8 && !b16)
-    return fail(TX_INVALID_ARGUMENT, "%s: operands must be bf16 or fp16 (both the same) or fp8 (got %d, %d)",
-                what, int(a_type), int(b_type));
+  const bool f32 = a_type == TX_F32 && b_type == TX_F32, i8 = a_type == TX_I8 && b_type == TX_I8;
+  if (!fp8 && !b16 && !f32 && !i8)
+    return fail(TX_INVALID_ARGUMENT,
+                "%s: operands must be bf16, fp16, fp32 or int8 (both the same) or fp8 (got %d, %d)", what,
+                int(a_type), int(b_type));
   if (layout != TX_B_NK && layout != TX_B_KN)
     return fail(TX_INVALID_ARGUMENT, "%s: B layout %d", what, int(layout));
-  if (fp8 && layout != TX_B_NK) return fail(TX_UNSUPPORTED, "%s: fp8 operands take B stored N x K", what);
-  if (d_type != TX_F32 && d_type != TX_BF16 && d_type != TX_F16)
+  if (!b16 && layout != TX_B_NK)
+    return fail(TX_UNSUPPORTED, "%s: fp8, fp32 and int8 operands take B stored N x K", what);
+  if (f32 || i8) {
+    if (d_type != (f32 ? TX_F32 : TX_I32))
+      return fail(TX_INVALID_ARGUMENT, "%s: %s operands give %s output (got type %d)", what, f32 ? "fp32" : "int8",
+                  f32 ? "fp32" : "int32", int(d_type));
+  } else if (d_type != TX_F32 && d_type != TX_BF16 && d_type != TX_F16) {
     return fail(TX_INVALID_ARGUMENT, "%s: output type must be fp32, bf16 or fp16 (got %d)", what, int(d_type));
-  const size_t de = d_type == TX_F32 ? 4 : 2;
+  }
+  const size_t de = (d_type == TX_F32 || d_type == TX_I32) ? 4 : 2;
   const bool kn = layout == TX_B_KN && K > 0;
   TX_TRY(check_gemm(what, A, lda, B, kn ? K : ldb, D, ldd, M, N, K, de));
   if (kn && ldb < N)
@@ -554,10 +562,23 @@ static tx_status dot_acc(const void *A, tx_dtype a_type, int64_t lda, const floa
   if (Cacc) {
     if (ld_acc < N || !aligned(Cacc, 4))
       return fail(TX_INVALID_ARGUMENT, "%s: C needs ldc >= N and 4-byte alignment", what);
-    if (static_cast<const void *>(Cacc) == D && !(d_type == TX_F32 && ld_acc == ldd))
-      return fail(TX_INVALID_ARGUMENT, "%s: C may be D itself only for an fp32 D with the same stride", what);
+    if (static_cast<const void *>(Cacc) == D && !(de == 4 && ld_acc == ldd))
+      return fail(TX_INVALID_ARGUMENT, "%s: C may be D itself only for an fp32 / int32 D with the same stride",
+                  what);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (f32 || i8) {
+    // the generic 128 x 128 tile with 32-bit outputs; its epilogue adds C
+    const int es = f32 ? 4 : 1;
+    static const int wf[] = {16, 8, 4}, wi[] = {16, 4, 1};
+    const int vec = pick_vec(A, lda * es, B, ldb * es, K * es, f32 ? wf : wi, 3);
+    tx_gemm_args g{A, B, D, nullptr, nullptr, lda, ldb, ldd, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
+    g.acc = Cacc;
+    g.ld_acc = ld_acc;
+    char kname[48];
+    std::snprintf(kname, sizeof kname, "tx_gemm_%s_128x128_v%d", f32 ? "f32" : "i8", vec);
+    return launch_gemm(kname, CodeObject::GemmBf16, g, 128, 128, s);
+  }
   tx_gemm_args args{A, B, D, sa, sb, lda, ldb, ldd, int32_t(M), int32_t(N), int32_t(K), 0, 0, 0};
   args.epi = 1;
   args.act = EPI_ACT_NONE;

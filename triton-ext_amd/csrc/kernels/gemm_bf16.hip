@@ -24,6 +24,15 @@ using namespace txg;
   TX_GEMM16(PFX, EL, SFX, OUT, 128x128, 128, 128, 2, 2, 8)            \
   TX_GEMM16(PFX, EL, SFX, OUT, 128x128, 128, 128, 2, 2, 2)
 
+// fp32 and int8 tt.dot (tx_dot_acc): tx_gemm_{f32,i8}_128x128_v<load width>
+// (the 256 x 256 tile's accumulators and 32-bit fragments spill)
+#define TX_GEMM32_GENERIC(PFX, EL, OUT, V0, V1, V2)            \
+  TX_GEMM16(PFX, EL, , OUT, 128x128, 128, 128, 2, 2, V0)      \
+  TX_GEMM16(PFX, EL, , OUT, 128x128, 128, 128, 2, 2, V1)      \
+  TX_GEMM16(PFX, EL, , OUT, 128x128, 128, 128, 2, 2, V2)
+TX_GEMM32_GENERIC(f32, EL_F32, OUT_F32, 16, 8, 4)
+TX_GEMM32_GENERIC(i8, EL_I8, OUT_I32, 16, 4, 1)
+
 TX_GEMM16_GENERIC(bf16, EL_BF16, , OUT_BF16)
 TX_GEMM16_GENERIC(bf16, EL_BF16, _out_f16, OUT_F16)
 TX_GEMM16_GENERIC(f16, EL_F16, , OUT_F16)

@@ -7,16 +7,20 @@
 namespace txg {
 
 // Operand element kinds for the MFMA selection.
-enum { EL_BF16 = 0, EL_E4M3 = 1, EL_E5M2 = 2, EL_E2M1 = 4, EL_F16 = 5 };  // e2m1: fp4, two per byte along K
+enum { EL_BF16 = 0, EL_E4M3 = 1, EL_E5M2 = 2, EL_E2M1 = 4, EL_F16 = 5, EL_F32 = 6, EL_I8 = 7 };  // e2m1: fp4, two per byte along K
 
-// Output element types of the tiles (16-bit kinds round to nearest even).
-enum GemmOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2 };
+// Output element types of the tiles (16-bit kinds round to nearest even;
+// int32: the int8 dot's exact sums, wrapping modulo 2^32).
+enum GemmOut { OUT_BF16 = 0, OUT_F16 = 1, OUT_F32 = 2, OUT_I32 = 3 };
 
 template <int EL_A, int EL_B, int BM_, int BN_, int WM_, int WN_, int VEC_>
 struct GemmCfg {
   static constexpr int EL_A_ = EL_A, EL_B_ = EL_B;
-  static constexpr bool FP8 = EL_A != EL_BF16 && EL_A != EL_F16;  // else 16-bit operands
+  static constexpr bool FP8 = EL_A == EL_E4M3 || EL_A == EL_E5M2 || EL_A == EL_E2M1;  // the f8f6f4 MFMA
   static constexpr bool F16 = EL_A == EL_F16;
+  static constexpr bool F32 = EL_A == EL_F32;  // fp32 operands (v_mfma_f32_16x16x4_f32)
+  static constexpr bool I8 = EL_A == EL_I8;    // int8 operands (v_mfma_i32_16x16x64_i8)
+  static constexpr int ES = F32 ? 4 : (FP8 || I8) ? 1 : 2;  // operand bytes per element
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, VEC = VEC_;
   static constexpr int T = 64 * WM * WN;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -33,7 +37,24 @@ template <int EL> struct F8Code { static constexpr int v = EL == EL_E5M2 ? 1 : E
 
 template <class C>
 __device__ __forceinline__ f32x4 mfma_step(f32x4 acc, const u32x4 (&mfa)[2], const u32x4 (&mfb)[2]) {
-  if constexpr (C::F16) {
+  if constexpr (C::F32) {
+    // 8 fp32 K values per lane: one 4-K instruction per value (lane group g
+    // holds K 8g .. 8g + 7 of the step, so instruction j sums K j, 8 + j, ...)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(mfa[h][j]), __uint_as_float(mfb[h][j]), acc,
+                                                   0, 0, 0);
+  } else if constexpr (C::I8) {
+    // the int32 accumulators live in the fp32 registers' bits
+    txd::i32x4 c = __builtin_bit_cast(txd::i32x4, acc);
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(txd::i32x4, mfa[0]),
+                                              __builtin_bit_cast(txd::i32x4, mfb[0]), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(txd::i32x4, mfa[1]),
+                                              __builtin_bit_cast(txd::i32x4, mfb[1]), c, 0, 0, 0);
+    acc = __builtin_bit_cast(f32x4, c);
+  } else if constexpr (C::F16) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(txd::f16x8, mfa[0]),
                                                  __builtin_bit_cast(txd::f16x8, mfb[0]), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(txd::f16x8, mfa[1]),
@@ -57,7 +78,9 @@ __device__ __forceinline__ f32x4 mfma_step(f32x4 acc, const u32x4 (&mfa)[2], con
 
 template <class C, int OUT = OUT_BF16>
 __device__ __forceinline__ void gemm_tile(const tx_gemm_args &a) {
-  static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "generic tile: bf16 out, or fp16 out of 16-bit operands");
+  static_assert((C::F32 && OUT == OUT_F32) || (C::I8 && OUT == OUT_I32) ||
+                    (!C::F32 && !C::I8 && (OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8))),
+                "generic tile: bf16 out, fp16 out of 16-bit operands, fp32 out of fp32, int32 out of int8");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE_BYTES];
 
   int tm, tn;
@@ -65,7 +88,7 @@ __device__ __forceinline__ void gemm_tile(const tx_gemm_args &a) {
   const int m0 = tm * C::BM, n0 = tn * C::BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % C::WM, wn = wave / C::WM;
-  constexpr int ES = C::FP8 ? 1 : 2;
+  constexpr int ES = C::ES;
   const int kb_end = a.K * ES;
   const int ksteps = (kb_end + kRowBytes - 1) / kRowBytes;
   const uint8_t *Ab = reinterpret_cast<const uint8_t *>(a.A);
@@ -149,6 +172,34 @@ __device__ __forceinline__ void gemm_tile(const tx_gemm_args &a) {
   }
 
   // Epilogue: lane owns C[m][n .. n+3] of every 16x16 block.
+  if constexpr (OUT == OUT_F32 || OUT == OUT_I32) {
+    // 32-bit outputs (fp32 and int8 operands), plus tt.dot's accumulator
+    // operand when given (fp32, or int32 bits for int8: added modulo 2^32)
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int m = m0 + wm * C::WTM + fm * 16 + frow;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn) {
+        const int n = n0 + wn * C::WTN + fn * 16 + 4 * fg;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (n + j >= a.N) continue;
+          const int64_t ci = int64_t(m) * a.ldc + n + j, ai = int64_t(m) * a.ld_acc + n + j;
+          if constexpr (OUT == OUT_I32) {
+            uint32_t r = __float_as_uint(acc[fn][fm][j]);
+            if (a.acc) r += reinterpret_cast<const uint32_t *>(a.acc)[ai];
+            static_cast<uint32_t *>(a.C)[ci] = r;
+          } else {
+            float r = acc[fn][fm][j];
+            if (a.acc) r += a.acc[ai];
+            static_cast<float *>(a.C)[ci] = r;
+          }
+        }
+      }
+    }
+    return;
+  }
   uint16_t *Cb = reinterpret_cast<uint16_t *>(a.C);
   const bool cvec = ((reinterpret_cast<uintptr_t>(a.C) & 7) == 0) && ((a.ldc & 3) == 0);
 #pragma unroll

@@ -46,6 +46,7 @@ _TX_DTYPE = {
     torch.int64: _lib.I64,
     torch.uint64: _lib.U64,
     torch.float64: _lib.F64,
+    torch.int8: _lib.I8,
 }
 _FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
 
@@ -287,18 +288,24 @@ def dot_acc(a: torch.Tensor, b: torch.Tensor, acc: torch.Tensor | None = None, *
     column-major operand (``b_layout="nk"``) or row-major K x N (``"kn"``,
     16-bit operands only).  Operands both bf16 or both fp16, or fp8 (any
     pairing) with fp32 ``scale_a[M]`` and ``scale_b[N]`` multiplying the
-    product.  acc: fp32 M x N or None; out: fp32 (default), bf16 or fp16, and
-    may be acc itself when fp32 (accumulate in place)."""
+    product.  Two fp32 operands give fp32 (ieee products and sums) and two
+    int8 operands int32 (exact, wrapping), both with b as N x K.  acc: fp32
+    (int32 for int8) M x N or None; out: fp32 (default), bf16 or fp16, and
+    may be acc itself when 32-bit (accumulate in place)."""
     _on_gpu(a, b, acc, scale_a, scale_b, out)
     if a.dim() != 2 or b.dim() != 2:
         raise ValueError("dot_acc takes 2-D operands")
     if b_layout not in ("nk", "kn"):
         raise ValueError(f"b_layout must be 'nk' or 'kn' (got {b_layout!r})")
     fp8 = a.dtype in _FP8 and b.dtype in _FP8
-    if not fp8 and not (a.dtype in _DOT16 and b.dtype == a.dtype):
-        raise ValueError(f"dot_acc takes two bf16, two fp16 or two fp8 operands (got {a.dtype}, {b.dtype})")
-    if fp8 and b_layout != "nk":
-        raise ValueError("fp8 operands take b as its N x K storage")
+    wide = a.dtype in (torch.float32, torch.int8) and b.dtype == a.dtype
+    if not fp8 and not wide and not (a.dtype in _DOT16 and b.dtype == a.dtype):
+        raise ValueError("dot_acc takes two bf16, fp16, fp32 or int8 operands, or two fp8 "
+                         f"(got {a.dtype}, {b.dtype})")
+    if (fp8 or wide) and b_layout != "nk":
+        raise ValueError("fp8, fp32 and int8 operands take b as its N x K storage")
+    if wide:  # fp32 -> fp32, int8 -> int32 (exact, wrapping)
+        out_dtype = torch.float32 if a.dtype == torch.float32 else torch.int32
     if fp8 != (scale_a is not None and scale_b is not None) or (not fp8 and (scale_a is not None or
                                                                              scale_b is not None)):
         raise ValueError("scale_a and scale_b go with fp8 operands, and only with them")
@@ -311,10 +318,11 @@ def dot_acc(a: torch.Tensor, b: torch.Tensor, acc: torch.Tensor | None = None, *
     if fp8 and (scale_a.dtype != torch.float32 or scale_b.dtype != torch.float32 or scale_a.numel() != M
                 or scale_b.numel() != N or not scale_a.is_contiguous() or not scale_b.is_contiguous()):
         raise ValueError("scales must be contiguous fp32 vectors of length M and N")
-    if acc is not None and (acc.dtype != torch.float32 or tuple(acc.shape) != (M, N) or acc.stride(1) != 1):
-        raise ValueError("acc must be a row-major fp32 M x N tensor")
-    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
-        raise ValueError("out_dtype must be fp32, bf16 or fp16")
+    acc_dtype = torch.int32 if a.dtype == torch.int8 else torch.float32
+    if acc is not None and (acc.dtype != acc_dtype or tuple(acc.shape) != (M, N) or acc.stride(1) != 1):
+        raise ValueError(f"acc must be a row-major {acc_dtype} M x N tensor")
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.int32):
+        raise ValueError("out_dtype must be fp32, bf16 or fp16 (int32 for int8 operands)")
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
     if out.dtype != out_dtype or tuple(out.shape) != (M, N) or out.stride(1) != 1:

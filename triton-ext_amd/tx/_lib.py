@@ -26,7 +26,7 @@ STATUS_NAMES = {
 }
 
 # tx_dtype
-F32, FP8E4M3FN, FP8E5M2, BF16, I32, U32, F16, FP4E2M1, I64, U64, F64 = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10
+F32, FP8E4M3FN, FP8E5M2, BF16, I32, U32, F16, FP4E2M1, I64, U64, F64, I8 = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 # tx_rounding (ops/NewOps.cpp:270-286 numbering)
 RTNE, RTZ, RS = 0, 1, 2
