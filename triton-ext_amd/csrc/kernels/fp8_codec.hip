@@ -633,10 +633,13 @@ __device__ __forceinline__ float block_absmax(float amax, float *red) {
   return amax;
 }
 
-// fp32 rows of at most kRowRegs 16-byte vectors per thread (K <= 16384)
-// stay in registers between the absmax and the codes (5% faster at 8192 x
-// 8192; for bf16 rows the two-pass form measured 30% faster).
-constexpr int kRowRegs = 16;
+// Rows of at most RowRegs<XT> 16-byte vectors per thread (fp32: 16, K <=
+// 16384; bf16: 4, K <= 8192) stay in registers between the absmax and the
+// codes, so each row is read from memory once.  (fp32: 5% faster at 8192 x
+// 8192 than a second pass from cache.  bf16 with the fp32 budget of 16
+// vectors, 64 registers for 4 used, measured 30% slower than two passes.)
+template <int XT>
+constexpr int RowRegs = XT == 0 ? 8 : 4;
 
 // Row-wise absmax quantiser (the fp8 GEMM's per-row / per-column scales):
 //   amax = max |x| over the row (NaN ignored), 1 if that is 0
@@ -651,20 +654,21 @@ __device__ __forceinline__ void quant_row(const tx_quant_args &a) {
   __shared__ float red[kBlock / 64];
   float *scales = static_cast<float *>(a.scales);
   const int tid = threadIdx.x;
-  const bool in_regs = XT == 0 && a.vec && a.K % VE == 0 && a.K / VE <= int64_t(kBlock) * kRowRegs;
+  constexpr int RR = RowRegs<XT>;
+  const bool in_regs = a.vec && a.K % VE == 0 && a.K / VE <= int64_t(kBlock) * RR;
   if (in_regs) {
     const int nvec = int(a.K / VE);
     for (int64_t r = blockIdx.x; r < a.rows; r += gridDim.x) {
       const uint8_t *xrow = static_cast<const uint8_t *>(a.x) + r * a.ldx * (XT == 0 ? 4 : 2);
-      txd::u32x4 p[kRowRegs];
+      txd::u32x4 p[RR];
 #pragma unroll
-      for (int j = 0; j < kRowRegs; ++j) {
+      for (int j = 0; j < RR; ++j) {
         const int i = tid + kBlock * j;
         if (i < nvec) p[j] = *reinterpret_cast<const txd::u32x4 *>(xrow + 16 * int64_t(i));
       }
       float amax = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kRowRegs; ++j)
+      for (int j = 0; j < RR; ++j)
         if (tid + kBlock * j < nvec) amax = vec_absmax<XT>(p[j], amax);
       amax = block_absmax(amax, red);
       if (amax == 0.0f) amax = 1.0f;
@@ -672,7 +676,7 @@ __device__ __forceinline__ void quant_row(const tx_quant_args &a) {
       if (tid == 0) scales[r] = amax / FMAX;
       uint8_t *qrow = a.q + r * a.ldq;
 #pragma unroll
-      for (int j = 0; j < kRowRegs; ++j) {
+      for (int j = 0; j < RR; ++j) {
         const int i = tid + kBlock * j;
         if (i < nvec) row_codes<FMT, XT>(p[j], mult, qrow, i);
       }
