@@ -318,8 +318,9 @@ TX_API tx_status tx_histogram(const int32_t *x, const uint8_t *mask, int64_t n, 
  * tt.atomic_cas in scatter form: for every i < n with mask[i] != 0 (mask may
  * be NULL) and 0 <= idx[i] < nbins, atomically
  *   old[i] = bins[idx[i]]; if (old[i] == cmp[i]) bins[idx[i]] = val[i];
- * comparing the 32-bit patterns (bins_type TX_I32, TX_U32 or TX_F32; cmp
- * and val of the same type).  Replaces Triton's per-lane lowering of
+ * comparing the bit patterns (bins_type TX_I32, TX_U32, TX_F32, TX_I64,
+ * TX_U64 or TX_F64; cmp, val and old of the same type).  Replaces Triton's
+ * per-lane lowering of
  * tl.atomic_cas (tt.atomic_cas, passed through at
  * uTLXConversionPatterns.cpp:610).  old may be NULL; dropped updates return
  * 0.  Updates of one bin apply one at a time in an order the hardware

@@ -200,3 +200,42 @@ def test_xchg_64bit(tx, dev, dt):
     wb = w.view(torch.int64).numpy()
     for b in range(100):
         assert got[b] in set(wb[k == b].tolist())
+
+
+@pytest.mark.parametrize("dt", [torch.int64, torch.float64])
+def test_cas_64bit(tx, dev, dt):
+    """tt.atomic_cas on 64-bit bins: unique indices give the closed form
+    (swap where the bin equals cmp, bit for bit: -0 != +0 for fp64); a ticket
+    chain on repeated indices (cmp = the previous ticket) advances each bin
+    exactly once per ticket taken."""
+    g = np.random.default_rng(7)
+    nbins = 20_000
+    perm = g.permutation(nbins).astype(np.int32)
+    b0 = g.integers(-2**62, 2**62, nbins)
+    hit = g.random(nbins) < 0.5
+    cmp = np.where(hit, b0[perm], b0[perm] ^ 1)
+    val = g.integers(-2**62, 2**62, nbins)
+    T = lambda x: torch.from_numpy(np.ascontiguousarray(x)).view(dt)
+    bins = T(b0).to(dev)
+    old = tx.atomic_cas(bins, torch.from_numpy(perm).to(dev), T(cmp).to(dev), T(val).to(dev)).cpu()
+    assert torch.equal(old.view(torch.int64), torch.from_numpy(b0[perm]))
+    want = b0.copy()
+    want[perm[hit]] = val[hit]
+    assert np.array_equal(bins.cpu().view(torch.int64).numpy(), want)
+    # ticket chain: every update of a bin tries to move it from t to t + 1 for
+    # t = 0 .. count - 1; each bin ends at the number of successful tries, and
+    # the successes are exactly the tickets 0 .. final - 1, each once
+    k = g.integers(0, 50, 4000).astype(np.int32)
+    tickets = np.concatenate([np.arange(np.sum(k == b)) for b in range(50)])
+    order = np.concatenate([np.flatnonzero(k == b) for b in range(50)])
+    kk = k[order]
+    cmpi = tickets.astype(np.int64)
+    vali = cmpi + 1
+    if dt == torch.float64:
+        cmpi, vali = cmpi.astype(np.float64).view(np.int64), vali.astype(np.float64).view(np.int64)
+    bins2 = torch.zeros(50, dtype=dt, device=dev)
+    old2 = tx.atomic_cas(bins2, torch.from_numpy(kk).to(dev), T(cmpi).to(dev), T(vali).to(dev)).cpu()
+    fin = bins2.cpu().numpy()
+    for b in range(50):
+        ok = old2.numpy()[kk == b] == (T(cmpi).numpy()[kk == b])
+        assert fin[b] == ok.sum()

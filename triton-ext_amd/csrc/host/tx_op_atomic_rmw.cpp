@@ -235,21 +235,24 @@ static tx_status atomic_cas_scatter(void *bins, tx_dtype bins_type, int64_t nbin
   if (nbins > INT32_MAX)
     return fail(TX_UNSUPPORTED, "tx_atomic_cas_scatter: nbins %lld exceeds int32 indexing",
                 (long long)nbins);
-  if (bins_type != TX_I32 && bins_type != TX_U32 && bins_type != TX_F32)
-    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: bins must be 32-bit (got type %d)",
+  const bool w64 = bins_type == TX_I64 || bins_type == TX_U64 || bins_type == TX_F64;
+  if (bins_type != TX_I32 && bins_type != TX_U32 && bins_type != TX_F32 && !w64)
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: bins must be 32- or 64-bit (got type %d)",
                 int(bins_type));
   if (n == 0) return TX_SUCCESS;
   if (!idx || !cmp || !val || (!bins && nbins > 0))
     return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: NULL buffer");
-  if (!aligned(idx, 4) || !aligned(cmp, 4) || !aligned(val, 4) || (bins && !aligned(bins, 4)) ||
-      (old && !aligned(old, 4)))
-    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: buffers must be 4-byte aligned");
+  const size_t es = w64 ? 8 : 4;
+  if (!aligned(idx, 4) || !aligned(cmp, es) || !aligned(val, es) || (bins && !aligned(bins, es)) ||
+      (old && !aligned(old, es)))
+    return fail(TX_INVALID_ARGUMENT, "tx_atomic_cas_scatter: idx must be 4-byte and bins / cmp / val / old "
+                "%zu-byte aligned", es);
   tx_cas_args args{bins, idx, static_cast<const uint32_t *>(cmp), static_cast<const uint32_t *>(val),
                    mask, static_cast<uint32_t *>(old), n, int32_t(nbins), 0};
+  const char *kname = w64 ? "tx_scatter_cas64" : "tx_scatter_cas";
   hipFunction_t fn;
-  TX_TRY(get_kernel(CodeObject::Scatter, "tx_scatter_cas", &fn));
-  return launch(fn, direct_grid(n), 1, 256, static_cast<hipStream_t>(stream), &args, sizeof args,
-                "tx_scatter_cas");
+  TX_TRY(get_kernel(CodeObject::Scatter, kname, &fn));
+  return launch(fn, direct_grid(n), 1, 256, static_cast<hipStream_t>(stream), &args, sizeof args, kname);
 }
 
 // Table form: operands = {bins (result slot), idx, cmp, val, mask, old, nbins,

@@ -728,6 +728,20 @@ TX_KERNEL void __launch_bounds__(256) tx_scatter_xchg(const tx_scatter_args a) {
   }
 }
 
+// 64-bit bins (int64 / uint64 / fp64 bit patterns): the same on 64-bit words.
+TX_KERNEL void __launch_bounds__(256) tx_scatter_cas64(const tx_cas_args a) {
+  unsigned long long *bins = static_cast<unsigned long long *>(a.bins);
+  const unsigned long long *cmp = reinterpret_cast<const unsigned long long *>(a.cmp);
+  const unsigned long long *val = reinterpret_cast<const unsigned long long *>(a.val);
+  unsigned long long *old = reinterpret_cast<unsigned long long *>(a.old);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) {
+    const int32_t k = a.idx[i];
+    unsigned long long r = 0ull;
+    if (k >= 0 && k < a.nbins && (!a.mask || a.mask[i] != 0)) r = atomicCAS(bins + k, cmp[i], val[i]);
+    if (old) old[i] = r;
+  }
+}
+
 TX_KERNEL void __launch_bounds__(256) tx_scatter_cas(const tx_cas_args a) {
   uint32_t *bins = static_cast<uint32_t *>(a.bins);
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += int64_t(gridDim.x) * 256) {

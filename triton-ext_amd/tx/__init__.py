@@ -189,14 +189,15 @@ def atomic_cas(bins: torch.Tensor, idx: torch.Tensor, cmp: torch.Tensor, val: to
                mask: torch.Tensor | None = None, return_old: bool = True):
     """tt.atomic_cas, scatter form: for every i (not masked off, idx in range),
     atomically old[i] = bins[idx[i]]; if old[i] == cmp[i]: bins[idx[i]] = val[i]
-    (32-bit patterns compared bit for bit; int32, uint32 or fp32 bins).
+    (bit patterns compared bit for bit; int32, uint32, fp32, int64, uint64 or
+    fp64 bins).
     Returns old (the tt.atomic_cas result; 0 for dropped updates), or bins
     when return_old is False."""
     _on_gpu(bins, idx, cmp, val, mask)
     if idx.dtype != torch.int32:
         raise ValueError("idx must be int32")
-    if bins.dtype not in (torch.int32, torch.uint32, torch.float32):
-        raise ValueError("atomic_cas takes int32, uint32 or fp32 bins")
+    if bins.dtype not in (torch.int32, torch.uint32, torch.float32, torch.int64, torch.uint64, torch.float64):
+        raise ValueError("atomic_cas takes int32, uint32, fp32, int64, uint64 or fp64 bins")
     if cmp.dtype != bins.dtype or val.dtype != bins.dtype:
         raise ValueError("cmp, val and bins must have the same dtype")
     for t in (bins, idx, cmp, val) + ((mask,) if mask is not None else ()):
