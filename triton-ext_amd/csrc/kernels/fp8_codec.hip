@@ -105,6 +105,39 @@ constexpr int kBlock = 256;
 constexpr int kVecPerThread = 4;                         // float4 loads per thread
 constexpr int kChunk = kBlock * kVecPerThread * 4;       // elements per block step
 
+// Four fp32 values -> four fp8 codes (code i in byte i), round to nearest
+// even, not saturating, by gfx950's packed converts: without clamping,
+// v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 give exactly encode_rtne<FMT, false>'s
+// code for every fp32 input that is not a NaN (a device sweep over all 2^32
+// patterns found no difference: ties, subnormals, overflow to NaN / Inf and
+// Inf included).  NaN inputs differ: e4m3fn gives 0xFF for every NaN (0x7F |
+// sign wanted), so positive NaNs are first replaced by +Inf, whose code is
+// 0x7F (a signed min with 0x7F800000 leaves every other pattern alone);
+// e5m2 gives 0xFE for every NaN, a code no other input produces, so those
+// bytes are rewritten to 0x7F | the input's sign.
+template <int FMT>
+__device__ __forceinline__ uint32_t encode4_rtne_hw(const txd::u32x4 &v) {
+  if constexpr (FMT == E4M3FN) {
+    auto fix = [](uint32_t u) { return __int_as_float(min(int(u), 0x7F800000)); };
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(fix(v.x), fix(v.y), 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(fix(v.z), fix(v.w), w, true);
+    return uint32_t(w);
+  } else {
+    int w = __builtin_amdgcn_cvt_pk_bf8_f32(__uint_as_float(v.x), __uint_as_float(v.y), 0, false);
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(__uint_as_float(v.z), __uint_as_float(v.w), w, true);
+    const uint32_t t = uint32_t(w) ^ 0xFEFEFEFEu;                      // zero bytes: NaN inputs
+    // bit 7 of each zero byte of t; the borrow can also flag a byte of t equal
+    // to 0x01 above a zero byte, i.e. a code 0xFF, which the converter never
+    // gives (a NaN gives 0xFE, every other input its encode_rtne code)
+    const uint32_t nan7 = (t - 0x01010101u) & ~t & 0x80808080u;
+    if (nan7 == 0u) return uint32_t(w);
+    // byte i of `sign` holds byte 3 (sign and top exponent bits) of value i
+    const uint32_t sign = __builtin_amdgcn_perm(v.y, v.x, 0x0c0c0703u) | __builtin_amdgcn_perm(v.w, v.z, 0x07030c0cu);
+    const uint32_t mask = (nan7 >> 7) * 0xFFu;
+    return (uint32_t(w) & ~mask) | ((sign & 0x80808080u) | 0x7F7F7F7Fu) & mask;
+  }
+}
+
 // Vector encode: [start, n) with (n - start) a multiple of kChunk, src 16-byte
 // aligned, dst 4-byte aligned, start a multiple of 4.
 template <int FMT, bool SAT, bool RTZ>
@@ -120,12 +153,15 @@ __device__ __forceinline__ void encode_vec(const tx_fp8_codec_args &a) {
       v[j] = __builtin_nontemporal_load(src + w0 + j * kBlock);
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) {
-      const uint32_t b0 = encode<FMT, SAT, RTZ>(v[j].x);
-      const uint32_t b1 = encode<FMT, SAT, RTZ>(v[j].y);
-      const uint32_t b2 = encode<FMT, SAT, RTZ>(v[j].z);
-      const uint32_t b3 = encode<FMT, SAT, RTZ>(v[j].w);
-      __builtin_nontemporal_store(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24),
-                                  dst + w0 + j * kBlock);
+      if constexpr (!SAT && !RTZ) {
+        __builtin_nontemporal_store(encode4_rtne_hw<FMT>(v[j]), dst + w0 + j * kBlock);
+      } else {
+        const uint32_t b0 = encode<FMT, SAT, RTZ>(v[j].x);
+        const uint32_t b1 = encode<FMT, SAT, RTZ>(v[j].y);
+        const uint32_t b2 = encode<FMT, SAT, RTZ>(v[j].z);
+        const uint32_t b3 = encode<FMT, SAT, RTZ>(v[j].w);
+        __builtin_nontemporal_store(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24), dst + w0 + j * kBlock);
+      }
     }
   }
 }
