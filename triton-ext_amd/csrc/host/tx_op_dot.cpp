@@ -970,7 +970,7 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
                 "%s: needs 16-byte aligned x and W rows (ldx %% 8 == 0, ldw %% 16 == 0)", what);
   tx_gemv_args args{static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(W), scales,
                     static_cast<uint16_t *>(y), ldx, ldw, ld_scales, ldy, int32_t(M), int32_t(N),
-                    int32_t(K), int32_t(group)};
+                    int32_t(K), int32_t(group), 0, 0};
   char kname[48];
   hipFunction_t fn;
   if (M == 1 && K * 2 <= 32768) {  // x fits the kernel's LDS stage
@@ -981,15 +981,25 @@ static tx_status gemv_fp8_dequant(const void *x, int64_t ldx, const void *W, tx_
     return launch(fn, unsigned((N + 7) / 8), 1, 256, static_cast<hipStream_t>(stream), &args, sizeof args,
                   kname, unsigned(K * 2));
   }
-  // 16 or 32 W rows per workgroup, K split over its wavefronts.  Many column
-  // blocks: 4 wavefronts, each with two 16-row W blocks sharing its x reads
-  // once x has more than a few rows.  Few: one W block per workgroup and 16
-  // wavefronts (8 with 2 or 4 blocks of M) to keep enough loads in flight.
+  // Up to 16 or 32 W rows per workgroup, K split over its wavefronts.  Many
+  // column blocks: 4 wavefronts, each with two 16-row W blocks sharing its x
+  // reads, and the rows spread evenly over a whole number of workgroups per
+  // CU (N = 14336: 512 workgroups of 28 rows, where 448 of 32 left 64 CUs with
+  // half the bytes of the others and the rest finishing 3-5 us later).  Few:
+  // one W block per workgroup and 16 wavefronts (8 with 2 or 4 blocks of M)
+  // to keep enough loads in flight.
   const int mblocks = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  const bool wide = (N + 15) / 16 >= 2 * int64_t(cu_count());
+  const int64_t cus = cu_count();
+  const bool wide = (N + 15) / 16 >= 2 * cus;
   const int waves = wide ? 4 : (mblocks == 1 ? 16 : 8);
-  const int nb = (wide && M > 4) ? 2 : 1;
-  const int64_t grid = (N + 16 * nb - 1) / (16 * nb);
+  const int nb = wide ? 2 : 1;
+  int64_t rows = 16 * nb;
+  if (wide) {
+    const int64_t nwg = ((N + rows - 1) / rows + cus - 1) / cus * cus;
+    rows = (N + nwg - 1) / nwg;
+  }
+  args.rows_per_wg = int32_t(rows);
+  const int64_t grid = (N + rows - 1) / rows;
   std::snprintf(kname, sizeof kname, "tx_gemv_fp8_%s_w%d_m%d_b%d", fw, waves, mblocks, nb);
   TX_TRY(get_kernel(CodeObject::Gemv, kname, &fn));
   return launch(fn, unsigned(grid), 1, unsigned(64 * waves), static_cast<hipStream_t>(stream), &args,

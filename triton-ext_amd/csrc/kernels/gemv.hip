@@ -2,14 +2,18 @@
 //   y[m,n] = bf16_rne( sum_g s[n,g] * sum_{k in g} x[m,k] * W[n,k] )
 // x bf16 (M <= 64 rows), W fp8 N x K row-major, s fp32 N x (K/group).
 //
-// HBM-bound on W, which is read once.  A workgroup owns 16 rows of W (16
-// output columns) and splits K over its wavefronts.  A wave streams its rows
-// in rounds of 256 bytes per row: each of the 4 loads of a round reads 4
-// whole 256-byte row segments, two rounds are in flight in registers, and a
-// round is transposed through a private 4 KiB LDS tile (chunk c of row r at
-// chunk c ^ (r & 15): conflict-free for both the row writes and the fragment
-// reads) so that lane (r, g) holds 32 codes of row r per 128-element slice.
-// The per-wave partial sums are reduced across the workgroup in LDS.
+// HBM-bound on W, which is read once.  A workgroup owns up to 16 or 32 rows
+// of W (one or two 16-row blocks, 16 output columns each; the host spreads
+// the rows evenly over a whole number of workgroups per CU) and splits K over
+// its wavefronts.  A wave streams its rows in rounds of 256 bytes per row:
+// each of the 4 loads of a round reads 4 whole 256-byte row segments, two
+// rounds are in flight in registers, and a round is transposed through a
+// private 4 KiB LDS tile per block (chunk c of row r at chunk c ^ (r & 15))
+// into MFMA fragments.  Each round's x fragments and group scales are loaded
+// with its W, two rounds ahead: the CU serves vector loads in order, so x
+// loaded where it is used (an L2 hit) would wait behind the W round in
+// flight.  No load sits on a conditional path (see the schedule below).  The
+// per-wave partial sums are reduced across the workgroup in LDS.
 //
 // Dequantisation is gfx950's scaled fp8 -> bf16 pair conversion
 // (v_cvt_scalef32_pk_bf16_bf8 / _fp8, scale 1): two instructions per four
@@ -50,7 +54,10 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * 16 * NB;
+  // This workgroup's W rows: [n0, n_end), at most 16 NB of them (the host
+  // sizes rows_per_wg so that every CU gets the same number of rows).
+  const int n0 = blockIdx.x * a.rows_per_wg;
+  const int n_end = min(a.N, n0 + a.rows_per_wg);
   const int r = lane & 15, g = lane >> 4;
   const int nslices = a.K / kSlice;  // host guarantees K % 128 == 0
   const int per_wave = (nslices + kWaves - 1) / kWaves;
@@ -60,8 +67,9 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
   const int slices_per_group = a.group / kSlice;  // host: group % 128 == 0
 
   // Load j (0..3) of a round of block b: W row 16b + 4j + lane / 16, bytes
-  // 16 (lane % 16) of that row's 256-byte segment.  Rows past N read the last
-  // row (valid memory) and are never stored.
+  // 16 (lane % 16) of that row's 256-byte segment.  Rows past the
+  // workgroup's range read its last row (the same addresses in one load, so
+  // no extra traffic) and are never stored.
   const uint8_t *wp[NB][4];
   int wpos[4];
   uint8_t *tile = lds + wave * NB * kTile;
@@ -71,62 +79,73 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int n = n0 + 16 * b + row;
-      wp[b][j] = a.W + int64_t(n < a.N ? n : a.N - 1) * a.ldw + 16 * (lane & 15);
+      wp[b][j] = a.W + int64_t(n < n_end ? n : n_end - 1) * a.ldw;
     }
     wpos[j] = row * 256 + (((lane & 15) ^ (row & 15)) << 4);
   }
-  int rpos[kRound][2];
-#pragma unroll
-  for (int u = 0; u < kRound; ++u)
-#pragma unroll
-    for (int e = 0; e < 2; ++e) rpos[u][e] = r * 256 + (((8 * u + 2 * g + e) ^ r) << 4);
+  // Fragment reads: MFMA i of slice u takes codes 32 i + 8 g .. + 7 of row r,
+  // 8 bytes at chunk 8 u + 2 i + g / 2 of the row's 256-byte segment.
+  auto rpos = [&](int u, int i) { return r * 256 + (((8 * u + 2 * i + (g >> 1)) ^ r) << 4) + 8 * (g & 1); };
 
-  // This lane's output columns (W rows 16b + r) and their group scales,
-  // loaded once (up to 8 groups; longer ranges fall back to a load per group).
+  // This lane's output columns (W rows 16b + r); their group scales travel
+  // with each round's x fragments.
   const float *srow[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     const int nc = n0 + 16 * b + r;
-    srow[b] = a.scales + int64_t(nc < a.N ? nc : a.N - 1) * a.ld_scales;
+    srow[b] = a.scales + int64_t(nc < n_end ? nc : n_end - 1) * a.ld_scales;
   }
-  const int g_first = s_begin / slices_per_group;
-  float scl[NB][8];
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int gi = g_first + j;
-      scl[b][j] = (gi * slices_per_group < nslices) ? srow[b][gi] : 0.0f;
-    }
-  auto scale_of = [&](int b, int grp) -> float {
-    const int j = grp - g_first;
-    float v = (j >= 0 && j < 8) ? scl[b][0] : srow[b][grp];
-#pragma unroll
-    for (int t = 1; t < 8; ++t) v = (j == t) ? scl[b][t] : v;
-    return v;
-  };
   // x rows past M read row M-1: MFMA output rows are independent and rows
   // past M are never stored, so no masking is needed.
   const uint16_t *xrow[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 16 + r;
-    xrow[mb] = a.x + int64_t(m < a.M ? m : a.M - 1) * a.ldx + 32 * g;
+    xrow[mb] = a.x + int64_t(m < a.M ? m : a.M - 1) * a.ldx + 8 * g;
   }
 
   struct Round {
     txd::u32x4 w[NB][4];
   };
+  // Every lane loads (no per-lane select, whose merge would make the wave
+  // wait for the load right away): in a round with one slice left, lanes 8..15
+  // re-read the slice's last chunk, which lands in the unused half of the tile.
   auto fetch = [&](int q, Round &f) {
     const int s = s_begin + q * kRound;
     const int valid = min(kRound, s_end - s) * kSlice;
+    const int off = s * kSlice + min(16 * (lane & 15), valid - 16);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        f.w[b][j] = 16 * (lane & 15) < valid
-                        ? __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(wp[b][j] + int64_t(s) * kSlice))
-                        : txd::u32x4{0u, 0u, 0u, 0u};
+        f.w[b][j] = __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(wp[b][j] + off));
+  };
+  // x fragments of round q (slices past the wave's range repeat its last one).
+  // They are loaded a round ahead and before the W loads two rounds ahead, so
+  // waiting for them (memory counters retire in order) never waits for W.
+  // With more than one 16-row block of x, or 16 wavefronts (128 registers
+  // each), two rounds of fragments would not fit the registers: those kernels
+  // load x where it is used (and wait for the W round in flight before it).
+  constexpr bool kXAhead = MB == 1 && kWaves <= 4;
+  struct XRound {
+    txd::u32x4 v[kXAhead ? kRound : 1][MB][4];
+    float sc[kRound][NB];  // group scale of each slice's group
+  };
+  auto x_frags = [&](int su, txd::u32x4 (&xv)[MB][4]) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xv[mb][i] = *reinterpret_cast<const txd::u32x4 *>(xrow[mb] + su * kSlice + 32 * i);
+  };
+  auto load_x = [&](int q, XRound &xr) {
+#pragma unroll
+    for (int u = 0; u < kRound; ++u) {
+      const int su = min(s_begin + q * kRound + u, s_end - 1);
+      if constexpr (kXAhead) x_frags(su, xr.v[u]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xr.sc[u][b] = srow[b][su / slices_per_group];
+    }
   };
 
   txd::f32x4 acc[NB][MB], part[NB][MB];
@@ -136,9 +155,10 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
     for (int i = 0; i < MB; ++i) acc[b][i] = part[b][i] = txd::f32x4{0.f, 0.f, 0.f, 0.f};
   bool fresh = true;  // the next MFMA chain starts from zero
 
-  // Slice s: lane (r, g) holds 32 codes of W row r at k = 32g .. 32g + 31 of
-  // the slice; MFMA i takes k = 32g + 8i .. +7 of both W and x.
-  auto compute = [&](int q, const Round &f) {
+  // Slice s: MFMA i takes k = 32 i + 8 g .. + 7 of the slice in lane (r, g),
+  // of both W and x (so that a lane group's x loads read 64 contiguous bytes
+  // of each row: 16 cache-line halves per load instead of 32 lines).
+  auto compute = [&](int q, const Round &f, const XRound &xr) {
     const int s = s_begin + q * kRound;
     const int ns = min(kRound, s_end - s);
 #pragma unroll
@@ -151,19 +171,23 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
       if (u < ns) {
         const int su = s + u;
         txd::u32x4 xv[MB][4];
+        if constexpr (kXAhead) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+          for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            xv[mb][i] = *reinterpret_cast<const txd::u32x4 *>(xrow[mb] + su * kSlice + 8 * i);
+            for (int i = 0; i < 4; ++i) xv[mb][i] = xr.v[u][mb][i];
+        } else {
+          x_frags(su, xv);
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          const txd::u32x4 c0 = *reinterpret_cast<const txd::u32x4 *>(tile + b * kTile + rpos[u][0]);
-          const txd::u32x4 c1 = *reinterpret_cast<const txd::u32x4 *>(tile + b * kTile + rpos[u][1]);
-          const uint32_t words[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
           uint32_t wb[16];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) fp8x4_to_bf16x4<FMT>(words[t], wb[2 * t], wb[2 * t + 1]);
+          for (int i = 0; i < 4; ++i) {
+            const txd::u32x2 c = *reinterpret_cast<const txd::u32x2 *>(tile + b * kTile + rpos(u, i));
+            fp8x4_to_bf16x4<FMT>(c.x, wb[4 * i], wb[4 * i + 1]);
+            fp8x4_to_bf16x4<FMT>(c.y, wb[4 * i + 2], wb[4 * i + 3]);
+          }
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -177,10 +201,9 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
         fresh = false;
         // close the group when its last slice is done (uniform)
         if ((su + 1) % slices_per_group == 0 || su + 1 == nslices) {
-          const int grp = su / slices_per_group;
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
-            const float sc = scale_of(b, grp);
+            const float sc = xr.sc[u][b];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
           }
@@ -191,28 +214,57 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
     asm volatile("" ::: "memory");
   };
 
-  Round buf[kDepth];
-#pragma unroll
-  for (int d = 0; d < kDepth; ++d)
-    if (d < nrounds) fetch(d, buf[d]);
-  for (int q0 = 0; q0 < nrounds; q0 += kDepth) {
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      const int q = q0 + d;
-      if (q < nrounds) {
-        compute(q, buf[d]);
-        if (q + kDepth < nrounds) fetch(q + kDepth, buf[d]);
-      }
+  // Two rounds in flight, each with its x fragments and scales (requested
+  // just before its W).  No load is issued on a conditional path: the
+  // compiler's wait counts merge over branches and would otherwise wait for
+  // every outstanding load at the loop head.  So the steady-state loop takes
+  // two rounds per iteration and always fetches, the last one to three rounds
+  // are straight-line tails, and the prologue's second round re-reads round 0
+  // when the wave has only one.
+  static_assert(kDepth == 2, "the schedule below keeps two rounds in flight");
+  if (nrounds > 0) {
+    Round b0, b1;
+    XRound x0, x1;
+    load_x(0, x0);
+    fetch(0, b0);
+    load_x(min(1, nrounds - 1), x1);
+    fetch(min(1, nrounds - 1), b1);
+    int q = 0;
+    for (; q + 3 < nrounds; q += 2) {
+      compute(q, b0, x0);
+      load_x(q + 2, x0);
+      fetch(q + 2, b0);
+      compute(q + 1, b1, x1);
+      load_x(q + 3, x1);
+      fetch(q + 3, b1);
     }
-  }
-  // A group split across two waves leaves a partial in both; scale it here.
-  if (!fresh) {
-    const int grp = (s_end - 1) / slices_per_group;
+    const int rem = nrounds - q;  // 1, 2 or 3
+    bool last0 = true;            // the last round's scales are in x0
+    if (rem == 3) {
+      compute(q, b0, x0);
+      load_x(q + 2, x0);
+      fetch(q + 2, b0);
+      compute(q + 1, b1, x1);
+      compute(q + 2, b0, x0);
+    } else if (rem == 2) {
+      compute(q, b0, x0);
+      compute(q + 1, b1, x1);
+      last0 = false;
+    } else {
+      compute(q, b0, x0);
+    }
+    // A group split across two waves leaves a partial in both; scale it
+    // here with the scale of the wave's last slice.
+    if (!fresh) {
+      const int ul = (s_end - 1 - s_begin) % kRound;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const float sc = scale_of(b, grp);
+      for (int b = 0; b < NB; ++b) {
+        const float s0 = ul == 0 ? x0.sc[0][b] : x0.sc[kRound - 1][b];
+        const float s1 = ul == 0 ? x1.sc[0][b] : x1.sc[kRound - 1][b];
+        const float sc = last0 ? s0 : s1;
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
+        for (int mb = 0; mb < MB; ++mb) acc[b][mb] += part[b][mb] * sc;
+      }
     }
   }
 
@@ -231,7 +283,7 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) t += red[(w * MB + mb) * 64 + lane];
       const int ncol = n0 + 16 * b + r;
-      if (ncol < a.N) {
+      if (ncol < n_end) {
         const float v[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -346,6 +398,7 @@ __device__ __forceinline__ void gemv_lin(const tx_gemv_args &a) {
           a.y[int64_t(m) * a.ldy + row0 + r] = uint16_t(txd::f32_to_bf16_bits(acc[r][m]));
   }
 }
+
 
 }  // namespace
 

@@ -198,6 +198,8 @@ typedef struct tx_gemv_args {
   int32_t N;
   int32_t K;
   int32_t group;
+  int32_t rows_per_wg; /* MFMA kernels: W rows per workgroup (at most 16 per W block) */
+  int32_t pad_;
 } tx_gemv_args;
 
 #endif /* TX_KERNEL_ARGS_H */
