@@ -478,7 +478,7 @@ static tx_status dot_fp8_impl(const char *what, const void *A, tx_dtype a_type, 
   // Decode-sized M: stream B once with the skinny kernel (16 columns per
   // workgroup, K split over its wavefronts).
   if (M <= kSkinnyMaxM && K % 128 == 0 && aligned(A, 16) && aligned(B, 16) && lda % 16 == 0 &&
-      ldb % 16 == 0) {
+      ldb % 16 == 0 && ldb <= INT32_MAX / 16 && lda <= INT32_MAX / 64) {  // 32-bit buffer offsets
     const int mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     const int64_t grid = (N + 15) / 16;
     // Many column blocks: 4 wavefronts each, with long K ranges per wave;

@@ -80,9 +80,12 @@ TX_GEMM_FP8_FAST_EPI(e5m2, e4m3fn, EL_E5M2, EL_E4M3)
 
 // Kernel names: tx_gemm_fp8_<a>_<b>_skinny_w<waves>_m<16-row blocks of M>
 // (the small-grid variant with 4 blocks of M has 8 wavefronts: 16 would not
-// fit its registers in 128 VGPRs).
-#define TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, MB)                                       \
-  TX_KERNEL void __launch_bounds__(64 * W) tx_gemm_fp8_##FA##_##FB##_skinny_w##W##_m##MB( \
+// fit its registers in 128 VGPRs).  The 4-wave kernel for one block of M
+// is held to 4 workgroups per CU (128 registers): its grid at N = 14336 is
+// 3.5 workgroups per CU, which must all be resident at once.
+#define TX_GEMM_FP8_SKINNY(FA, FB, ELA, ELB, W, MB)                                            \
+  TX_KERNEL void __launch_bounds__(64 * W, (W == 4 && MB == 1) ? 4 : 1)                        \
+      tx_gemm_fp8_##FA##_##FB##_skinny_w##W##_m##MB(                                           \
       const tx_gemm_args a) {                                                            \
     skinny_fp8_tile<ELA, ELB, W, MB>(a);                                                 \
   }

@@ -45,15 +45,21 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
   // Load j (0..3) of a round: row 4j + lane / 16 of the block, bytes
   // 16 (lane % 16) of that row's 256-byte segment.  Rows past N read the
   // last row (valid memory) and are never stored.
-  const uint8_t *B = reinterpret_cast<const uint8_t *>(a.B);
-  const uint8_t *bp[4];
+  // Buffer loads with 32-bit lane offsets from one resource per operand (the
+  // host keeps 16 ldb and 64 lda below 2^31), which leaves the registers of
+  // 64-bit row pointers to the loads in flight.
+  constexpr int kNt = 2;  // buffer load cache policy: non-temporal
+  const int rows_valid = min(16, a.N - n0);
+  const __amdgpu_buffer_rsrc_t brs =
+      make_rsrc(reinterpret_cast<const uint8_t *>(a.B) + int64_t(n0) * a.ldb,
+                uint32_t(rows_valid - 1) * uint32_t(a.ldb) + uint32_t(a.K));
+  uint32_t boff[4];
   int wpos[4];
   uint8_t *tile = lds + wave * kTile;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = 4 * j + (lane >> 4);
-    const int n = n0 + row;
-    bp[j] = B + int64_t(n < a.N ? n : a.N - 1) * a.ldb + 16 * (lane & 15);
+    boff[j] = uint32_t(min(row, rows_valid - 1)) * uint32_t(a.ldb);
     wpos[j] = row * 256 + (((lane & 15) ^ (row & 15)) << 4);
   }
   // Fragment read offsets: slice u of a round, pieces e = 0, 1 (logical
@@ -64,25 +70,47 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) rpos[u][e] = r * 256 + (((8 * u + 2 * g + e) ^ r) << 4);
   // A rows past M read the last valid row and are never stored.
-  const uint8_t *arow[MB];
+  const __amdgpu_buffer_rsrc_t ars = make_rsrc(a.A, uint32_t(a.M - 1) * uint32_t(a.lda) + uint32_t(a.K));
+  uint32_t aoff[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 16 + r;
-    arow[mb] = reinterpret_cast<const uint8_t *>(a.A) + int64_t(m < a.M ? m : a.M - 1) * a.lda + 32 * g;
+    aoff[mb] = uint32_t(m < a.M ? m : a.M - 1) * uint32_t(a.lda) + 32 * g;
   }
 
+  // A round's B loads and (one 16-row block of A, 4 waves) its A fragments,
+  // loaded together two rounds ahead of use: the CU serves vector loads in
+  // order, so A loaded where it is used (a cache hit) would wait behind the
+  // B round in flight.  With more blocks of A the fragments would not fit
+  // the registers and are loaded where used.
+  constexpr bool kAAhead = MB == 1;
   struct Round {
     txd::u32x4 w[4];
+    txd::u32x4 xa[kAAhead ? kRound : 1][MB][2];
   };
-  // Round q's loads; in a round with one slice left the upper half reads zeros.
+  auto a_frags = [&](int s, int u, int ns, txd::u32x4 (&xa)[MB][2]) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t o = aoff[mb] + uint32_t(s + (u < ns ? u : 0)) * kSlice;
+      xa[mb][0] = __builtin_bit_cast(txd::u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, int(o), 0, 0));
+      xa[mb][1] = __builtin_bit_cast(txd::u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, int(o + 16), 0, 0));
+    }
+  };
+  // Round q's loads.  Every lane loads (no per-lane select: its merge would
+  // make the wave wait for the load right away); in a round with one slice
+  // left, lanes 8..15 re-read the slice's last chunk into the unused half of
+  // the tile.
   auto fetch = [&](int q, Round &f) {
     const int s = s_begin + q * kRound;
     const int valid = min(kRound, s_end - s) * kSlice;
+    if constexpr (kAAhead) {
+#pragma unroll
+      for (int u = 0; u < kRound; ++u) a_frags(s, u, valid / kSlice, f.xa[u]);
+    }
+    const uint32_t off = uint32_t(s * kSlice + min(16 * (lane & 15), valid - 16));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      f.w[j] = 16 * (lane & 15) < valid
-                   ? __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(bp[j] + int64_t(s) * kSlice))
-                   : txd::u32x4{0u, 0u, 0u, 0u};
+      f.w[j] = __builtin_bit_cast(txd::u32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, int(boff[j] + off), 0, kNt));
   };
   txd::f32x4 acc[MB];
 #pragma unroll
@@ -92,13 +120,14 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
     const int ns = min(kRound, s_end - s);
     txd::u32x4 xa[kRound][MB][2];
 #pragma unroll
-    for (int u = 0; u < kRound; ++u)
+    for (int u = 0; u < kRound; ++u) {
+      if constexpr (kAAhead) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const txd::u32x4 *xp = reinterpret_cast<const txd::u32x4 *>(arow[mb] + (s + (u < ns ? u : 0)) * kSlice);
-        xa[u][mb][0] = xp[0];
-        xa[u][mb][1] = xp[1];
+        for (int mb = 0; mb < MB; ++mb) xa[u][mb][0] = f.xa[u][mb][0], xa[u][mb][1] = f.xa[u][mb][1];
+      } else {
+        a_frags(s, u, ns, xa[u]);
       }
+    }
     // Transpose through the wave's tile (LDS operations of one wave complete
     // in order, so the reads see the writes and the next round's writes
     // follow these reads).
@@ -123,19 +152,55 @@ __device__ __forceinline__ void skinny_fp8_tile(const tx_gemm_args &a) {
     asm volatile("" ::: "memory");
   };
 
-  // Round slots are compile-time registers: slot d holds rounds congruent to
-  // d mod kDepth, refilled right after its round is consumed.
-  Round buf[kDepth];
+  // Two rounds in flight.  With A loaded ahead, no load is issued on a
+  // conditional path: the compiler's wait counts merge over branches and
+  // would otherwise wait for every outstanding load at the loop head.  So
+  // that schedule takes two rounds per loop iteration and always fetches,
+  // the last one to three rounds are straight-line tails, and the prologue's
+  // second round re-reads round 0 when the wave has only one.  (The other
+  // variants load A where used, which waits for the B round in flight anyway;
+  // they keep the shorter loop, which needs fewer registers.)
+  static_assert(kDepth == 2, "the schedules below keep two rounds in flight");
+  if constexpr (kAAhead) {
+    if (nrounds > 0) {
+      Round b0, b1;
+      fetch(0, b0);
+      fetch(min(1, nrounds - 1), b1);
+      int q = 0;
+      for (; q + 3 < nrounds; q += 2) {
+        compute(q, b0);
+        fetch(q + 2, b0);
+        compute(q + 1, b1);
+        fetch(q + 3, b1);
+      }
+      const int rem = nrounds - q;  // 1, 2 or 3
+      if (rem == 3) {
+        compute(q, b0);
+        fetch(q + 2, b0);
+        compute(q + 1, b1);
+        compute(q + 2, b0);
+      } else if (rem == 2) {
+        compute(q, b0);
+        compute(q + 1, b1);
+      } else {
+        compute(q, b0);
+      }
+    }
+  } else {
+    // Round slots are compile-time registers: slot d holds rounds congruent
+    // to d mod kDepth, refilled right after its round is consumed.
+    Round buf[kDepth];
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d)
-    if (d < nrounds) fetch(d, buf[d]);
-  for (int q0 = 0; q0 < nrounds; q0 += kDepth) {
+    for (int d = 0; d < kDepth; ++d)
+      if (d < nrounds) fetch(d, buf[d]);
+    for (int q0 = 0; q0 < nrounds; q0 += kDepth) {
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      const int q = q0 + d;
-      if (q < nrounds) {
-        compute(q, buf[d]);
-        if (q + kDepth < nrounds) fetch(q + kDepth, buf[d]);
+      for (int d = 0; d < kDepth; ++d) {
+        const int q = q0 + d;
+        if (q < nrounds) {
+          compute(q, buf[d]);
+          if (q + kDepth < nrounds) fetch(q + kDepth, buf[d]);
+        }
       }
     }
   }
