@@ -10,6 +10,14 @@ import torch
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
+# Several checks below pass stand-in device addresses (0x40, 0x100) that the
+# call must reject before touching memory.  On a machine with a GPU, a request
+# that validation accepts (for instance after the library starts serving a
+# conversion it used to refuse) would launch a kernel on them and fault the
+# card, so there they are skipped: they belong to the CPU suite.
+stand_in_addresses = pytest.mark.skipif(torch.cuda.is_available(),
+                                        reason="stand-in device addresses: CPU-only checks")
+
 
 def declared_symbols():
     with open(os.path.join(REPO, "include", "tx_plugin.h")) as f:
@@ -82,18 +90,22 @@ def test_null_operand_array_is_rejected(tx):
     lambda L: L.tx_dot_fp8_scaled(None, 0, 4, None, None, 1, 4, None, None, 4, 4, 4, 4, None),
     lambda L: L.tx_gemv_fp8_dequant(None, 128, None, 2, 128, None, 1, 0, None, 4, 1, 4, 128, None),
 ])
+@stand_in_addresses
 def test_bad_arguments_are_status_codes(tx, call):
     st = call(tx.lib)
     assert st == tx._lib.INVALID_ARGUMENT, (st, tx._lib.last_error())
     assert tx._lib.last_error()
 
 
+@stand_in_addresses
 def test_unsupported_requests(tx):
     L = tx.lib
     st = L.tx_gemv_fp8_dequant(None, 100, None, 2, 100, None, 1, 128, None, 4, 65, 4, 100, None)
     assert st == tx._lib.UNSUPPORTED
-    st = L.tx_fp_to_fp(ctypes.c_void_p(64), 0, ctypes.c_void_p(64), 3, 10, 0, 0, None)
-    assert st in (tx._lib.UNSUPPORTED, tx._lib.NO_DEVICE)
+    # int32 -> fp32 is no tt.fp_to_fp conversion (served pairs are refused
+    # only by type, never reached here)
+    st = L.tx_fp_to_fp(ctypes.c_void_p(64), 4, ctypes.c_void_p(64), 0, 10, 0, 0, None)
+    assert st == tx._lib.UNSUPPORTED and "is not served" in tx._lib.last_error()
     st = L.tx_fp_to_fp(ctypes.c_void_p(64), 0, ctypes.c_void_p(64), 1, 10, 2, 0, None)
     assert st == tx._lib.UNSUPPORTED and "random bits" in tx._lib.last_error()
 
@@ -212,6 +224,7 @@ _P = ctypes.c_void_p(256)   # a non-NULL, 256-byte aligned stand-in: these calls
     (lambda L: L.tx_quantize_mx(_P, 6, 128, _P, 1, 128, _P, 4, 4, 128, None), "INVALID_ARGUMENT", "fp32 or bf16"),
     (lambda L: L.tx_quantize_rowwise(_P, 0, 128, _P, 3, 128, _P, 4, 128, None), "INVALID_ARGUMENT", "fp8"),
 ])
+@stand_in_addresses
 def test_new_entry_points_validate_arguments(tx, call, status, msg):
     """Argument errors of the epilogue, MX, grouped / batched and quantiser
     entry points come back as status codes with a message, before any device
