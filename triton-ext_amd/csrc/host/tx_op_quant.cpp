@@ -69,7 +69,7 @@ tx_status quantize_mx(const void *x, tx_dtype x_type, int64_t ldx, void *q, tx_d
   // 8-byte q stores at multiples of 8 elements; x loads as for the row path
   tx_quant_args a{x, static_cast<uint8_t *>(q), scales, ldx, ldq, ld_scales, rows, K,
                   quant_vec(x, x_type, ldx, q, ldq, K, 8) ? 1 : 0, 0};
-  const int64_t threads = rows * (K / 32) * 4;
+  const int64_t threads = rows * (K / 32) * (x_type == TX_F32 ? 4 : 2);  // lanes per 32-element block
   const int64_t grid = std::min<int64_t>((threads + 255) / 256, int64_t(cu_count()) * 32);
   return launch(fn, unsigned(grid), 1, 256, static_cast<hipStream_t>(stream), &a, sizeof a, kname);
 }

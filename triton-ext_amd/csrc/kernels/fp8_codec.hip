@@ -528,13 +528,20 @@ __device__ __forceinline__ float clamp_keep_nan(float v) {
   return v > FMAX ? FMAX : (v < -FMAX ? -FMAX : v);
 }
 
-// One thread's 8 elements of a block: load, block amax (the 4 lanes of a
-// block exchange theirs), codes, store.
+// Lanes per 32-element block of the MX quantiser: 4 for fp32 input (8
+// elements, two 16-byte loads each), 2 for bf16 (16 elements, two 16-byte
+// loads: four lanes of 8 bf16 moved half as many bytes per instruction, and
+// that path ran at 0.58 of HBM against the fp32 one's 0.69).
 template <int XT>
-__device__ __forceinline__ void mx_load(const tx_quant_args &a, int64_t t, int64_t nb, float (&v)[8]) {
-  const int64_t blk = t >> 2;
+constexpr int MxLanes = XT == 0 ? 4 : 2;
+
+// One thread's E = 32 / MxLanes elements of a block.
+template <int XT>
+__device__ __forceinline__ void mx_load(const tx_quant_args &a, int64_t t, int64_t nb, float (&v)[32 / MxLanes<XT>]) {
+  constexpr int L = MxLanes<XT>, E = 32 / L;
+  const int64_t blk = t / L;
   const int64_t r = blk / nb;
-  const int64_t col = (blk % nb) * 32 + (t & 3) * 8;
+  const int64_t col = (blk % nb) * 32 + (t % L) * E;
   const uint8_t *xrow = static_cast<const uint8_t *>(a.x) + r * a.ldx * (XT == 0 ? 4 : 2);
   if (a.vec) {
     if constexpr (XT == 0) {
@@ -543,50 +550,56 @@ __device__ __forceinline__ void mx_load(const tx_quant_args &a, int64_t t, int64
       v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
       v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
     } else {
-      const txd::u32x4 p = *reinterpret_cast<const txd::u32x4 *>(xrow + 2 * col);
-      const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+      const txd::u32x4 p0 = *reinterpret_cast<const txd::u32x4 *>(xrow + 2 * col);
+      const txd::u32x4 p1 = *reinterpret_cast<const txd::u32x4 *>(xrow + 2 * col + 16);
+      const uint32_t w[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         v[2 * i] = __uint_as_float(w[i] << 16);
         v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
       }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = load_x<XT>(xrow, col + i);
+    for (int i = 0; i < E; ++i) v[i] = load_x<XT>(xrow, col + i);
   }
 }
 
-template <int FMT>
-__device__ __forceinline__ void mx_store(const tx_quant_args &a, int64_t t, int64_t nb, const float (&v)[8]) {
+// Block amax over the block's lanes, the e8m0 scale, codes, stores.
+template <int FMT, int XT>
+__device__ __forceinline__ void mx_store(const tx_quant_args &a, int64_t t, int64_t nb, const float (&v)[32 / MxLanes<XT>]) {
+  constexpr int L = MxLanes<XT>, E = 32 / L;
   constexpr float FMAX = FMT == E4M3FN ? 448.0f : 57344.0f;
-  const int64_t blk = t >> 2;
+  const int64_t blk = t / L;
   const int64_t r = blk / nb, cb = blk % nb;
-  const int64_t col = cb * 32 + (t & 3) * 8;
+  const int64_t col = cb * 32 + (t % L) * E;
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) amax = absmax_step(amax, v[i]);
-  amax = absmax_step(amax, __shfl_xor(amax, 1));
-  amax = absmax_step(amax, __shfl_xor(amax, 2));
+  for (int i = 0; i < E; ++i) amax = absmax_step(amax, v[i]);
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) amax = absmax_step(amax, __shfl_xor(amax, o));
   const float descale = amax / FMAX;
   const uint32_t e = ((__float_as_uint(descale) + 0x007FFFFFu) & 0x7F800000u) >> 23;
   const float rounded = __uint_as_float(e << 23);
   const float quant = e == 0 ? 0.0f : 1.0f / rounded;
-  float c0[4], c1[4];
+  uint32_t code[E / 4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    c0[i] = clamp_keep_nan<FMT>(v[i] * quant);
-    c1[i] = clamp_keep_nan<FMT>(v[i + 4] * quant);
+  for (int k = 0; k < E / 4; ++k) {
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = clamp_keep_nan<FMT>(v[4 * k + i] * quant);
+    code[k] = encode_clamped4_hw<FMT>(c);
   }
-  const uint32_t lo = encode_clamped4_hw<FMT>(c0), hi = encode_clamped4_hw<FMT>(c1);
   uint8_t *qrow = a.q + r * a.ldq;
   if (a.vec) {
-    *reinterpret_cast<txd::u32x2 *>(qrow + col) = txd::u32x2{lo, hi};
+#pragma unroll
+    for (int k = 0; k < E / 8; ++k)
+      *reinterpret_cast<txd::u32x2 *>(qrow + col + 8 * k) = txd::u32x2{code[2 * k], code[2 * k + 1]};
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qrow[col + i] = uint8_t((i < 4 ? lo >> (8 * i) : hi >> (8 * (i - 4))) & 0xFFu);
+    for (int i = 0; i < E; ++i) qrow[col + i] = uint8_t((code[i / 4] >> (8 * (i % 4))) & 0xFFu);
   }
-  if ((t & 3) == 0) static_cast<uint8_t *>(a.scales)[r * a.ld_s + cb] = uint8_t(e);
+  if (t % L == 0) static_cast<uint8_t *>(a.scales)[r * a.ld_s + cb] = uint8_t(e);
 }
 
 // MX quantiser, following the reference's _compute_scale_and_quantize
@@ -597,25 +610,21 @@ __device__ __forceinline__ void mx_store(const tx_quant_args &a, int64_t t, int6
 //   e        = ((bits(descale) + 0x007FFFFF) & 0x7F800000) >> 23   -> the e8m0 scale
 //   q        = fp8_rne(clamp(x * (1 / 2^(e-127)), +-fmax))  (x * 0 when e = 0;
 //              NaN inputs stay NaN), converted by encode_clamped4_hw
-// Four lanes share a block, eight elements each; the block's amax is
-// combined with two lane exchanges.  (Taking two or four blocks per trip,
+// MxLanes<XT> lanes share a block; the block's amax is combined with one
+// (bf16) or two (fp32) lane exchanges.  (Taking two or four blocks per trip,
 // their loads issued together, measured 7-16% slower at 8192 x 8192.)
 template <int FMT, int XT>
 __device__ __forceinline__ void quant_mx(const tx_quant_args &a) {
-  constexpr int U = 1;
+  constexpr int L = MxLanes<XT>;
   const int64_t nb = a.K / 32;
-  const int64_t total = a.rows * nb * 4;
+  const int64_t total = a.rows * nb * L;
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-  // total and stride are multiples of 4, so the 4 lanes of a block are
-  // always active together
-  for (int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t0 < total; t0 += U * stride) {
-    float v[U][8];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (t0 + u * stride < total) mx_load<XT>(a, t0 + u * stride, nb, v[u]);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (t0 + u * stride < total) mx_store<FMT>(a, t0 + u * stride, nb, v[u]);
+  // total and stride are multiples of L, so the lanes of a block are always
+  // active together
+  for (int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t0 < total; t0 += stride) {
+    float v[32 / L];
+    mx_load<XT>(a, t0, nb, v);
+    mx_store<FMT, XT>(a, t0, nb, v);
   }
 }
 
