@@ -359,6 +359,30 @@ def test_fp8_skinny_shapes(tx, oracle, dev, M, N, K, fa, fb):
     check_close(C, r32, r16, FP8_TOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 8200, 1024), (5, 100, 640), (33, 300, 384), (40, 3000, 256)])
+def test_fp8_skinny_strided(tx, oracle, dev, M, N, K):
+    """The skinny kernel's buffer ranges follow the row pitch: A and B as
+    K-column views of wider rows (lda = K + 128, ldb = K + 256), with ragged
+    last 16-row blocks of M and N; the bytes past K in each row are NaN codes
+    that must never be read."""
+    g = np.random.default_rng(M * 7 + N)
+    aq = g.integers(0, 256, size=(M, K), dtype=np.uint8)
+    bq = g.integers(0, 256, size=(N, K), dtype=np.uint8)
+    for q in (aq, bq):
+        q[(q & 0x7F) == 0x7F] &= 0xFE
+    a_wide = np.full((M, K + 128), 0x7F, dtype=np.uint8)
+    b_wide = np.full((N, K + 256), 0x7F, dtype=np.uint8)
+    a_wide[:, :K] = aq
+    b_wide[:, :K] = bq
+    sa = g.uniform(0.5, 2, M).astype(np.float32) * 1e-3
+    sb = g.uniform(0.5, 2, N).astype(np.float32) * 1e-3
+    A = torch.from_numpy(a_wide).to(dev).view(torch.float8_e4m3fn)[:, :K]
+    B = torch.from_numpy(b_wide).to(dev).view(torch.float8_e4m3fn)[:, :K]
+    C = _np_bits(tx.dot_scaled_rowcol(A, torch.from_numpy(sa).to(dev), B, torch.from_numpy(sb).to(dev)))
+    r32, r16 = oracle.gemm_fp8_scaled_rows(aq, bq, sa, sb, 0, M)
+    check_close(C, r32, r16, FP8_TOL)
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (512, 14336, 4096), (8192, 14336, 4096),
                                    (16, 4096, 14336), (512, 4096, 14336), (8192, 4096, 14336),
                                    (8192, 8192, 8192)])
