@@ -120,9 +120,10 @@ __device__ __forceinline__ void gemv_body(const tx_gemv_args &a) {
       for (int j = 0; j < 4; ++j)
         f.w[b][j] = __builtin_nontemporal_load(reinterpret_cast<const txd::u32x4 *>(wp[b][j] + off));
   };
-  // x fragments of round q (slices past the wave's range repeat its last one).
-  // They are loaded a round ahead and before the W loads two rounds ahead, so
-  // waiting for them (memory counters retire in order) never waits for W.
+  // x fragments and group scales of round q (slices past the wave's range
+  // repeat its last one), loaded just before the round's W, two rounds ahead
+  // of use: waiting for them (memory counters retire in order) then waits only
+  // for loads issued before them, never for a later W round.
   // With more than one 16-row block of x, or 16 wavefronts (128 registers
   // each), two rounds of fragments would not fit the registers: those kernels
   // load x where it is used (and wait for the W round in flight before it).
