@@ -130,6 +130,41 @@ def test_reference_test_op_8192(tx, oracle, dev):
     assert rel.item() <= TOL, rel.item()
 
 
+@pytest.mark.parametrize("fmt,out_fmt", [(F16, F16), (F16, BF16), (BF16, BF16), (BF16, F16)])
+def test_row_major_b_read_in_tile(tx, oracle, dev, fmt, out_fmt):
+    """Products the persistent tile takes (at least one 256 x 256 tile per CU,
+    K a whole number of 64-element steps, N a multiple of 8) read the
+    row-major b in place through transposing LDS reads.  Partial last row and
+    column tiles; every output element against the oracle, then tile by tile
+    so that a misplaced block cannot hide behind the others."""
+    M, N, K = 4100, 4104, 192
+    A, Bkn = _inputs(M, N, K, fmt, seed=M + N + K + fmt)
+    odt = torch.float16 if out_fmt == F16 else torch.bfloat16
+    C = tx.dot_kn(_t(A, fmt, dev), _t(Bkn, fmt, dev), out_dtype=odt)
+    r32, r16 = oracle.gemm16_rows(A, Bkn, 0, M, fmt=fmt, b_kn=True, out_fmt=out_fmt)
+    got = _bits(C)
+    check16(got, r32, r16, out_fmt)
+    for m0 in range(0, M, 256):
+        for n0 in range(0, N, 256):
+            t = (slice(m0, m0 + 256), slice(n0, n0 + 256))
+            check16(got[t], r32[t], r16[t], out_fmt)
+
+
+def test_row_major_b_read_in_tile_strided(tx, oracle, dev):
+    """b a view of wider K rows (pitch N + 72) whose padding holds NaN codes:
+    the last column tile reads the padding into columns past N, whose
+    products are dropped; no NaN may reach a stored column."""
+    M, N, K = 4096, 4032, 256
+    A, Bkn = _inputs(M, N, K, F16, seed=77)
+    bbig = torch.full((K, N + 72), float("nan"), dtype=torch.float16, device=dev)
+    b = bbig[:, :N]
+    b.copy_(_t(Bkn, F16, dev))
+    C = tx.dot_kn(_t(A, F16, dev), b)
+    assert not torch.isnan(C).any()
+    r32, r16 = oracle.gemm16_rows(A, Bkn, 0, M, fmt=F16, b_kn=True)
+    check16(_bits(C), r32, r16, F16)
+
+
 @pytest.mark.parametrize("S", [256, 512, 1024, 2048, 4096])
 def test_reference_benchmark_shapes(tx, oracle, dev, S):
     A, Bkn = _inputs(S, S, S, F16, seed=S)

@@ -362,6 +362,26 @@ static tx_status transpose_kn(const char *what, tx_gemm_args &args, hipStream_t 
   return TX_SUCCESS;
 }
 
+// A row-major K x N B read in place by the persistent tile (`base`_persist_kn):
+// a product launch_fast would give that tile (at least one 256 x 256 tile
+// per CU, no column strip split off, the `_persist` conditions: K a whole
+// number of 64-element steps, N a multiple of 8, C rows 16-byte aligned),
+// A and B and their rows 16-byte aligned, and both addressable with 32-bit
+// byte offsets (B: its K rows plus a 256-column tile).
+static bool persist_kn_ok(const tx_gemm_args &args) {
+  const int64_t M = args.M, N = args.N, K = args.K, cus = cu_count();
+  const int64_t tiles_m = (M + 255) / 256, full = N / 256, tail = N % 256;
+  if (tiles_m * ((N + 255) / 256) < cus) return false;
+  const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
+  const int64_t rounds_main = (tiles_m * full + cus - 1) / cus;
+  if (full > 0 && tail > 0 && tail <= kStripMaxN && rounds_main < rounds_all) return false;
+  const char *pv = persist_variant(args, K * 2, 2);
+  if (!pv || std::strcmp(pv, "_persist") != 0) return false;
+  const int64_t lim = int64_t(1) << 31;
+  return aligned(args.A, 16) && (args.lda * 2) % 16 == 0 && (M - 1) * args.lda * 2 + K * 2 + 16 < lim &&
+         aligned(args.B, 16) && (args.ldb * 2) % 16 == 0 && (K - 1) * args.ldb * 2 + N * 2 + 512 < lim;
+}
+
 // tt.dot with 16-bit operands (bf16 / fp16) and a 16-bit output.  Kernel
 // names: tx_gemm_<operands>_<variant>[_out_<output>]; the split-K reduce
 // is the output type's.
@@ -390,6 +410,18 @@ static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda
   tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
                     int32_t(K), 0, 0, 0};
   if (kn) {
+    if (persist_kn_ok(args)) {
+      // the persistent tile reads the row-major B itself (no transpose pass)
+      char kname[96];
+      std::snprintf(kname, sizeof kname, "%s_persist_kn", base);
+      args.tiles_m = int32_t((M + 255) / 256);
+      args.tiles_n = int32_t((N + 255) / 256);
+      args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
+      hipFunction_t fn;
+      TX_TRY(get_kernel(CodeObject::GemmBf16, kname, &fn));
+      const int64_t grid = std::min<int64_t>(int64_t(args.tiles_m) * args.tiles_n, cu_count());
+      return launch(fn, unsigned(grid), 1, 64 * kPersistWaves, s, &args, sizeof args, kname);
+    }
     ScratchLease ws;  // held until every launch using it is enqueued
     TX_TRY(transpose_kn(what, args, s, ws));
     return launch_fast(base, reduce, CodeObject::GemmBf16, args, int64_t(args.K) * 2, 2, s, true);

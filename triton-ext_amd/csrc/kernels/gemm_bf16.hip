@@ -57,7 +57,9 @@ TX_GEMM16_FAST(f16, EL_F16, _out_bf16, OUT_BF16)
 // for products of at least one 256 x 256 tile per CU whose K is a whole
 // number (>= 2) of 64-element steps, N a multiple of 8 and C 16-byte aligned;
 // _persist_kt: any K of at least 128 elements, rows of A and B 4-byte
-// aligned, C rows of any alignment.
+// aligned, C rows of any alignment; _persist_kn: B row-major K x N (ldb
+// elements per K row), K a whole number of 64-element steps, B and its rows
+// 16-byte aligned.
 #include "gemm_persist.h"
 
 #define TX_GEMM16_PERSIST(PFX, EL, SFX, OUT)                                                              \
@@ -66,6 +68,9 @@ TX_GEMM16_FAST(f16, EL_F16, _out_bf16, OUT_BF16)
   }                                                                                                       \
   TX_KERNEL void __launch_bounds__(256) tx_gemm_##PFX##_fast##SFX##_persist_kt(const tx_gemm_args a) { \
     gemm_persist<GemmCfg<EL, EL, 256, 256, 2, 2, 16>, OUT, false, true>(a);                                \
+  }                                                                                                       \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_##PFX##_fast##SFX##_persist_kn(const tx_gemm_args a) { \
+    gemm_persist<GemmCfg<EL, EL, 256, 256, 2, 2, 16>, OUT, false, false, true>(a);                         \
   }
 
 TX_GEMM16_PERSIST(bf16, EL_BF16, , OUT_BF16)

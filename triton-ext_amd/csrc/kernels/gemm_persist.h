@@ -46,6 +46,18 @@ namespace txg {
 namespace persist {
 constexpr int kWaves = 4;
 
+// Chunk swizzle of a K-major B slot (row-major K x N operand), by K row mod 4.
+__device__ __forceinline__ constexpr int kn_swz(int rho) { return ((rho << 1) ^ (rho << 2)) & 14; }
+
+// s_waitcnt lgkmcnt(N) that the two fragments depend on (their values come
+// from LDS reads issued in inline asm, which the compiler does not wait for).
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tie(txd::i32x4 &x, txd::i32x4 &y) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
+}
+// The same dependency on a wait already made (the barrier's).
+__device__ __forceinline__ void tie(txd::i32x4 &x, txd::i32x4 &y) { asm volatile("" : "+v"(x), "+v"(y)); }
+
 // Buffer resource for rows r0 .. r0 + 255 of an operand with `rows` rows of
 // `ld_b` bytes, K step bytes kb_end: rows past the operand's end are outside
 // the range.
@@ -61,11 +73,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, in
 // shared fields q->g: tile t of the workgroup is (problem p, m tile, n tile)
 // of expert p's rows offsets[p] .. offsets[p + 1] of A, C and scale_a against
 // B + p stride_b and scale_b + p stride_sb.
-template <class C, int OUT = OUT_BF16, bool GROUPED = false, bool KTAIL = false>
+//
+// BKN: B is row-major K x N (16-bit operands, K a whole number of steps).  A
+// step of B is then 64 K rows of the tile's 256 columns (512 bytes each),
+// DMA'd into a K-major slot whose 16-byte chunk c of K row k sits at
+// c ^ kn_swz(k mod 4), and each B fragment is two transposing LDS reads
+// (ds_read_b64_tr_b16): in each 16-lane group, lane s reads 4 columns at K
+// row s / 4 and lane d receives column d's 4 K values, the register layout
+// the MFMA takes.  The swizzle keeps a group's 4 rows x 2 chunks on 8
+// distinct 16-byte bank groups of 128 bytes, and a 32-lane half's 4 rows x
+// 4 chunks on 16 of 256 bytes.
+template <class C, int OUT = OUT_BF16, bool GROUPED = false, bool KTAIL = false, bool BKN = false>
 __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_grouped_args *q = nullptr) {
   using namespace fast;
   static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "bf16 output, or fp16 out of 16-bit operands");
   static_assert(!KTAIL || (!C::FP8 && !GROUPED), "ragged K: 16-bit operands, one product");
+  static_assert(!BKN || (!C::FP8 && !GROUPED && !KTAIL), "row-major B: 16-bit operands, whole K steps");
   constexpr int NW = persist::kWaves;
   constexpr int TM = 128, TN = 128, FM = 4, FN = 4;
   constexpr int NM = FM * FN, NF = FM + FN, NR = 2 * NF;
@@ -99,9 +122,18 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     vo[0][e] = uint32_t(8 * (BLKA * wave + e) + (lane >> 3)) * lda_b + kch[e];
-    vo[1][e] = uint32_t(8 * (BLKB * wave + e) + (lane >> 3)) * ldb_b + kch[e];
+    if constexpr (BKN) {
+      // block j: K rows 2 (BLKB wave + j) and + 1 of the step, lane p
+      // filling chunk position p mod 32 of row + p / 32
+      const int kr = 2 * (BLKB * wave + e) + (lane >> 5);
+      vo[1][e] = uint32_t(kr) * ldb_b + 16u * uint32_t((lane & 31) ^ persist::kn_swz(kr & 3));
+    } else {
+      vo[1][e] = uint32_t(8 * (BLKB * wave + e) + (lane >> 3)) * ldb_b + kch[e];
+    }
   }
-  const uint32_t ld8[2] = {8u * lda_b, 8u * ldb_b};
+  const uint32_t ld8[2] = {8u * lda_b, (BKN ? 2u : 8u) * ldb_b};
+  // bytes of an operand's K step in its rows
+  const uint32_t kstep_b[2] = {uint32_t(kStep), BKN ? 64u * ldb_b : uint32_t(kStep)};
   // KTAIL: the lane offsets of the last K step (scalar offset - 16 there)
   const KTail kt = make_ktail(kb_end);
   uint32_t vl[2][2];
@@ -167,8 +199,15 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     constexpr int op = decltype(op_tag)::value;
     if (c.t < T) {
       const TileDesc d = desc(c.t);
-      c.rs = op == 0 ? persist::tile_rsrc(d.A, d.tm * 256, d.rows, lda_b, kb_end)
-                     : persist::tile_rsrc(d.B, d.tn * 256, a.N, ldb_b, kb_end);
+      if constexpr (BKN && op == 1) {
+        // columns 256 tn .. of all K rows, the range ending at the last
+        // row's last column (columns past N in earlier rows read that
+        // row's padding or the next row: their products are not stored)
+        c.rs = make_rsrc(d.B + int64_t(d.tn) * 512, uint32_t(a.K - 1) * ldb_b + uint32_t(a.N - d.tn * 256) * 2u);
+      } else {
+        c.rs = op == 0 ? persist::tile_rsrc(d.A, d.tm * 256, d.rows, lda_b, kb_end)
+                       : persist::tile_rsrc(d.B, d.tn * 256, a.N, ldb_b, kb_end);
+      }
     } else {
       c.rs = make_rsrc(op == 0 ? a.A : a.B, 0u);
     }
@@ -186,7 +225,8 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
     const bool lk = KTAIL && c.k == KS - 1;  // (c.k >= 1 there)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *)dst, 16, lk ? vl[op][j & 1] : vo[op][j & 1],
-                                             uint32_t(c.k) * kStep + uint32_t(j & ~1) * ld8[op] - (lk ? 16u : 0u),
+                                             uint32_t(c.k) * kstep_b[op] + uint32_t(j & ~1) * ld8[op] -
+                                                 (lk ? 16u : 0u),
                                              0, 0);
   };
 
@@ -200,13 +240,55 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
       ro[0][h][e] = off(wm * TM + frow, chunk);
       ro[1][h][e] = off(wn * TN + frow, chunk);
     }
+  // BKN: the B fragment reads' lane offsets in a slot, per 32-column block
+  // fn, for K row 16 g + s / 4 (g = lane / 32, s = lane mod 16) and columns
+  // 32 fn + 16 ((lane / 16) mod 2) + 4 (s mod 4) .. + 3 of the wave's; half
+  // h, piece e and read r add K rows 32 h + 8 e + 4 r (a multiple of 4, so
+  // the swizzle is the lane's).
+  int bko[BKN ? FN : 1];
+  const uint32_t lds_base = uint32_t(reinterpret_cast<uintptr_t>((lds_u8 *)lds));
+  if constexpr (BKN) {
+    const int s16 = lane & 15, rho = s16 >> 2;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int n = wn * TN + 32 * fn + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
+      bko[fn] = (16 * fg + rho) * 512 + (((n >> 3) ^ persist::kn_swz(rho)) << 4) + 8 * ((n >> 2) & 1);
+    }
+  }
   txd::i32x4 fr[2][NF][2];
   auto read = [&](int slot_a, int slot_b, auto h_tag, auto r_tag) {
     constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
     constexpr int f = o == 0 ? 0 : o == 1 ? FM : o <= FM ? o - 1 : o;
     const uint8_t *Sp = lds + (f < FM ? slot_a : slot_b) * kSlotBytes;
-    const int byte = f < FM ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - FM);
-    fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(Sp + byte);
+    if constexpr (BKN && f >= FM) {
+      // Inline asm: the compiler puts a vmcnt(0) (a drain of every operand
+      // load in flight) before the intrinsic form of this read whenever an
+      // LDS-DMA load is pending.  Its results are waited for explicitly:
+      // kn_wait in the K step's first half, the barrier in the second.
+      constexpr int c0 = (32 * h + 8 * e) * 512;
+      const uint32_t addr = lds_base + uint32_t((f < FM ? slot_a : slot_b) * kSlotBytes + bko[f - FM]);
+      txd::u32x2 lo, hi;
+      asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                   : "=&v"(lo), "=&v"(hi)
+                   : "v"(addr), "i"(c0), "i"(c0 + 4 * 512)
+                   : "memory");
+      fr[h][f][e] = txd::i32x4{int(lo[0]), int(lo[1]), int(hi[0]), int(hi[1])};
+    } else {
+      const int byte = f < FM ? ro[0][h][e] + 4096 * f : ro[1][h][e] + 4096 * (f - FM);
+      fr[h][f][e] = *reinterpret_cast<const txd::i32x4 *>(Sp + byte);
+    }
+  };
+  // BKN: wait for the first half's B block fn before its first MFMA.  The
+  // half's reads are issued in the order of `read`: A0 (2 LDS operations),
+  // B0 (4), A1, A2, A3 (2 each), B1, B2, B3 (4 each); LDS operations complete
+  // in order, so at most the operations issued after B fn may be left
+  // outstanding (capped at lgkmcnt's 15; extra scalar loads in flight only
+  // make the wait longer).  The asm ties the fragments to the wait.
+  auto kn_wait = [&](auto fn_tag) {
+    constexpr int fn = decltype(fn_tag)::value;
+    constexpr int after = fn == 0 ? 2 * (FM - 1) + 4 * (FN - 1) : 4 * (FN - 1 - fn);
+    constexpr int n = after > 15 ? 15 : after;
+    persist::lgkm_wait_tie<n>(fr[0][FM + fn][0], fr[0][FM + fn][1]);
   };
   txd::f32x16 acc[FN][FM];
   // MFMA i of a K half: B block i / FM against A block i % FM; FIRST: the
@@ -255,6 +337,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     if (clear) ktail_clear<NF>(fr[0], 0, fg, kt);
     static_for<NM>([&](auto I) {
       constexpr int i = decltype(I)::value;
+      if constexpr (BKN && i % FM == 0) kn_wait(std::integral_constant<int, i / FM>{});
       mma(H0{}, I, first_tag);
       __builtin_amdgcn_sched_barrier(0);
       constexpr int r0 = spread_lo(i, NR, RW), r1 = spread_hi(i, NR, RW);
@@ -262,6 +345,10 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
       __builtin_amdgcn_sched_barrier(0);
     });
     wait_and_barrier<VM>();
+    if constexpr (BKN) {
+      // the barrier's lgkmcnt(0) completed the second half's B reads
+      static_for<FN>([&](auto fn) { persist::tie(fr[1][FM + decltype(fn)::value][0], fr[1][FM + decltype(fn)::value][1]); });
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (clear) ktail_clear<NF>(fr[1], 1, fg, kt);
     static_for<NM>([&](auto I) {
