@@ -131,22 +131,26 @@ def test_reference_test_op_8192(tx, oracle, dev):
 
 
 @pytest.mark.parametrize("fmt,out_fmt", [(F16, F16), (F16, BF16), (BF16, BF16), (BF16, F16)])
-def test_row_major_b_read_in_tile(tx, oracle, dev, fmt, out_fmt):
+@pytest.mark.parametrize("shape", [(4100, 4104, 192),    # 256 x 256 tiles
+                                   (2100, 2056, 256),    # 128 x 128 tiles
+                                   (4096, 2048, 128)])   # 128 x 128, two tiles per workgroup
+def test_row_major_b_read_in_tile(tx, oracle, dev, fmt, out_fmt, shape):
     """Products the persistent tile takes (at least one 256 x 256 tile per CU,
-    K a whole number of 64-element steps, N a multiple of 8) read the
-    row-major b in place through transposing LDS reads.  Partial last row and
-    column tiles; every output element against the oracle, then tile by tile
-    so that a misplaced block cannot hide behind the others."""
-    M, N, K = 4100, 4104, 192
+    or else one 128 x 128 tile per CU; K a whole number of 64-element steps,
+    N a multiple of 8) read the row-major b in place through transposing LDS
+    reads.  Partial last row and column tiles; every output element against
+    the oracle, then tile by tile so that a misplaced block cannot hide
+    behind the others."""
+    M, N, K = shape
     A, Bkn = _inputs(M, N, K, fmt, seed=M + N + K + fmt)
     odt = torch.float16 if out_fmt == F16 else torch.bfloat16
     C = tx.dot_kn(_t(A, fmt, dev), _t(Bkn, fmt, dev), out_dtype=odt)
     r32, r16 = oracle.gemm16_rows(A, Bkn, 0, M, fmt=fmt, b_kn=True, out_fmt=out_fmt)
     got = _bits(C)
     check16(got, r32, r16, out_fmt)
-    for m0 in range(0, M, 256):
-        for n0 in range(0, N, 256):
-            t = (slice(m0, m0 + 256), slice(n0, n0 + 256))
+    for m0 in range(0, M, 128):
+        for n0 in range(0, N, 128):
+            t = (slice(m0, m0 + 128), slice(n0, n0 + 128))
             check16(got[t], r32[t], r16[t], out_fmt)
 
 

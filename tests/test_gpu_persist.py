@@ -1,8 +1,9 @@
 """GPU parity of the persistent 4-wavefront GEMM tile (gemm_persist.h).
 
 The library takes it for 256 x 256-tiled products with at least one tile per
-CU, K a whole number (>= 2) of 128-byte steps, N a multiple of 8 and a
-16-byte aligned C.  These shapes exercise what that tile adds over the
+CU (16-bit operands with fewer: 128 x 128 tiles, at least one per CU), K a
+whole number (>= 2) of 128-byte steps, N a multiple of 8 and a 16-byte
+aligned C.  These shapes exercise what that tile adds over the
 one-workgroup-per-tile kernel: workgroups that walk several tiles (tile
 counts that are and are not a multiple of the CU count), the operand stream
 crossing tile boundaries (the first steps of the next tile loaded during the
@@ -74,7 +75,11 @@ def test_persist_fp8_strided_out(tx, oracle, dev):
 
 
 @pytest.mark.parametrize("fmt,out_fmt", [(3, 3), (3, 6), (6, 6), (6, 3)])
-@pytest.mark.parametrize("M,N,K", [(4352, 4096, 128), (4196, 4168, 192)])
+@pytest.mark.parametrize("M,N,K", [(4352, 4096, 128), (4196, 4168, 192),
+                                   # fewer 256 x 256 tiles than CUs: 128 x 128 tiles
+                                   (2048, 2048, 256),    # one tile per CU
+                                   (2100, 2056, 192),    # partial last row and column tiles
+                                   (4096, 2048, 128)])   # two tiles per workgroup, two K steps
 def test_persist_16bit_full_output(tx, oracle, dev, fmt, out_fmt, M, N, K):
     import workloads
     g = np.random.default_rng(fmt * 7 + out_fmt + M)
@@ -95,3 +100,14 @@ def test_persist_16bit_full_output(tx, oracle, dev, fmt, out_fmt, M, N, K):
         scale = np.abs(ref).max()
         assert np.abs(got - ref).max() / scale <= BF16_TOL
         assert np.mean(C != r16) <= 0.05
+    # tile by tile (128 x 128 covers both tile sizes): a misplaced or
+    # skipped tile cannot hide behind the others
+    for m0 in range(0, M, 128):
+        for n0 in range(0, N, 128):
+            t = (slice(m0, m0 + 128), slice(n0, n0 + 128))
+            if out_fmt == 3:
+                check_close(C[t], r32[t], r16[t], BF16_TOL)
+            else:
+                ref = r32[t].astype(np.float64)
+                got = C[t].view(np.float16).astype(np.float64)
+                assert np.abs(got - ref).max() / np.abs(r32).max() <= BF16_TOL

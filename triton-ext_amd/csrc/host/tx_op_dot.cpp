@@ -193,6 +193,22 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
     }
     return launch_big(args);
   }
+  if (!narrow && persist && es == 2) {
+    // fewer 256 x 256 tiles than CUs, at least one 128 x 128 tile per CU:
+    // the persistent tile at 128 x 128 (16-bit operands), no K split
+    const char *pv = persist_variant(args, k_bytes, es);
+    const int64_t tm128 = (args.M + 127) / 128, tn128 = (args.N + 127) / 128;
+    if (tm128 * tn128 >= cus && pv && std::strcmp(pv, "_persist") == 0) {
+      std::snprintf(kname, sizeof kname, "%s_persist128", base);
+      args.tiles_m = int32_t(tm128);
+      args.tiles_n = int32_t(tn128);
+      args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
+      hipFunction_t fn;
+      TX_TRY(get_kernel(co, kname, &fn));
+      const int64_t grid = std::min<int64_t>(tm128 * tn128, cus);
+      return launch(fn, unsigned(grid), 1, 64 * kPersistWaves, s, &args, sizeof args, kname);
+    }
+  }
   std::snprintf(kname, sizeof kname, "%s_n128", base);
   const int64_t tiles = tiles_m * ((args.N + 127) / 128);
   const int64_t ksteps = (k_bytes + 127) / 128;
@@ -362,24 +378,32 @@ static tx_status transpose_kn(const char *what, tx_gemm_args &args, hipStream_t 
   return TX_SUCCESS;
 }
 
-// A row-major K x N B read in place by the persistent tile (`base`_persist_kn):
-// a product launch_fast would give that tile (at least one 256 x 256 tile
-// per CU, no column strip split off, the `_persist` conditions: K a whole
-// number of 64-element steps, N a multiple of 8, C rows 16-byte aligned),
-// A and B and their rows 16-byte aligned, and both addressable with 32-bit
-// byte offsets (B: its K rows plus a 256-column tile).
-static bool persist_kn_ok(const tx_gemm_args &args) {
+// A row-major K x N B read in place by the persistent tile: the tile edge
+// (256: `base`_persist_kn, 128: `base`_persist128_kn) launch_fast would give
+// the product (256: at least one 256 x 256 tile per CU and no column strip
+// split off; 128: fewer 256 x 256 tiles but at least one 128 x 128 tile per
+// CU), under the `_persist` conditions (K a whole number of 64-element
+// steps, N a multiple of 8, C rows 16-byte aligned), with A and B and their
+// rows 16-byte aligned and both addressable with 32-bit byte offsets (B: its
+// K rows plus a tile of columns).  0: the transpose pass instead.
+static int persist_kn_tile(const tx_gemm_args &args) {
   const int64_t M = args.M, N = args.N, K = args.K, cus = cu_count();
   const int64_t tiles_m = (M + 255) / 256, full = N / 256, tail = N % 256;
-  if (tiles_m * ((N + 255) / 256) < cus) return false;
-  const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
-  const int64_t rounds_main = (tiles_m * full + cus - 1) / cus;
-  if (full > 0 && tail > 0 && tail <= kStripMaxN && rounds_main < rounds_all) return false;
+  int bt = 256;
+  if (tiles_m * ((N + 255) / 256) < cus) {
+    if (((M + 127) / 128) * ((N + 127) / 128) < cus) return 0;
+    bt = 128;
+  } else {
+    const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
+    const int64_t rounds_main = (tiles_m * full + cus - 1) / cus;
+    if (full > 0 && tail > 0 && tail <= kStripMaxN && rounds_main < rounds_all) return 0;
+  }
   const char *pv = persist_variant(args, K * 2, 2);
-  if (!pv || std::strcmp(pv, "_persist") != 0) return false;
+  if (!pv || std::strcmp(pv, "_persist") != 0) return 0;
   const int64_t lim = int64_t(1) << 31;
-  return aligned(args.A, 16) && (args.lda * 2) % 16 == 0 && (M - 1) * args.lda * 2 + K * 2 + 16 < lim &&
-         aligned(args.B, 16) && (args.ldb * 2) % 16 == 0 && (K - 1) * args.ldb * 2 + N * 2 + 512 < lim;
+  const bool ok = aligned(args.A, 16) && (args.lda * 2) % 16 == 0 && (M - 1) * args.lda * 2 + K * 2 + 16 < lim &&
+                  aligned(args.B, 16) && (args.ldb * 2) % 16 == 0 && (K - 1) * args.ldb * 2 + N * 2 + 512 < lim;
+  return ok ? bt : 0;
 }
 
 // tt.dot with 16-bit operands (bf16 / fp16) and a 16-bit output.  Kernel
@@ -410,12 +434,12 @@ static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda
   tx_gemm_args args{A, B, C, nullptr, nullptr, lda, ldb, ldc, int32_t(M), int32_t(N),
                     int32_t(K), 0, 0, 0};
   if (kn) {
-    if (persist_kn_ok(args)) {
+    if (const int bt = persist_kn_tile(args)) {
       // the persistent tile reads the row-major B itself (no transpose pass)
       char kname[96];
-      std::snprintf(kname, sizeof kname, "%s_persist_kn", base);
-      args.tiles_m = int32_t((M + 255) / 256);
-      args.tiles_n = int32_t((N + 255) / 256);
+      std::snprintf(kname, sizeof kname, "%s_persist%s_kn", base, bt == 128 ? "128" : "");
+      args.tiles_m = int32_t((M + bt - 1) / bt);
+      args.tiles_n = int32_t((N + bt - 1) / bt);
       args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
       hipFunction_t fn;
       TX_TRY(get_kernel(CodeObject::GemmBf16, kname, &fn));

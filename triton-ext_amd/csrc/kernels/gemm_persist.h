@@ -1,18 +1,20 @@
 // Persistent 4-wavefront GEMM for aligned operands whose K is a whole number
 // of 128-byte steps (KTAIL, 16-bit operands: rows 4-byte aligned, any K of
 // at least two steps, read as fast::KTail describes, and C rows of any
-// alignment): one workgroup per CU walks its share of the 256 x 256
-// tiles, and the LDS-DMA pipeline of gemm_fast.h runs as one continuous
+// alignment): one workgroup per CU walks its share of the BT x BT tiles
+// (BT = 256, or 128 for products with fewer 256 x 256 tiles than CUs),
+// and the LDS-DMA pipeline of gemm_fast.h runs as one continuous
 // stream of (tile, K step) pairs, so the first steps of the next tile are
 // loaded while the current one finishes and no tile pays a pipeline fill.
 //
 // Layout per workgroup: 4 wavefronts (one per SIMD) in a 2 x 2 grid, each
-// owning a 128 x 128 block of the tile; the 16 accumulator blocks of 32 x 32
-// (256 registers) live in AGPRs.  Against the 8-wavefront tile this reads a
+// owning a BT / 2 square block of the tile; its accumulator blocks of 32 x 32
+// (BT = 256: 16 blocks, 256 registers) live in AGPRs.  Against the
+// 8-wavefront tile this reads a
 // third less from LDS per MFMA (1 KiB instead of 1.5), which the power-
 // limited clock turns into speed.
 //
-// The K loop is that of gemm_fast_tile_at (ring of 5 LDS slots of 32 KiB,
+// The K loop is that of gemm_fast_tile_at (ring of 5 LDS slots of BT x 128 bytes,
 // B of step s+2 and A of step s+3 loaded during the second half of step s,
 // fragments one 64-byte half ahead in registers, one barrier per step), with
 // s counting steps over all tiles of the workgroup.  Each operand's loads go
@@ -32,8 +34,9 @@
 // loads of step s+3 are deferred so that their LDS slot stages the output:
 // per 32 x 32 block the accumulators are scaled, rounded to bf16 / fp16
 // (RNE), and lanes l and l + 32 exchange halves (v_permlane32_swap); each
-// wave writes its 32 x 128 block to its own 8 KiB of that slot, reads back
-// 4 rows of 256 bytes per instruction and stores them through a buffer
+// wave writes its 32 x BT / 2 block to its own quarter of that slot, reads
+// back whole rows (BT = 256: 4 of 256 bytes) per instruction and stores them
+// through a buffer
 // resource for C (stores past M / N are dropped).  The first K step of each
 // tile starts its MFMAs from a zero accumulator operand, so the accumulators
 // are never cleared explicitly.
@@ -58,12 +61,13 @@ __device__ __forceinline__ void lgkm_wait_tie(txd::i32x4 &x, txd::i32x4 &y) {
 // The same dependency on a wait already made (the barrier's).
 __device__ __forceinline__ void tie(txd::i32x4 &x, txd::i32x4 &y) { asm volatile("" : "+v"(x), "+v"(y)); }
 
-// Buffer resource for rows r0 .. r0 + 255 of an operand with `rows` rows of
+// Buffer resource for rows r0 .. r0 + BT - 1 of an operand with `rows` rows of
 // `ld_b` bytes, K step bytes kb_end: rows past the operand's end are outside
 // the range.
+template <int BT>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, int r0, int rows, uint32_t ld_b,
                                                             uint32_t kb_end) {
-  const int valid = min(256, rows - r0);
+  const int valid = min(BT, rows - r0);
   return make_rsrc(static_cast<const uint8_t *>(base) + int64_t(r0) * ld_b, uint32_t(valid - 1) * ld_b + kb_end);
 }
 }  // namespace persist
@@ -75,7 +79,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, in
 // B + p stride_b and scale_b + p stride_sb.
 //
 // BKN: B is row-major K x N (16-bit operands, K a whole number of steps).  A
-// step of B is then 64 K rows of the tile's 256 columns (512 bytes each),
+// step of B is then 64 K rows of the tile's BT columns (2 BT bytes each),
 // DMA'd into a K-major slot whose 16-byte chunk c of K row k sits at
 // c ^ kn_swz(k mod 4), and each B fragment is two transposing LDS reads
 // (ds_read_b64_tr_b16): in each 16-lane group, lane s reads 4 columns at K
@@ -83,19 +87,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, in
 // the MFMA takes.  The swizzle keeps a group's 4 rows x 2 chunks on 8
 // distinct 16-byte bank groups of 128 bytes, and a 32-lane half's 4 rows x
 // 4 chunks on 16 of 256 bytes.
-template <class C, int OUT = OUT_BF16, bool GROUPED = false, bool KTAIL = false, bool BKN = false>
+template <class C, int OUT = OUT_BF16, bool GROUPED = false, bool KTAIL = false, bool BKN = false, int BT = 256>
 __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_grouped_args *q = nullptr) {
   using namespace fast;
   static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "bf16 output, or fp16 out of 16-bit operands");
   static_assert(!KTAIL || (!C::FP8 && !GROUPED), "ragged K: 16-bit operands, one product");
   static_assert(!BKN || (!C::FP8 && !GROUPED && !KTAIL), "row-major B: 16-bit operands, whole K steps");
+  static_assert(BT == 256 || BT == 128, "tile 256 x 256 or 128 x 128");
   constexpr int NW = persist::kWaves;
-  constexpr int TM = 128, TN = 128, FM = 4, FN = 4;
+  constexpr int TM = BT / 2, TN = BT / 2, FM = TM / 32, FN = TN / 32;
   constexpr int NM = FM * FN, NF = FM + FN, NR = 2 * NF;
-  constexpr int BLKA = 32 / NW, BLKB = 32 / NW, ND = BLKA + BLKB;
+  constexpr int SB = BT * kStep;  // one operand of one K step
+  constexpr int BLKA = SB / 1024 / NW, BLKB = BLKA, ND = BLKA + BLKB;
   constexpr int RW = NM / 2;
   constexpr bool ROWCOL = C::FP8;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
+  // BKN: bytes of a K row of the B tile, and K rows per 1 KiB DMA block
+  constexpr int KRB = 2 * BT, RPB = 1024 / KRB, CPR = KRB / 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * SB];
 
   // m tiles: the grouped product's real count is only on the device
   const int tiles_m = GROUPED ? q->tile_prefix[q->groups] : a.tiles_m;
@@ -123,15 +131,16 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
   for (int e = 0; e < 2; ++e) {
     vo[0][e] = uint32_t(8 * (BLKA * wave + e) + (lane >> 3)) * lda_b + kch[e];
     if constexpr (BKN) {
-      // block j: K rows 2 (BLKB wave + j) and + 1 of the step, lane p
-      // filling chunk position p mod 32 of row + p / 32
-      const int kr = 2 * (BLKB * wave + e) + (lane >> 5);
-      vo[1][e] = uint32_t(kr) * ldb_b + 16u * uint32_t((lane & 31) ^ persist::kn_swz(kr & 3));
+      // block j: K rows RPB (BLKB wave + j) .. + RPB - 1 of the step, lane p
+      // filling chunk position p mod CPR of row + p / CPR (row mod 4
+      // depends on the block's parity only)
+      const int kr = RPB * (BLKB * wave + e) + lane / CPR;
+      vo[1][e] = uint32_t(kr) * ldb_b + 16u * uint32_t((lane % CPR) ^ persist::kn_swz(kr & 3));
     } else {
       vo[1][e] = uint32_t(8 * (BLKB * wave + e) + (lane >> 3)) * ldb_b + kch[e];
     }
   }
-  const uint32_t ld8[2] = {8u * lda_b, (BKN ? 2u : 8u) * ldb_b};
+  const uint32_t ld8[2] = {8u * lda_b, (BKN ? uint32_t(RPB) : 8u) * ldb_b};
   // bytes of an operand's K step in its rows
   const uint32_t kstep_b[2] = {uint32_t(kStep), BKN ? 64u * ldb_b : uint32_t(kStep)};
   // KTAIL: the lane offsets of the last K step (scalar offset - 16 there)
@@ -200,13 +209,13 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     if (c.t < T) {
       const TileDesc d = desc(c.t);
       if constexpr (BKN && op == 1) {
-        // columns 256 tn .. of all K rows, the range ending at the last
+        // columns BT tn .. of all K rows, the range ending at the last
         // row's last column (columns past N in earlier rows read that
         // row's padding or the next row: their products are not stored)
-        c.rs = make_rsrc(d.B + int64_t(d.tn) * 512, uint32_t(a.K - 1) * ldb_b + uint32_t(a.N - d.tn * 256) * 2u);
+        c.rs = make_rsrc(d.B + int64_t(d.tn) * KRB, uint32_t(a.K - 1) * ldb_b + uint32_t(a.N - d.tn * BT) * 2u);
       } else {
-        c.rs = op == 0 ? persist::tile_rsrc(d.A, d.tm * 256, d.rows, lda_b, kb_end)
-                       : persist::tile_rsrc(d.B, d.tn * 256, a.N, ldb_b, kb_end);
+        c.rs = op == 0 ? persist::tile_rsrc<BT>(d.A, d.tm * BT, d.rows, lda_b, kb_end)
+                       : persist::tile_rsrc<BT>(d.B, d.tn * BT, a.N, ldb_b, kb_end);
       }
     } else {
       c.rs = make_rsrc(op == 0 ? a.A : a.B, 0u);
@@ -222,7 +231,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
   auto load_op = [&](const Cursor &c, int slot, auto op_tag, auto j_tag) {
     constexpr int op = decltype(op_tag)::value, j = decltype(j_tag)::value;
     constexpr int blk = op == 0 ? BLKA : BLKB;
-    uint8_t *dst = lds + slot * kSlotBytes + (blk * wave + j) * 1024;
+    uint8_t *dst = lds + slot * SB + (blk * wave + j) * 1024;
     const bool lk = KTAIL && c.k == KS - 1;  // (c.k >= 1 there)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *)dst, 16, lk ? vl[op][j & 1] : vo[op][j & 1],
                                              uint32_t(c.k) * kstep_b[op] + uint32_t(j & ~1) * ld8[op] -
@@ -252,25 +261,25 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
       const int n = wn * TN + 32 * fn + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
-      bko[fn] = (16 * fg + rho) * 512 + (((n >> 3) ^ persist::kn_swz(rho)) << 4) + 8 * ((n >> 2) & 1);
+      bko[fn] = (16 * fg + rho) * KRB + (((n >> 3) ^ persist::kn_swz(rho)) << 4) + 8 * ((n >> 2) & 1);
     }
   }
   txd::i32x4 fr[2][NF][2];
   auto read = [&](int slot_a, int slot_b, auto h_tag, auto r_tag) {
     constexpr int h = decltype(h_tag)::value, r = decltype(r_tag)::value, e = r % 2, o = r / 2;
     constexpr int f = o == 0 ? 0 : o == 1 ? FM : o <= FM ? o - 1 : o;
-    const uint8_t *Sp = lds + (f < FM ? slot_a : slot_b) * kSlotBytes;
+    const uint8_t *Sp = lds + (f < FM ? slot_a : slot_b) * SB;
     if constexpr (BKN && f >= FM) {
       // Inline asm: the compiler puts a vmcnt(0) (a drain of every operand
       // load in flight) before the intrinsic form of this read whenever an
       // LDS-DMA load is pending.  Its results are waited for explicitly:
       // kn_wait in the K step's first half, the barrier in the second.
-      constexpr int c0 = (32 * h + 8 * e) * 512;
-      const uint32_t addr = lds_base + uint32_t((f < FM ? slot_a : slot_b) * kSlotBytes + bko[f - FM]);
+      constexpr int c0 = (32 * h + 8 * e) * KRB;
+      const uint32_t addr = lds_base + uint32_t((f < FM ? slot_a : slot_b) * SB + bko[f - FM]);
       txd::u32x2 lo, hi;
       asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
                    : "=&v"(lo), "=&v"(hi)
-                   : "v"(addr), "i"(c0), "i"(c0 + 4 * 512)
+                   : "v"(addr), "i"(c0), "i"(c0 + 4 * KRB)
                    : "memory");
       fr[h][f][e] = txd::i32x4{int(lo[0]), int(lo[1]), int(hi[0]), int(hi[1])};
     } else {
@@ -375,22 +384,25 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
   // The epilogue issues exactly kEpiStores stores per wave, then the last
   // step's deferred BLKA loads of A; the next tile's first barrier may
   // leave all of them in flight.
-  constexpr int kEpiStores = FM * 8;
+  // staging geometry: the wave's 32 x TN block as 32 rows of SRB bytes
+  // (CH 16-byte chunks), read back SPI rows per instruction
+  constexpr int SRB = 2 * TN, CH = SRB / 16, SPI = 64 / CH;
+  constexpr int kEpiStores = FM * (32 / SPI);
   using VmAfterEpi = std::integral_constant<int, BLKB + kEpiStores>;
   static_assert(BLKB + kEpiStores < 64, "vmcnt range");
   // Scale loads issued before the last step (row scales, 16 column-scale
   // vectors) that its barrier leaves in flight with the step's own A loads.
-  constexpr int kScaleLoads = ROWCOL ? FM + 16 : 0;
+  constexpr int kScaleLoads = ROWCOL ? FM + 4 * FN : 0;
   using VmLast = std::integral_constant<int, BLKA + kScaleLoads>;
   static_assert(BLKA + kScaleLoads < 64, "vmcnt range");
 
-  // Staging: wave w owns bytes 8 KiB w .. +8 KiB of the slot its last step's
-  // A s+3 loads would have filled (the same bytes those loads fill once the
-  // epilogue is done, so no other wave ever touches them): 32 rows x 256
-  // bytes, 16-byte chunk c of row r at c ^ (r % 16).
+  // Staging: wave w owns bytes 32 SRB w .. + 32 SRB of the slot its last
+  // step's A s+3 loads would have filled (the same bytes those loads fill
+  // once the epilogue is done, so no other wave ever touches them): 32 rows
+  // of SRB bytes, 16-byte chunk c of row r at c ^ (r % CH).
   for (int t = 0; t < T; ++t) {
     const TileDesc d = desc(t);
-    const int m0 = d.tm * 256, n0 = d.tn * 256;
+    const int m0 = d.tm * BT, n0 = d.tn * BT;
     // C as a buffer: a store whose row or column block lies past M / N gets
     // an offset past the range and is dropped (N is a multiple of 8, so a
     // 16-byte column block is wholly in or out).  KTAIL: rows of C may have
@@ -429,7 +441,9 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     const int stage_slot = sb;  // the last step's B slot: its A s+3 loads go there
     step(std::false_type{}, VmLast{}, std::true_type{});  // the last step (KS >= 2)
     if constexpr (ROWCOL) {
-      asm volatile("s_waitcnt vmcnt(%4)" : "+v"(sav[0]), "+v"(sav[1]), "+v"(sav[2]), "+v"(sav[3]) : "n"(BLKB));
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(BLKB) : "memory");
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) asm volatile("" : "+v"(sav[fm]));
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
         asm volatile("" : "+v"(sb4[fn][0]), "+v"(sb4[fn][1]), "+v"(sb4[fn][2]), "+v"(sb4[fn][3]));
@@ -437,9 +451,9 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     // Epilogue, per 32-row block fm: scale, round, and exchange halves so
     // that lane l < 32 holds columns 16 p .. 16 p + 7 and lane l + 32
     // columns 16 p + 8 .. + 15 of row l % 32 (p = 2 fn + pr); stage the
-    // wave's 32 x 128 block, then store 4 rows of 256 bytes per instruction.
-    uint8_t *stg = lds + stage_slot * kSlotBytes + wave * 8192;
-    const int srow = lane >> 4, schunk = lane & 15;  // read-back: row 4 i + srow, chunk schunk
+    // wave's 32 x TN block, then store SPI rows of SRB bytes per instruction.
+    uint8_t *stg = lds + stage_slot * SB + wave * (32 * SRB);
+    const int srow = lane / CH, schunk = lane % CH;  // read-back: row SPI i + srow, chunk schunk
     const int n_st = n0 + wn * TN + 8 * schunk;
     const uint32_t coloff = n_st < a.N ? uint32_t(n_st) * 2u + cmis : kOob;
     static_for<FM>([&](auto fm_tag) {
@@ -470,14 +484,14 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
             o[2 + d] = sw[1];
           }
           const int chunk = 2 * (2 * fn + pr) + fg;
-          *reinterpret_cast<txd::u32x4 *>(stg + frow * 256 + ((chunk ^ (frow & 15)) << 4)) =
+          *reinterpret_cast<txd::u32x4 *>(stg + frow * SRB + ((chunk ^ (frow & (CH - 1))) << 4)) =
               txd::u32x4{o[0], o[1], o[2], o[3]};
         }
       });
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = 4 * i + srow;
-        const txd::u32x4 w = *reinterpret_cast<const txd::u32x4 *>(stg + r * 256 + ((schunk ^ (r & 15)) << 4));
+      for (int i = 0; i < 32 / SPI; ++i) {
+        const int r = SPI * i + srow;
+        const txd::u32x4 w = *reinterpret_cast<const txd::u32x4 *>(stg + r * SRB + ((schunk ^ (r & (CH - 1))) << 4));
         const int m = m0 + wm * TM + fm * 32 + r;
         const uint32_t voff = (m >= d.rows || coloff == kOob) ? kOob : uint32_t(m) * uint32_t(a.ldc) * 2u + coloff;
         __builtin_amdgcn_raw_buffer_store_b128(w, crs, voff, 0, 0);
