@@ -258,8 +258,8 @@ def dot(a: torch.Tensor, b_nk: torch.Tensor, out: torch.Tensor | None = None, *,
 def dot_kn(a: torch.Tensor, b_kn: torch.Tensor, out: torch.Tensor | None = None, *,
            out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """dot with b stored row-major K x N (rows of N contiguous), the layout of
-    the reference's matmul caller; b is transposed into the library's stream
-    scratch first."""
+    the reference's matmul caller; read in place by the persistent tiles,
+    otherwise transposed into the library's stream scratch first."""
     return _dot16(a, b_kn, _lib.B_KN, out, out_dtype)
 
 
