@@ -133,10 +133,13 @@ def test_reference_test_op_8192(tx, oracle, dev):
 @pytest.mark.parametrize("fmt,out_fmt", [(F16, F16), (F16, BF16), (BF16, BF16), (BF16, F16)])
 @pytest.mark.parametrize("shape", [(4100, 4104, 192),    # 256 x 256 tiles
                                    (2100, 2056, 256),    # 128 x 128 tiles
-                                   (4096, 2048, 128)])   # 128 x 128, two tiles per workgroup
+                                   (4096, 2048, 128),    # 128 x 128, two tiles per workgroup
+                                   (1030, 1032, 192),    # 64 x 64 tiles
+                                   (2048, 1024, 128),    # 64 x 64, two tiles per workgroup
+                                   (512, 512, 512)])     # 64 x 64, fewer tiles than CUs
 def test_row_major_b_read_in_tile(tx, oracle, dev, fmt, out_fmt, shape):
     """Products the persistent tile takes (at least one 256 x 256 tile per CU,
-    or else one 128 x 128 tile per CU; K a whole number of 64-element steps,
+    or else one 128 x 128 or 64 x 64 tile per CU; K a whole number of 64-element steps,
     N a multiple of 8) read the row-major b in place through transposing LDS
     reads.  Partial last row and column tiles; every output element against
     the oracle, then tile by tile so that a misplaced block cannot hide
@@ -148,9 +151,10 @@ def test_row_major_b_read_in_tile(tx, oracle, dev, fmt, out_fmt, shape):
     r32, r16 = oracle.gemm16_rows(A, Bkn, 0, M, fmt=fmt, b_kn=True, out_fmt=out_fmt)
     got = _bits(C)
     check16(got, r32, r16, out_fmt)
-    for m0 in range(0, M, 128):
-        for n0 in range(0, N, 128):
-            t = (slice(m0, m0 + 128), slice(n0, n0 + 128))
+    tb = 64 if M * N <= 1 << 22 else 128
+    for m0 in range(0, M, tb):
+        for n0 in range(0, N, tb):
+            t = (slice(m0, m0 + tb), slice(n0, n0 + tb))
             check16(got[t], r32[t], r16[t], out_fmt)
 
 

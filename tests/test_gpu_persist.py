@@ -1,7 +1,8 @@
 """GPU parity of the persistent 4-wavefront GEMM tile (gemm_persist.h).
 
 The library takes it for 256 x 256-tiled products with at least one tile per
-CU (16-bit operands with fewer: 128 x 128 tiles, at least one per CU), K a
+CU (16-bit operands with fewer: 128 x 128, else 64 x 64 tiles, at least one
+per CU), K a
 whole number (>= 2) of 128-byte steps, N a multiple of 8 and a 16-byte
 aligned C.  These shapes exercise what that tile adds over the
 one-workgroup-per-tile kernel: workgroups that walk several tiles (tile
@@ -79,7 +80,13 @@ def test_persist_fp8_strided_out(tx, oracle, dev):
                                    # fewer 256 x 256 tiles than CUs: 128 x 128 tiles
                                    (2048, 2048, 256),    # one tile per CU
                                    (2100, 2056, 192),    # partial last row and column tiles
-                                   (4096, 2048, 128)])   # two tiles per workgroup, two K steps
+                                   (4096, 2048, 128),    # two tiles per workgroup, two K steps
+                                   # fewer 128 x 128 tiles than CUs: 64 x 64 tiles
+                                   (1024, 1024, 256),    # one tile per CU
+                                   (1030, 1032, 192),    # partial last row and column tiles
+                                   (2048, 1024, 128),    # two tiles per workgroup
+                                   # fewer 64 x 64 tiles than CUs, at most 32 K steps
+                                   (512, 512, 512), (200, 136, 1024)])
 def test_persist_16bit_full_output(tx, oracle, dev, fmt, out_fmt, M, N, K):
     import workloads
     g = np.random.default_rng(fmt * 7 + out_fmt + M)
@@ -100,11 +107,13 @@ def test_persist_16bit_full_output(tx, oracle, dev, fmt, out_fmt, M, N, K):
         scale = np.abs(ref).max()
         assert np.abs(got - ref).max() / scale <= BF16_TOL
         assert np.mean(C != r16) <= 0.05
-    # tile by tile (128 x 128 covers both tile sizes): a misplaced or
-    # skipped tile cannot hide behind the others
-    for m0 in range(0, M, 128):
-        for n0 in range(0, N, 128):
-            t = (slice(m0, m0 + 128), slice(n0, n0 + 128))
+    # tile by tile (blocks of 128 x 128, 64 x 64 for the small products:
+    # within one tile of every size taken): a misplaced or skipped tile
+    # cannot hide behind the others
+    tb = 64 if M * N <= 1 << 22 else 128
+    for m0 in range(0, M, tb):
+        for n0 in range(0, N, tb):
+            t = (slice(m0, m0 + tb), slice(n0, n0 + tb))
             if out_fmt == 3:
                 check_close(C[t], r32[t], r16[t], BF16_TOL)
             else:

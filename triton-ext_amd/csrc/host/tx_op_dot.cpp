@@ -133,6 +133,18 @@ const char *persist_variant(const tx_gemm_args &args, int64_t k_bytes, int es) {
   return es == 2 && aligned(args.C, 2) ? "_persist_kt" : nullptr;
 }
 
+// The persistent tile's edge for a product with fewer 256 x 256 tiles than
+// CUs: 128 with at least one 128 x 128 tile per CU, else 64 with at least one
+// 64 x 64 tile per CU, or with fewer when a tile is at most kSmallMaxSteps
+// 128-byte K steps (one short launch beats the K split and its reduce);
+// else 0 (the 256 x 128 tile with K split).
+constexpr int64_t kSmallMaxSteps = 32;
+int small_persist_tile(int64_t M, int64_t N, int64_t k_bytes, int64_t cus) {
+  for (int bt : {128, 64})
+    if (((M + bt - 1) / bt) * ((N + bt - 1) / bt) >= cus) return bt;
+  return (k_bytes + 127) / 128 <= kSmallMaxSteps ? 64 : 0;
+}
+
 // `narrow` sends the whole product to the 256 x 128 tile (the column tail
 // of a wide product: at most kStripMaxN columns, and any K the 256 x 128
 // tile takes, decided before the main part is launched).
@@ -194,18 +206,18 @@ tx_status launch_fast(const char *base, const char *reduce, CodeObject co, tx_ge
     return launch_big(args);
   }
   if (!narrow && persist && es == 2) {
-    // fewer 256 x 256 tiles than CUs, at least one 128 x 128 tile per CU:
-    // the persistent tile at 128 x 128 (16-bit operands), no K split
+    // fewer 256 x 256 tiles than CUs: the persistent tile at the edge
+    // small_persist_tile picks (16-bit operands), no K split
     const char *pv = persist_variant(args, k_bytes, es);
-    const int64_t tm128 = (args.M + 127) / 128, tn128 = (args.N + 127) / 128;
-    if (tm128 * tn128 >= cus && pv && std::strcmp(pv, "_persist") == 0) {
-      std::snprintf(kname, sizeof kname, "%s_persist128", base);
-      args.tiles_m = int32_t(tm128);
-      args.tiles_n = int32_t(tn128);
+    const int bt = small_persist_tile(args.M, args.N, k_bytes, cus);
+    if (bt && pv && std::strcmp(pv, "_persist") == 0) {
+      std::snprintf(kname, sizeof kname, "%s_persist%d", base, bt);
+      args.tiles_m = int32_t((args.M + bt - 1) / bt);
+      args.tiles_n = int32_t((args.N + bt - 1) / bt);
       args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);
       hipFunction_t fn;
       TX_TRY(get_kernel(co, kname, &fn));
-      const int64_t grid = std::min<int64_t>(tm128 * tn128, cus);
+      const int64_t grid = std::min<int64_t>(int64_t(args.tiles_m) * args.tiles_n, cus);
       return launch(fn, unsigned(grid), 1, 64 * kPersistWaves, s, &args, sizeof args, kname);
     }
   }
@@ -379,10 +391,10 @@ static tx_status transpose_kn(const char *what, tx_gemm_args &args, hipStream_t 
 }
 
 // A row-major K x N B read in place by the persistent tile: the tile edge
-// (256: `base`_persist_kn, 128: `base`_persist128_kn) launch_fast would give
-// the product (256: at least one 256 x 256 tile per CU and no column strip
-// split off; 128: fewer 256 x 256 tiles but at least one 128 x 128 tile per
-// CU), under the `_persist` conditions (K a whole number of 64-element
+// (256: `base`_persist_kn, 128 / 64: `base`_persist128_kn / _persist64_kn)
+// launch_fast would give the product (256: at least one 256 x 256 tile per
+// CU and no column strip split off; else small_persist_tile), under the
+// `_persist` conditions (K a whole number of 64-element
 // steps, N a multiple of 8, C rows 16-byte aligned), with A and B and their
 // rows 16-byte aligned and both addressable with 32-bit byte offsets (B: its
 // K rows plus a tile of columns).  0: the transpose pass instead.
@@ -391,8 +403,8 @@ static int persist_kn_tile(const tx_gemm_args &args) {
   const int64_t tiles_m = (M + 255) / 256, full = N / 256, tail = N % 256;
   int bt = 256;
   if (tiles_m * ((N + 255) / 256) < cus) {
-    if (((M + 127) / 128) * ((N + 127) / 128) < cus) return 0;
-    bt = 128;
+    bt = small_persist_tile(M, N, K * 2, cus);
+    if (!bt) return 0;
   } else {
     const int64_t rounds_all = (tiles_m * (full + (tail > 0)) + cus - 1) / cus;
     const int64_t rounds_main = (tiles_m * full + cus - 1) / cus;
@@ -437,7 +449,8 @@ static tx_status dot16(const char *what, const void *A, tx_dtype ab, int64_t lda
     if (const int bt = persist_kn_tile(args)) {
       // the persistent tile reads the row-major B itself (no transpose pass)
       char kname[96];
-      std::snprintf(kname, sizeof kname, "%s_persist%s_kn", base, bt == 128 ? "128" : "");
+      if (bt == 256) std::snprintf(kname, sizeof kname, "%s_persist_kn", base);
+      else std::snprintf(kname, sizeof kname, "%s_persist%d_kn", base, bt);
       args.tiles_m = int32_t((M + bt - 1) / bt);
       args.tiles_n = int32_t((N + bt - 1) / bt);
       args.group_m = std::min<int32_t>(kGroupM, args.tiles_m);

@@ -59,8 +59,9 @@ TX_GEMM16_FAST(f16, EL_F16, _out_bf16, OUT_BF16)
 // _persist_kt: any K of at least 128 elements, rows of A and B 4-byte
 // aligned, C rows of any alignment; _persist_kn: B row-major K x N (ldb
 // elements per K row), K a whole number of 64-element steps, B and its rows
-// 16-byte aligned; _persist128[_kn]: the same on 128 x 128 tiles, for
-// products with fewer 256 x 256 tiles than CUs.
+// 16-byte aligned; _persist128[_kn] / _persist64[_kn]: the same on 128 x 128
+// / 64 x 64 tiles, for products with fewer 256 x 256 / 128 x 128 tiles than
+// CUs.
 #include "gemm_persist.h"
 
 #define TX_GEMM16_PERSIST(PFX, EL, SFX, OUT)                                                              \
@@ -78,6 +79,12 @@ TX_GEMM16_FAST(f16, EL_F16, _out_bf16, OUT_BF16)
   }                                                                                                       \
   TX_KERNEL void __launch_bounds__(256) tx_gemm_##PFX##_fast##SFX##_persist128_kn(const tx_gemm_args a) { \
     gemm_persist<GemmCfg<EL, EL, 256, 256, 2, 2, 16>, OUT, false, false, true, 128>(a);                    \
+  }                                                                                                       \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_##PFX##_fast##SFX##_persist64(const tx_gemm_args a) {  \
+    gemm_persist<GemmCfg<EL, EL, 256, 256, 2, 2, 16>, OUT, false, false, false, 64>(a);                    \
+  }                                                                                                       \
+  TX_KERNEL void __launch_bounds__(256) tx_gemm_##PFX##_fast##SFX##_persist64_kn(const tx_gemm_args a) { \
+    gemm_persist<GemmCfg<EL, EL, 256, 256, 2, 2, 16>, OUT, false, false, true, 64>(a);                     \
   }
 
 TX_GEMM16_PERSIST(bf16, EL_BF16, , OUT_BF16)

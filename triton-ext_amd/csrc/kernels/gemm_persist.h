@@ -2,7 +2,8 @@
 // of 128-byte steps (KTAIL, 16-bit operands: rows 4-byte aligned, any K of
 // at least two steps, read as fast::KTail describes, and C rows of any
 // alignment): one workgroup per CU walks its share of the BT x BT tiles
-// (BT = 256, or 128 for products with fewer 256 x 256 tiles than CUs),
+// (BT = 256; 128 or 64 for products with fewer 256 x 256 / 128 x 128 tiles
+// than CUs),
 // and the LDS-DMA pipeline of gemm_fast.h runs as one continuous
 // stream of (tile, K step) pairs, so the first steps of the next tile are
 // loaded while the current one finishes and no tile pays a pipeline fill.
@@ -49,8 +50,12 @@ namespace txg {
 namespace persist {
 constexpr int kWaves = 4;
 
-// Chunk swizzle of a K-major B slot (row-major K x N operand), by K row mod 4.
-__device__ __forceinline__ constexpr int kn_swz(int rho) { return ((rho << 1) ^ (rho << 2)) & 14; }
+// Chunk swizzle of a K-major B slot (row-major K x N operand), by K row mod
+// 4, for K rows of krb bytes: 256 or more, (0, 6, 12, 10); 128 (8 chunks,
+// two rows per 256 bytes of banks), (0, 2, 4, 6).
+__device__ __forceinline__ constexpr int kn_swz(int rho, int krb) {
+  return krb >= 256 ? ((rho << 1) ^ (rho << 2)) & 14 : rho << 1;
+}
 
 // s_waitcnt lgkmcnt(N) that the two fragments depend on (their values come
 // from LDS reads issued in inline asm, which the compiler does not wait for).
@@ -81,25 +86,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *base, in
 // BKN: B is row-major K x N (16-bit operands, K a whole number of steps).  A
 // step of B is then 64 K rows of the tile's BT columns (2 BT bytes each),
 // DMA'd into a K-major slot whose 16-byte chunk c of K row k sits at
-// c ^ kn_swz(k mod 4), and each B fragment is two transposing LDS reads
+// c ^ kn_swz(k mod 4, 2 BT), and each B fragment is two transposing LDS reads
 // (ds_read_b64_tr_b16): in each 16-lane group, lane s reads 4 columns at K
 // row s / 4 and lane d receives column d's 4 K values, the register layout
 // the MFMA takes.  The swizzle keeps a group's 4 rows x 2 chunks on 8
 // distinct 16-byte bank groups of 128 bytes, and a 32-lane half's 4 rows x
-// 4 chunks on 16 of 256 bytes.
+// 4 chunks on 16 of 256 bytes (for 128-byte rows, two to 256 bytes of
+// banks: on 8 of 128 and on 16 half-row positions).
 template <class C, int OUT = OUT_BF16, bool GROUPED = false, bool KTAIL = false, bool BKN = false, int BT = 256>
 __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_grouped_args *q = nullptr) {
   using namespace fast;
   static_assert(OUT == OUT_BF16 || (OUT == OUT_F16 && !C::FP8), "bf16 output, or fp16 out of 16-bit operands");
   static_assert(!KTAIL || (!C::FP8 && !GROUPED), "ragged K: 16-bit operands, one product");
   static_assert(!BKN || (!C::FP8 && !GROUPED && !KTAIL), "row-major B: 16-bit operands, whole K steps");
-  static_assert(BT == 256 || BT == 128, "tile 256 x 256 or 128 x 128");
+  static_assert(BT == 256 || BT == 128 || BT == 64, "tile 256, 128 or 64 square");
   constexpr int NW = persist::kWaves;
   constexpr int TM = BT / 2, TN = BT / 2, FM = TM / 32, FN = TN / 32;
   constexpr int NM = FM * FN, NF = FM + FN, NR = 2 * NF;
   constexpr int SB = BT * kStep;  // one operand of one K step
   constexpr int BLKA = SB / 1024 / NW, BLKB = BLKA, ND = BLKA + BLKB;
-  constexpr int RW = NM / 2;
+  constexpr int RW = NM >= 2 ? NM / 2 : 1;
   constexpr bool ROWCOL = C::FP8;
   // BKN: bytes of a K row of the B tile, and K rows per 1 KiB DMA block
   constexpr int KRB = 2 * BT, RPB = 1024 / KRB, CPR = KRB / 16;
@@ -135,7 +141,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
       // filling chunk position p mod CPR of row + p / CPR (row mod 4
       // depends on the block's parity only)
       const int kr = RPB * (BLKB * wave + e) + lane / CPR;
-      vo[1][e] = uint32_t(kr) * ldb_b + 16u * uint32_t((lane % CPR) ^ persist::kn_swz(kr & 3));
+      vo[1][e] = uint32_t(kr) * ldb_b + 16u * uint32_t((lane % CPR) ^ persist::kn_swz(kr & 3, KRB));
     } else {
       vo[1][e] = uint32_t(8 * (BLKB * wave + e) + (lane >> 3)) * ldb_b + kch[e];
     }
@@ -261,7 +267,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
       const int n = wn * TN + 32 * fn + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
-      bko[fn] = (16 * fg + rho) * KRB + (((n >> 3) ^ persist::kn_swz(rho)) << 4) + 8 * ((n >> 2) & 1);
+      bko[fn] = (16 * fg + rho) * KRB + (((n >> 3) ^ persist::kn_swz(rho, KRB)) << 4) + 8 * ((n >> 2) & 1);
     }
   }
   txd::i32x4 fr[2][NF][2];
