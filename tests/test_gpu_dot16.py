@@ -173,6 +173,42 @@ def test_row_major_b_read_in_tile_strided(tx, oracle, dev):
     check16(_bits(C), r32, r16, F16)
 
 
+@pytest.mark.parametrize("kn", [False, True])
+@pytest.mark.parametrize("fmt", [F16, BF16])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 128),   # 256 x 256 persistent tile
+                                   (2048, 2048, 128),   # 128 x 128
+                                   (1024, 1024, 128),   # 64 x 64, one tile per CU
+                                   (512, 512, 128)])    # 64 x 64, fewer tiles than CUs
+def test_persistent_tiles_round_exactly_and_keep_nonfinite(tx, oracle, dev, kn, fmt, M, N, K):
+    """One nonzero per row of A, so every output is a single 16-bit product,
+    exact in fp32: each persistent tile size, with b as N x K and read in place
+    as row-major K x N, must round it as the oracle does, bit for bit, on every
+    output.  Row 0 of A holds +Inf and row 1 a NaN; column 5 of b is zero, so
+    row 0 is Inf with b's sign except NaN (Inf x 0) in column 5, and row 1 is
+    NaN throughout."""
+    g = np.random.default_rng(M + 7 * fmt + int(kn))
+    codes = (lambda x: x.astype(np.float16).view(np.uint16)) if fmt == F16 else (
+        lambda x: __import__("workloads").to_bf16_bits(x))
+    a = np.zeros((M, K), np.float32)
+    a[np.arange(M), np.arange(M) % K] = g.uniform(0.5, 2.0, M) * g.choice([-1.0, 1.0], M)
+    b = (g.uniform(0.5, 2.0, (K, N)) * g.choice([-1.0, 1.0], (K, N))).astype(np.float32)
+    b[:, 5] = 0.0
+    A, Bkn = codes(a), codes(b)
+    A[0, 0] = 0x7C00 if fmt == F16 else 0x7F80
+    A[1, 1] = 0x7E00 if fmt == F16 else 0x7FC0
+    at, bt = _t(A, fmt, dev), _t(Bkn, fmt, dev)
+    C = _bits(tx.dot_kn(at, bt) if kn else tx.dot(at, bt.t().contiguous()))
+    Cf = widen(C, fmt)
+    cols = np.arange(N) != 5
+    assert np.all(np.isinf(Cf[0, cols])) and np.array_equal(np.signbit(Cf[0, cols]), np.signbit(b[0, cols]))
+    assert np.isnan(Cf[0, 5]) and np.all(np.isnan(Cf[1]))
+    _, r16 = oracle.gemm16_rows(A, Bkn, 2, M, fmt=fmt, b_kn=True)
+    got = C[2:]
+    nz = widen(r16, fmt) != 0
+    assert np.array_equal(got[nz], r16[nz]), np.argwhere(got != r16)[:5]
+    assert np.all(widen(got[~nz], fmt) == 0)
+
+
 @pytest.mark.parametrize("S", [256, 512, 1024, 2048, 4096])
 def test_reference_benchmark_shapes(tx, oracle, dev, S):
     A, Bkn = _inputs(S, S, S, F16, seed=S)
