@@ -281,7 +281,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
       // LDS-DMA load is pending.  Its results are waited for explicitly:
       // kn_wait in the K step's first half, the barrier in the second.
       constexpr int c0 = (32 * h + 8 * e) * KRB;
-      const uint32_t addr = lds_base + uint32_t((f < FM ? slot_a : slot_b) * SB + bko[f - FM]);
+      const uint32_t addr = lds_base + uint32_t(slot_b * SB + bko[f - FM]);
       txd::u32x2 lo, hi;
       asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
                    : "=&v"(lo), "=&v"(hi)
@@ -295,7 +295,7 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
   };
   // BKN: wait for the first half's B block fn before its first MFMA.  The
   // half's reads are issued in the order of `read`: A0 (2 LDS operations),
-  // B0 (4), A1, A2, A3 (2 each), B1, B2, B3 (4 each); LDS operations complete
+  // B0 (4), A1 .. A(FM-1) (2 each), B1 .. B(FN-1) (4 each); LDS operations complete
   // in order, so at most the operations issued after B fn may be left
   // outstanding (capped at lgkmcnt's 15; extra scalar loads in flight only
   // make the wait longer).  The asm ties the fragments to the wait.
