@@ -360,8 +360,8 @@ TX_API tx_status tx_dot_bf16(const void *A, int64_t lda, const void *B,
  * A: row-major M x K, row stride lda (elements).
  * B: b_layout TX_B_NK (N rows of K, ldb >= K) or TX_B_KN (K rows of N,
  *    ldb >= N).  A TX_B_KN operand is read in place when the product takes
- *    the persistent tile (at least one 128 x 128 tile per CU, K a multiple
- *    of 64, N a multiple of 8, 16-byte aligned rows); otherwise it is first
+ *    the persistent tile (at least one 64 x 64 tile per CU or K <= 2048, K a
+ *    multiple of 64, N a multiple of 8, 16-byte aligned rows); otherwise it is first
  *    transposed into the library's stream scratch (N rows of K rounded up
  *    to 64, zero-filled), which fails with TX_GENERIC_FAILURE if that
  *    allocation fails.
