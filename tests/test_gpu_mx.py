@@ -173,6 +173,60 @@ def test_mx_quantised_config(tx, oracle, dev, M, N, K):
     assert np.array_equal(got2, 2 * got)
 
 
+def _tile_rows(M):
+    """Two rows of every 256-row tile (its first and a seeded one), the last row."""
+    g = np.random.default_rng(M)
+    rows = {M - 1}
+    for m0 in range(0, M, 256):
+        rows |= {m0, int(g.integers(m0, min(M, m0 + 256)))}
+    return sorted(rows)
+
+
+@pytest.mark.parametrize("M,N,K,fa,fb,out", [
+    (4096, 4096, 256, 1, 1, "bf16"),    # one tile per CU, two K steps
+    (4196, 4168, 384, 2, 1, "f16"),     # partial last row and column tiles
+    (4352, 4096, 256, 1, 2, "bf16"),    # 272 tiles: some workgroups walk two
+    (4096, 4352, 512, 2, 2, "bf16")])
+def test_mx_large_tiles(tx, oracle, dev, M, N, K, fa, fb, out):
+    """Products of at least one 256 x 256 tile per CU (several rounds of
+    workgroups, partial edge tiles), bf16 / fp16 out: two rows of every
+    256-row tile (all columns) against the oracle, and for bf16 the whole
+    output's exact doubling when every scale of A goes up by one."""
+    g = np.random.default_rng(M + N + K + fa)
+    aq, bq = _codes(g, (M, K), fa), _codes(g, (N, K), fb)
+    nb = K // 32
+    lo, hi = (108, 118) if out == "f16" else (118, 134)
+    sa = g.integers(lo, hi, (M, nb), dtype=np.uint8)
+    sb = g.integers(lo, hi, (N, nb), dtype=np.uint8)
+    got = _run(tx, dev, aq, sa, bq, sb, fa, fb, out)
+    for r in _tile_rows(M):
+        ref, mag, bmax = oracle.gemm_mx_rows(aq, sa, bq, sb, r, r + 1, fa, fb, block_max=True)
+        check_mx(got[r:r + 1], ref, mag, bmax, K, out)
+    if out == "bf16":
+        assert np.array_equal(_run(tx, dev, aq, sa + 1, bq, sb, fa, fb, out), 2 * got)
+
+
+@pytest.mark.parametrize("M,N,K,out", [(4096, 4096, 512, "bf16"), (4196, 4168, 768, "f16"),
+                                       (4352, 4096, 512, "bf16")])
+def test_mx_fp4_large_tiles(tx, oracle, dev, M, N, K, out):
+    """fp4 x fp4 products of at least one 256 x 256 tile per CU (two scale
+    dwords per row and step): two rows of every 256-row tile against the
+    oracle, and for bf16 the exact doubling under sa + 1."""
+    g = np.random.default_rng(M * 5 + N + K)
+    pa = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    pb = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    nb = K // 32
+    lo, hi = (112, 122) if out == "f16" else (118, 136)
+    sa = g.integers(lo, hi, (M, nb), dtype=np.uint8)
+    sb = g.integers(lo, hi, (N, nb), dtype=np.uint8)
+    got = _run_fp4(tx, dev, pa, sa, pb, sb, out)
+    for r in _tile_rows(M):
+        ref, mag, bmax = oracle.gemm_mx_rows(pa, sa, pb, sb, r, r + 1, fmt_a=4, fmt_b=4, block_max=True)
+        check_mx(got[r:r + 1], ref, mag, bmax, K, out)
+    if out == "bf16":
+        assert np.array_equal(_run_fp4(tx, dev, pa, sa + 1, pb, sb, out), 2 * got)
+
+
 def test_mx_table_op_and_errors(tx, oracle, dev):
     from tx import _lib
     g = np.random.default_rng(3)

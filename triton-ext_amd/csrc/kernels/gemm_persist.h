@@ -458,8 +458,21 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
     // that lane l < 32 holds columns 16 p .. 16 p + 7 and lane l + 32
     // columns 16 p + 8 .. + 15 of row l % 32 (p = 2 fn + pr); stage the
     // wave's 32 x TN block, then store SPI rows of SRB bytes per instruction.
+    // The accumulators are read below in inline asm, for which the compiler
+    // inserts no wait states after the MFMAs that write them: the last step's
+    // final MFMAs stay above this point, and 32 wait states (a 16-pass MFMA's
+    // result needs about 19) pass before the first read.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     uint8_t *stg = lds + stage_slot * SB + wave * (32 * SRB);
-    const int srow = lane / CH, schunk = lane % CH;  // read-back: row SPI i + srow, chunk schunk
+    // The lane's staging offsets are recomputed for each tile from an opaque
+    // copy of the lane index: hoisted out of the tile loop, they would hold
+    // registers through the whole K loop (fp8: 238 -> 206 VGPRs).
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int efrow = el & 31, efg = el >> 5;
+    const int srow = el / CH, schunk = el % CH;  // read-back: row SPI i + srow, chunk schunk
     const int n_st = n0 + wn * TN + 8 * schunk;
     const uint32_t coloff = n_st < a.N ? uint32_t(n_st) * 2u + cmis : kOob;
     static_for<FM>([&](auto fm_tag) {
@@ -489,8 +502,8 @@ __device__ __forceinline__ void gemm_persist(const tx_gemm_args &a, const tx_gro
             o[d] = sw[0];
             o[2 + d] = sw[1];
           }
-          const int chunk = 2 * (2 * fn + pr) + fg;
-          *reinterpret_cast<txd::u32x4 *>(stg + frow * SRB + ((chunk ^ (frow & (CH - 1))) << 4)) =
+          const int chunk = 2 * (2 * fn + pr) + efg;
+          *reinterpret_cast<txd::u32x4 *>(stg + efrow * SRB + ((chunk ^ (efrow & (CH - 1))) << 4)) =
               txd::u32x4{o[0], o[1], o[2], o[3]};
         }
       });
