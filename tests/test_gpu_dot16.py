@@ -173,6 +173,28 @@ def test_row_major_b_read_in_tile_strided(tx, oracle, dev):
     check16(_bits(C), r32, r16, F16)
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 128), (2048, 2048, 256), (1024, 1032, 192)])
+def test_row_major_b_in_tile_all_strided(tx, oracle, dev, M, N, K):
+    """The in-place row-major-b tiles (256, 128 and 64 square) on views: A
+    rows of K + 64 elements, b K rows of N + 72 with NaN codes in the
+    padding, and the output a view of rows N + 40 wide whose padding must
+    keep its contents."""
+    A, Bkn = _inputs(M, N, K, F16, seed=M + K)
+    abig = torch.zeros((M, K + 64), dtype=torch.float16, device=dev)
+    a = abig[:, :K]
+    a.copy_(_t(A, F16, dev))
+    bbig = torch.full((K, N + 72), float("nan"), dtype=torch.float16, device=dev)
+    b = bbig[:, :N]
+    b.copy_(_t(Bkn, F16, dev))
+    cbig = torch.full((M, N + 40), 0x7777, dtype=torch.int16, device=dev)
+    out = cbig.view(torch.float16)[:, :N]
+    tx.dot_kn(a, b, out=out)
+    allb = cbig.cpu().numpy().view(np.uint16)
+    assert np.all(allb[:, N:] == 0x7777)
+    r32, r16 = oracle.gemm16_rows(A, Bkn, 0, M, fmt=F16, b_kn=True)
+    check16(allb[:, :N], r32, r16, F16)
+
+
 @pytest.mark.parametrize("kn", [False, True])
 @pytest.mark.parametrize("fmt", [F16, BF16])
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 128),   # 256 x 256 persistent tile
