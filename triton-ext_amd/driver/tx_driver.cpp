@@ -2,7 +2,9 @@
 // libtxamd.so only (no Python, no torch), the way a Triton-extension host or
 // a C++ serving stack would drive the ops.  It prints the registration
 // table (txGetPluginInfo), runs each hot-path entry point once on device
-// buffers it allocates, and checks the results against closed forms: inputs
+// buffers it allocates, calls tt.fp_to_fp, tt.dot and tt.atomic_rmw again
+// through the table (txFindOp / txInvokeOp, the OpInfo operand convention),
+// and checks the results against closed forms: inputs
 // are chosen so that every output is exactly representable, so the checks
 // are bit-exact.  Without --check it then times the fp8 scaled GEMM at 8192^3
 // and the 16 Mi fp32 -> e4m3fn convert with HIP events, after enough untimed
@@ -175,6 +177,74 @@ void check_gemv() {
   HIP_CHECK(hipFree(dy));
 }
 
+tx_value ptr_v(const void *p) {
+  tx_value v{};
+  v.kind = TX_VALUE_PTR;
+  v.u.ptr = const_cast<void *>(p);
+  return v;
+}
+
+tx_value int_v(int64_t i) {
+  tx_value v{};
+  v.kind = TX_VALUE_INT;
+  v.u.i = i;
+  return v;
+}
+
+// The same ops through the registration table, as Triton's loader reaches a
+// plugin's ops: txFindOp / txInvokeOp with the OpInfo operand convention
+// (operands[0] the result slot, inputs after it, options as integers).
+void check_table_ops() {
+  std::printf("txFindOp / txInvokeOp\n");
+  const tx_op_info *dot = txFindOp("tt.dot");
+  expect(dot && dot->fn && dot->signature && std::strncmp(dot->signature, "C:", 2) == 0,
+         "tt.dot is registered with its operand signature");
+  expect(txFindOp("tt.no_such_op") == nullptr, "an unknown name is not found");
+  expect(txInvokeOp("tt.no_such_op", nullptr, 0, nullptr) == TX_UNKNOWN_OP, "invoking it returns TX_UNKNOWN_OP");
+
+  {  // tt.fp_to_fp: e4m3fn 0x38 (1.0) -> fp32
+    const int64_t n = 4096;
+    uint8_t *src = to_device(std::vector<uint8_t>(n, 0x38));
+    float *dst = nullptr;
+    HIP_CHECK(hipMalloc(&dst, n * sizeof(float)));
+    tx_value ops[7] = {ptr_v(dst), ptr_v(src), int_v(n), int_v(TX_FP8E4M3FN), int_v(TX_F32), int_v(TX_RTNE), int_v(0)};
+    TX_CHECK(txInvokeOp("tt.fp_to_fp", ops, 7, nullptr));
+    HIP_CHECK(hipDeviceSynchronize());
+    expect(all_equal(to_host(dst, n), 1.0f), "tt.fp_to_fp (7 operands): 4096 codes 0x38 decode to 1");
+    HIP_CHECK(hipFree(src));
+    HIP_CHECK(hipFree(dst));
+  }
+  {  // tt.dot, 9 operands: bf16, B N x K; A 1, B 0.5 -> C = 0.5 K
+    const int64_t M = 256, N = 256, K = 256;
+    uint16_t *dA = to_device(std::vector<uint16_t>(M * K, 0x3F80));
+    uint16_t *dB = to_device(std::vector<uint16_t>(N * K, 0x3F00));
+    uint16_t *dC = nullptr;
+    HIP_CHECK(hipMalloc(&dC, M * N * 2));
+    tx_value ops[9] = {ptr_v(dC), ptr_v(dA), ptr_v(dB), int_v(M), int_v(N), int_v(K), int_v(K), int_v(K), int_v(N)};
+    TX_CHECK(txInvokeOp("tt.dot", ops, 9, nullptr));
+    HIP_CHECK(hipDeviceSynchronize());
+    expect(all_equal(to_host(dC, M * N), uint16_t(0x4300)), "tt.dot (9 operands): 256^3 bf16, every output 128");
+    HIP_CHECK(hipFree(dA));
+    HIP_CHECK(hipFree(dB));
+    HIP_CHECK(hipFree(dC));
+  }
+  {  // tt.atomic_rmw: 2^16 int32 ones into 1024 bins, (3 i) mod 1024
+    const int64_t n = int64_t(1) << 16, nbins = 1024;
+    std::vector<int32_t> idx(n);
+    for (int64_t i = 0; i < n; ++i) idx[i] = int32_t((3 * i) % nbins);
+    int32_t *didx = to_device(idx), *dval = to_device(std::vector<int32_t>(n, 1));
+    int32_t *dbins = to_device(std::vector<int32_t>(nbins, 0));
+    tx_value ops[9] = {ptr_v(dbins), ptr_v(didx), ptr_v(dval), ptr_v(nullptr), ptr_v(nullptr),
+                       int_v(nbins), int_v(n),    int_v(TX_I32), int_v(TX_RMW_ADD)};
+    TX_CHECK(txInvokeOp("tt.atomic_rmw", ops, 9, nullptr));
+    HIP_CHECK(hipDeviceSynchronize());
+    expect(all_equal(to_host(dbins, nbins), int32_t(n / nbins)), "tt.atomic_rmw (9 operands): every bin counts 64");
+    HIP_CHECK(hipFree(didx));
+    HIP_CHECK(hipFree(dval));
+    HIP_CHECK(hipFree(dbins));
+  }
+}
+
 // Average milliseconds of `iters` launches of f after `warm` untimed ones.
 template <class F>
 float time_ms(F &&f, int warm, int iters) {
@@ -242,6 +312,7 @@ int main(int argc, char **argv) {
   check_dot_fp8();
   check_dot16_kn();
   check_gemv();
+  check_table_ops();
   if (!check_only && g_failures == 0) bench();
   std::printf("%d check(s) failed\n", g_failures);
   txShutdown();
