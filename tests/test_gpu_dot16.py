@@ -195,6 +195,24 @@ def test_row_major_b_in_tile_all_strided(tx, oracle, dev, M, N, K):
     check16(allb[:, :N], r32, r16, F16)
 
 
+@pytest.mark.parametrize("kn", [True, False])
+@pytest.mark.parametrize("fmt", [F16, BF16])
+@pytest.mark.parametrize("M,N,K", [(1, 8, 128), (3, 24, 192), (65, 72, 128), (17, 136, 256),
+                                   (200, 8, 2048), (130, 264, 640)])
+def test_tiny_products_on_the_persistent_tile(tx, oracle, dev, kn, fmt, M, N, K):
+    """Products far below one tile per CU that still meet the persistent
+    tile's conditions (K a whole number of 64-element steps, at least two and
+    at most 32 128-byte steps; N a multiple of 8; rows 16-byte aligned) run on
+    the 64 x 64 tile, with a row-major b read in place: from one partial tile
+    (M = 1, N = 8) to a few, every row, column and K position past the
+    product outside the buffer ranges (zeros in, stores dropped)."""
+    A, Bkn = _inputs(M, N, K, fmt, seed=5 * M + N + K)
+    a = _t(A, fmt, dev)
+    C = tx.dot_kn(a, _t(Bkn, fmt, dev)) if kn else tx.dot(a, _t(Bkn.T, fmt, dev))
+    r32, r16 = oracle.gemm16_rows(A, Bkn, 0, M, fmt=fmt, b_kn=True)
+    check16(_bits(C), r32, r16, fmt)
+
+
 @pytest.mark.parametrize("kn", [False, True])
 @pytest.mark.parametrize("fmt", [F16, BF16])
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 128),   # 256 x 256 persistent tile
